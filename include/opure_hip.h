@@ -1,0 +1,315 @@
+/*
+ * opure_hip.h -- the C-ABI that replaces the reference's D3D12 dispatch layer
+ * (src/core/Opure_Dx12.h, src/core/Opure_Shaders.h) for the speculative-
+ * decoding verify path, implemented with hand-written gfx950 HIP kernels.
+ *
+ * Conventions
+ *   - Every function returns int: OPURE_OK (0) or a negative OPURE_E_* code.
+ *     opure_last_error() returns the calling thread's last message.  No C++
+ *     exception crosses this boundary; the C++ engine turns codes back into
+ *     opure::Error, as OPURE_CHECK / ThrowError do (Opure_Platform.h:45-85).
+ *   - Device pointers are plain void* obtained from opure_buf_alloc (or any
+ *     HIP allocation on the same device).  Argument structs are POD and are
+ *     read during the call only.
+ *   - One stream per device.  Calls on one device are not thread-safe; the
+ *     caller serialises them (the reference's server does, Opure_Server.cpp:21-25).
+ *   - Kernel entry points enqueue work and return; opure_stream_sync waits.
+ *     Uploads and downloads are synchronous, like UploadToBuffer /
+ *     ReadbackFromBuffer (Opure_Dx12.h:230-244).
+ *
+ * Data layouts (all row-major)
+ *   linear (OPURE_W_F32)     w: float[out][in]
+ *   linear (OPURE_W_I8PC)    w: int8[out][in], scale: fp16[out]; y = scale[o] * sum_i w*x
+ *   linear (OPURE_W_I4G128)  w: uint8[out][in/2], element 2i in the high nibble
+ *                            (Opure_Streamer.cpp:403-426 nibble order, unsigned),
+ *                            scale, zero: bf16[out][in/128]; w(o,i) = s*(q - z)
+ *   activations              [rows][width] in OPURE_A_F32 / F16 / BF16
+ *   KV pool                  [n_layers][n_pages][2 (K,V)][n_kv_heads][page_size][head_dim]
+ *                            in the model's activation format; page_table
+ *                            int32[batch][max_pages_per_seq] (-1 = none)
+ *   rope table               float cos[max_pos][head_dim/2], sin[...] (interleaved
+ *                            pairs (2p, 2p+1), Opure_RoPE.usf:7-10)
+ */
+#ifndef OPURE_HIP_H
+#define OPURE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define OPURE_OK              0
+#define OPURE_E_INVALID      -1   /* null / misaligned pointer, bad shape or enum */
+#define OPURE_E_NODEVICE     -2   /* no HIP device at that ordinal */
+#define OPURE_E_HIP          -3   /* HIP runtime error; message has the detail */
+#define OPURE_E_OOM          -4   /* device allocation failed */
+#define OPURE_E_UNSUPPORTED  -5   /* weight/activation combination not built */
+#define OPURE_E_CAPACITY     -6   /* rows > OPURE_MAX_ROWS, ctx past capacity, pages missing */
+
+#define OPURE_MAX_ROWS       16   /* verify rows per launch (batch * (K+1)) */
+#define OPURE_PAGE_SIZE      16   /* KV tokens per page */
+
+enum { OPURE_W_F32 = 0, OPURE_W_I8PC = 1, OPURE_W_I4G128 = 2 };
+enum { OPURE_A_F32 = 0, OPURE_A_F16 = 1, OPURE_A_BF16 = 2 };
+enum { OPURE_ROPE_GPU = 0, OPURE_ROPE_CPUREF = 1 };
+enum { OPURE_EPI_STORE = 0, OPURE_EPI_RESIDUAL = 1, OPURE_EPI_SWIGLU = 2 };
+enum { OPURE_ACCEPT_NONE = 0, OPURE_ACCEPT_GREEDY = 1, OPURE_ACCEPT_REJECTION = 2 };
+
+typedef struct opure_dev opure_dev;
+typedef struct opure_graph opure_graph;
+
+/* ---- device: replaces dx12::Device::Initialize/Shutdown (Opure_Dx12.h:186-187) */
+int         opure_dev_create(int ordinal, opure_dev** out);
+int         opure_dev_destroy(opure_dev* dev);
+const char* opure_dev_name(const opure_dev* dev);
+uint64_t    opure_dev_hbm_bytes(const opure_dev* dev);
+const char* opure_last_error(void);
+
+/* ---- buffers: replaces GpuBuffer::Create/Destroy and the upload/readback
+ *      calls (Opure_Dx12.h:155-156, :230-244) */
+typedef struct opure_upload_range {
+    void*       dptr;
+    uint64_t    offset;
+    const void* src;
+    uint64_t    bytes;
+} opure_upload_range;
+
+int opure_buf_alloc(opure_dev* dev, uint64_t bytes, void** dptr);
+int opure_buf_free(opure_dev* dev, void* dptr);
+int opure_buf_upload(opure_dev* dev, void* dptr, uint64_t offset, const void* src, uint64_t bytes);
+int opure_buf_upload_ranges(opure_dev* dev, const opure_upload_range* ranges, uint32_t n);
+int opure_buf_download(opure_dev* dev, void* dst, const void* dptr, uint64_t offset, uint64_t bytes);
+/* fills `count` 32-bit words with `value` using a kernel (safe inside graph capture) */
+int opure_buf_fill_u32(opure_dev* dev, void* dptr, uint32_t value, uint64_t count);
+int opure_buf_copy(opure_dev* dev, void* dst, const void* src, uint64_t bytes);
+
+/* ---- stream: replaces ResetCommandList / ExecuteAndWait (Opure_Dx12.h:273-274) */
+int opure_stream_begin(opure_dev* dev);
+int opure_stream_sync(opure_dev* dev);
+
+/* ---- graphs: capture a whole verify step once, replay it per step */
+int opure_graph_begin(opure_dev* dev);
+int opure_graph_end(opure_dev* dev, opure_graph** out);
+int opure_graph_launch(opure_dev* dev, opure_graph* g);
+int opure_graph_destroy(opure_graph* g);
+
+/* ---- timing: replaces Begin/EndTimestamp + ResolveTimestampMs (Opure_Dx12.h:267-270) */
+int opure_timer_begin(opure_dev* dev);
+int opure_timer_end(opure_dev* dev);
+int opure_timer_ms(opure_dev* dev, float* ms);
+
+/* ---- host helper: RoPE cos/sin table.  OPURE_ROPE_GPU uses theta^(-2p/hd)
+ *      for pair p (Opure_RoPE.usf:56); OPURE_ROPE_CPUREF uses theta^(-4p/hd)
+ *      (Opure_CpuReference.cpp:179).  Computed in double, stored as float. */
+int opure_rope_table(double theta, uint32_t head_dim, uint32_t max_pos, uint32_t mode,
+                     float* cos_out, float* sin_out);
+
+/* ---- model description ------------------------------------------------ */
+typedef struct opure_linear {
+    const void* w;
+    const void* scale;      /* I8PC: fp16[out]; I4G128: bf16[out][in/128] */
+    const void* zero;       /* I4G128: bf16[out][in/128] */
+    uint32_t    out, in;
+} opure_linear;
+
+typedef struct opure_layer_weights {
+    const float* attn_norm;   /* [hidden] fp32 */
+    const float* mlp_norm;    /* [hidden] fp32 */
+    opure_linear qkv;         /* rows [q; k; v] = (n_heads + 2 n_kv_heads) * head_dim */
+    opure_linear o;           /* hidden x n_heads*head_dim */
+    opure_linear gate_up;     /* rows [gate; up] = 2 ffn */
+    opure_linear down;        /* hidden x ffn */
+} opure_layer_weights;
+
+typedef struct opure_model {
+    uint32_t n_layers, hidden, n_heads, n_kv_heads, head_dim, ffn, vocab;
+    float    rms_eps;
+    float    attn_scale;      /* 1.0 = the reference (no 1/sqrt(head_dim)) */
+    uint32_t wfmt;            /* OPURE_W_* (all linears, embed and lm_head) */
+    uint32_t afmt;            /* OPURE_A_*: activations fed to GEMVs and the KV cache */
+    const float* rope_cos;    /* device [rope_max_pos][head_dim/2] */
+    const float* rope_sin;
+    uint32_t rope_max_pos;
+    opure_linear embed;       /* [vocab][hidden] */
+    opure_linear lm_head;     /* [vocab][hidden] (same pointers as embed when tied) */
+    const float* final_norm;  /* [hidden] */
+    const opure_layer_weights* layers;   /* HOST array [n_layers] of device pointers */
+} opure_model;
+
+typedef struct opure_kv {
+    void*    pool;
+    uint32_t n_pages;
+    uint32_t page_size;       /* must be OPURE_PAGE_SIZE */
+    int32_t* page_table;      /* device [batch][max_pages_per_seq] */
+    uint32_t max_pages_per_seq;
+} opure_kv;
+
+/* ---- batched GEMV: replaces GEMVMain / GEMVQuantMain (Opure_GEMV.usf:40-89,
+ *      Opure_GEMV_Quant.usf:39-95).  Scores all M <= OPURE_MAX_ROWS activation
+ *      rows in one pass over the weights.
+ *        STORE:    y[m][o]  = sum_i W[o][i] x[m][i]            (y in yfmt)
+ *        RESIDUAL: y[m][o] += sum_i W[o][i] x[m][i]            (y fp32)
+ *        SWIGLU:   W rows = [gate; up] (out = 2F); y[m][f] = silu(g) * u  (y in yfmt)
+ *      Weight/activation pairs built: F32/F32, I8PC/F16, I4G128/F16, I4G128/BF16. */
+typedef struct opure_gemv_args {
+    opure_linear W;
+    const void*  x;           /* [M][W.in] in xfmt */
+    void*        y;
+    uint32_t     M;
+    uint32_t     xfmt, yfmt;
+    uint32_t     epilogue;    /* OPURE_EPI_* */
+} opure_gemv_args;
+
+int opure_gemv_batched_f32(opure_dev* dev, const opure_gemv_args* a);
+int opure_gemv_batched_i8pc(opure_dev* dev, const opure_gemv_args* a);
+int opure_gemv_batched_i4g128(opure_dev* dev, const opure_gemv_args* a);
+
+/* ---- paged decode attention for K+1 query rows: replaces AttentionMain{hd}
+ *      and the never-dispatched SpeculativeVerifyMain{hd}
+ *      (Opure_FlashAttention_Decode.usf:58-179, Opure_SpeculativeDecode.usf:60-189).
+ *      q [batch*rows][n_heads*head_dim] (afmt), row j of sequence b sits at
+ *      position seq_len[b]+j and sees positions 0..seq_len[b]+j; query head h
+ *      reads KV head h / (n_heads/n_kv_heads).  out has q's shape and format. */
+typedef struct opure_attn_args {
+    const opure_model* model; /* n_heads, n_kv_heads, head_dim, attn_scale, afmt */
+    const opure_kv*    kv;
+    uint32_t           layer;
+    uint32_t           batch, rows;
+    const int32_t*     seq_len;     /* device [batch] */
+    uint32_t           max_ctx;     /* host upper bound on seq_len[b] + rows */
+    const void*        q;
+    void*              out;
+} opure_attn_args;
+
+int opure_attn_decode_paged(opure_dev* dev, const opure_attn_args* a);
+
+/* ---- acceptance ------------------------------------------------------- */
+/* Greedy: argmax per row (ties -> lowest index; the reference's ArgMaxMain,
+ * Opure_ArgMax.usf:33-86, re-specified), longest matching draft prefix, then
+ * the correction (or bonus) token.  out_tokens[b][0..n] = accepted drafts then
+ * the final token, -1 after.  Rejection (Leviathan et al. 2023): accept draft
+ * x_j iff u_j * q_j(x_j) < p_j(x_j), u_j = Philox(seed; pos_base[b]+j, b, 1);
+ * on rejection sample max(0, p - q) normalised, after K accepts sample p_K,
+ * both by inverse CDF on Philox(seed; pos_base[b]+n, b, 2).  Probabilities use
+ * an exact fixed-point partition sum (see accept.hip).  dist_out[b][V] (may
+ * be NULL) receives the distribution the final token was drawn from. */
+typedef struct opure_accept_args {
+    uint32_t       batch, k, vocab;
+    const float*   target_logits;   /* [batch][k+1][vocab] */
+    const float*   draft_logits;    /* [batch][k][vocab] (rejection only) */
+    const int32_t* drafts;          /* [batch][drafts_stride], first k used */
+    uint32_t       drafts_stride;
+    float          temperature;     /* rejection only, > 0 */
+    uint64_t       seed;
+    const uint32_t* pos_base;       /* device [batch] or NULL (all 0) */
+    int32_t*       out_tokens;      /* [batch][k+1] */
+    int32_t*       accepted;        /* [batch] */
+    float*         dist_out;        /* [batch][vocab] or NULL */
+} opure_accept_args;
+
+int opure_accept_greedy(opure_dev* dev, const opure_accept_args* a);
+int opure_accept_rejection(opure_dev* dev, const opure_accept_args* a);
+
+/* sample one id per row from softmax(logits/temperature) (Philox stream
+ * `stream`, counter (pos[r], seq[r])): drafting at temperature. */
+typedef struct opure_sample_args {
+    uint32_t        rows, vocab;
+    const float*    logits;         /* [rows][vocab] */
+    float           temperature;
+    uint64_t        seed;
+    const uint32_t* pos;            /* device [rows] */
+    const uint32_t* seq;            /* device [rows] */
+    uint32_t        stream;
+    int32_t*        out;            /* device [rows] */
+} opure_sample_args;
+
+int opure_sample_rows(opure_dev* dev, const opure_sample_args* a);
+
+/* Philox4x32-10 test hook: out[i] = word 0 of Philox(seed; pos[i], seq[i], stream, 0). */
+int opure_philox_uniform(opure_dev* dev, uint64_t seed, const uint32_t* pos, const uint32_t* seq,
+                         uint32_t stream, uint32_t n, uint32_t* out);
+
+/* ---- KV rollback: after accepting accepted[b] of k drafts, the valid cache
+ *      is seq_len[b] + accepted[b] + 1 tokens.  Slots past it that the verify
+ *      step wrote are overwritten with poison_bits (when poison != 0), pages
+ *      wholly past it are released: page_table entry -> -1 and the id appended
+ *      to freed[b][...].  Replaces the broken EvictOldestKV
+ *      (Opure_VoxelEngine.cpp:721-763). */
+typedef struct opure_rollback_args {
+    const opure_model* model;
+    const opure_kv*    kv;           /* kv->page_table is updated in place */
+    uint32_t           batch, k;
+    const int32_t*     seq_len;
+    const int32_t*     accepted;
+    int32_t*           new_seq_len;
+    int32_t*           freed;        /* [batch][freed_stride] or NULL */
+    uint32_t           freed_stride;
+    int32_t*           n_freed;      /* [batch] or NULL */
+    uint32_t           poison;
+    uint32_t           poison_bits;  /* element bits in the model's afmt */
+} opure_rollback_args;
+
+int opure_kv_rollback(opure_dev* dev, const opure_rollback_args* a);
+
+/* ---- one verify step: embedding, every layer (RMSNorm -> fused QKV GEMV
+ *      with RoPE and paged KV append -> paged attention -> o_proj + residual
+ *      -> RMSNorm -> gate/up GEMV with SwiGLU -> down_proj + residual), final
+ *      RMSNorm, LM head, then the acceptance stage and rollback.  Replaces
+ *      VoxelEngine::RecordForward (Opure_VoxelEngine.cpp:189-536) for K+1
+ *      rows and a batch of sequences. */
+typedef struct opure_verify_args {
+    const opure_model* model;
+    const opure_kv*    kv;
+    uint32_t           batch, rows;  /* rows = K + 1; batch * rows <= OPURE_MAX_ROWS */
+    const int32_t*     tokens;       /* device [batch][rows]: last token, then K drafts */
+    const int32_t*     seq_len;      /* device [batch] */
+    uint32_t           max_ctx;      /* host upper bound on seq_len[b] + rows */
+    float*             logits;       /* device [batch][rows][vocab] */
+    uint32_t           accept_mode;  /* OPURE_ACCEPT_* */
+    const float*       draft_logits; /* rejection: [batch][rows-1][vocab] */
+    float              temperature;
+    uint64_t           seed;
+    const uint32_t*    pos_base;     /* device [batch] or NULL */
+    int32_t*           out_tokens;   /* [batch][rows] */
+    int32_t*           accepted;     /* [batch] */
+    float*             dist_out;     /* [batch][vocab] or NULL */
+    uint32_t           rollback;     /* 1: run opure_kv_rollback after acceptance */
+    int32_t*           new_seq_len;  /* [batch] (required when rollback) */
+    int32_t*           freed;
+    uint32_t           freed_stride;
+    int32_t*           n_freed;
+    uint32_t           poison;
+    uint32_t           poison_bits;
+} opure_verify_args;
+
+/* Sizes the device's internal workspace for this model and shape; call it
+ * before capturing a verify step into a graph (capture cannot allocate). */
+int opure_verify_reserve(opure_dev* dev, const opure_model* model, uint32_t batch, uint32_t rows,
+                         uint32_t max_ctx);
+int opure_verify_step(opure_dev* dev, const opure_verify_args* a);
+
+/* ---- diagnostics: the device workspace of the last verify step, so a test
+ *      can read layer intermediates (run with n_layers = 1 to see layer 0).
+ *      The counterpart of ReadActBank / RunLayersTraced (Opure_VoxelEngine.h:
+ *      173-178, :226-227).  offsets[0..4] = byte offsets of x (fp32 residual,
+ *      [rows][hidden]), xn (normed, afmt), q (afmt), att (afmt), h (afmt). */
+int opure_debug_workspace(opure_dev* dev, void** ptr, uint64_t* bytes);
+int opure_debug_verify_offsets(const opure_model* model, uint32_t batch, uint32_t rows, uint32_t max_ctx,
+                               uint64_t offsets[5]);
+
+/* ---- synthetic seeded weights (N(0, std) from Philox, stream `tensor_id`)
+ *      and device-side quantisers, so full-size models need no host copy. */
+int opure_synth_normal_f32(opure_dev* dev, float* dst, uint64_t n, uint64_t seed, uint32_t tensor_id,
+                           float std, float mean);
+int opure_quantize_i8pc(opure_dev* dev, const float* w, uint32_t out, uint32_t in, int8_t* q,
+                        uint16_t* scale_f16);
+int opure_quantize_i4g128(opure_dev* dev, const float* w, uint32_t out, uint32_t in, uint8_t* q,
+                          uint16_t* scale_bf16, uint16_t* zero_bf16);
+int opure_convert_f32(opure_dev* dev, const float* src, void* dst, uint32_t afmt, uint64_t n);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,246 @@
+// ============================================================================
+//  internal.h -- shared host and device internals of libopure_hip.
+// ============================================================================
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "../../include/opure_hip.h"
+
+// ---------------------------------------------------------------------------
+//  Host side: device object, errors, workspace
+// ---------------------------------------------------------------------------
+struct opure_dev {
+    int         ordinal = 0;
+    hipStream_t stream = nullptr;
+    hipEvent_t  ev_begin = nullptr, ev_end = nullptr;
+    char        name[256] = {0};
+    uint64_t    hbm = 0;
+    int         n_cu = 0;
+    bool        capturing = false;
+    // Grow-only workspace used by the kernels (split-K partials, attention
+    // partials, activations of a verify step) and a zeroed counter array.
+    void*       ws = nullptr;
+    uint64_t    ws_bytes = 0;
+    uint32_t*   counters = nullptr;     // zero between launches
+    uint64_t    counter_words = 0;
+};
+
+struct opure_graph {
+    hipGraph_t     graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+};
+
+namespace opure_hip {
+
+int set_error(int code, const char* fmt, ...);
+int hip_fail(hipError_t e, const char* what);
+const char* afmt_name(uint32_t afmt);
+int  ensure_workspace(opure_dev* dev, uint64_t bytes, uint64_t counter_words);
+inline uint64_t align_up(uint64_t v, uint64_t a) { return (v + a - 1) / a * a; }
+inline uint32_t act_bytes(uint32_t afmt) { return afmt == OPURE_A_F32 ? 4u : 2u; }
+
+#define OPURE_HIP_TRY(expr)                                                  \
+    do {                                                                     \
+        hipError_t _e = (expr);                                              \
+        if (_e != hipSuccess) return ::opure_hip::hip_fail(_e, #expr);      \
+    } while (0)
+
+#define OPURE_REQUIRE(cond, code, ...)                                       \
+    do {                                                                     \
+        if (!(cond)) return ::opure_hip::set_error((code), __VA_ARGS__);     \
+    } while (0)
+
+#define OPURE_LAUNCH_CHECK(what)                                             \
+    do {                                                                     \
+        hipError_t _e = hipGetLastError();                                   \
+        if (_e != hipSuccess) return ::opure_hip::hip_fail(_e, what);       \
+    } while (0)
+
+// ---- GEMV launcher shared by the public entry points and the verify step --
+enum GemvEpi : uint32_t {
+    EPI_STORE = OPURE_EPI_STORE,
+    EPI_RESIDUAL = OPURE_EPI_RESIDUAL,
+    EPI_SWIGLU = OPURE_EPI_SWIGLU,
+    EPI_QKV = 3,       // RoPE on q/k rows, q stored, k/v appended to the paged cache
+    EPI_LOGITS = 4,    // fp32 logits plus a per-tile (value, index) argmax partial
+};
+
+struct QkvEpilogue {
+    uint32_t qdim = 0, kvdim = 0, head_dim = 0, n_kv_heads = 0;
+    const float* rope_cos = nullptr;
+    const float* rope_sin = nullptr;
+    uint32_t rope_max_pos = 0;
+    const int32_t* seq_len = nullptr;
+    uint32_t rows_per_seq = 1;
+    void* kv_pool = nullptr;
+    const int32_t* page_table = nullptr;
+    uint32_t max_pages = 0, n_pages = 0, layer = 0;
+};
+
+struct LogitsEpilogue {
+    float*   am_val = nullptr;   // [n_tiles][M]
+    int32_t* am_idx = nullptr;
+};
+
+struct GemvCall {
+    opure_linear W{};
+    uint32_t wfmt = 0;
+    const void* x = nullptr;
+    uint32_t xfmt = 0;
+    uint32_t M = 0;
+    void* y = nullptr;
+    uint32_t yfmt = 0;
+    uint32_t epi = EPI_STORE;
+    QkvEpilogue qkv{};
+    LogitsEpilogue logits{};
+};
+
+struct GemvShape {
+    uint32_t tiles = 0;     // 16-row output tiles
+    uint32_t groups = 0;    // workgroups along the rows (4 tiles each)
+    uint32_t splits = 0;    // workgroups along K
+    uint32_t kr = 0;        // K elements per split
+};
+
+GemvShape gemv_shape(uint32_t wfmt, uint32_t out, uint32_t in);
+uint64_t  gemv_partial_bytes(const GemvShape& s);
+int       gemv_validate(const GemvCall& c);
+// `partials` and `counters` must hold gemv_partial_bytes(shape) and shape.groups words.
+int       gemv_launch(opure_dev* dev, const GemvCall& c, float* partials, uint32_t* counters);
+
+// ---- attention (attention.hip) ---------------------------------------------
+uint32_t attn_chunk(uint32_t head_dim);
+uint64_t attn_partial_bytes(uint32_t batch, uint32_t n_kv, uint32_t group, uint32_t rows, uint32_t hd, uint32_t max_ctx);
+int      attn_validate(const opure_model* m, const opure_kv* kv, uint32_t batch, uint32_t rows, uint32_t max_ctx);
+int      attn_launch(opure_dev* dev, const opure_model* m, const opure_kv* kv, uint32_t layer, uint32_t batch,
+                     uint32_t rows, const int32_t* seq_len, uint32_t max_ctx, const void* q, void* out, float* part);
+
+// ---- acceptance and rollback (accept.hip) ----------------------------------
+uint32_t argmax_parts(uint32_t vocab);
+uint64_t accept_ws_bytes(uint32_t batch, uint32_t k, uint32_t vocab, uint32_t mode);
+int      accept_validate(const opure_accept_args* a, bool rejection);
+int      greedy_from_partials(opure_dev* dev, const float* am_val, const int32_t* am_idx, uint32_t parts,
+                              uint32_t batch, uint32_t K, const int32_t* drafts, uint32_t stride, int32_t* out_tokens,
+                              int32_t* accepted, const int32_t* seq_len, int32_t* new_seq_len);
+int      accept_greedy_launch(opure_dev* dev, const opure_accept_args* a, void* ws, const int32_t* seq_len,
+                              int32_t* new_seq_len);
+int      accept_rejection_launch(opure_dev* dev, const opure_accept_args* a, void* ws, uint32_t* counters,
+                                 const int32_t* seq_len, int32_t* new_seq_len);
+int      rollback_validate(const opure_rollback_args* a);
+int      rollback_launch(opure_dev* dev, const opure_rollback_args* a);
+
+}  // namespace opure_hip
+
+// ---------------------------------------------------------------------------
+//  Device side: numerics shared with the CPU oracle bit for bit
+// ---------------------------------------------------------------------------
+namespace opure_dev_math {
+
+__device__ __forceinline__ float bits_f(uint32_t u) { return __uint_as_float(u); }
+__device__ __forceinline__ uint32_t f_bits(float f) { return __float_as_uint(f); }
+
+// Cody-Waite reduced degree-7 Taylor exp, same operations as orc_expf.
+__device__ __forceinline__ float expf_ref(float x)
+{
+    if (x != x) return x;
+    if (x > 88.72283935546875f) return __builtin_huge_valf();
+    if (x < -87.33654022216797f) return 0.0f;
+    const float LOG2E = static_cast<float>(1.4426950408889634);
+    const float LN2_HI = 0.693145751953125f;
+    const float LN2_LO = static_cast<float>(0.6931471805599453 - 0.693145751953125);
+    const float kf = __builtin_rintf(__fmul_rn(x, LOG2E));
+    float r = __fmaf_rn(-kf, LN2_HI, x);
+    r = __fmaf_rn(-kf, LN2_LO, r);
+    float p = static_cast<float>(1.0 / 5040.0);
+    p = __fmaf_rn(p, r, static_cast<float>(1.0 / 720.0));
+    p = __fmaf_rn(p, r, static_cast<float>(1.0 / 120.0));
+    p = __fmaf_rn(p, r, static_cast<float>(1.0 / 24.0));
+    p = __fmaf_rn(p, r, static_cast<float>(1.0 / 6.0));
+    p = __fmaf_rn(p, r, 0.5f);
+    p = __fmaf_rn(p, r, 1.0f);
+    p = __fmaf_rn(p, r, 1.0f);
+    const int k = static_cast<int>(kf);
+    if (k > 127) return __fmul_rn(__fmul_rn(p, bits_f(254u << 23)), 2.0f);
+    return __fmul_rn(p, bits_f(static_cast<uint32_t>(k + 127) << 23));
+}
+
+__device__ __forceinline__ uint32_t philox_u32(uint64_t seed, uint32_t c0, uint32_t c1, uint32_t c2)
+{
+    uint32_t c3 = 0u;
+    uint32_t k0 = static_cast<uint32_t>(seed), k1 = static_cast<uint32_t>(seed >> 32);
+#pragma unroll
+    for (int r = 0; r < 10; ++r)
+    {
+        if (r > 0) { k0 += 0x9E3779B9u; k1 += 0xBB67AE85u; }
+        const uint32_t lo0 = 0xD2511F53u * c0, hi0 = __umulhi(0xD2511F53u, c0);
+        const uint32_t lo1 = 0xCD9E8D57u * c2, hi1 = __umulhi(0xCD9E8D57u, c2);
+        const uint32_t n0 = hi1 ^ c1 ^ k0, n2 = hi0 ^ c3 ^ k1;
+        c0 = n0; c1 = lo1; c2 = n2; c3 = lo0;
+    }
+    return c0;
+}
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) { return bits_f(static_cast<uint32_t>(h) << 16); }
+
+__device__ __forceinline__ uint16_t f32_to_bf16(float f)
+{
+    const uint32_t x = f_bits(f);
+    if ((x & 0x7FFFFFFFu) > 0x7F800000u) return static_cast<uint16_t>((x >> 16) | 0x40u);
+    return static_cast<uint16_t>((x + 0x7FFFu + ((x >> 16) & 1u)) >> 16);
+}
+
+__device__ __forceinline__ float f16_to_f32(uint16_t h)
+{
+    _Float16 v;
+    __builtin_memcpy(&v, &h, 2);
+    return static_cast<float>(v);
+}
+
+__device__ __forceinline__ uint16_t f32_to_f16(float f)
+{
+    const _Float16 v = static_cast<_Float16>(f);
+    uint16_t h;
+    __builtin_memcpy(&h, &v, 2);
+    return h;
+}
+
+template <int AF>
+__device__ __forceinline__ float load_act(const void* base, uint64_t i)
+{
+    if constexpr (AF == OPURE_A_F32) return static_cast<const float*>(base)[i];
+    else if constexpr (AF == OPURE_A_F16) return f16_to_f32(static_cast<const uint16_t*>(base)[i]);
+    else return bf16_to_f32(static_cast<const uint16_t*>(base)[i]);
+}
+
+__device__ __forceinline__ float load_act_rt(const void* base, uint64_t i, uint32_t af)
+{
+    if (af == OPURE_A_F32) return static_cast<const float*>(base)[i];
+    const uint16_t h = static_cast<const uint16_t*>(base)[i];
+    return af == OPURE_A_F16 ? f16_to_f32(h) : bf16_to_f32(h);
+}
+
+__device__ __forceinline__ void store_act_rt(void* base, uint64_t i, float v, uint32_t af)
+{
+    if (af == OPURE_A_F32) { static_cast<float*>(base)[i] = v; return; }
+    static_cast<uint16_t*>(base)[i] = af == OPURE_A_F16 ? f32_to_f16(v) : f32_to_bf16(v);
+}
+
+__device__ __forceinline__ float round_act_rt(float v, uint32_t af)
+{
+    if (af == OPURE_A_F16) return f16_to_f32(f32_to_f16(v));
+    if (af == OPURE_A_BF16) return bf16_to_f32(f32_to_bf16(v));
+    return v;
+}
+
+// silu(g) * u in the order of Opure_CpuReference.cpp:195-196
+__device__ __forceinline__ float swiglu(float g, float u)
+{
+    const float s = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf_ref(-g)));
+    return __fmul_rn(__fmul_rn(g, s), u);
+}
+
+}  // namespace opure_dev_math

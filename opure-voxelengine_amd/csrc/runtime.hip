@@ -1,0 +1,438 @@
+// ============================================================================
+//  runtime.hip -- device, buffers, stream, graphs, timers, workspace, and the
+//  seeded synthetic-weight helpers.  Replaces dx12::Device / GpuBuffer /
+//  CommandScope (src/core/Opure_Dx12.h:144-337): one HIP stream per device,
+//  plain device pointers instead of five fixed bank bindings, hipGraphs
+//  instead of a recorded command list.
+// ============================================================================
+#include "internal.h"
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+
+namespace opure_hip {
+
+static thread_local char g_err[1024] = "";
+
+int set_error(int code, const char* fmt, ...)
+{
+    va_list ap;
+    va_start(ap, fmt);
+    std::vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int hip_fail(hipError_t e, const char* what)
+{
+    const int code = (e == hipErrorOutOfMemory || e == hipErrorMemoryAllocation) ? OPURE_E_OOM : OPURE_E_HIP;
+    return set_error(code, "%s failed: %s (%d)", what, hipGetErrorString(e), static_cast<int>(e));
+}
+
+const char* afmt_name(uint32_t afmt)
+{
+    switch (afmt) { case OPURE_A_F32: return "f32"; case OPURE_A_F16: return "f16"; case OPURE_A_BF16: return "bf16"; }
+    return "?";
+}
+
+__global__ void k_fill_u32(uint32_t* p, uint32_t v, uint64_t n)
+{
+    for (uint64_t i = blockIdx.x * static_cast<uint64_t>(blockDim.x) + threadIdx.x; i < n;
+         i += static_cast<uint64_t>(gridDim.x) * blockDim.x)
+        p[i] = v;
+}
+
+int ensure_workspace(opure_dev* dev, uint64_t bytes, uint64_t counter_words)
+{
+    bytes = align_up(bytes ? bytes : 256, 256);
+    if (bytes > dev->ws_bytes)
+    {
+        OPURE_REQUIRE(!dev->capturing, OPURE_E_CAPACITY,
+                      "workspace too small during graph capture (%llu < %llu bytes): call "
+                      "opure_verify_reserve before capturing", (unsigned long long)dev->ws_bytes,
+                      (unsigned long long)bytes);
+        OPURE_HIP_TRY(hipStreamSynchronize(dev->stream));
+        if (dev->ws) OPURE_HIP_TRY(hipFree(dev->ws));
+        dev->ws = nullptr;
+        dev->ws_bytes = 0;
+        OPURE_HIP_TRY(hipMalloc(&dev->ws, bytes));
+        dev->ws_bytes = bytes;
+    }
+    if (counter_words > dev->counter_words)
+    {
+        OPURE_REQUIRE(!dev->capturing, OPURE_E_CAPACITY,
+                      "counter array too small during graph capture: call opure_verify_reserve first");
+        OPURE_HIP_TRY(hipStreamSynchronize(dev->stream));
+        if (dev->counters) OPURE_HIP_TRY(hipFree(dev->counters));
+        dev->counters = nullptr;
+        dev->counter_words = 0;
+        const uint64_t words = align_up(counter_words, 1024);
+        OPURE_HIP_TRY(hipMalloc(&dev->counters, words * 4));
+        // counters must read zero before the first kernel that uses them; each
+        // user leaves them zero again when it finishes
+        hipLaunchKernelGGL(k_fill_u32, dim3(64), dim3(256), 0, dev->stream, dev->counters, 0u, words);
+        OPURE_LAUNCH_CHECK("k_fill_u32");
+        OPURE_HIP_TRY(hipStreamSynchronize(dev->stream));
+        dev->counter_words = words;
+    }
+    return OPURE_OK;
+}
+
+}  // namespace opure_hip
+
+using namespace opure_hip;
+
+// ---------------------------------------------------------------------------
+extern "C" {
+
+const char* opure_last_error(void) { return g_err; }
+
+int opure_dev_create(int ordinal, opure_dev** out)
+{
+    OPURE_REQUIRE(out != nullptr, OPURE_E_INVALID, "opure_dev_create: out is null");
+    *out = nullptr;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0)
+        return set_error(OPURE_E_NODEVICE, "no HIP device available");
+    OPURE_REQUIRE(ordinal >= 0 && ordinal < n, OPURE_E_NODEVICE, "device ordinal %d out of range (%d devices)",
+                  ordinal, n);
+    OPURE_HIP_TRY(hipSetDevice(ordinal));
+    hipDeviceProp_t prop;
+    OPURE_HIP_TRY(hipGetDeviceProperties(&prop, ordinal));
+    opure_dev* d = new opure_dev();
+    d->ordinal = ordinal;
+    std::snprintf(d->name, sizeof(d->name), "%s (%s)", prop.name, prop.gcnArchName);
+    d->hbm = prop.totalGlobalMem;
+    d->n_cu = prop.multiProcessorCount;
+    hipError_t e = hipStreamCreateWithFlags(&d->stream, hipStreamNonBlocking);
+    if (e == hipSuccess) e = hipEventCreate(&d->ev_begin);
+    if (e == hipSuccess) e = hipEventCreate(&d->ev_end);
+    if (e != hipSuccess)
+    {
+        delete d;
+        return hip_fail(e, "opure_dev_create");
+    }
+    *out = d;
+    return OPURE_OK;
+}
+
+int opure_dev_destroy(opure_dev* dev)
+{
+    if (!dev) return OPURE_OK;
+    hipSetDevice(dev->ordinal);
+    hipStreamSynchronize(dev->stream);
+    if (dev->ws) hipFree(dev->ws);
+    if (dev->counters) hipFree(dev->counters);
+    if (dev->ev_begin) hipEventDestroy(dev->ev_begin);
+    if (dev->ev_end) hipEventDestroy(dev->ev_end);
+    if (dev->stream) hipStreamDestroy(dev->stream);
+    delete dev;
+    return OPURE_OK;
+}
+
+const char* opure_dev_name(const opure_dev* dev) { return dev ? dev->name : ""; }
+uint64_t opure_dev_hbm_bytes(const opure_dev* dev) { return dev ? dev->hbm : 0; }
+
+int opure_buf_alloc(opure_dev* dev, uint64_t bytes, void** dptr)
+{
+    OPURE_REQUIRE(dev && dptr, OPURE_E_INVALID, "opure_buf_alloc: null argument");
+    OPURE_REQUIRE(!dev->capturing, OPURE_E_INVALID, "opure_buf_alloc during graph capture");
+    *dptr = nullptr;
+    // rounded up to 256 bytes like GpuBuffer::Create (Opure_Dx12.cpp:104-147)
+    OPURE_HIP_TRY(hipMalloc(dptr, align_up(bytes ? bytes : 1, 256)));
+    return OPURE_OK;
+}
+
+int opure_buf_free(opure_dev* dev, void* dptr)
+{
+    OPURE_REQUIRE(dev, OPURE_E_INVALID, "opure_buf_free: null device");
+    if (!dptr) return OPURE_OK;
+    OPURE_HIP_TRY(hipStreamSynchronize(dev->stream));
+    OPURE_HIP_TRY(hipFree(dptr));
+    return OPURE_OK;
+}
+
+int opure_buf_upload(opure_dev* dev, void* dptr, uint64_t offset, const void* src, uint64_t bytes)
+{
+    OPURE_REQUIRE(dev && dptr && (src || !bytes), OPURE_E_INVALID, "opure_buf_upload: null argument");
+    if (!bytes) return OPURE_OK;
+    OPURE_HIP_TRY(hipMemcpyAsync(static_cast<char*>(dptr) + offset, src, bytes, hipMemcpyHostToDevice,
+                                 dev->stream));
+    OPURE_HIP_TRY(hipStreamSynchronize(dev->stream));
+    return OPURE_OK;
+}
+
+int opure_buf_upload_ranges(opure_dev* dev, const opure_upload_range* r, uint32_t n)
+{
+    OPURE_REQUIRE(dev && (r || !n), OPURE_E_INVALID, "opure_buf_upload_ranges: null argument");
+    for (uint32_t i = 0; i < n; ++i)
+    {
+        OPURE_REQUIRE(r[i].dptr && (r[i].src || !r[i].bytes), OPURE_E_INVALID, "upload range %u: null pointer", i);
+        if (r[i].bytes)
+            OPURE_HIP_TRY(hipMemcpyAsync(static_cast<char*>(r[i].dptr) + r[i].offset, r[i].src, r[i].bytes,
+                                         hipMemcpyHostToDevice, dev->stream));
+    }
+    OPURE_HIP_TRY(hipStreamSynchronize(dev->stream));
+    return OPURE_OK;
+}
+
+int opure_buf_download(opure_dev* dev, void* dst, const void* dptr, uint64_t offset, uint64_t bytes)
+{
+    OPURE_REQUIRE(dev && dptr && (dst || !bytes), OPURE_E_INVALID, "opure_buf_download: null argument");
+    if (!bytes) return OPURE_OK;
+    OPURE_HIP_TRY(hipMemcpyAsync(dst, static_cast<const char*>(dptr) + offset, bytes, hipMemcpyDeviceToHost,
+                                 dev->stream));
+    OPURE_HIP_TRY(hipStreamSynchronize(dev->stream));
+    return OPURE_OK;
+}
+
+int opure_buf_fill_u32(opure_dev* dev, void* dptr, uint32_t value, uint64_t count)
+{
+    OPURE_REQUIRE(dev && dptr, OPURE_E_INVALID, "opure_buf_fill_u32: null argument");
+    OPURE_REQUIRE((reinterpret_cast<uintptr_t>(dptr) & 3u) == 0, OPURE_E_INVALID, "opure_buf_fill_u32: misaligned");
+    if (!count) return OPURE_OK;
+    const uint64_t blocks = count / 256 + 1 < 4096 ? count / 256 + 1 : 4096;
+    hipLaunchKernelGGL(k_fill_u32, dim3(static_cast<uint32_t>(blocks)), dim3(256), 0, dev->stream,
+                       static_cast<uint32_t*>(dptr), value, count);
+    OPURE_LAUNCH_CHECK("k_fill_u32");
+    return OPURE_OK;
+}
+
+int opure_buf_copy(opure_dev* dev, void* dst, const void* src, uint64_t bytes)
+{
+    OPURE_REQUIRE(dev && dst && src, OPURE_E_INVALID, "opure_buf_copy: null argument");
+    if (!bytes) return OPURE_OK;
+    OPURE_HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, dev->stream));
+    return OPURE_OK;
+}
+
+int opure_stream_begin(opure_dev* dev)
+{
+    OPURE_REQUIRE(dev, OPURE_E_INVALID, "opure_stream_begin: null device");
+    OPURE_HIP_TRY(hipSetDevice(dev->ordinal));
+    return OPURE_OK;
+}
+
+int opure_stream_sync(opure_dev* dev)
+{
+    OPURE_REQUIRE(dev, OPURE_E_INVALID, "opure_stream_sync: null device");
+    OPURE_HIP_TRY(hipStreamSynchronize(dev->stream));
+    return OPURE_OK;
+}
+
+int opure_graph_begin(opure_dev* dev)
+{
+    OPURE_REQUIRE(dev && !dev->capturing, OPURE_E_INVALID, "opure_graph_begin: null device or already capturing");
+    OPURE_HIP_TRY(hipStreamBeginCapture(dev->stream, hipStreamCaptureModeThreadLocal));
+    dev->capturing = true;
+    return OPURE_OK;
+}
+
+int opure_graph_end(opure_dev* dev, opure_graph** out)
+{
+    OPURE_REQUIRE(dev && out && dev->capturing, OPURE_E_INVALID, "opure_graph_end: not capturing");
+    dev->capturing = false;
+    *out = nullptr;
+    opure_graph* g = new opure_graph();
+    hipError_t e = hipStreamEndCapture(dev->stream, &g->graph);
+    if (e == hipSuccess) e = hipGraphInstantiate(&g->exec, g->graph, nullptr, nullptr, 0);
+    if (e != hipSuccess)
+    {
+        if (g->graph) hipGraphDestroy(g->graph);
+        delete g;
+        return hip_fail(e, "opure_graph_end");
+    }
+    *out = g;
+    return OPURE_OK;
+}
+
+int opure_graph_launch(opure_dev* dev, opure_graph* g)
+{
+    OPURE_REQUIRE(dev && g && g->exec, OPURE_E_INVALID, "opure_graph_launch: null argument");
+    OPURE_HIP_TRY(hipGraphLaunch(g->exec, dev->stream));
+    return OPURE_OK;
+}
+
+int opure_graph_destroy(opure_graph* g)
+{
+    if (!g) return OPURE_OK;
+    if (g->exec) hipGraphExecDestroy(g->exec);
+    if (g->graph) hipGraphDestroy(g->graph);
+    delete g;
+    return OPURE_OK;
+}
+
+int opure_timer_begin(opure_dev* dev)
+{
+    OPURE_REQUIRE(dev, OPURE_E_INVALID, "opure_timer_begin: null device");
+    OPURE_HIP_TRY(hipEventRecord(dev->ev_begin, dev->stream));
+    return OPURE_OK;
+}
+
+int opure_timer_end(opure_dev* dev)
+{
+    OPURE_REQUIRE(dev, OPURE_E_INVALID, "opure_timer_end: null device");
+    OPURE_HIP_TRY(hipEventRecord(dev->ev_end, dev->stream));
+    return OPURE_OK;
+}
+
+int opure_timer_ms(opure_dev* dev, float* ms)
+{
+    OPURE_REQUIRE(dev && ms, OPURE_E_INVALID, "opure_timer_ms: null argument");
+    OPURE_HIP_TRY(hipEventSynchronize(dev->ev_end));
+    OPURE_HIP_TRY(hipEventElapsedTime(ms, dev->ev_begin, dev->ev_end));
+    return OPURE_OK;
+}
+
+int opure_rope_table(double theta, uint32_t head_dim, uint32_t max_pos, uint32_t mode, float* cos_out,
+                     float* sin_out)
+{
+    OPURE_REQUIRE(cos_out && sin_out && head_dim >= 2 && head_dim % 2 == 0 && theta > 0.0, OPURE_E_INVALID,
+                  "opure_rope_table: bad argument");
+    OPURE_REQUIRE(mode == OPURE_ROPE_GPU || mode == OPURE_ROPE_CPUREF, OPURE_E_INVALID, "opure_rope_table: mode");
+    const uint32_t half = head_dim / 2;
+    for (uint32_t p = 0; p < half; ++p)
+    {
+        const double ch = mode == OPURE_ROPE_CPUREF ? 2.0 * p : static_cast<double>(p);
+        const double inv_freq = std::pow(theta, -2.0 * ch / static_cast<double>(head_dim));
+        for (uint32_t pos = 0; pos < max_pos; ++pos)
+        {
+            const double t = static_cast<double>(pos) * inv_freq;
+            cos_out[static_cast<uint64_t>(pos) * half + p] = static_cast<float>(std::cos(t));
+            sin_out[static_cast<uint64_t>(pos) * half + p] = static_cast<float>(std::sin(t));
+        }
+    }
+    return OPURE_OK;
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+//  Synthetic weights and quantisers
+// ---------------------------------------------------------------------------
+namespace {
+
+using namespace opure_dev_math;
+
+// Box-Muller over two Philox words keyed by (seed; index pair, tensor, 7).
+__global__ void k_synth_normal(float* dst, uint64_t n, uint64_t seed, uint32_t tensor, float std_, float mean)
+{
+    for (uint64_t i = blockIdx.x * static_cast<uint64_t>(blockDim.x) + threadIdx.x; i < (n + 1) / 2;
+         i += static_cast<uint64_t>(gridDim.x) * blockDim.x)
+    {
+        const uint32_t lo = static_cast<uint32_t>(i), hi = static_cast<uint32_t>(i >> 32);
+        const uint32_t a = philox_u32(seed, lo, hi ^ (tensor << 8), 7u);
+        const uint32_t b = philox_u32(seed ^ 0x9E3779B97F4A7C15ull, lo, hi ^ (tensor << 8), 7u);
+        const float u1 = (static_cast<float>(a >> 8) + 1.0f) * (1.0f / 16777216.0f);   // (0, 1]
+        const float u2 = static_cast<float>(b >> 8) * (1.0f / 16777216.0f);
+        const float r = sqrtf(-2.0f * logf(u1));
+        float s, c;
+        sincosf(6.283185307179586f * u2, &s, &c);
+        dst[2 * i] = mean + std_ * r * c;
+        if (2 * i + 1 < n) dst[2 * i + 1] = mean + std_ * r * s;
+    }
+}
+
+// one wave per row: absmax -> fp16 scale -> int8 with round-to-nearest
+__global__ void k_quant_i8pc(const float* w, uint32_t out, uint32_t in, int8_t* q, uint16_t* scale)
+{
+    const uint32_t row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const uint32_t lane = threadIdx.x & 63;
+    if (row >= out) return;
+    const float* r = w + static_cast<uint64_t>(row) * in;
+    float m = 0.0f;
+    for (uint32_t i = lane; i < in; i += 64) m = fmaxf(m, fabsf(r[i]));
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    const uint16_t s16 = f32_to_f16(fmaxf(m, 1e-8f) / 127.0f);
+    const float s = f16_to_f32(s16);
+    if (lane == 0) scale[row] = s16;
+    for (uint32_t i = lane; i < in; i += 64)
+    {
+        float v = rintf(r[i] / s);
+        v = fminf(fmaxf(v, -127.0f), 127.0f);
+        q[static_cast<uint64_t>(row) * in + i] = static_cast<int8_t>(v);
+    }
+}
+
+// one thread per (row, group of 128): asymmetric min/max -> bf16 scale, zero
+__global__ void k_quant_i4g128(const float* w, uint32_t out, uint32_t in, uint8_t* q, uint16_t* scale,
+                               uint16_t* zero)
+{
+    const uint32_t G = in / 128;
+    const uint64_t idx = blockIdx.x * static_cast<uint64_t>(blockDim.x) + threadIdx.x;
+    if (idx >= static_cast<uint64_t>(out) * G) return;
+    const uint32_t row = static_cast<uint32_t>(idx / G), g = static_cast<uint32_t>(idx % G);
+    const float* r = w + static_cast<uint64_t>(row) * in + g * 128;
+    float mn = r[0], mx = r[0];
+    for (int i = 1; i < 128; ++i) { mn = fminf(mn, r[i]); mx = fmaxf(mx, r[i]); }
+    const uint16_t sb = f32_to_bf16(fmaxf(mx - mn, 1e-8f) / 15.0f);
+    const float s = bf16_to_f32(sb);
+    const uint16_t zb = f32_to_bf16(-mn / s);
+    const float z = bf16_to_f32(zb);
+    scale[idx] = sb;
+    zero[idx] = zb;
+    uint8_t* dst = q + static_cast<uint64_t>(row) * (in / 2) + g * 64;
+    for (int i = 0; i < 128; i += 2)
+    {
+        const float a = fminf(fmaxf(rintf(r[i] / s + z), 0.0f), 15.0f);
+        const float b = fminf(fmaxf(rintf(r[i + 1] / s + z), 0.0f), 15.0f);
+        dst[i / 2] = static_cast<uint8_t>((static_cast<uint32_t>(a) << 4) | static_cast<uint32_t>(b));
+    }
+}
+
+__global__ void k_convert_f32(const float* src, void* dst, uint32_t afmt, uint64_t n)
+{
+    for (uint64_t i = blockIdx.x * static_cast<uint64_t>(blockDim.x) + threadIdx.x; i < n;
+         i += static_cast<uint64_t>(gridDim.x) * blockDim.x)
+        store_act_rt(dst, i, src[i], afmt);
+}
+
+uint32_t grid_for(uint64_t n, uint32_t block) { const uint64_t g = (n + block - 1) / block; return g > 65535 ? 65535u : (g ? static_cast<uint32_t>(g) : 1u); }
+
+}  // namespace
+
+extern "C" {
+
+int opure_synth_normal_f32(opure_dev* dev, float* dst, uint64_t n, uint64_t seed, uint32_t tensor_id, float std_,
+                           float mean)
+{
+    OPURE_REQUIRE(dev && dst, OPURE_E_INVALID, "opure_synth_normal_f32: null argument");
+    if (!n) return OPURE_OK;
+    hipLaunchKernelGGL(k_synth_normal, dim3(grid_for((n + 1) / 2, 256)), dim3(256), 0, dev->stream, dst, n, seed,
+                       tensor_id, std_, mean);
+    OPURE_LAUNCH_CHECK("k_synth_normal");
+    return OPURE_OK;
+}
+
+int opure_quantize_i8pc(opure_dev* dev, const float* w, uint32_t out, uint32_t in, int8_t* q, uint16_t* scale)
+{
+    OPURE_REQUIRE(dev && w && q && scale && out && in, OPURE_E_INVALID, "opure_quantize_i8pc: bad argument");
+    hipLaunchKernelGGL(k_quant_i8pc, dim3((out + 3) / 4), dim3(256), 0, dev->stream, w, out, in, q, scale);
+    OPURE_LAUNCH_CHECK("k_quant_i8pc");
+    return OPURE_OK;
+}
+
+int opure_quantize_i4g128(opure_dev* dev, const float* w, uint32_t out, uint32_t in, uint8_t* q, uint16_t* scale,
+                          uint16_t* zero)
+{
+    OPURE_REQUIRE(dev && w && q && scale && zero && out && in, OPURE_E_INVALID, "opure_quantize_i4g128: bad argument");
+    OPURE_REQUIRE(in % 128 == 0, OPURE_E_INVALID, "opure_quantize_i4g128: in (%u) must be a multiple of 128", in);
+    const uint64_t n = static_cast<uint64_t>(out) * (in / 128);
+    hipLaunchKernelGGL(k_quant_i4g128, dim3(static_cast<uint32_t>((n + 255) / 256)), dim3(256), 0, dev->stream, w,
+                       out, in, q, scale, zero);
+    OPURE_LAUNCH_CHECK("k_quant_i4g128");
+    return OPURE_OK;
+}
+
+int opure_convert_f32(opure_dev* dev, const float* src, void* dst, uint32_t afmt, uint64_t n)
+{
+    OPURE_REQUIRE(dev && src && dst && afmt <= OPURE_A_BF16, OPURE_E_INVALID, "opure_convert_f32: bad argument");
+    if (!n) return OPURE_OK;
+    hipLaunchKernelGGL(k_convert_f32, dim3(grid_for(n, 256)), dim3(256), 0, dev->stream, src, dst, afmt, n);
+    OPURE_LAUNCH_CHECK("k_convert_f32");
+    return OPURE_OK;
+}
+
+}  // extern "C"

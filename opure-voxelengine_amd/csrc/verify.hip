@@ -1,0 +1,361 @@
+// ============================================================================
+//  verify.hip -- one speculative-decoding verify step on the GPU.
+//
+//  Replaces VoxelEngine::RecordForward (src/engine/Opure_VoxelEngine.cpp:189-536),
+//  which recorded 1 + 14 L + 2 barriered dispatches per token for ONE token.
+//  A verify step scores K+1 rows of B sequences in one pass over the weights:
+//
+//    embed gather (dequantised)                        x  [MR][h]  fp32 residual
+//    per layer:
+//      rmsnorm(x, attn_norm)                           xn [MR][h]  afmt
+//      gemv qkv   + RoPE, q store, paged K/V append    q  [MR][nh*hd]
+//      paged attention (split-K chunks + combine)      att[MR][nh*hd]
+//      gemv o     + residual add                       x += o
+//      rmsnorm(x, mlp_norm)                            xn
+//      gemv gate/up + SwiGLU                           h  [MR][ffn]
+//      gemv down  + residual add                       x += down
+//    rmsnorm(x, final_norm); gemv lm_head -> logits + per-tile argmax partials
+//    acceptance (greedy from the partials, or rejection sampling)
+//    rollback of rejected positions
+//
+//  Every launch goes to the device's one stream, so a whole step can be
+//  captured once into a hipGraph and replayed (opure_verify_reserve sizes the
+//  workspace first, because capture cannot allocate).
+// ============================================================================
+#include "internal.h"
+
+using namespace opure_dev_math;
+
+namespace {
+
+__global__ __launch_bounds__(256) void k_embed(const int32_t* tokens, opure_linear E, uint32_t wfmt, uint32_t h,
+                                               uint32_t vocab, float* x)
+{
+    const uint32_t r = blockIdx.x;
+    const int32_t t = tokens[r];
+    float* xr = x + static_cast<uint64_t>(r) * h;
+    if (t < 0 || static_cast<uint32_t>(t) >= vocab)
+    {
+        // an id outside the vocabulary poisons its row instead of reading out of bounds
+        for (uint32_t i = threadIdx.x; i < h; i += 256u) xr[i] = __builtin_nanf("");
+        return;
+    }
+    const uint64_t base = static_cast<uint64_t>(t) * h;
+    for (uint32_t i = threadIdx.x; i < h; i += 256u)
+    {
+        float v;
+        if (wfmt == OPURE_W_F32) v = static_cast<const float*>(E.w)[base + i];
+        else if (wfmt == OPURE_W_I8PC)
+            v = __fmul_rn(static_cast<float>(static_cast<const int8_t*>(E.w)[base + i]),
+                          f16_to_f32(static_cast<const uint16_t*>(E.scale)[t]));
+        else
+        {
+            const uint8_t byte = static_cast<const uint8_t*>(E.w)[(base + i) >> 1];
+            const uint32_t q = ((base + i) & 1u) ? (byte & 0x0Fu) : (byte >> 4);
+            const uint64_t g = static_cast<uint64_t>(t) * (h / 128u) + i / 128u;
+            v = __fmul_rn(bf16_to_f32(static_cast<const uint16_t*>(E.scale)[g]),
+                          __fsub_rn(static_cast<float>(q), bf16_to_f32(static_cast<const uint16_t*>(E.zero)[g])));
+        }
+        xr[i] = v;
+    }
+}
+
+// x * rsqrt(mean(x^2) + eps) * g  (Opure_RMSNorm.usf:44-78), one workgroup per row
+__global__ __launch_bounds__(256) void k_rmsnorm(const float* x, const float* g, uint32_t d, float eps, void* y,
+                                                 uint32_t afmt)
+{
+    __shared__ float red[4];
+    const uint32_t r = blockIdx.x;
+    const float* xr = x + static_cast<uint64_t>(r) * d;
+    float ss = 0.0f;
+    for (uint32_t i = threadIdx.x; i < d; i += 256u) ss = __fmaf_rn(xr[i], xr[i], ss);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+    if ((threadIdx.x & 63u) == 0) red[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    const float tot = (red[0] + red[1]) + (red[2] + red[3]);
+    const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(tot, static_cast<float>(d)), eps)));
+    for (uint32_t i = threadIdx.x; i < d; i += 256u)
+        store_act_rt(y, static_cast<uint64_t>(r) * d + i, __fmul_rn(__fmul_rn(xr[i], inv), g[i]), afmt);
+}
+
+}  // namespace
+
+namespace opure_hip {
+
+struct VerifyPlan {
+    uint64_t x = 0, xn = 0, q = 0, att = 0, h = 0, am_val = 0, am_idx = 0, attn = 0, gemv = 0, rej = 0, total = 0;
+    uint64_t counters = 0;
+    uint32_t gemv_groups = 0;
+    uint32_t lm_tiles = 0;
+};
+
+static VerifyPlan make_plan(const opure_model* m, uint32_t B, uint32_t R, uint32_t max_ctx)
+{
+    VerifyPlan p;
+    const uint64_t MR = static_cast<uint64_t>(B) * R;
+    const uint32_t eb = act_bytes(m->afmt);
+    const uint32_t qdim = m->n_heads * m->head_dim, kvdim = m->n_kv_heads * m->head_dim;
+    uint64_t off = 0;
+    auto take = [&](uint64_t bytes) { const uint64_t o = off; off += align_up(bytes ? bytes : 1, 256); return o; };
+    p.x = take(MR * m->hidden * 4u);
+    p.xn = take(MR * m->hidden * eb);
+    p.q = take(MR * qdim * eb);
+    p.att = take(MR * qdim * eb);
+    p.h = take(MR * m->ffn * eb);
+    p.lm_tiles = m->vocab / 16u;
+    p.am_val = take(static_cast<uint64_t>(p.lm_tiles) * MR * 4u);
+    p.am_idx = take(static_cast<uint64_t>(p.lm_tiles) * MR * 4u);
+    p.attn = take(attn_partial_bytes(B, m->n_kv_heads, m->n_heads / m->n_kv_heads, R, m->head_dim, max_ctx));
+    uint64_t gp = 0;
+    uint32_t gg = 0;
+    const uint32_t shapes[5][2] = {{qdim + 2u * kvdim, m->hidden}, {m->hidden, qdim}, {2u * m->ffn, m->hidden},
+                                   {m->hidden, m->ffn}, {m->vocab, m->hidden}};
+    for (const auto& s : shapes)
+    {
+        const GemvShape gs = gemv_shape(m->wfmt, s[0], s[1]);
+        if (gemv_partial_bytes(gs) > gp) gp = gemv_partial_bytes(gs);
+        if (gs.groups > gg) gg = gs.groups;
+    }
+    p.gemv = take(gp);
+    p.rej = take(accept_ws_bytes(B, R - 1u, m->vocab, OPURE_ACCEPT_REJECTION));
+    p.total = off;
+    p.gemv_groups = gg;
+    p.counters = static_cast<uint64_t>(gg) + B;
+    return p;
+}
+
+static int check_linear(const opure_linear& L, uint32_t out, uint32_t in, const char* what, uint32_t wfmt)
+{
+    OPURE_REQUIRE(L.w && L.out == out && L.in == in, OPURE_E_INVALID, "verify: %s is %ux%u (w=%p), expected %ux%u", what,
+                  L.out, L.in, L.w, out, in);
+    if (wfmt == OPURE_W_I8PC) OPURE_REQUIRE(L.scale, OPURE_E_INVALID, "verify: %s has no scales", what);
+    if (wfmt == OPURE_W_I4G128) OPURE_REQUIRE(L.scale && L.zero, OPURE_E_INVALID, "verify: %s has no scale/zero", what);
+    return OPURE_OK;
+}
+
+static int check_model(const opure_model* m, const opure_kv* kv, uint32_t B, uint32_t R, uint32_t max_ctx)
+{
+    OPURE_REQUIRE(m && kv && m->layers && m->final_norm && m->rope_cos && m->rope_sin, OPURE_E_INVALID,
+                  "verify: null model field");
+    OPURE_REQUIRE(m->n_layers >= 1 && m->hidden >= 16 && m->vocab >= 16 && m->vocab % 16 == 0 && m->ffn >= 16,
+                  OPURE_E_INVALID, "verify: bad model shape");
+    const bool ok = (m->wfmt == OPURE_W_F32 && m->afmt == OPURE_A_F32) ||
+                    (m->wfmt == OPURE_W_I8PC && m->afmt == OPURE_A_F16) ||
+                    (m->wfmt == OPURE_W_I4G128 && (m->afmt == OPURE_A_F16 || m->afmt == OPURE_A_BF16));
+    OPURE_REQUIRE(ok, OPURE_E_UNSUPPORTED, "verify: weights %u with %s activations are not built", m->wfmt,
+                  afmt_name(m->afmt));
+    int rc = attn_validate(m, kv, B, R, max_ctx);
+    if (rc) return rc;
+    OPURE_REQUIRE(max_ctx <= m->rope_max_pos, OPURE_E_CAPACITY, "verify: max_ctx %u beyond the RoPE table (%u)", max_ctx,
+                  m->rope_max_pos);
+    OPURE_REQUIRE(R >= 1 && R - 1u < 64u, OPURE_E_CAPACITY, "verify: rows %u", R);
+    const uint32_t qdim = m->n_heads * m->head_dim, kvdim = m->n_kv_heads * m->head_dim;
+    if ((rc = check_linear(m->embed, m->vocab, m->hidden, "embed", m->wfmt))) return rc;
+    if ((rc = check_linear(m->lm_head, m->vocab, m->hidden, "lm_head", m->wfmt))) return rc;
+    for (uint32_t L = 0; L < m->n_layers; ++L)
+    {
+        const opure_layer_weights& W = m->layers[L];
+        OPURE_REQUIRE(W.attn_norm && W.mlp_norm, OPURE_E_INVALID, "verify: layer %u norm gains missing", L);
+        if ((rc = check_linear(W.qkv, qdim + 2u * kvdim, m->hidden, "qkv", m->wfmt))) return rc;
+        if ((rc = check_linear(W.o, m->hidden, qdim, "o_proj", m->wfmt))) return rc;
+        if ((rc = check_linear(W.gate_up, 2u * m->ffn, m->hidden, "gate_up", m->wfmt))) return rc;
+        if ((rc = check_linear(W.down, m->hidden, m->ffn, "down", m->wfmt))) return rc;
+    }
+    return OPURE_OK;
+}
+
+}  // namespace opure_hip
+
+using namespace opure_hip;
+
+extern "C" {
+
+int opure_verify_reserve(opure_dev* dev, const opure_model* model, uint32_t batch, uint32_t rows, uint32_t max_ctx)
+{
+    OPURE_REQUIRE(dev && model, OPURE_E_INVALID, "opure_verify_reserve: null argument");
+    OPURE_REQUIRE(batch >= 1 && rows >= 1 && batch * rows <= OPURE_MAX_ROWS, OPURE_E_CAPACITY,
+                  "opure_verify_reserve: batch*rows = %u exceeds %d", batch * rows, OPURE_MAX_ROWS);
+    const VerifyPlan p = make_plan(model, batch, rows, max_ctx);
+    return ensure_workspace(dev, p.total, p.counters);
+}
+
+int opure_debug_workspace(opure_dev* dev, void** ptr, uint64_t* bytes)
+{
+    OPURE_REQUIRE(dev && ptr && bytes, OPURE_E_INVALID, "opure_debug_workspace: null argument");
+    *ptr = dev->ws;
+    *bytes = dev->ws_bytes;
+    return OPURE_OK;
+}
+
+int opure_debug_verify_offsets(const opure_model* model, uint32_t batch, uint32_t rows, uint32_t max_ctx,
+                               uint64_t offsets[5])
+{
+    OPURE_REQUIRE(model && offsets && batch && rows, OPURE_E_INVALID, "opure_debug_verify_offsets: bad argument");
+    const VerifyPlan p = make_plan(model, batch, rows, max_ctx);
+    offsets[0] = p.x;
+    offsets[1] = p.xn;
+    offsets[2] = p.q;
+    offsets[3] = p.att;
+    offsets[4] = p.h;
+    return OPURE_OK;
+}
+
+int opure_verify_step(opure_dev* dev, const opure_verify_args* a)
+{
+    OPURE_REQUIRE(dev && a && a->model && a->kv && a->tokens && a->seq_len && a->logits, OPURE_E_INVALID,
+                  "opure_verify_step: null argument");
+    const opure_model* m = a->model;
+    const opure_kv* kv = a->kv;
+    const uint32_t B = a->batch, R = a->rows, MR = B * R;
+    int rc = check_model(m, kv, B, R, a->max_ctx);
+    if (rc) return rc;
+    OPURE_REQUIRE(a->accept_mode <= OPURE_ACCEPT_REJECTION, OPURE_E_INVALID, "verify: accept_mode %u", a->accept_mode);
+    if (a->accept_mode != OPURE_ACCEPT_NONE)
+    {
+        OPURE_REQUIRE(R >= 2 && a->out_tokens && a->accepted, OPURE_E_INVALID,
+                      "verify: acceptance needs rows >= 2, out_tokens and accepted");
+        if (a->accept_mode == OPURE_ACCEPT_REJECTION)
+            OPURE_REQUIRE(a->draft_logits && a->temperature > 0.0f, OPURE_E_INVALID,
+                          "verify: rejection needs draft_logits and temperature > 0");
+    }
+    if (a->rollback)
+        OPURE_REQUIRE(a->accept_mode != OPURE_ACCEPT_NONE && a->new_seq_len, OPURE_E_INVALID,
+                      "verify: rollback needs acceptance and new_seq_len");
+
+    const VerifyPlan P = make_plan(m, B, R, a->max_ctx);
+    rc = ensure_workspace(dev, P.total, P.counters);
+    if (rc) return rc;
+    char* ws = static_cast<char*>(dev->ws);
+    float* x = reinterpret_cast<float*>(ws + P.x);
+    void* xn = ws + P.xn;
+    void* q = ws + P.q;
+    void* att = ws + P.att;
+    void* hbuf = ws + P.h;
+    float* gpart = reinterpret_cast<float*>(ws + P.gemv);
+    uint32_t* gcnt = dev->counters;
+    const uint32_t qdim = m->n_heads * m->head_dim, kvdim = m->n_kv_heads * m->head_dim;
+
+    hipLaunchKernelGGL(k_embed, dim3(MR), dim3(256), 0, dev->stream, a->tokens, m->embed, m->wfmt, m->hidden, m->vocab, x);
+    OPURE_LAUNCH_CHECK("k_embed");
+
+    GemvCall c;
+    c.wfmt = m->wfmt;
+    c.xfmt = m->afmt;
+    c.M = MR;
+    for (uint32_t L = 0; L < m->n_layers; ++L)
+    {
+        const opure_layer_weights& W = m->layers[L];
+        hipLaunchKernelGGL(k_rmsnorm, dim3(MR), dim3(256), 0, dev->stream, x, W.attn_norm, m->hidden, m->rms_eps, xn,
+                           m->afmt);
+        OPURE_LAUNCH_CHECK("k_rmsnorm");
+
+        c.W = W.qkv;
+        c.x = xn;
+        c.y = q;
+        c.yfmt = m->afmt;
+        c.epi = EPI_QKV;
+        c.qkv.qdim = qdim;
+        c.qkv.kvdim = kvdim;
+        c.qkv.head_dim = m->head_dim;
+        c.qkv.n_kv_heads = m->n_kv_heads;
+        c.qkv.rope_cos = m->rope_cos;
+        c.qkv.rope_sin = m->rope_sin;
+        c.qkv.rope_max_pos = m->rope_max_pos;
+        c.qkv.seq_len = a->seq_len;
+        c.qkv.rows_per_seq = R;
+        c.qkv.kv_pool = kv->pool;
+        c.qkv.page_table = kv->page_table;
+        c.qkv.max_pages = kv->max_pages_per_seq;
+        c.qkv.n_pages = kv->n_pages;
+        c.qkv.layer = L;
+        if ((rc = gemv_validate(c)) || (rc = gemv_launch(dev, c, gpart, gcnt))) return rc;
+
+        if ((rc = attn_launch(dev, m, kv, L, B, R, a->seq_len, a->max_ctx, q, att,
+                              reinterpret_cast<float*>(ws + P.attn))))
+            return rc;
+
+        c.W = W.o;
+        c.x = att;
+        c.y = x;
+        c.yfmt = OPURE_A_F32;
+        c.epi = EPI_RESIDUAL;
+        if ((rc = gemv_validate(c)) || (rc = gemv_launch(dev, c, gpart, gcnt))) return rc;
+
+        hipLaunchKernelGGL(k_rmsnorm, dim3(MR), dim3(256), 0, dev->stream, x, W.mlp_norm, m->hidden, m->rms_eps, xn,
+                           m->afmt);
+        OPURE_LAUNCH_CHECK("k_rmsnorm");
+
+        c.W = W.gate_up;
+        c.x = xn;
+        c.y = hbuf;
+        c.yfmt = m->afmt;
+        c.epi = EPI_SWIGLU;
+        if ((rc = gemv_validate(c)) || (rc = gemv_launch(dev, c, gpart, gcnt))) return rc;
+
+        c.W = W.down;
+        c.x = hbuf;
+        c.y = x;
+        c.yfmt = OPURE_A_F32;
+        c.epi = EPI_RESIDUAL;
+        if ((rc = gemv_validate(c)) || (rc = gemv_launch(dev, c, gpart, gcnt))) return rc;
+    }
+
+    hipLaunchKernelGGL(k_rmsnorm, dim3(MR), dim3(256), 0, dev->stream, x, m->final_norm, m->hidden, m->rms_eps, xn,
+                       m->afmt);
+    OPURE_LAUNCH_CHECK("k_rmsnorm");
+    c.W = m->lm_head;
+    c.x = xn;
+    c.y = a->logits;
+    c.yfmt = OPURE_A_F32;
+    c.epi = EPI_LOGITS;
+    c.logits.am_val = reinterpret_cast<float*>(ws + P.am_val);
+    c.logits.am_idx = reinterpret_cast<int32_t*>(ws + P.am_idx);
+    if ((rc = gemv_validate(c)) || (rc = gemv_launch(dev, c, gpart, gcnt))) return rc;
+
+    if (a->accept_mode == OPURE_ACCEPT_GREEDY)
+    {
+        rc = greedy_from_partials(dev, c.logits.am_val, c.logits.am_idx, P.lm_tiles, B, R - 1u, a->tokens + 1, R,
+                                  a->out_tokens, a->accepted, nullptr, nullptr);
+        if (rc) return rc;
+    }
+    else if (a->accept_mode == OPURE_ACCEPT_REJECTION)
+    {
+        opure_accept_args aa{};
+        aa.batch = B;
+        aa.k = R - 1u;
+        aa.vocab = m->vocab;
+        aa.target_logits = a->logits;
+        aa.draft_logits = a->draft_logits;
+        aa.drafts = a->tokens + 1;
+        aa.drafts_stride = R;
+        aa.temperature = a->temperature;
+        aa.seed = a->seed;
+        aa.pos_base = a->pos_base;
+        aa.out_tokens = a->out_tokens;
+        aa.accepted = a->accepted;
+        aa.dist_out = a->dist_out;
+        rc = accept_rejection_launch(dev, &aa, ws + P.rej, dev->counters + P.gemv_groups, nullptr, nullptr);
+        if (rc) return rc;
+    }
+    if (a->rollback)
+    {
+        opure_rollback_args rb{};
+        rb.model = m;
+        rb.kv = kv;
+        rb.batch = B;
+        rb.k = R - 1u;
+        rb.seq_len = a->seq_len;
+        rb.accepted = a->accepted;
+        rb.new_seq_len = a->new_seq_len;
+        rb.freed = a->freed;
+        rb.freed_stride = a->freed_stride;
+        rb.n_freed = a->n_freed;
+        rb.poison = a->poison;
+        rb.poison_bits = a->poison_bits;
+        if ((rc = rollback_validate(&rb)) || (rc = rollback_launch(dev, &rb))) return rc;
+    }
+    return OPURE_OK;
+}
+
+}  // extern "C"

@@ -21,7 +21,7 @@
 //                         Opure_RoPE.usf:56 (GPU) or Opure_CpuReference.cpp:179
 //    orc_swiglu           Opure_CpuReference.cpp:191-198
 //    orc_attention_paged  Opure_CpuReference.cpp:259-305 (two-pass softmax in
-//                         double, V accumulation rounded to float per step),
+//                         double; V accumulated in double, see the function),
 //                         GQA map Opure_FlashAttention_Decode.usf:71-72,
 //                         KV append Opure_RoPE.usf:105-114 (rotated K, raw V)
 //    orc_verify_forward   per-token order of Opure_CpuReference.cpp:225-345,
@@ -377,7 +377,7 @@ void orc_attention_paged(const orc_model* m, const orc_kv* kv, uint32_t layer,
     const uint32_t hd = m->head_dim, nh = m->n_heads, group = nh / m->n_kv_heads;
     const int32_t* pt = kv->page_table + static_cast<uint64_t>(seq) * kv->max_pages_per_seq;
     std::vector<double> scores;
-    std::vector<float> o(hd);
+    std::vector<double> o(hd);
     for (uint32_t j = 0; j < R; ++j)
     {
         const uint32_t seqLen = ctx + j + 1;
@@ -398,23 +398,43 @@ void orc_attention_paged(const orc_model* m, const orc_kv* kv, uint32_t layer,
             }
             double sum = 0.0;
             for (uint32_t s = 0; s < seqLen; ++s) { const double e = std::exp(scores[s] - mx); scores[s] = e; sum += e; }
-            std::fill(o.begin(), o.end(), 0.0f);
+            // The reference rounds this accumulator to float after every position
+            // (Opure_CpuReference.cpp:297) although its header promises double
+            // throughout (Opure_CpuReference.h:19-21); the oracle keeps it in
+            // double, which only removes error: an attention output over a long
+            // context is a heavily cancelled sum.
+            std::fill(o.begin(), o.end(), 0.0);
             for (uint32_t s = 0; s < seqLen; ++s)
             {
                 const uint64_t base = kv_index(m, kv, layer, pt[s / kv->page_size], 1, kvh, s % kv->page_size);
                 const double w = scores[s];
-                for (uint32_t d = 0; d < hd; ++d)
-                    o[d] = static_cast<float>(double(o[d]) + w * double(load_act(kv->pool, base + d, m->afmt)));
+                for (uint32_t d = 0; d < hd; ++d) o[d] += w * double(load_act(kv->pool, base + d, m->afmt));
             }
             const double invSum = 1.0 / (sum > 0.0 ? sum : 1.0);
             float* oRow = out + (static_cast<uint64_t>(j) * nh + hq) * hd;
-            for (uint32_t d = 0; d < hd; ++d) oRow[d] = static_cast<float>(double(o[d]) * invSum);
+            for (uint32_t d = 0; d < hd; ++d) oRow[d] = static_cast<float>(o[d] * invSum);
         }
     }
 }
 
+static int verify_impl(const orc_model* m, orc_kv* kv, uint32_t B, uint32_t R,
+                       const int32_t* tokens, const int32_t* seq_len, float* logits, float* trace);
+
 int orc_verify_forward(const orc_model* m, orc_kv* kv, uint32_t B, uint32_t R,
                        const int32_t* tokens, const int32_t* seq_len, float* logits)
+{
+    return verify_impl(m, kv, B, R, tokens, seq_len, logits, nullptr);
+}
+
+int orc_verify_forward_traced(const orc_model* m, orc_kv* kv, uint32_t B, uint32_t R,
+                              const int32_t* tokens, const int32_t* seq_len, float* logits,
+                              float* trace)
+{
+    return verify_impl(m, kv, B, R, tokens, seq_len, logits, trace);
+}
+
+static int verify_impl(const orc_model* m, orc_kv* kv, uint32_t B, uint32_t R,
+                       const int32_t* tokens, const int32_t* seq_len, float* logits, float* trace)
 {
     if (!m || !kv || !tokens || !seq_len || !logits || B == 0 || R == 0) return -1;
     const uint32_t h = m->hidden, hd = m->head_dim, nh = m->n_heads, nkv = m->n_kv_heads;
@@ -503,6 +523,13 @@ int orc_verify_forward(const orc_model* m, orc_kv* kv, uint32_t B, uint32_t R,
         orc_round_act(att.data(), att.size(), m->afmt);
         orc_gemv(&P.o, m->wfmt, att.data(), proj.data(), MR);
         for (uint64_t i = 0; i < x.size(); ++i) x[i] = x[i] + proj[i];
+        if (trace && L == 0)
+        {
+            float* t = trace;
+            std::memcpy(t, q.data(), q.size() * 4); t += q.size();
+            std::memcpy(t, att.data(), att.size() * 4); t += att.size();
+            std::memcpy(t, x.data(), x.size() * 4);
+        }
 
         orc_rmsnorm_rows(x.data(), P.mlp_norm, xn.data(), MR, h, m->rms_eps, m->afmt);
         orc_gemv(&P.gate_up, m->wfmt, xn.data(), gu.data(), MR);
@@ -513,9 +540,17 @@ int orc_verify_forward(const orc_model* m, orc_kv* kv, uint32_t B, uint32_t R,
         orc_round_act(hh.data(), hh.size(), m->afmt);
         orc_gemv(&P.down, m->wfmt, hh.data(), proj.data(), MR);
         for (uint64_t i = 0; i < x.size(); ++i) x[i] = x[i] + proj[i];
+        if (trace && L == 0)
+        {
+            float* t = trace + 2 * q.size() + x.size();
+            std::memcpy(t, hh.data(), hh.size() * 4); t += hh.size();
+            std::memcpy(t, x.data(), x.size() * 4);
+        }
     }
 
     orc_rmsnorm_rows(x.data(), m->final_norm, xn.data(), MR, h, m->rms_eps, m->afmt);
+    if (trace)
+        std::memcpy(trace + 2 * q.size() + 2 * x.size() + hh.size(), xn.data(), xn.size() * 4);
     orc_gemv(&m->lm_head, m->wfmt, xn.data(), logits, MR);
     return 0;
 }
@@ -527,10 +562,15 @@ void orc_argmax_rows(const float* logits, uint32_t rows, uint32_t V, int32_t* id
 {
     for (uint32_t r = 0; r < rows; ++r)
     {
+        // NaN logits count as -inf; ties and an all -inf row go to the lowest index
         const float* row = logits + static_cast<uint64_t>(r) * V;
-        float best = row[0];
+        float best = -HUGE_VALF;
         uint32_t bi = 0;
-        for (uint32_t v = 1; v < V; ++v) if (row[v] > best) { best = row[v]; bi = v; }
+        for (uint32_t v = 0; v < V; ++v)
+        {
+            const float c = row[v] != row[v] ? -HUGE_VALF : row[v];
+            if (c > best) { best = c; bi = v; }
+        }
         if (idx) idx[r] = static_cast<int32_t>(bi);
         if (val) val[r] = best;
     }
@@ -563,7 +603,8 @@ namespace {
 // sum, any parallel reduction order gives the same bits.
 struct RowStats { std::vector<float> e; std::vector<uint64_t> E; uint64_t S = 0; };
 
-inline uint64_t to_fixed(float v) { return static_cast<uint64_t>(static_cast<double>(v) * 4294967296.0 + 0.5); }
+// v in [0, 1]; NaN and non-positive values map to 0
+inline uint64_t to_fixed(float v) { return v > 0.0f ? static_cast<uint64_t>(static_cast<double>(v) * 4294967296.0 + 0.5) : 0u; }
 
 void row_stats(const float* logits, uint32_t V, float tau, RowStats& st)
 {

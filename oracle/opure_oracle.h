@@ -114,6 +114,15 @@ void orc_attention_paged(const orc_model* m, const orc_kv* kv, uint32_t layer,
 int orc_verify_forward(const orc_model* m, orc_kv* kv, uint32_t B, uint32_t R,
                        const int32_t* tokens, const int32_t* seq_len, float* logits);
 
+/* As orc_verify_forward, also recording layer 0's intermediates (the
+ * reference's ForwardTraced idea, Opure_CpuReference.h:48-54):
+ * trace = [q (MR*nh*hd, after RoPE, rounded) | att (MR*nh*hd) | x after the
+ *          attention residual (MR*h) | h (MR*ffn) | x after the layer (MR*h) |
+ *          final normed x (MR*h)] */
+int orc_verify_forward_traced(const orc_model* m, orc_kv* kv, uint32_t B, uint32_t R,
+                              const int32_t* tokens, const int32_t* seq_len, float* logits,
+                              float* trace);
+
 /* ---- acceptance -------------------------------------------------------- */
 /* greedy: target_logits [B][K+1][V]; drafts [B][K].
  * out_tokens [B][K+1] (emitted: accepted drafts then the correction/bonus,

@@ -90,6 +90,8 @@ def _declare(L):
     L.orc_attention_paged.restype = None
     L.orc_verify_forward.argtypes = [C.POINTER(OrcModel), C.POINTER(OrcKV), u32, u32, vp, vp, vp]
     L.orc_verify_forward.restype = C.c_int
+    L.orc_verify_forward_traced.argtypes = [C.POINTER(OrcModel), C.POINTER(OrcKV), u32, u32, vp, vp, vp, vp]
+    L.orc_verify_forward_traced.restype = C.c_int
     L.orc_argmax_rows.argtypes = [vp, u32, u32, vp, vp]; L.orc_argmax_rows.restype = None
     L.orc_accept_greedy.argtypes = [vp, vp, u32, u32, u32, vp, vp]; L.orc_accept_greedy.restype = None
     L.orc_accept_rejection.argtypes = [vp, vp, vp, u32, u32, u32, f32, u64, vp, vp, vp, vp]
@@ -319,6 +321,29 @@ def verify_forward(model: HostModel, kv: HostKV, tokens: np.ndarray, seq_len: np
     if rc != 0:
         raise ValueError(f"orc_verify_forward failed: {rc}")
     return logits
+
+
+def verify_forward_traced(model: HostModel, kv: HostKV, tokens: np.ndarray, seq_len: np.ndarray):
+    """Returns logits and layer 0's intermediates {q, att, x_attn, h, x_layer, xn_final}."""
+    c = model.cfg
+    tokens = np.ascontiguousarray(tokens, dtype=np.int32)
+    seq_len = np.ascontiguousarray(seq_len, dtype=np.int32)
+    B, R = tokens.shape
+    MR = B * R
+    qd, h, ff = c["n_heads"] * c["head_dim"], c["hidden"], c["ffn"]
+    sizes = [("q", qd), ("att", qd), ("x_attn", h), ("h", ff), ("x_layer", h), ("xn_final", h)]
+    trace = np.zeros(sum(MR * w for _, w in sizes), dtype=np.float32)
+    logits = np.zeros((B, R, c["vocab"]), dtype=np.float32)
+    kv._mk()
+    rc = lib().orc_verify_forward_traced(C.byref(model.desc), C.byref(kv.desc), B, R, _p(tokens), _p(seq_len),
+                                         _p(logits), _p(trace))
+    if rc != 0:
+        raise ValueError(f"orc_verify_forward_traced failed: {rc}")
+    out, off = {}, 0
+    for name, w in sizes:
+        out[name] = trace[off:off + MR * w].reshape(MR, w)
+        off += MR * w
+    return logits, out
 
 
 def accept_greedy(target_logits: np.ndarray, drafts: np.ndarray):

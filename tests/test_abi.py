@@ -1,0 +1,87 @@
+"""CPU checks of the C-ABI library: it loads, exports every entry point that
+include/opure_hip.h declares, and its host-only helpers and error paths behave
+(no kernel is launched here)."""
+import ctypes as C
+import os
+import re
+
+import numpy as np
+import pytest
+
+import opure_hip as H
+import oracle as O
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_symbols():
+    text = open(os.path.join(ROOT, "include", "opure_hip.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(opure_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    L = H.lib()
+    names = declared_symbols()
+    assert len(names) >= 35
+    missing = [n for n in names if not hasattr(L, n)]
+    assert not missing, missing
+
+
+def test_binding_declares_every_symbol():
+    L = H.lib()
+    for n in declared_symbols():
+        assert getattr(L, n).argtypes is not None, n
+
+
+@pytest.mark.parametrize("mode", [H.ROPE_GPU, H.ROPE_CPUREF])
+def test_rope_table_matches_oracle(mode):
+    a = H.rope_table(500000.0, 128, 1024, mode)
+    b = O.rope_table(500000.0, 128, 1024, mode)
+    assert np.array_equal(a[0], b[0]) and np.array_equal(a[1], b[1])
+
+
+def test_error_paths_without_device():
+    L = H.lib()
+    assert L.opure_rope_table(10000.0, 3, 4, 0, None, None) == H.E_INVALID
+    assert b"bad argument" in L.opure_last_error()
+    assert L.opure_dev_create(0, None) == H.E_INVALID
+    assert L.opure_gemv_batched_f32(None, None) == H.E_INVALID
+    assert L.opure_verify_step(None, None) == H.E_INVALID
+    assert L.opure_kv_rollback(None, None) == H.E_INVALID
+    assert L.opure_graph_destroy(None) == H.OK
+
+
+STRUCTS = {
+    "opure_linear": H.Linear, "opure_layer_weights": H.LayerWeights, "opure_model": H.Model,
+    "opure_kv": H.KV, "opure_gemv_args": H.GemvArgs, "opure_attn_args": H.AttnArgs,
+    "opure_accept_args": H.AcceptArgs, "opure_sample_args": H.SampleArgs,
+    "opure_rollback_args": H.RollbackArgs, "opure_verify_args": H.VerifyArgs,
+}
+
+
+def test_struct_layouts_match_header(tmp_path):
+    """Compile a probe against include/opure_hip.h and compare every struct's
+    size and field offsets with the ctypes mirror."""
+    import subprocess
+    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "opure_hip.h"', "int main(void){"]
+    for cname, cls in STRUCTS.items():
+        lines.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')
+        for fname, _ in cls._fields_:
+            cf = "in" if fname == "in_" else fname
+            lines.append(f'printf("{cname} {fname} %zu\\n", offsetof({cname}, {cf}));')
+    lines.append("return 0;}")
+    src = tmp_path / "probe.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "probe"
+    subprocess.run(["gcc", "-I", os.path.join(ROOT, "include"), str(src), "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split("\n")
+    got = {}
+    for ln in out:
+        if ln.strip():
+            a, b, c = ln.split()
+            got[(a, b)] = int(c)
+    for cname, cls in STRUCTS.items():
+        assert got[(cname, "size")] == C.sizeof(cls), cname
+        for fname, _ in cls._fields_:
+            assert got[(cname, fname)] == getattr(cls, fname).offset, (cname, fname)

@@ -1,0 +1,359 @@
+"""GPU parity of the individual kernels against the CPU oracle, through the C-ABI.
+
+Bars: integer/index work (argmax, acceptance, sampling, Philox, rollback) is
+bit-exact; fp32 GEMV/attention within fp32 accumulation error; fp16/bf16
+outputs within one storage ulp plus accumulation error.  Every GEMV is also
+checked for row independence (M=1 equals row 0 of M=16, bit for bit) and
+run-to-run determinism.
+"""
+import ctypes as C
+import os
+
+import numpy as np
+import pytest
+
+import opure_hip as H
+import oracle as O
+from gpu_util import say
+
+pytestmark = pytest.mark.gpu
+GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+@pytest.fixture(scope="module")
+def dev():
+    d = H.Dev(0)
+    say("device:", d.name, d.hbm_bytes >> 30, "GiB")
+    yield d
+    d.close()
+
+
+def to_act(x, afmt):
+    x = np.asarray(x, dtype=np.float32)
+    if afmt == H.A_F32:
+        return x.copy(), x.copy()
+    if afmt == H.A_F16:
+        b = x.astype(np.float16).view(np.uint16)
+        return b, b.view(np.float16).astype(np.float32)
+    b = O.np_f32_to_bf16_bits(x).reshape(x.shape)
+    return b, O.bf16_bits_to_f32(b).reshape(x.shape)
+
+
+def from_act(b, afmt):
+    if afmt == H.A_F32:
+        return b.astype(np.float32)
+    if afmt == H.A_F16:
+        return b.view(np.float16).astype(np.float32)
+    return O.bf16_bits_to_f32(b).reshape(b.shape)
+
+
+def dev_linear(dev, lin):
+    w = dev.upload(lin["w"])
+    s = dev.upload(lin["scale"]) if lin.get("scale") is not None else None
+    z = dev.upload(lin["zero"]) if lin.get("zero") is not None else None
+    return H.Linear(int(w), int(s) if s else None, int(z) if z else None, lin["out"], lin["in"]), (w, s, z)
+
+
+def run_gemv(dev, wfmt, lin_desc, x_bits, M, xfmt, yfmt, epi, y_init=None):
+    out = lin_desc.out // 2 if epi == H.EPI_SWIGLU else lin_desc.out
+    eb = 4 if yfmt == H.A_F32 else 2
+    xb = dev.upload(x_bits[:M])
+    yb = dev.alloc(M * out * eb)
+    if y_init is not None:
+        dev.write(yb, y_init[:M])
+    H.gemv(dev, wfmt, lin_desc, xb, yb, M, xfmt, yfmt, epi)
+    dev.sync()
+    y = dev.download(yb, np.float32 if yfmt == H.A_F32 else np.uint16, (M, out))
+    xb.free()
+    yb.free()
+    return y
+
+
+GEMV_CASES = [
+    # wfmt, afmt, out, in
+    (H.W_F32, H.A_F32, 960, 576),
+    (H.W_F32, H.A_F32, 576, 1536),
+    (H.W_F32, H.A_F32, 4096, 576),
+    (H.W_I8PC, H.A_F16, 3072, 2048),
+    (H.W_I8PC, H.A_F16, 2048, 8192),
+    (H.W_I8PC, H.A_F16, 8192, 2048),
+    (H.W_I4G128, H.A_F16, 1024, 4096),
+    (H.W_I4G128, H.A_BF16, 6144, 4096),
+    (H.W_I4G128, H.A_BF16, 4096, 14336),
+]
+
+
+def _ids(c):
+    return f"w{c[0]}-a{c[1]}-{c[2]}x{c[3]}"
+
+
+@pytest.mark.parametrize("case", GEMV_CASES, ids=[_ids(c) for c in GEMV_CASES])
+def test_gemv_store_residual_matches_oracle(dev, case):
+    wfmt, afmt, out, inn = case
+    say("gemv", _ids(case))
+    rng = np.random.default_rng(out * 7 + inn)
+    lin = O.make_linear(rng, out, inn, wfmt)
+    desc, keep = dev_linear(dev, lin)
+    x_bits, x_f = to_act(rng.standard_normal((16, inn)), afmt)
+    ref = O.gemv(lin, wfmt, x_f)
+    absref = np.abs(x_f).astype(np.float64) @ np.abs(O.dequant(lin, wfmt)).T
+    slack = 20.0 if (wfmt == H.W_I4G128 and afmt == H.A_BF16) else 1.0
+    y16 = run_gemv(dev, wfmt, desc, x_bits, 16, afmt, H.A_F32, H.EPI_STORE)
+    err = np.abs(y16 - ref)
+    assert np.all(err <= 1e-5 * slack * absref + 1e-6), (err.max(), (err / (absref + 1e-9)).max())
+    for M in (1, 6):
+        yM = run_gemv(dev, wfmt, desc, x_bits, M, afmt, H.A_F32, H.EPI_STORE)
+        assert np.array_equal(yM, y16[:M])                  # independent of M, bit for bit
+    again = run_gemv(dev, wfmt, desc, x_bits, 16, afmt, H.A_F32, H.EPI_STORE)
+    assert np.array_equal(again, y16)                        # deterministic
+    y0 = rng.standard_normal((16, out)).astype(np.float32)
+    yr = run_gemv(dev, wfmt, desc, x_bits, 5, afmt, H.A_F32, H.EPI_RESIDUAL, y_init=y0)
+    assert np.array_equal(yr, (y0[:5] + y16[:5]).astype(np.float32))
+    for b in keep:
+        if b:
+            b.free()
+
+
+@pytest.mark.parametrize("case", [(H.W_F32, H.A_F32, 3072, 576), (H.W_I8PC, H.A_F16, 16384, 2048),
+                                  (H.W_I4G128, H.A_BF16, 2048, 4096)], ids=["f32", "i8", "i4bf16"])
+def test_gemv_swiglu_matches_oracle(dev, case):
+    wfmt, afmt, out, inn = case
+    say("gemv swiglu", case)
+    rng = np.random.default_rng(out + inn)
+    lin = O.make_linear(rng, out, inn, wfmt)
+    desc, keep = dev_linear(dev, lin)
+    x_bits, x_f = to_act(rng.standard_normal((16, inn)), afmt)
+    gu = O.gemv(lin, wfmt, x_f)
+    F = out // 2
+    g, u = gu[:, :F].copy(), gu[:, F:].copy()
+    h = np.zeros_like(g)
+    O.lib().orc_swiglu(g.ctypes.data, u.ctypes.data, h.ctypes.data, g.size)
+    y = from_act(run_gemv(dev, wfmt, desc, x_bits, 16, afmt, afmt, H.EPI_SWIGLU), afmt)
+    tol = 1e-4 if afmt == H.A_F32 else (2e-3 if afmt == H.A_F16 else 1.6e-2)
+    np.testing.assert_allclose(y, h, rtol=tol, atol=1e-4 * max(1.0, np.abs(h).max()))
+    for b in keep:
+        if b:
+            b.free()
+
+
+def test_gemv_known_answer_fixtures(dev):
+    g = np.load(os.path.join(GOLD, "gemv_f32.npz"))
+    lin = {"w": g["W"], "out": 64, "in": 128}
+    desc, keep = dev_linear(dev, lin)
+    y = run_gemv(dev, H.W_F32, desc, g["X"][None, :], 1, H.A_F32, H.A_F32, H.EPI_STORE)[0]
+    rms = np.sqrt(np.mean((y.astype(np.float64) - g["ref"]) ** 2))
+    assert rms <= 1e-5 * np.abs(g["ref"]).max()
+    q = np.load(os.path.join(GOLD, "gemv_quant.npz"))
+    s16 = np.full(64, np.float16(q["sW"][0])).view(np.uint16)
+    lin = {"w": q["q"], "scale": s16, "out": 64, "in": 128}
+    desc, keep2 = dev_linear(dev, lin)
+    xb, xf = to_act(q["X"][None, :], H.A_F16)
+    y = run_gemv(dev, H.W_I8PC, desc, xb, 1, H.A_F16, H.A_F32, H.EPI_STORE)[0]
+    want = O.gemv(lin, H.W_I8PC, xf)[0]     # activations enter as fp16 on this path
+    np.testing.assert_allclose(y, want, rtol=1e-5, atol=1e-5)
+
+
+def test_gemv_rejects_bad_shapes(dev):
+    lin = {"w": np.zeros((24, 128), np.float32), "out": 24, "in": 128}
+    desc, keep = dev_linear(dev, lin)
+    x = dev.upload(np.zeros((1, 128), np.float32))
+    y = dev.alloc(24 * 4)
+    with pytest.raises(H.OpureError) as e:
+        H.gemv(dev, H.W_F32, desc, x, y, 1, H.A_F32, H.A_F32, H.EPI_STORE)
+    assert e.value.code == H.E_INVALID
+    with pytest.raises(H.OpureError) as e:
+        H.gemv(dev, H.W_F32, desc, x, y, 17, H.A_F32, H.A_F32, H.EPI_STORE)
+    assert e.value.code == H.E_CAPACITY
+    with pytest.raises(H.OpureError) as e:
+        H.gemv(dev, H.W_I8PC, desc, x, y, 1, H.A_F32, H.A_F32, H.EPI_STORE)
+    assert e.value.code == H.E_UNSUPPORTED
+
+
+# ---------------------------------------------------------------------------
+def attn_model(n_heads, n_kv, hd, afmt, scale=1.0, n_layers=1):
+    m = H.Model()
+    m.n_layers, m.n_heads, m.n_kv_heads, m.head_dim, m.afmt, m.attn_scale = n_layers, n_heads, n_kv, hd, afmt, scale
+    return m
+
+
+def run_attn(dev, m, pool_bits, pt, seq_len, R, q_bits, layer=0):
+    B = pt.shape[0]
+    pb = dev.upload(pool_bits)
+    ptb = dev.upload(pt.astype(np.int32))
+    sl = dev.upload(np.asarray(seq_len, dtype=np.int32))
+    qb = dev.upload(q_bits)
+    ob = dev.alloc(q_bits.nbytes)
+    kv = H.KV(int(pb), pool_bits.shape[1], 16, int(ptb), pt.shape[1])
+    a = H.AttnArgs(C.pointer(m), C.pointer(kv), layer, B, R, int(sl), int(max(seq_len)) + R, int(qb), int(ob))
+    H.check(H.lib().opure_attn_decode_paged(dev.h, C.byref(a)))
+    dev.sync()
+    out = dev.download(ob, q_bits.dtype, q_bits.shape)
+    for b in (pb, ptb, sl, qb, ob):
+        b.free()
+    return out
+
+
+@pytest.mark.parametrize("hd", [32, 64, 96, 128, 160, 192, 224, 256])
+def test_attention_known_answers(dev, hd):
+    g = np.load(os.path.join(GOLD, f"attention_hd{hd}.npz"))
+    pool = np.zeros((1, 1, 2, 2, 16, hd), np.float32)
+    pool[0, 0, 0, :, :7] = g["K"]
+    pool[0, 0, 1, :, :7] = g["V"]
+    out = run_attn(dev, attn_model(4, 2, hd, H.A_F32), pool, np.zeros((1, 1)), [6], 1,
+                   np.ascontiguousarray(g["Q"].reshape(1, -1)))
+    rms = np.sqrt(np.mean((out.ravel().astype(np.float64) - g["ref"].ravel()) ** 2))
+    assert rms <= 1e-5 * np.abs(g["ref"]).max()
+
+
+@pytest.mark.parametrize("afmt", [H.A_F32, H.A_F16, H.A_BF16], ids=["f32", "f16", "bf16"])
+def test_attention_paged_matches_oracle(dev, afmt):
+    say("attention afmt", afmt)
+    rng = np.random.default_rng(31 + afmt)
+    nh, nkv, hd, R, B, ps = 8, 2, 64, 5, 2, 16
+    ctx = [131, 37]
+    n_pages = 24
+    mcfg = dict(n_layers=2, hidden=64, n_heads=nh, n_kv_heads=nkv, head_dim=hd, ffn=64, vocab=64,
+                wfmt=O.W_F32, afmt=afmt)
+    hm = O.HostModel(**mcfg, attn_scale=0.125, max_pos=512, seed=1)
+    kv = O.HostKV(hm, n_pages=n_pages, batch=B, max_pages_per_seq=12)
+    kv.fill_random(rng, 1.0)
+    perm = rng.permutation(n_pages)
+    kv.page_table[0, :10] = perm[:10]
+    kv.page_table[1, :4] = perm[10:14]
+    q_bits, q_f = to_act(rng.standard_normal((B * R, nh * hd)), afmt)
+    want = np.zeros_like(q_f)
+    kv._mk()
+    for b in range(B):
+        qb = np.ascontiguousarray(q_f[b * R:(b + 1) * R])
+        ob = np.zeros_like(qb)
+        O.lib().orc_attention_paged(C.byref(hm.desc), C.byref(kv.desc), 1, b, ctx[b], R, qb.ctypes.data,
+                                    ob.ctypes.data)
+        want[b * R:(b + 1) * R] = ob
+    m = attn_model(nh, nkv, hd, afmt, 0.125, n_layers=2)
+    got = run_attn(dev, m, kv.pool, kv.page_table, ctx, R, q_bits, layer=1)
+    got_f = from_act(got, afmt)
+    if afmt == H.A_F32:
+        np.testing.assert_allclose(got_f, want, rtol=2e-5, atol=2e-5)
+    else:
+        want_r = to_act(want, afmt)[1]
+        ulp = 2e-3 if afmt == H.A_F16 else 1.6e-2
+        np.testing.assert_allclose(got_f, want_r, rtol=ulp, atol=ulp * 0.1)
+    # row j of a 5-row call equals a 1-row call at position ctx+j, bit for bit
+    for j in range(R):
+        one = run_attn(dev, m, kv.pool, kv.page_table[:1], [ctx[0] + j], 1, q_bits[j:j + 1], layer=1)
+        assert np.array_equal(one[0], got[j])
+
+
+# ---------------------------------------------------------------------------
+def run_accept(dev, fn, t, q, drafts, temperature=1.0, seed=0, pos_base=None, want_dist=False):
+    B, K1, V = t.shape
+    tb = dev.upload(t)
+    qb = dev.upload(q) if q is not None else None
+    db = dev.upload(np.ascontiguousarray(drafts, dtype=np.int32))
+    pbb = dev.upload(np.asarray(pos_base, dtype=np.uint32)) if pos_base is not None else None
+    ot = dev.alloc(B * K1 * 4)
+    ac = dev.alloc(B * 4)
+    di = dev.alloc(B * V * 4) if want_dist else None
+    a = H.AcceptArgs(B, K1 - 1, V, int(tb), int(qb) if qb else None, int(db), K1 - 1, temperature, seed,
+                     int(pbb) if pbb else None, int(ot), int(ac), int(di) if di else None)
+    H.check(fn(dev.h, C.byref(a)))
+    dev.sync()
+    res = (dev.download(ot, np.int32, (B, K1)), dev.download(ac, np.int32, (B,)),
+           dev.download(di, np.float32, (B, V)) if di else None)
+    for b in (tb, qb, db, pbb, ot, ac, di):
+        if b:
+            b.free()
+    return res
+
+
+def test_accept_greedy_bit_exact(dev):
+    rng = np.random.default_rng(41)
+    B, K, V = 6, 5, 50000
+    t = rng.standard_normal((B, K + 1, V)).astype(np.float32)
+    am = t.argmax(-1)
+    drafts = am[:, :K].astype(np.int32).copy()
+    for b in range(B):
+        if b % 3:
+            drafts[b, b % K] = (drafts[b, b % K] + 1) % V
+    t[0, 0, 777] = t[0, 0].max()            # exact tie: lowest index must win
+    t[1, 2, 5] = np.nan                      # NaN counts as -inf
+    out, acc, _ = run_accept(dev, H.lib().opure_accept_greedy, t, None, drafts)
+    w_out, w_acc = O.accept_greedy(t, drafts)
+    assert np.array_equal(acc, w_acc) and np.array_equal(out, w_out)
+
+
+@pytest.mark.parametrize("B,K,V,tau", [(8, 8, 49152, 1.0), (4, 3, 1000, 0.8), (64, 8, 49152, 1.0)],
+                         ids=["b8k8", "small-t0.8", "c2-full"])
+def test_accept_rejection_bit_exact(dev, B, K, V, tau):
+    say("rejection", B, K, V, tau)
+    rng = np.random.default_rng(B * 100 + K)
+    t = (rng.standard_normal((B, K + 1, V)) * 3).astype(np.float32)
+    q = (rng.standard_normal((B, K, V)) * 3).astype(np.float32)
+    # drafts drawn from q on Philox stream 0 (the C2 recipe), one seeded half accepted more often
+    q[: B // 2] = t[: B // 2, :K] + (rng.standard_normal((B // 2, K, V)) * 0.3).astype(np.float32)
+    pos = np.repeat(np.arange(K)[None], B, 0).ravel()
+    seq = np.repeat(np.arange(B)[:, None], K, 1).ravel()
+    drafts = O.sample_rows(q.reshape(B * K, V), tau, 2024, pos, seq, 0).reshape(B, K)
+    pos_base = rng.integers(0, 4096, size=B)
+    out, acc, dist = run_accept(dev, H.lib().opure_accept_rejection, t, q, drafts, tau, 2024, pos_base, True)
+    w_out, w_acc, w_dist = O.accept_rejection(t, q, drafts, tau, 2024, pos_base)
+    assert np.array_equal(acc, w_acc), (acc, w_acc)
+    assert np.array_equal(out, w_out)
+    assert np.abs(dist - w_dist).max() <= 1e-6
+    say("mean accepted", acc.mean())
+
+
+def test_sample_rows_and_philox_bit_exact(dev):
+    rng = np.random.default_rng(51)
+    rows, V = 37, 32000
+    lg = (rng.standard_normal((rows, V)) * 2).astype(np.float32)
+    pos = rng.integers(0, 1 << 20, rows).astype(np.uint32)
+    seq = rng.integers(0, 64, rows).astype(np.uint32)
+    lb, pb, sb = dev.upload(lg), dev.upload(pos), dev.upload(seq)
+    ob = dev.alloc(rows * 4)
+    a = H.SampleArgs(rows, V, int(lb), 0.8, 99, int(pb), int(sb), 0, int(ob))
+    H.check(H.lib().opure_sample_rows(dev.h, C.byref(a)))
+    dev.sync()
+    got = dev.download(ob, np.int32, (rows,))
+    assert np.array_equal(got, O.sample_rows(lg, 0.8, 99, pos, seq, 0))
+    n = 4096
+    pos = rng.integers(0, 1 << 31, n).astype(np.uint32)
+    seq = rng.integers(0, 1 << 31, n).astype(np.uint32)
+    pb, sb, ob = dev.upload(pos), dev.upload(seq), dev.alloc(n * 4)
+    seed = 0xDEADBEEFCAFEF00D
+    H.check(H.lib().opure_philox_uniform(dev.h, seed, int(pb), int(sb), 2, n, int(ob)))
+    dev.sync()
+    got = dev.download(ob, np.uint32, (n,))
+    want = np.array([O.lib().orc_philox_u32(seed, int(p), int(s), 2) for p, s in zip(pos, seq)], dtype=np.uint32)
+    assert np.array_equal(got, want)
+
+
+def test_rollback_bit_exact(dev):
+    hm = O.HostModel(n_layers=2, hidden=64, n_heads=4, n_kv_heads=2, head_dim=32, ffn=64, vocab=64,
+                     wfmt=O.W_I8PC, afmt=O.A_F16, seed=3)
+    kv = O.HostKV(hm, n_pages=10, batch=3, max_pages_per_seq=4)
+    kv.fill_random(np.random.default_rng(2))
+    kv.page_table[0, :3] = [5, 1, 2]
+    kv.page_table[1, :2] = [0, 3]
+    kv.page_table[2, :2] = [7, 8]
+    seq_len = np.array([14, 9, 26], np.int32)
+    acc = np.array([1, 5, 0], np.int32)
+    pool0, pt0 = kv.pool.copy(), kv.page_table.copy()
+    want_len, want_freed, want_nf = O.kv_rollback(kv, hm, 5, seq_len, acc, poison_bits=0x7E00)
+    cfg = dict(hm.cfg)
+    dkv = H.DeviceKV(dev, cfg, 10, 3, 4)
+    dkv.set_pool(pool0)
+    dkv.set_page_table(pt0)
+    m = attn_model(4, 2, 32, H.A_F16, n_layers=2)
+    sl, ac = dev.upload(seq_len), dev.upload(acc)
+    nl, fr, nf = dev.alloc(12), dev.alloc(3 * 8 * 4), dev.alloc(12)
+    dev.fill_u32(fr, 0xFFFFFFFF, 24)
+    a = H.RollbackArgs(C.pointer(m), C.pointer(dkv.desc), 3, 5, int(sl), int(ac), int(nl), int(fr), 8, int(nf), 1,
+                       0x7E00)
+    H.check(H.lib().opure_kv_rollback(dev.h, C.byref(a)))
+    dev.sync()
+    assert np.array_equal(dev.download(nl, np.int32, (3,)), want_len)
+    assert np.array_equal(dev.download(nf, np.int32, (3,)), want_nf)
+    assert np.array_equal(dev.download(fr, np.int32, (3, 8)), want_freed)
+    assert np.array_equal(dkv.get_page_table(), kv.page_table)
+    assert np.array_equal(dkv.get_pool(), kv.pool)

@@ -1,0 +1,294 @@
+"""GPU parity of the whole verify step (opure_verify_step) against the CPU oracle.
+
+- logits within max_abs 1e-4 (fp32 path) or 2e-2 (fp16/bf16 paths);
+- the K/V rows the step appends agree with the oracle's;
+- the in-step acceptance equals the oracle's acceptance applied to the same
+  GPU logits, bit for bit, and equals the oracle's own decision wherever the
+  oracle's top-1/top-2 gap exceeds the logit tolerance;
+- a K+1-row step equals K+1 single-row steps bit for bit (so greedy
+  speculative decoding reproduces greedy decoding exactly on the GPU);
+- a captured hipGraph replays to the eager result;
+- rollback restores the cache and length as the oracle does.
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import opure_hip as H
+import oracle as O
+import spec_loop
+from gpu_util import VerifyRunner, device_kv, device_model, say, top2_gap
+
+pytestmark = pytest.mark.gpu
+
+FMTS = [(O.W_F32, O.A_F32, 1e-4), (O.W_I8PC, O.A_F16, 2e-2), (O.W_I4G128, O.A_F16, 2e-2),
+        (O.W_I4G128, O.A_BF16, 2e-2)]
+FMT_IDS = ["f32", "i8-f16", "i4-f16", "i4-bf16"]
+
+
+@pytest.fixture(scope="module")
+def dev():
+    d = H.Dev(0)
+    yield d
+    d.close()
+
+
+def small_model(wfmt, afmt, n_layers=2, seed=5, tied=True, vocab=1024, hidden=256, ffn=512, heads=(4, 2), hd=64,
+                max_pos=1024, theta=10000.0, attn_scale=0.125):
+    return O.HostModel(n_layers=n_layers, hidden=hidden, n_heads=heads[0], n_kv_heads=heads[1], head_dim=hd,
+                       ffn=ffn, vocab=vocab, wfmt=wfmt, afmt=afmt, attn_scale=attn_scale, theta=theta,
+                       max_pos=max_pos, tied=tied, seed=seed, norm_jitter=0.1)
+
+
+def self_drafts(m, kv_o, pool0, tokens, seq_len, seq=0):
+    """Sequence `seq` drafts its own greedy continuation: row j+1 := argmax of
+    row j, built one row at a time because row j depends on rows <= j."""
+    toks = np.array(tokens, np.int32).copy()
+    for j in range(toks.shape[1] - 1):
+        kv_o.pool[...] = pool0
+        lg = O.verify_forward(m, kv_o, toks, np.asarray(seq_len, np.int32))
+        toks[seq, j + 1] = int(np.argmax(lg[seq, j]))
+    kv_o.pool[...] = pool0
+    return toks
+
+
+def random_cache(m, B, ctx_max, n_pages, seed):
+    rng = np.random.default_rng(seed)
+    mp = (ctx_max + 15) // 16
+    kv = O.HostKV(m, n_pages=n_pages, batch=B, max_pages_per_seq=mp)
+    kv.fill_random(rng, 1.0)
+    perm = rng.permutation(n_pages)
+    for b in range(B):
+        kv.page_table[b] = perm[b * mp:(b + 1) * mp]
+    return kv
+
+
+@pytest.mark.parametrize("fmt", FMTS, ids=FMT_IDS)
+def test_verify_step_matches_oracle(dev, fmt):
+    wfmt, afmt, tol = fmt
+    say("verify small", FMT_IDS[FMTS.index(fmt)])
+    m = small_model(wfmt, afmt, tied=wfmt != O.W_I4G128)
+    B, R = 2, 5
+    kv = random_cache(m, B, 320, 48, seed=7)
+    seq_len = np.array([251, 96], np.int32)
+    rng = np.random.default_rng(3)
+    tokens = rng.integers(0, m.cfg["vocab"], size=(B, R)).astype(np.int32)
+    dm, dkv = device_model(dev, m), device_kv(dev, m, kv)
+    run = VerifyRunner(dev, dm, dkv, B, R, max_ctx=320)
+    want_pool = kv.pool.copy()
+    kv_o = O.HostKV(m, n_pages=kv.n_pages, batch=B, max_pages_per_seq=kv.max_pages)
+    kv_o.pool[...] = kv.pool
+    kv_o.page_table[...] = kv.page_table
+    # sequence 0 drafts the oracle's own greedy continuation, so acceptance is exercised
+    tokens = self_drafts(m, kv_o, want_pool, tokens, seq_len, seq=0)
+    kv_o.pool[...] = want_pool
+    want = O.verify_forward(m, kv_o, tokens, seq_len)
+    run.step(tokens, seq_len, accept=H.ACCEPT_GREEDY)
+    got = run.get_logits()
+    err = np.abs(got - want).max()
+    say("max_abs logits", err)
+    assert err <= tol
+    # appended K/V rows
+    gpool = dkv.get_pool()
+    if afmt == O.A_F32:
+        assert np.abs(gpool - kv_o.pool).max() <= 1e-4
+    else:
+        import npref
+        assert np.abs(npref.act_to_f32(gpool, afmt) - npref.act_to_f32(kv_o.pool, afmt)).max() <= 2e-2
+    # acceptance inside the step == oracle acceptance on the same GPU logits (bit-exact)
+    out, acc = run.get_accept()
+    w_out, w_acc = O.accept_greedy(got, tokens[:, 1:])
+    assert np.array_equal(out, w_out) and np.array_equal(acc, w_acc)
+    # and == the oracle's own decision wherever its top-1/top-2 gap exceeds the tolerance
+    o_out, o_acc = O.accept_greedy(want, tokens[:, 1:])
+    if np.all(top2_gap(want) > tol):
+        assert np.array_equal(out, o_out) and np.array_equal(acc, o_acc)
+    say("accepted", acc, "oracle", o_acc)
+    assert acc[0] == R - 1
+
+
+@pytest.mark.parametrize("fmt", FMTS[:2], ids=FMT_IDS[:2])
+def test_rows_equal_single_row_steps(dev, fmt):
+    wfmt, afmt, _ = fmt
+    m = small_model(wfmt, afmt)
+    kv = random_cache(m, 1, 256, 16, seed=9)
+    dm = device_model(dev, m)
+    dkv = device_kv(dev, m, kv)
+    tokens = np.array([[11, 22, 33, 44, 55, 66]], np.int32)
+    multi = VerifyRunner(dev, dm, dkv, 1, 6, 256)
+    multi.step(tokens, [150])
+    lm = multi.get_logits()
+    dkv.set_pool(kv.pool)
+    one = VerifyRunner(dev, dm, dkv, 1, 1, 256)
+    for j in range(6):
+        one.step(tokens[:, j:j + 1], [150 + j])
+        assert np.array_equal(one.get_logits()[0, 0], lm[0, j]), j
+
+
+def test_graph_replay_equals_eager(dev):
+    m = small_model(O.W_I8PC, O.A_F16)
+    kv = random_cache(m, 2, 256, 32, seed=13)
+    dm, dkv = device_model(dev, m), device_kv(dev, m, kv)
+    run = VerifyRunner(dev, dm, dkv, 2, 4, 256)
+    tokens = np.array([[1, 2, 3, 4], [5, 6, 7, 8]], np.int32)
+    run.step(tokens, [100, 30], accept=H.ACCEPT_GREEDY)
+    eager = run.get_logits()
+    eager_acc = run.get_accept()
+    a = run.args(accept=H.ACCEPT_GREEDY)
+    dev.graph_begin()
+    H.check(H.lib().opure_verify_step(dev.h, C.byref(a)))
+    g = dev.graph_end()
+    for i in range(4):
+        dev.fill_u32(run.logits, 0x7FC00000, 2 * 4 * m.cfg["vocab"])   # eager work between replays
+        dev.sync()
+        dev.graph_launch(g)
+        dev.sync()
+        assert np.array_equal(run.get_logits(), eager), i
+        o, acc = run.get_accept()
+        assert np.array_equal(o, eager_acc[0]) and np.array_equal(acc, eager_acc[1])
+    dev.graph_destroy(g)
+
+
+def test_verify_with_rollback_matches_oracle(dev):
+    m = small_model(O.W_I8PC, O.A_F16)
+    B, R = 2, 6
+    kv = random_cache(m, B, 512, 64, seed=17)
+    seq_len = np.array([300, 120], np.int32)
+    kv_o = O.HostKV(m, n_pages=kv.n_pages, batch=B, max_pages_per_seq=kv.max_pages)
+    kv_o.pool[...] = kv.pool
+    kv_o.page_table[...] = kv.page_table
+    tokens = np.random.default_rng(2).integers(0, m.cfg["vocab"], size=(B, R)).astype(np.int32)
+    dm, dkv = device_model(dev, m), device_kv(dev, m, kv)
+    run = VerifyRunner(dev, dm, dkv, B, R, 512)
+    run.step(tokens, seq_len, accept=H.ACCEPT_GREEDY, rollback=True, poison=True, poison_bits=0x7E00,
+             free_pages=True)
+    got = run.get_logits()
+    out, acc = run.get_accept()
+    O.verify_forward(m, kv_o, tokens, seq_len)
+    w_out, w_acc = O.accept_greedy(got, tokens[:, 1:])
+    assert np.array_equal(acc, w_acc)
+    new_len, freed, nf = O.kv_rollback(kv_o, m, R - 1, seq_len, acc, poison_bits=0x7E00)
+    assert np.array_equal(dev.download(run.new_len, np.int32, (B,)), new_len)
+    assert np.array_equal(dev.download(run.n_freed, np.int32, (B,)), nf)
+    assert np.array_equal(dkv.get_page_table(), kv_o.page_table)
+    gpool = dkv.get_pool()
+    # rolled-back slots carry the poison on both sides; kept slots agree within tolerance
+    assert np.array_equal(gpool == 0x7E00, kv_o.pool == 0x7E00)
+    import npref
+    keep = kv_o.pool != 0x7E00
+    diff = np.abs(npref.act_to_f32(gpool, O.A_F16) - npref.act_to_f32(kv_o.pool, O.A_F16))
+    assert diff[keep].max() <= 2e-2
+
+
+def _full_width(wfmt, afmt, shape, n_layers, vocab, seed, attn_scale):
+    h, nh, nkv, hd, ff = shape
+    return O.HostModel(n_layers=n_layers, hidden=h, n_heads=nh, n_kv_heads=nkv, head_dim=hd, ffn=ff, vocab=vocab,
+                       wfmt=wfmt, afmt=afmt, attn_scale=attn_scale, theta=500000.0, max_pos=8192 + 64,
+                       tied=wfmt == O.W_I8PC, seed=seed)
+
+
+# attn_scale 1.0 is the reference's literal (unscaled) attention; 1/sqrt(hd) the
+# Llama-3 value used for the Llama-shaped configurations
+@pytest.mark.parametrize("cfg", [
+    ("c3-1b-int8-2layers-unscaled", O.W_I8PC, O.A_F16, (2048, 32, 8, 64, 8192), 128256, 2048, 6, 1.0),
+    ("c3-1b-int8-2layers", O.W_I8PC, O.A_F16, (2048, 32, 8, 64, 8192), 128256, 2048, 6, 0.125),
+    ("c4-8b-int4-2layers", O.W_I4G128, O.A_BF16, (4096, 32, 8, 128, 14336), 16384, 8192, 8, 128 ** -0.5),
+], ids=lambda c: c[0] if isinstance(c, tuple) else str(c))
+def test_full_width_two_layers(dev, cfg):
+    name, wfmt, afmt, shape, vocab, ctx, R, scale = cfg
+    say("full width", name)
+    m = _full_width(wfmt, afmt, shape, 2, vocab, seed=101, attn_scale=scale)
+    kv = random_cache(m, 1, ctx + R, (ctx + R + 15) // 16, seed=5)
+    seq_len = np.array([ctx], np.int32)
+    tokens = np.random.default_rng(1).integers(0, vocab, size=(1, R)).astype(np.int32)
+    dm, dkv = device_model(dev, m), device_kv(dev, m, kv)
+    run = VerifyRunner(dev, dm, dkv, 1, R, ctx + R)
+    O.set_threads(16)
+    try:
+        kv_o = O.HostKV(m, n_pages=kv.n_pages, batch=1, max_pages_per_seq=kv.max_pages)
+        kv_o.pool[...] = kv.pool
+        kv_o.page_table[...] = kv.page_table
+        tokens = self_drafts(m, kv_o, kv.pool, tokens, seq_len)   # the oracle's greedy continuation
+    finally:
+        O.set_threads(1)
+    O.set_threads(16)
+    try:
+        want = O.verify_forward(m, kv_o, tokens, seq_len)
+    finally:
+        O.set_threads(1)
+    dkv.set_pool(kv.pool)
+    run.step(tokens, seq_len, accept=H.ACCEPT_GREEDY)
+    got = run.get_logits()
+    err = np.abs(got - want).max()
+    gap = top2_gap(want).min()
+    say(name, "max_abs", err, "min top2 gap", gap)
+    assert err <= 2e-2
+    out, acc = run.get_accept()
+    w_out, w_acc = O.accept_greedy(got, tokens[:, 1:])
+    assert np.array_equal(out, w_out) and np.array_equal(acc, w_acc)
+    if gap > 2e-2:
+        o_out, o_acc = O.accept_greedy(want, tokens[:, 1:])
+        assert np.array_equal(out, o_out) and np.array_equal(acc, o_acc)
+        assert acc[0] == R - 1
+
+
+def test_c1_shape_speculative_equals_greedy(dev):
+    """SmolLM-135M shape (hidden 576, 9/3 heads, hd 64, ffn 1536, vocab 49152),
+    4 target layers and a 1-layer draft, fp32, K=4: the GPU's speculative output
+    equals its greedy output bit for bit, and the oracle's greedy tokens."""
+    shape = dict(hidden=576, n_heads=9, n_kv_heads=3, head_dim=64, ffn=1536, vocab=49152, wfmt=O.W_F32,
+                 afmt=O.A_F32, attn_scale=1.0, theta=10000.0, max_pos=512, tied=True, norm_jitter=0.0)
+    tgt = O.HostModel(n_layers=4, seed=71, **shape)
+    drf = O.HostModel(n_layers=1, seed=72, **shape)
+    prompt = list(np.random.default_rng(0).integers(0, 49152, 32))
+    n_new, K = 24, 4
+    dms = {"t": device_model(dev, tgt), "d": device_model(dev, drf)}
+    kvs = {}
+    runners = {}
+    for key, hm in (("t", tgt), ("d", drf)):
+        kvh = O.HostKV(hm, n_pages=8, batch=1, max_pages_per_seq=8)
+        kvh.page_table[0] = np.arange(8)
+        kvs[key] = device_kv(dev, hm, kvh)
+
+    def runner(key, R):
+        if (key, R) not in runners:
+            runners[(key, R)] = VerifyRunner(dev, dms[key], kvs[key], 1, R, 128)
+        return runners[(key, R)]
+
+    def gpu_step(key, toks, ctx):
+        R = toks.shape[1]
+        out = []
+        for s in range(0, R, 16):            # long prompts are fed 16 rows at a time
+            r = runner(key, min(16, R - s))
+            r.step(toks[:, s:s + 16], [ctx + s])
+            out.append(r.get_logits())
+        return np.concatenate(out, axis=1)
+
+    def gpu_accept(toks, ctx):
+        r = runner("t", toks.shape[1])
+        r.step(toks, [ctx], accept=H.ACCEPT_GREEDY)
+        o, a = r.get_accept()
+        return o[0], int(a[0])
+
+    greedy_gpu, _ = spec_loop.greedy(gpu_step, prompt, n_new)
+    spec_gpu, hist = spec_loop.speculative(gpu_step, gpu_accept, prompt, n_new, K)
+    say("gpu greedy", greedy_gpu[:8], "accepted per step", hist)
+    assert spec_gpu == greedy_gpu
+
+    okv = {k: O.HostKV(hm, n_pages=8, batch=1, max_pages_per_seq=8) for k, hm in (("t", tgt), ("d", drf))}
+    for k in okv:
+        okv[k].page_table[0] = np.arange(8)
+    models = {"t": tgt, "d": drf}
+
+    def orc_step(key, toks, ctx):
+        return O.verify_forward(models[key], okv[key], toks, np.array([ctx], np.int32))
+
+    O.set_threads(16)
+    try:
+        greedy_orc, gaps = spec_loop.greedy(orc_step, prompt, n_new)
+    finally:
+        O.set_threads(1)
+    say("oracle min gap", min(gaps))
+    if min(gaps) > 1e-4:
+        assert greedy_orc == greedy_gpu
