@@ -1,0 +1,278 @@
+"""Benchmark of the speculative-decoding verify step on one MI355X.
+
+    python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--config c3|c4|c1]
+                    [--cpu-baseline auto|skip] [--no-kernel-timing]
+
+One step = one verify pass over K+1 rows: embedding, every layer (fused QKV
+GEMV + RoPE + paged KV append, paged attention, o_proj + residual, gate/up
+GEMV + SwiGLU, down + residual), LM head, greedy acceptance and KV rollback,
+replayed from a captured hipGraph with the model, cache and drafts resident in
+HBM.  The default workload is c3 (Llama-3.2-1B shape, int8 per-channel
+weights, fp16 activations, K=5, a 2048-token context prefilled by the model
+itself from random tokens, 16-token pages scattered over the pool).
+
+Drafts are the target's own greedy continuation, so all K drafts are accepted
+(the verify work does not depend on the drafts); the same step with random
+drafts is timed as well and reported beside it.
+
+Output: one JSON line (metric, value, ... roofline, cpu_baseline, parity).
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "opure-voxelengine_amd"))
+
+import opure_hip as H  # noqa: E402
+import synth  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+
+
+def log(*a):
+    print("[bench]", *a, file=sys.stderr, flush=True)
+
+
+class Verify:
+    """Device buffers and argument block for verify steps of one shape."""
+
+    def __init__(self, dev, model, kv_desc, B, R, max_ctx):
+        self.dev, self.model, self.B, self.R, self.max_ctx = dev, model, B, R, max_ctx
+        V = model.cfg["vocab"]
+        self.kv_desc = kv_desc
+        self.tokens = dev.alloc(B * R * 4)
+        self.seq_len = dev.alloc(B * 4)
+        self.new_len = dev.alloc(B * 4)
+        self.logits = dev.alloc(B * R * V * 4)
+        self.out_tokens = dev.alloc(B * R * 4)
+        self.accepted = dev.alloc(B * 4)
+        H.check(H.lib().opure_verify_reserve(dev.h, C.byref(model.desc), B, R, max_ctx))
+
+    def args(self, accept):
+        a = H.VerifyArgs()
+        a.model = C.pointer(self.model.desc)
+        a.kv = C.pointer(self.kv_desc)
+        a.batch, a.rows, a.max_ctx = self.B, self.R, self.max_ctx
+        a.tokens, a.seq_len, a.logits = int(self.tokens), int(self.seq_len), int(self.logits)
+        a.accept_mode = accept
+        a.out_tokens, a.accepted = int(self.out_tokens), int(self.accepted)
+        a.rollback = 1 if accept else 0
+        a.new_seq_len = int(self.new_len)
+        self._a = a
+        return a
+
+    def run(self, tokens, seq_len, accept=H.ACCEPT_NONE):
+        self.dev.write(self.tokens, np.ascontiguousarray(tokens, np.int32))
+        self.dev.write(self.seq_len, np.ascontiguousarray(seq_len, np.int32))
+        H.check(H.lib().opure_verify_step(self.dev.h, C.byref(self.args(accept))))
+
+    def logits_host(self, rows=None):
+        V = self.model.cfg["vocab"]
+        return self.dev.download(self.logits, np.float32, (self.B, self.R, V))
+
+
+def build_workload(dev, cfg_name, seed=1234):
+    cfg = dict(synth.CONFIGS[cfg_name])
+    K, ctx = cfg["K"], cfg["ctx"]
+    R = K + 1
+    t0 = time.time()
+    model = synth.SynthModel(dev, cfg, seed=seed, max_pos=ctx + 64)
+    log(f"model {cfg_name} built on device in {time.time() - t0:.1f}s")
+    rng = np.random.default_rng(seed)
+    n_pages = (ctx + R + 15) // 16 + 8
+    kv = H.DeviceKV(dev, cfg, n_pages, 1, n_pages)
+    pt = rng.permutation(n_pages).astype(np.int32)[None, :]
+    kv.set_page_table(pt)
+    # prefill: the model itself writes the context's K/V, 16 rows per step
+    prompt = rng.integers(0, cfg["vocab"], size=ctx).astype(np.int32)
+    pre = Verify(dev, model, kv.desc, 1, 16, ctx + R)
+    t0 = time.time()
+    for s in range(0, ctx - 16, 16):
+        pre.run(prompt[None, s:s + 16], [s])
+    last = ctx - (ctx - 16) // 16 * 16 if ctx > 16 else ctx
+    tail = Verify(dev, model, kv.desc, 1, last, ctx + R)
+    tail.run(prompt[None, ctx - last:], [ctx - last])
+    dev.sync()
+    nxt = int(np.argmax(tail.logits_host()[0, -1]))
+    log(f"prefilled {ctx} tokens in {time.time() - t0:.2f}s")
+    # self-drafts: the target's greedy continuation, one row at a time
+    one = Verify(dev, model, kv.desc, 1, 1, ctx + R)
+    drafts = []
+    tok = nxt
+    for j in range(K):
+        one.run([[tok]], [ctx + j])
+        tok = int(np.argmax(one.logits_host()[0, 0]))
+        drafts.append(tok)
+    step = Verify(dev, model, kv.desc, 1, R, ctx + R)
+    return dict(cfg=cfg, model=model, kv=kv, step=step, tokens=np.array([[nxt] + drafts], np.int32),
+                ctx=ctx, R=R, K=K, rng=rng)
+
+
+def time_graph(dev, step, tokens, ctx, warmup, steps):
+    step.dev.write(step.tokens, tokens)
+    step.dev.write(step.seq_len, np.array([ctx], np.int32))
+    a = step.args(H.ACCEPT_GREEDY)
+    dev.graph_begin()
+    H.check(H.lib().opure_verify_step(dev.h, C.byref(a)))
+    g = dev.graph_end()
+    for _ in range(warmup):
+        dev.graph_launch(g)
+    dev.sync()
+    t0 = time.perf_counter()
+    dev.timer_begin()
+    for _ in range(steps):
+        dev.graph_launch(g)
+    dev.timer_end()
+    gpu_ms = dev.timer_ms()
+    dev.sync()
+    wall_ms = (time.perf_counter() - t0) * 1e3
+    acc = dev.download(step.accepted, np.int32, (1,))
+    out = dev.download(step.out_tokens, np.int32, (1, step.R))
+    dev.graph_destroy(g)
+    return dict(ms_per_step=gpu_ms / steps, wall_ms_per_step=wall_ms / steps, accepted=int(acc[0]),
+                out_tokens=out[0].tolist())
+
+
+def time_dominant_gemv(dev, w, reps=5):
+    """Live timing of the gate/up GEMV (SwiGLU epilogue): one launch per layer,
+    rotating through the layers so the weights stream from HBM, each launch
+    bracketed by HIP events on the library's stream."""
+    m = w["model"]
+    cfg = m.cfg
+    M = w["R"]
+    eb = 2 if cfg["afmt"] != H.A_F32 else 4
+    x = dev.alloc(M * cfg["hidden"] * eb)
+    y = dev.alloc(M * cfg["ffn"] * eb)
+    H.check(H.lib().opure_convert_f32(dev.h, int(dev.upload(np.random.default_rng(0).standard_normal(
+        (M, cfg["hidden"])).astype(np.float32))), int(x), cfg["afmt"], M * cfg["hidden"]))
+    fn = {H.W_F32: H.lib().opure_gemv_batched_f32, H.W_I8PC: H.lib().opure_gemv_batched_i8pc,
+          H.W_I4G128: H.lib().opure_gemv_batched_i4g128}[cfg["wfmt"]]
+    times = []
+    for r in range(reps + 1):
+        for L in range(cfg["n_layers"]):
+            lin = synth.SynthModel._lin(m.layers[L]["gate_up"])
+            a = H.GemvArgs(lin, int(x), int(y), M, cfg["afmt"], cfg["afmt"], H.EPI_SWIGLU)
+            dev.timer_begin()
+            H.check(fn(dev.h, C.byref(a)))
+            dev.timer_end()
+            ms = dev.timer_ms()
+            if r > 0:
+                times.append(ms)
+    out, inn = 2 * cfg["ffn"], cfg["hidden"]
+    alg = synth.linear_bytes(cfg["wfmt"], out, inn) + M * inn * eb + M * cfg["ffn"] * eb
+    avg_ms = float(np.mean(times))
+    return dict(kernel=f"k_gemv<w{cfg['wfmt']},a{cfg['afmt']},swiglu> gate/up {out}x{inn}, M={M}",
+                bytes_per_launch=alg, avg_us=avg_ms * 1e3, gbs=alg / (avg_ms * 1e-3) / 1e9)
+
+
+def cpu_baseline(dev, w, gpu_logits, gpu_accept):
+    """The CPU oracle (scalar, one thread) timed on one verify step of the same
+    workload, after downloading the device's model and cache."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+
+    m, cfg, step = w["model"], w["cfg"], w["step"]
+    t0 = time.time()
+    host = m.download()
+    hm = O.HostModel.from_arrays(cfg, host)
+    kvd = w["kv"]
+    kv = O.HostKV(hm, n_pages=kvd.n_pages, batch=1, max_pages_per_seq=kvd.max_pages)
+    kv.pool[...] = kvd.get_pool()
+    kv.page_table[...] = kvd.get_page_table()
+    log(f"downloaded model + cache for the oracle in {time.time() - t0:.1f}s")
+    O.set_threads(1)
+    t0 = time.perf_counter()
+    want = O.verify_forward(hm, kv, w["tokens"], np.array([w["ctx"]], np.int32))
+    dt = time.perf_counter() - t0
+    out, acc = O.accept_greedy(want, w["tokens"][:, 1:])
+    err = float(np.abs(gpu_logits - want).max())
+    s = np.sort(want.astype(np.float64), axis=-1)
+    gap = float((s[..., -1] - s[..., -2]).min())
+    return dict(value=(int(acc[0]) + 1) / dt, unit="accepted tokens/s", cores=1, kind="port",
+                sample=f"one {cfg['n_layers']}-layer verify step ({w['R']} rows, ctx {w['ctx']}) of the same "
+                       f"workload through the scalar oracle: {dt:.1f}s"), dict(
+        logits_max_abs=err, oracle_min_top2_gap=gap, accepted_equal=bool(acc[0] == gpu_accept["accepted"]),
+        tokens_equal=bool(out[0].tolist() == gpu_accept["out_tokens"]))
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", default="c3", choices=sorted(synth.CONFIGS))
+    ap.add_argument("--cpu-baseline", default="auto", choices=["auto", "skip"])
+    ap.add_argument("--no-kernel-timing", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
+              "multi-GPU sharding is a design note, not a measured path", file=sys.stderr)
+        sys.exit(2)
+
+    dev = H.Dev(0)
+    log("device", dev.name)
+    w = build_workload(dev, args.config)
+    cfg, ctx, R, K = w["cfg"], w["ctx"], w["R"], w["K"]
+    res = time_graph(dev, w["step"], w["tokens"], ctx, args.warmup, args.steps)
+    gpu_logits = w["step"].logits_host()
+    log(f"self-drafts: {res['ms_per_step'] * 1e3:.1f} us/step, accepted {res['accepted']}/{K}")
+    rnd = w["tokens"].copy()
+    rnd[0, 1:] = w["rng"].integers(0, cfg["vocab"], K)
+    res_r = time_graph(dev, w["step"], rnd, ctx, args.warmup, args.steps)
+    log(f"random drafts: {res_r['ms_per_step'] * 1e3:.1f} us/step, accepted {res_r['accepted']}/{K}")
+    # restore the self-draft step's logits for the parity check (same cache state)
+    step_bytes = synth.verify_bytes(cfg, R, ctx)
+    step_gbs = step_bytes["total"] / (res["ms_per_step"] * 1e-3) / 1e9
+    kern = None if args.no_kernel_timing else time_dominant_gemv(dev, w)
+    if kern:
+        log(f"dominant kernel {kern['kernel']}: {kern['avg_us']:.1f} us, {kern['gbs']:.0f} GB/s")
+    cpu, parity = None, None
+    if args.cpu_baseline == "auto":
+        cpu, parity = cpu_baseline(dev, w, gpu_logits, res)
+        log("cpu baseline", cpu, "parity", parity)
+    value = (res["accepted"] + 1) / (res["ms_per_step"] * 1e-3)
+    names = {"c1": "SmolLM-135M-shape fp32", "c3": "Llama-3.2-1B-shape int8-pc/fp16",
+             "c4": "Llama-3-8B-shape int4-g128/bf16"}
+    line = {
+        "metric": "accepted tokens/s @1 GPU (1B int8, K=5); verify-step ms; % HBM peak",
+        "value": round(value, 1),
+        "unit": "accepted tokens/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(res["ms_per_step"], 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": {"c1": "f32", "c3": "int8 weights, f16 activations, f32 accumulate",
+                  "c4": "uint4 weights, bf16 activations, f32 accumulate"}[args.config],
+        "data": "synthetic: seeded N(0,0.02) weights quantised on device; context prefilled from random ids",
+        "config": {"workload": f"{args.config}: verify step, {names[args.config]}, {cfg['n_layers']} layers, "
+                               f"batch 1, K={K} ({R} rows), {ctx}-token paged context (16-token pages), greedy "
+                               "acceptance + rollback, hipGraph replay",
+                   "drafts": f"target's greedy continuation ({res['accepted']}/{K} accepted)",
+                   "accepted_tokens_per_s_random_drafts": round((res_r["accepted"] + 1) /
+                                                                (res_r["ms_per_step"] * 1e-3), 1),
+                   "random_drafts_accepted": res_r["accepted"],
+                   "step_bytes": step_bytes["total"], "step_GBps": round(step_gbs, 1),
+                   "step_frac_of_hbm_peak": round(step_gbs / HBM_PEAK_GBS, 4),
+                   "wall_ms_per_step": round(res["wall_ms_per_step"], 4)},
+    }
+    if kern:
+        line["roofline"] = {"bound": "hbm", "achieved": round(kern["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                            "frac": round(kern["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                            "kernel": kern["kernel"], "bytes_per_launch": kern["bytes_per_launch"],
+                            "avg_us": round(kern["avg_us"], 2)}
+    if cpu:
+        line["cpu_baseline"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in cpu.items()}
+        line["parity"] = parity
+    print(json.dumps(line), flush=True)
+    dev.close()
+
+
+if __name__ == "__main__":
+    main()

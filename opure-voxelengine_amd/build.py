@@ -25,9 +25,11 @@ ENGINE_LIB = os.path.join(LIB, "libopure_engine.so")
 
 ARCH = "gfx950"
 HIP_SOURCES = ["runtime.hip", "gemv.hip", "attention.hip", "accept.hip", "verify.hip"]
-# Packed-fp32 instructions stay off: they are emitted only from plain float
+# -ffp-contract=off: every float expression rounds as written (fmas are
+# explicit __fmaf_rn), like the CPU oracle.  Packed-fp32 instructions stay
+# off: they are emitted only from plain float
 # code by the compiler, and are kept out of every kernel in this library.
-HIP_FLAGS = ["-O3", "-std=c++20", "-fPIC", f"--offload-arch={ARCH}", "-Wall", "-Wno-unused-function",
+HIP_FLAGS = ["-O3", "-std=c++20", "-fPIC", f"--offload-arch={ARCH}", "-Wall", "-Wno-unused-function", "-ffp-contract=off",
              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
              "-I", os.path.join(ROOT, "include")]
 

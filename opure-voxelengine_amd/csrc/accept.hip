@@ -176,6 +176,73 @@ __global__ __launch_bounds__(256) void k_argmax_partial(ArgmaxParams p)
     }
 }
 
+struct RollbackParams {
+    void* pool;
+    int32_t* page_table;
+    uint32_t max_pages, n_pages, n_layers, n_kv, hd, afmt, K;
+    const int32_t* seq_len;
+    const int32_t* accepted;
+    int32_t* new_len;
+    int32_t* freed;
+    uint32_t freed_stride;
+    int32_t* n_freed;
+    uint32_t poison, poison_bits;
+};
+
+// Rollback of sequence b, run by one workgroup: poison the rolled-back slots,
+// then release the pages wholly past the new length.
+__device__ void rollback_seq(const RollbackParams& p, uint32_t b, uint32_t acc)
+{
+    int32_t* pt = p.page_table + static_cast<uint64_t>(b) * p.max_pages;
+    const uint32_t ctx = static_cast<uint32_t>(p.seq_len[b]);
+    if (acc > p.K) acc = p.K;
+    const uint32_t old_end = ctx + p.K + 1u, nl = ctx + acc + 1u;
+    if (p.poison)
+    {
+        const uint32_t per_pos = p.n_layers * 2u * p.n_kv * p.hd;
+        for (uint32_t pos = nl; pos < old_end; ++pos)
+        {
+            if (pos / OPURE_PAGE_SIZE >= p.max_pages) break;
+            const int32_t page = pt[pos / OPURE_PAGE_SIZE];
+            if (page < 0 || static_cast<uint32_t>(page) >= p.n_pages) continue;
+            for (uint32_t e = threadIdx.x; e < per_pos; e += NT)
+            {
+                const uint32_t d = e % p.hd, rest = e / p.hd;
+                const uint32_t h = rest % p.n_kv, rest2 = rest / p.n_kv;
+                const uint32_t s = rest2 % 2u, L = rest2 / 2u;
+                const uint64_t idx = ((((static_cast<uint64_t>(L) * p.n_pages + static_cast<uint32_t>(page)) * 2u + s) *
+                                       p.n_kv + h) * OPURE_PAGE_SIZE + pos % OPURE_PAGE_SIZE) * p.hd + d;
+                if (p.afmt == OPURE_A_F32) static_cast<uint32_t*>(p.pool)[idx] = p.poison_bits;
+                else static_cast<uint16_t*>(p.pool)[idx] = static_cast<uint16_t>(p.poison_bits);
+            }
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x == 0)
+    {
+        p.new_len[b] = static_cast<int32_t>(nl);
+        int32_t nf = 0;
+        if (p.freed)
+        {
+            const uint32_t first_free = (nl + OPURE_PAGE_SIZE - 1u) / OPURE_PAGE_SIZE;
+            const uint32_t last_used = (old_end - 1u) / OPURE_PAGE_SIZE;
+            for (uint32_t q = first_free; q <= last_used && q < p.max_pages; ++q)
+            {
+                if (pt[q] < 0) continue;
+                if (static_cast<uint32_t>(nf) < p.freed_stride) p.freed[static_cast<uint64_t>(b) * p.freed_stride + nf] = pt[q];
+                pt[q] = -1;
+                ++nf;
+            }
+        }
+        if (p.n_freed) p.n_freed[b] = nf;
+    }
+}
+
+__global__ __launch_bounds__(256) void k_rollback(RollbackParams p)
+{
+    rollback_seq(p, blockIdx.x, static_cast<uint32_t>(p.accepted[blockIdx.x]));
+}
+
 struct GreedyParams {
     const float* am_val;
     const int32_t* am_idx;
@@ -184,46 +251,69 @@ struct GreedyParams {
     uint32_t drafts_stride;
     int32_t* out_tokens;
     int32_t* accepted;
-    const int32_t* seq_len;     // optional: writes new_seq_len = seq_len + n + 1
-    int32_t* new_seq_len;
+    uint32_t rollback;          // 1: run the rollback of this sequence in the same workgroup
+    RollbackParams rb;
 };
 
+// One workgroup per sequence.  Each thread scans every row's partials at once
+// (16 rows per pass), then each row is reduced across the workgroup in a fixed
+// order: (greater value, then lower index) wins.
 __global__ __launch_bounds__(256) void k_accept_greedy(GreedyParams p)
 {
-    __shared__ float sv[4];
-    __shared__ int32_t si[4];
+    constexpr uint32_t RB = 16;
+    __shared__ float sv[4][RB];
+    __shared__ int32_t si[4][RB];
     __shared__ int32_t am[64];
+    __shared__ uint32_t s_n;
     const uint32_t b = blockIdx.x, R = p.K + 1u;
-    for (uint32_t j = 0; j < R; ++j)
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    for (uint32_t r0 = 0; r0 < R; r0 += RB)
     {
-        const uint32_t r = b * R + j;
-        float bv = -__builtin_huge_valf();
-        int32_t bi = 0x7FFFFFFF;
+        const uint32_t nr = min(RB, R - r0);
+        float bv[RB];
+        int32_t bi[RB];
+#pragma unroll
+        for (uint32_t i = 0; i < RB; ++i) { bv[i] = -__builtin_huge_valf(); bi[i] = 0x7FFFFFFF; }
         for (uint32_t part = threadIdx.x; part < p.parts; part += NT)
         {
-            const float v = p.am_val[static_cast<uint64_t>(part) * p.rows_total + r];
-            const int32_t i = p.am_idx[static_cast<uint64_t>(part) * p.rows_total + r];
-            if (v > bv || (v == bv && i < bi)) { bv = v; bi = i; }
+            const uint64_t base = static_cast<uint64_t>(part) * p.rows_total + b * R + r0;
+#pragma unroll
+            for (uint32_t i = 0; i < RB; ++i)
+            {
+                if (i >= nr) break;
+                const float v = p.am_val[base + i];
+                const int32_t x = p.am_idx[base + i];
+                if (v > bv[i] || (v == bv[i] && x < bi[i])) { bv[i] = v; bi[i] = x; }
+            }
         }
 #pragma unroll
-        for (int o = 32; o > 0; o >>= 1)
+        for (uint32_t i = 0; i < RB; ++i)
         {
-            const float ov = __shfl_xor(bv, o);
-            const int32_t oi = __shfl_xor(bi, o);
-            if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1)
+            {
+                const float ov = __shfl_xor(bv[i], o);
+                const int32_t oi = __shfl_xor(bi[i], o);
+                if (ov > bv[i] || (ov == bv[i] && oi < bi[i])) { bv[i] = ov; bi[i] = oi; }
+            }
+        }
+        if (lane == 0)
+        {
+#pragma unroll
+            for (uint32_t i = 0; i < RB; ++i) { sv[wave][i] = bv[i]; si[wave][i] = bi[i]; }
         }
         __syncthreads();
-        if ((threadIdx.x & 63u) == 0) { sv[threadIdx.x >> 6] = bv; si[threadIdx.x >> 6] = bi; }
-        __syncthreads();
-        if (threadIdx.x == 0)
+        if (threadIdx.x < nr)
         {
-            bv = sv[0]; bi = si[0];
+            const uint32_t i = threadIdx.x;
+            float v = sv[0][i];
+            int32_t x = si[0][i];
             for (int w = 1; w < 4; ++w)
-                if (sv[w] > bv || (sv[w] == bv && si[w] < bi)) { bv = sv[w]; bi = si[w]; }
-            am[j] = bi == 0x7FFFFFFF ? 0 : bi;
+                if (sv[w][i] > v || (sv[w][i] == v && si[w][i] < x)) { v = sv[w][i]; x = si[w][i]; }
+            am[r0 + i] = x == 0x7FFFFFFF ? 0 : x;
         }
+        __syncthreads();
     }
-    __syncthreads();
     if (threadIdx.x == 0)
     {
         uint32_t n = 0;
@@ -231,8 +321,10 @@ __global__ __launch_bounds__(256) void k_accept_greedy(GreedyParams p)
         for (uint32_t j = 0; j < R; ++j)
             p.out_tokens[b * R + j] = j < n ? p.drafts[static_cast<uint64_t>(b) * p.drafts_stride + j] : (j == n ? am[n] : -1);
         p.accepted[b] = static_cast<int32_t>(n);
-        if (p.new_seq_len) p.new_seq_len[b] = p.seq_len[b] + static_cast<int32_t>(n) + 1;
+        s_n = n;
     }
+    __syncthreads();
+    if (p.rollback) rollback_seq(p.rb, b, s_n);
 }
 
 // ---------------------------------------------------------------------------
@@ -389,69 +481,6 @@ __global__ void k_philox(uint64_t seed, const uint32_t* pos, const uint32_t* seq
     if (i < n) out[i] = philox_u32(seed, pos[i], seq[i], stream);
 }
 
-// ---------------------------------------------------------------------------
-struct RollbackParams {
-    void* pool;
-    int32_t* page_table;
-    uint32_t max_pages, n_pages, n_layers, n_kv, hd, afmt, K;
-    const int32_t* seq_len;
-    const int32_t* accepted;
-    int32_t* new_len;
-    int32_t* freed;
-    uint32_t freed_stride;
-    int32_t* n_freed;
-    uint32_t poison, poison_bits;
-};
-
-__global__ __launch_bounds__(256) void k_rollback(RollbackParams p)
-{
-    const uint32_t b = blockIdx.x;
-    int32_t* pt = p.page_table + static_cast<uint64_t>(b) * p.max_pages;
-    const uint32_t ctx = static_cast<uint32_t>(p.seq_len[b]);
-    uint32_t acc = static_cast<uint32_t>(p.accepted[b]);
-    if (acc > p.K) acc = p.K;
-    const uint32_t old_end = ctx + p.K + 1u, nl = ctx + acc + 1u;
-    if (p.poison)
-    {
-        const uint32_t per_pos = p.n_layers * 2u * p.n_kv * p.hd;
-        for (uint32_t pos = nl; pos < old_end; ++pos)
-        {
-            if (pos / OPURE_PAGE_SIZE >= p.max_pages) break;
-            const int32_t page = pt[pos / OPURE_PAGE_SIZE];
-            if (page < 0 || static_cast<uint32_t>(page) >= p.n_pages) continue;
-            for (uint32_t e = threadIdx.x; e < per_pos; e += NT)
-            {
-                const uint32_t d = e % p.hd, rest = e / p.hd;
-                const uint32_t h = rest % p.n_kv, rest2 = rest / p.n_kv;
-                const uint32_t s = rest2 % 2u, L = rest2 / 2u;
-                const uint64_t idx = ((((static_cast<uint64_t>(L) * p.n_pages + static_cast<uint32_t>(page)) * 2u + s) *
-                                       p.n_kv + h) * OPURE_PAGE_SIZE + pos % OPURE_PAGE_SIZE) * p.hd + d;
-                if (p.afmt == OPURE_A_F32) static_cast<uint32_t*>(p.pool)[idx] = p.poison_bits;
-                else static_cast<uint16_t*>(p.pool)[idx] = static_cast<uint16_t>(p.poison_bits);
-            }
-        }
-    }
-    __syncthreads();
-    if (threadIdx.x == 0)
-    {
-        p.new_len[b] = static_cast<int32_t>(nl);
-        int32_t nf = 0;
-        if (p.freed)
-        {
-            const uint32_t first_free = (nl + OPURE_PAGE_SIZE - 1u) / OPURE_PAGE_SIZE;
-            const uint32_t last_used = (old_end - 1u) / OPURE_PAGE_SIZE;
-            for (uint32_t q = first_free; q <= last_used && q < p.max_pages; ++q)
-            {
-                if (pt[q] < 0) continue;
-                if (static_cast<uint32_t>(nf) < p.freed_stride) p.freed[static_cast<uint64_t>(b) * p.freed_stride + nf] = pt[q];
-                pt[q] = -1;
-                ++nf;
-            }
-        }
-        if (p.n_freed) p.n_freed[b] = nf;
-    }
-}
-
 }  // namespace
 
 namespace opure_hip {
@@ -480,9 +509,33 @@ int accept_validate(const opure_accept_args* a, bool rejection)
     return OPURE_OK;
 }
 
+static RollbackParams rollback_params(const opure_rollback_args* a)
+{
+    const opure_model* m = a->model;
+    RollbackParams r;
+    r.pool = a->kv->pool;
+    r.page_table = a->kv->page_table;
+    r.max_pages = a->kv->max_pages_per_seq;
+    r.n_pages = a->kv->n_pages;
+    r.n_layers = m->n_layers;
+    r.n_kv = m->n_kv_heads;
+    r.hd = m->head_dim;
+    r.afmt = m->afmt;
+    r.K = a->k;
+    r.seq_len = a->seq_len;
+    r.accepted = a->accepted;
+    r.new_len = a->new_seq_len;
+    r.freed = a->freed;
+    r.freed_stride = a->freed_stride;
+    r.n_freed = a->n_freed;
+    r.poison = a->poison;
+    r.poison_bits = a->poison_bits;
+    return r;
+}
+
 int greedy_from_partials(opure_dev* dev, const float* am_val, const int32_t* am_idx, uint32_t parts, uint32_t batch,
                          uint32_t K, const int32_t* drafts, uint32_t stride, int32_t* out_tokens, int32_t* accepted,
-                         const int32_t* seq_len, int32_t* new_seq_len)
+                         const opure_rollback_args* rb)
 {
     GreedyParams g;
     g.am_val = am_val;
@@ -494,15 +547,14 @@ int greedy_from_partials(opure_dev* dev, const float* am_val, const int32_t* am_
     g.drafts_stride = stride;
     g.out_tokens = out_tokens;
     g.accepted = accepted;
-    g.seq_len = seq_len;
-    g.new_seq_len = new_seq_len;
+    g.rollback = rb ? 1u : 0u;
+    if (rb) g.rb = rollback_params(rb);
     hipLaunchKernelGGL(k_accept_greedy, dim3(batch), dim3(NT), 0, dev->stream, g);
     OPURE_LAUNCH_CHECK("k_accept_greedy");
     return OPURE_OK;
 }
 
-int accept_greedy_launch(opure_dev* dev, const opure_accept_args* a, void* ws, const int32_t* seq_len,
-                         int32_t* new_seq_len)
+int accept_greedy_launch(opure_dev* dev, const opure_accept_args* a, void* ws)
 {
     const uint32_t rows = a->batch * (a->k + 1u), parts = argmax_parts(a->vocab);
     ArgmaxParams ap;
@@ -516,7 +568,7 @@ int accept_greedy_launch(opure_dev* dev, const opure_accept_args* a, void* ws, c
     hipLaunchKernelGGL(k_argmax_partial, dim3(parts, rows), dim3(NT), 0, dev->stream, ap);
     OPURE_LAUNCH_CHECK("k_argmax_partial");
     return greedy_from_partials(dev, ap.am_val, ap.am_idx, parts, a->batch, a->k, a->drafts, a->drafts_stride,
-                                a->out_tokens, a->accepted, seq_len, new_seq_len);
+                                a->out_tokens, a->accepted, nullptr);
 }
 
 int accept_rejection_launch(opure_dev* dev, const opure_accept_args* a, void* ws, uint32_t* counters,
@@ -546,25 +598,7 @@ int accept_rejection_launch(opure_dev* dev, const opure_accept_args* a, void* ws
 
 int rollback_launch(opure_dev* dev, const opure_rollback_args* a)
 {
-    const opure_model* m = a->model;
-    RollbackParams r;
-    r.pool = a->kv->pool;
-    r.page_table = a->kv->page_table;
-    r.max_pages = a->kv->max_pages_per_seq;
-    r.n_pages = a->kv->n_pages;
-    r.n_layers = m->n_layers;
-    r.n_kv = m->n_kv_heads;
-    r.hd = m->head_dim;
-    r.afmt = m->afmt;
-    r.K = a->k;
-    r.seq_len = a->seq_len;
-    r.accepted = a->accepted;
-    r.new_len = a->new_seq_len;
-    r.freed = a->freed;
-    r.freed_stride = a->freed_stride;
-    r.n_freed = a->n_freed;
-    r.poison = a->poison;
-    r.poison_bits = a->poison_bits;
+    const RollbackParams r = rollback_params(a);
     hipLaunchKernelGGL(k_rollback, dim3(a->batch), dim3(NT), 0, dev->stream, r);
     OPURE_LAUNCH_CHECK("k_rollback");
     return OPURE_OK;
@@ -592,7 +626,7 @@ int opure_accept_greedy(opure_dev* dev, const opure_accept_args* a)
     if (rc) return rc;
     rc = ensure_workspace(dev, accept_ws_bytes(a->batch, a->k, a->vocab, OPURE_ACCEPT_GREEDY), 0);
     if (rc) return rc;
-    return accept_greedy_launch(dev, a, dev->ws, nullptr, nullptr);
+    return accept_greedy_launch(dev, a, dev->ws);
 }
 
 int opure_accept_rejection(opure_dev* dev, const opure_accept_args* a)

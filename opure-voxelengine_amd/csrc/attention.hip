@@ -23,6 +23,8 @@ using namespace opure_dev_math;
 
 namespace {
 
+typedef uint32_t u4v __attribute__((ext_vector_type(4)));
+
 struct AttnParams {
     const void* q;
     void* out;
@@ -49,7 +51,7 @@ __device__ __forceinline__ float wave_sum(float v)
     return v;
 }
 
-__global__ __launch_bounds__(256) void k_attn_chunk(AttnParams p)
+__global__ __launch_bounds__(256) void k_attn_chunk_generic(AttnParams p)
 {
     extern __shared__ __align__(16) float sm[];
     const uint32_t kh = blockIdx.x, c = blockIdx.y, b = blockIdx.z;
@@ -136,7 +138,119 @@ __global__ __launch_bounds__(256) void k_attn_chunk(AttnParams p)
     }
 }
 
-// one workgroup of hd threads per (row, query head): merge chunks in order
+// Fast path for head_dim <= 128 and 64-token chunks.  The chunk's K and V
+// slices of this KV head are staged once in LDS with 128-bit loads; each wave
+// then keeps one K row per lane (lane = token) and one or two V columns per
+// lane (lane = channel) in registers and walks its share of the query rows:
+// scores = K row . q (q broadcast from LDS), a wave-wide softmax over the 64
+// tokens, and out[d] = sum_t p_t V[t][d] with p broadcast from LDS.
+template <int HD, int AF>
+__global__ __launch_bounds__(256) void k_attn_chunk(AttnParams p)
+{
+    constexpr uint32_t CH = 64, EB = AF == OPURE_A_F32 ? 4u : 2u;
+    constexpr uint32_t ROWB = HD * EB + 16u;              // padded LDS row (bank spread)
+    constexpr uint32_t DPL = (HD + 63u) / 64u;             // V channels per lane
+    __shared__ __align__(16) uint8_t kt[CH * ROWB];
+    __shared__ __align__(16) uint8_t vt[CH * ROWB];
+    __shared__ __align__(16) float pbuf[4][CH];
+    extern __shared__ __align__(16) float qs[];            // [Gq][HD]
+
+    const uint32_t kh = blockIdx.x, c = blockIdx.y, b = blockIdx.z;
+    const uint32_t group = p.n_heads / p.n_kv, R = p.rows, Gq = group * R;
+    const uint32_t ctx = static_cast<uint32_t>(p.seq_len[b]);
+    const uint32_t total = ctx + R;
+    const uint32_t t0 = c * CH;
+    if (t0 >= total) return;
+    const int32_t* pt = p.page_table + static_cast<uint64_t>(b) * p.max_pages;
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+
+    for (uint32_t e = threadIdx.x; e < Gq * HD; e += 256u)
+    {
+        const uint32_t qi = e / HD, d = e - qi * HD;
+        const uint32_t j = qi / group, head = kh * group + (qi - j * group);
+        qs[e] = load_act_rt(p.q, (static_cast<uint64_t>(b * R + j) * p.n_heads + head) * HD + d, AF);
+    }
+    // stage K and V rows: 16-byte pieces, a page's 16 tokens of this head are contiguous
+    constexpr uint32_t PIECES = HD * EB / 16u;
+    for (uint32_t e = threadIdx.x; e < 2u * CH * PIECES; e += 256u)
+    {
+        const uint32_t kvsel = e / (CH * PIECES), rem = e - kvsel * CH * PIECES;
+        const uint32_t tl = rem / PIECES, pc = rem - tl * PIECES, pos = t0 + tl;
+        u4v val = {0u, 0u, 0u, 0u};
+        if (pos < total)
+        {
+            const int32_t page = pos / OPURE_PAGE_SIZE < p.max_pages ? pt[pos / OPURE_PAGE_SIZE] : -1;
+            if (page >= 0 && static_cast<uint32_t>(page) < p.n_pages)
+            {
+                const uint64_t idx = ((((static_cast<uint64_t>(p.layer) * p.n_pages + static_cast<uint32_t>(page)) * 2u + kvsel) *
+                                       p.n_kv + kh) * OPURE_PAGE_SIZE + pos % OPURE_PAGE_SIZE) * HD;
+                val = *reinterpret_cast<const u4v*>(static_cast<const uint8_t*>(p.pool) + idx * EB + pc * 16u);
+            }
+            else
+            {
+                // a missing page or a length past the table reads as NaN, never out of bounds
+                const uint32_t nan = AF == OPURE_A_F32 ? 0x7FC00000u : (AF == OPURE_A_F16 ? 0x7E007E00u : 0x7FC07FC0u);
+                val = {nan, nan, nan, nan};
+            }
+        }
+        *reinterpret_cast<u4v*>((kvsel ? vt : kt) + tl * ROWB + pc * 16u) = val;
+    }
+    __syncthreads();
+
+    // this lane's K row (token t0 + lane) and V channels (lane, lane + 64)
+    float kr[HD];
+#pragma unroll
+    for (uint32_t d = 0; d < HD; ++d)
+    {
+        if constexpr (AF == OPURE_A_F32) kr[d] = reinterpret_cast<const float*>(kt + lane * ROWB)[d];
+        else kr[d] = AF == OPURE_A_F16 ? f16_to_f32(reinterpret_cast<const uint16_t*>(kt + lane * ROWB)[d])
+                                       : bf16_to_f32(reinterpret_cast<const uint16_t*>(kt + lane * ROWB)[d]);
+    }
+    float vc[DPL][CH];
+#pragma unroll
+    for (uint32_t i = 0; i < DPL; ++i)
+    {
+        const uint32_t d = lane + 64u * i;
+#pragma unroll
+        for (uint32_t t = 0; t < CH; ++t)
+            vc[i][t] = d < HD ? load_act_rt(vt + t * ROWB, d, AF) : 0.0f;
+    }
+    const uint64_t pbase = ((static_cast<uint64_t>(b) * p.n_kv + kh) * p.nch + c) * Gq;
+    const uint32_t pos = t0 + lane;
+    for (uint32_t qi = wave; qi < Gq; qi += 4u)
+    {
+        const uint32_t j = qi / group;
+        const float* qr = qs + qi * HD;
+        float acc = 0.0f;
+#pragma unroll
+        for (uint32_t d = 0; d < HD; ++d) acc = __fmaf_rn(qr[d], kr[d], acc);
+        const float s = pos <= ctx + j ? __fmul_rn(acc, p.scale) : -__builtin_huge_valf();
+        const float mx = wave_max(s);
+        const float e = s == -__builtin_huge_valf() ? 0.0f : expf_ref(__fsub_rn(s, mx));
+        const float l = wave_sum(e);
+        pbuf[wave][lane] = e;
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+#pragma unroll
+        for (uint32_t i = 0; i < DPL; ++i)
+        {
+            float o = 0.0f;
+#pragma unroll
+            for (uint32_t t = 0; t < CH; ++t) o = __fmaf_rn(pbuf[wave][t], vc[i][t], o);
+            const uint32_t d = lane + 64u * i;
+            if (d < HD) p.part_acc[(pbase + qi) * HD + d] = o;
+        }
+        if (lane == 0)
+        {
+            p.part_ml[(pbase + qi) * 2u] = mx;
+            p.part_ml[(pbase + qi) * 2u + 1u] = l;
+        }
+        __builtin_amdgcn_wave_barrier();
+    }
+}
+
+// one workgroup of hd threads per (row, query head): merge chunks 0..last in
+// order; the loads of each group of 16 chunks are independent and issued together
 __global__ void k_attn_combine(AttnParams p)
 {
     const uint32_t head = blockIdx.x, r = blockIdx.y;     // r = b * R + j
@@ -146,18 +260,55 @@ __global__ void k_attn_combine(AttnParams p)
     uint32_t last = (static_cast<uint32_t>(p.seq_len[b]) + j) / p.chunk;
     if (last >= p.nch) last = p.nch - 1u;          // length beyond the launch bound: clamp, never overrun
     const uint64_t base = (static_cast<uint64_t>(b) * p.n_kv + kh) * p.nch;
+    constexpr uint32_t G = 16;
     float mx = -__builtin_huge_valf();
-    for (uint32_t c = 0; c <= last; ++c) mx = fmaxf(mx, p.part_ml[((base + c) * Gq + qi) * 2u]);
-    float num = 0.0f, den = 0.0f;
-    for (uint32_t c = 0; c <= last; ++c)
+    for (uint32_t c0 = 0; c0 <= last; c0 += G)
     {
-        const float m = p.part_ml[((base + c) * Gq + qi) * 2u];
-        const float w = m == -__builtin_huge_valf() ? 0.0f : expf_ref(__fsub_rn(m, mx));
-        den = __fmaf_rn(w, p.part_ml[((base + c) * Gq + qi) * 2u + 1u], den);
-        num = __fmaf_rn(w, p.part_acc[((base + c) * Gq + qi) * hd + d], num);
+        float m[G];
+#pragma unroll
+        for (uint32_t i = 0; i < G; ++i)
+            m[i] = c0 + i <= last ? p.part_ml[((base + c0 + i) * Gq + qi) * 2u] : -__builtin_huge_valf();
+#pragma unroll
+        for (uint32_t i = 0; i < G; ++i) mx = fmaxf(mx, m[i]);
+    }
+    float num = 0.0f, den = 0.0f;
+    for (uint32_t c0 = 0; c0 <= last; c0 += G)
+    {
+        float m[G], l[G], a[G];
+#pragma unroll
+        for (uint32_t i = 0; i < G; ++i)
+        {
+            const bool on = c0 + i <= last;
+            const uint64_t k = (base + c0 + i) * Gq + qi;
+            m[i] = on ? p.part_ml[k * 2u] : -__builtin_huge_valf();
+            l[i] = on ? p.part_ml[k * 2u + 1u] : 0.0f;
+            a[i] = on ? p.part_acc[k * hd + d] : 0.0f;
+        }
+#pragma unroll
+        for (uint32_t i = 0; i < G; ++i)
+        {
+            const float w = m[i] == -__builtin_huge_valf() ? 0.0f : expf_ref(__fsub_rn(m[i], mx));
+            den = __fmaf_rn(w, l[i], den);
+            num = __fmaf_rn(w, a[i], num);
+        }
     }
     const float o = __fdiv_rn(num, den > 0.0f ? den : 1.0f);
     store_act_rt(p.out, (static_cast<uint64_t>(r) * p.n_heads + head) * hd + d, o, p.afmt);
+}
+
+template <int HD, int AF>
+int launch_fast(opure_dev* dev, dim3 grid, uint32_t lds, const AttnParams& p)
+{
+    static bool configured = false;
+    if (!configured)
+    {
+        OPURE_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_attn_chunk<HD, AF>),
+                                          hipFuncAttributeMaxDynamicSharedMemorySize, 64 * 1024));
+        configured = true;
+    }
+    hipLaunchKernelGGL((k_attn_chunk<HD, AF>), grid, dim3(256), lds, dev->stream, p);
+    OPURE_LAUNCH_CHECK("k_attn_chunk");
+    return OPURE_OK;
 }
 
 }  // namespace
@@ -219,16 +370,33 @@ int attn_launch(opure_dev* dev, const opure_model* m, const opure_kv* kv, uint32
     const uint64_t q_elems = static_cast<uint64_t>(batch) * p.n_kv * p.nch * Gq;
     p.part_acc = part;
     p.part_ml = part + align_up(q_elems * p.hd * 4u, 256) / 4u;
-    const uint32_t lds = (Gq * p.hd + Gq * p.chunk + p.chunk * (p.hd + 1u)) * 4u;
-    static bool configured = false;
-    if (!configured)
+    const dim3 grid(p.n_kv, p.nch, batch);
+    const uint32_t hd = p.hd;
+    if (p.chunk == 64u && (hd == 64u || hd == 128u))
     {
-        OPURE_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_attn_chunk),
-                                          hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
-        configured = true;
+        const uint32_t lds = Gq * hd * 4u;
+        int rc;
+        if (hd == 64u && p.afmt == OPURE_A_F32) rc = launch_fast<64, OPURE_A_F32>(dev, grid, lds, p);
+        else if (hd == 64u && p.afmt == OPURE_A_F16) rc = launch_fast<64, OPURE_A_F16>(dev, grid, lds, p);
+        else if (hd == 64u) rc = launch_fast<64, OPURE_A_BF16>(dev, grid, lds, p);
+        else if (p.afmt == OPURE_A_F32) rc = launch_fast<128, OPURE_A_F32>(dev, grid, lds, p);
+        else if (p.afmt == OPURE_A_F16) rc = launch_fast<128, OPURE_A_F16>(dev, grid, lds, p);
+        else rc = launch_fast<128, OPURE_A_BF16>(dev, grid, lds, p);
+        if (rc) return rc;
     }
-    hipLaunchKernelGGL(k_attn_chunk, dim3(p.n_kv, p.nch, batch), dim3(256), lds, dev->stream, p);
-    OPURE_LAUNCH_CHECK("k_attn_chunk");
+    else
+    {
+        const uint32_t lds = (Gq * hd + Gq * p.chunk + p.chunk * (hd + 1u)) * 4u;
+        static bool configured = false;
+        if (!configured)
+        {
+            OPURE_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_attn_chunk_generic),
+                                              hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+            configured = true;
+        }
+        hipLaunchKernelGGL(k_attn_chunk_generic, grid, dim3(256), lds, dev->stream, p);
+        OPURE_LAUNCH_CHECK("k_attn_chunk_generic");
+    }
     hipLaunchKernelGGL(k_attn_combine, dim3(p.n_heads, batch * rows), dim3(p.hd), 0, dev->stream, p);
     OPURE_LAUNCH_CHECK("k_attn_combine");
     return OPURE_OK;

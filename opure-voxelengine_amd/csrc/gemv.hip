@@ -8,18 +8,19 @@
 //
 //  Mapping.  y^T[o][m] = sum_k W[o][k] X[m][k] is one 16 x 16 MFMA output
 //  tile per 16 weight rows: A = 16 weight rows x 32 k, B = 32 k x 16 rows of X
-//  (M padded to 16 with zeros).  One wave owns one tile; a workgroup of four
-//  waves owns 64 rows and one K range whose X slice is staged in LDS once.
-//  Lane l loads 16 contiguous weight bytes of row (l % 16) per 64-byte block,
-//  so a wave streams 16 rows x 64 B per block with 128-bit loads.  Weights
-//  are widened in registers:
+//  (M padded to 16 with zeros).  One workgroup owns one tile; its NW waves
+//  take interleaved 64-byte blocks of every row (so together they stream
+//  contiguous 64*NW-byte runs) and are combined through LDS in wave order.
+//  Lane l loads 16 contiguous weight bytes of row (l % 16) per block with a
+//  128-bit load, and its X fragment straight from L2.  Weights are widened in
+//  registers:
 //    f32   -> v_mfma_f32_16x16x4_f32, 4 MFMAs per 16-byte load
 //    int8  -> fp16 via the 1024+u exponent trick (exact), 2 x 16x16x32 f16
 //    uint4 -> fp16/bf16 via the same trick, 4 x 16x16x32 per 128-k group,
 //             the group's scale/zero applied to the fresh group accumulator
-//  K is split across workgroups when the rows alone cannot fill the chip;
-//  partial tiles are combined by the last-arriving workgroup in split order,
-//  so results are bitwise reproducible and independent of M.
+//  No workgroup talks to another (a device-scope fence on a multi-XCD part
+//  writes back and invalidates L2, which cost 10-20x in a split-K version), so
+//  results are bitwise reproducible and independent of M.
 // ============================================================================
 #include "internal.h"
 
@@ -42,17 +43,16 @@ struct KParams {
     uint32_t M;
     void* y;
     uint32_t yfmt;
-    uint32_t tiles, splits, kr;
-    float* partials;
-    uint32_t* counters;
+    uint32_t tiles;
     opure_hip::QkvEpilogue qkv;
     opure_hip::LogitsEpilogue lg;
 };
 
 template <int WF> struct WTraits;
-template <> struct WTraits<OPURE_W_F32>    { static constexpr uint32_t KB = 16;  static constexpr uint32_t KR_MIN = 256; static constexpr uint32_t KR_MAX = 1024; };
-template <> struct WTraits<OPURE_W_I8PC>   { static constexpr uint32_t KB = 64;  static constexpr uint32_t KR_MIN = 256; static constexpr uint32_t KR_MAX = 2048; };
-template <> struct WTraits<OPURE_W_I4G128> { static constexpr uint32_t KB = 128; static constexpr uint32_t KR_MIN = 512; static constexpr uint32_t KR_MAX = 2048; };
+// k elements per 64-byte block of one weight row
+template <> struct WTraits<OPURE_W_F32>    { static constexpr uint32_t KB = 16; };
+template <> struct WTraits<OPURE_W_I8PC>   { static constexpr uint32_t KB = 64; };
+template <> struct WTraits<OPURE_W_I4G128> { static constexpr uint32_t KB = 128; };
 
 __device__ __forceinline__ uint32_t weight_row(uint32_t epi, uint32_t tile, uint32_t r, uint32_t out)
 {
@@ -104,181 +104,132 @@ __device__ __forceinline__ void u4x8_to_pairs(uint32_t d, uint32_t (&o)[4])
     }
 }
 
-template <int WF, int AF, int EPI>
-__global__ __launch_bounds__(256) void k_gemv(KParams p)
+template <int WF, int AF, int EPI, int NW>
+__global__ __launch_bounds__(NW * 64) void k_gemv(KParams p)
 {
     using T = WTraits<WF>;
     constexpr uint32_t EBX = AF == OPURE_A_F32 ? 4u : 2u;
     constexpr uint32_t U = 8;                       // blocks in flight per lane
-    extern __shared__ __align__(16) uint8_t smem[];
-    __shared__ uint32_t s_last;
+    __shared__ f4_t red[NW][64];
+    // uint4 only: this tile's 16 rows x G groups of (scale, zero + bias)
+    extern __shared__ __align__(16) float sz[];
 
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
     const uint32_t g4 = lane >> 4, r16 = lane & 15u;
-    const uint32_t group = blockIdx.x, split = blockIdx.y;
-    const uint32_t k0 = split * p.kr;
-    const uint32_t kr = min(p.kr, p.in - k0);
+    const uint32_t tile = blockIdx.x;
     const uint32_t M = p.M;
-    const uint32_t tile = group * 4u + wave;
-    const bool active = tile < p.tiles;
+    const uint32_t G = p.in / 128u;
 
-    // ---- stage X[0..M)[k0 .. k0+kr) in LDS ---------------------------------
-    const uint32_t row_bytes = kr * EBX;
-    const uint32_t lds_stride = p.kr * EBX + 16u;
-    {
-        const uint32_t vpr = row_bytes / 16u;
-        for (uint32_t v = threadIdx.x; v < M * vpr; v += 256u)
-        {
-            const uint32_t m = v / vpr, c = v - m * vpr;
-            const u4_t val = *reinterpret_cast<const u4_t*>(p.x + (static_cast<uint64_t>(m) * p.in + k0) * EBX + c * 16u);
-            *reinterpret_cast<u4_t*>(smem + m * lds_stride + c * 16u) = val;
-        }
-    }
-    // group sums of X and this workgroup's scales/zeros (uint4 only)
-    float* xsum = reinterpret_cast<float*>(smem + M * lds_stride);          // [M][G]
-    float* sz = xsum + 16u * (p.kr / 128u);                                  // [64 rows][G][2]
-    const uint32_t G = WF == OPURE_W_I4G128 ? kr / 128u : 0u;
     if constexpr (WF == OPURE_W_I4G128)
     {
-        const uint32_t Gall = p.in / 128u, g0 = k0 / 128u;
-        for (uint32_t e = threadIdx.x; e < 64u * G; e += 256u)
+        for (uint32_t e = threadIdx.x; e < 16u * G; e += NW * 64u)
         {
-            const uint32_t rloc = e / G, gl = e - rloc * G;
-            const uint32_t t = group * 4u + rloc / 16u;
-            float s = 0.0f, z = 0.0f;
-            if (t < p.tiles)
-            {
-                const uint32_t wr = weight_row(EPI, t, rloc & 15u, p.out);
-                const uint64_t gi = static_cast<uint64_t>(wr) * Gall + g0 + gl;
-                s = bf16_to_f32(static_cast<const uint16_t*>(p.scale)[gi]);
-                z = bf16_to_f32(static_cast<const uint16_t*>(p.zero)[gi]);
-                if constexpr (AF == OPURE_A_BF16) z += 128.0f;
-            }
-            sz[(rloc * G + gl) * 2u] = s;
-            sz[(rloc * G + gl) * 2u + 1u] = z;
-        }
-    }
-    __syncthreads();
-    if constexpr (WF == OPURE_W_I4G128)
-    {
-        for (uint32_t e = threadIdx.x; e < M * G; e += 256u)
-        {
-            const uint32_t m = e / G, gl = e - m * G;
-            const uint8_t* row = smem + m * lds_stride + gl * 128u * EBX;
-            float acc = 0.0f;
-            for (uint32_t i = 0; i < 128u; ++i)
-            {
-                uint16_t h;
-                __builtin_memcpy(&h, row + 2u * i, 2);
-                acc += AF == OPURE_A_F16 ? f16_to_f32(h) : bf16_to_f32(h);
-            }
-            xsum[m * G + gl] = acc;
+            const uint32_t r = e / G, g = e - r * G;
+            const uint64_t gi = static_cast<uint64_t>(weight_row(EPI, tile, r, p.out)) * G + g;
+            float z = bf16_to_f32(static_cast<const uint16_t*>(p.zero)[gi]);
+            if constexpr (AF == OPURE_A_BF16) z += 128.0f;
+            sz[(r * G + g) * 2u] = bf16_to_f32(static_cast<const uint16_t*>(p.scale)[gi]);
+            sz[(r * G + g) * 2u + 1u] = z;
         }
         __syncthreads();
     }
 
-    // ---- stream this wave's 16 weight rows through the matrix core --------
+    // ---- stream 16 weight rows; wave w takes blocks w, w+NW, ... of K -------
+    constexpr uint32_t WBITS = WF == OPURE_W_F32 ? 32u : (WF == OPURE_W_I8PC ? 8u : 4u);
+    const uint64_t w_row_bytes = static_cast<uint64_t>(p.in) * WBITS / 8u;
+    const uint8_t* wp = p.w + weight_row(EPI, tile, r16, p.out) * w_row_bytes + 16u * g4;
+    const bool xon = r16 < M;
+    const uint8_t* xrow = p.x + static_cast<uint64_t>(xon ? r16 : 0u) * p.in * EBX;
+    const uint32_t nblk = p.in / T::KB;
     f4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
-    if (active)
+    for (uint32_t b0 = wave; b0 < nblk; b0 += U * NW)
     {
-        constexpr uint32_t WBITS = WF == OPURE_W_F32 ? 32u : (WF == OPURE_W_I8PC ? 8u : 4u);
-        const uint64_t w_row_bytes = static_cast<uint64_t>(p.in) * WBITS / 8u;
-        const uint32_t wr = weight_row(EPI, tile, r16, p.out);
-        const uint8_t* wp = p.w + wr * w_row_bytes + static_cast<uint64_t>(k0) * WBITS / 8u + 16u * g4;
-        const bool xon = r16 < M;
-        const uint8_t* xrow = smem + r16 * lds_stride;
-        const uint32_t nblk = kr / T::KB;
-        for (uint32_t b0 = 0; b0 < nblk; b0 += U)
+        u4_t wv[U];
+#pragma unroll
+        for (uint32_t u = 0; u < U; ++u)
+            if (b0 + u * NW < nblk) wv[u] = __builtin_nontemporal_load(reinterpret_cast<const u4_t*>(wp + (b0 + u * NW) * 64u));
+#pragma unroll
+        for (uint32_t u = 0; u < U; ++u)
         {
-            u4_t wv[U];
-#pragma unroll
-            for (uint32_t u = 0; u < U; ++u)
-                if (b0 + u < nblk) wv[u] = __builtin_nontemporal_load(reinterpret_cast<const u4_t*>(wp + (b0 + u) * 64u));
-#pragma unroll
-            for (uint32_t u = 0; u < U; ++u)
+            const uint32_t blk = b0 + u * NW;
+            if (blk >= nblk) break;
+            const uint32_t kb = blk * T::KB;
+            if constexpr (WF == OPURE_W_F32)
             {
-                if (b0 + u >= nblk) break;
-                const uint32_t kb = (b0 + u) * T::KB;
-                if constexpr (WF == OPURE_W_F32)
-                {
-                    f4_t xv = {0.0f, 0.0f, 0.0f, 0.0f};
-                    if (xon) xv = *reinterpret_cast<const f4_t*>(xrow + (kb + 4u * g4) * 4u);
-                    const f4_t wf = __builtin_bit_cast(f4_t, wv[u]);
+                f4_t xv = {0.0f, 0.0f, 0.0f, 0.0f};
+                if (xon) xv = *reinterpret_cast<const f4_t*>(xrow + (kb + 4u * g4) * 4u);
+                const f4_t wf = __builtin_bit_cast(f4_t, wv[u]);
 #pragma unroll
-                    for (int t = 0; t < 4; ++t)
-                        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(wf[t], xv[t], acc, 0, 0, 0);
+                for (int t = 0; t < 4; ++t)
+                    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(wf[t], xv[t], acc, 0, 0, 0);
+            }
+            else if constexpr (WF == OPURE_W_I8PC)
+            {
+                u4_t x0 = {0u, 0u, 0u, 0u}, x1 = {0u, 0u, 0u, 0u};
+                if (xon)
+                {
+                    x0 = *reinterpret_cast<const u4_t*>(xrow + (kb + 16u * g4) * 2u);
+                    x1 = *reinterpret_cast<const u4_t*>(xrow + (kb + 16u * g4) * 2u + 16u);
                 }
-                else if constexpr (WF == OPURE_W_I8PC)
-                {
-                    u4_t x0 = {0u, 0u, 0u, 0u}, x1 = {0u, 0u, 0u, 0u};
-                    if (xon)
-                    {
-                        x0 = *reinterpret_cast<const u4_t*>(xrow + (kb + 16u * g4) * 2u);
-                        x1 = *reinterpret_cast<const u4_t*>(xrow + (kb + 16u * g4) * 2u + 16u);
-                    }
-                    uint32_t a[8];
+                uint32_t a[8];
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) i8x4_to_f16(wv[u][j], a[2 * j], a[2 * j + 1]);
-                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(a[0], a[1], a[2], a[3]),
-                                                                 as_half8(x0[0], x0[1], x0[2], x0[3]), acc, 0, 0, 0);
-                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(a[4], a[5], a[6], a[7]),
-                                                                 as_half8(x1[0], x1[1], x1[2], x1[3]), acc, 0, 0, 0);
-                }
-                else
-                {
-                    // one 128-k quantisation group: fresh accumulator, then scale/zero
-                    f4_t blk = {0.0f, 0.0f, 0.0f, 0.0f};
+                for (int j = 0; j < 4; ++j) i8x4_to_f16(wv[u][j], a[2 * j], a[2 * j + 1]);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(a[0], a[1], a[2], a[3]),
+                                                             as_half8(x0[0], x0[1], x0[2], x0[3]), acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(a[4], a[5], a[6], a[7]),
+                                                             as_half8(x1[0], x1[1], x1[2], x1[3]), acc, 0, 0, 0);
+            }
+            else
+            {
+                // one 128-k quantisation group: fresh accumulator, then scale/zero
+                f4_t blkacc = {0.0f, 0.0f, 0.0f, 0.0f};
+                float xs = 0.0f;
 #pragma unroll
-                    for (int j = 0; j < 4; ++j)
+                for (int j = 0; j < 4; ++j)
+                {
+                    u4_t xj = {0u, 0u, 0u, 0u};
+                    if (xon) xj = *reinterpret_cast<const u4_t*>(xrow + (kb + 32u * g4 + 8u * j) * 2u);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
                     {
-                        u4_t xj = {0u, 0u, 0u, 0u};
-                        if (xon) xj = *reinterpret_cast<const u4_t*>(xrow + (kb + 32u * g4 + 8u * j) * 2u);
-                        uint32_t a[4];
-                        u4x8_to_pairs<AF>(wv[u][j], a);
+                        const uint32_t pr = xj[e];
                         if constexpr (AF == OPURE_A_F16)
-                            blk = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(a[0], a[1], a[2], a[3]),
-                                                                         as_half8(xj[0], xj[1], xj[2], xj[3]), blk, 0, 0, 0);
+                            xs += f16_to_f32(static_cast<uint16_t>(pr)) + f16_to_f32(static_cast<uint16_t>(pr >> 16));
                         else
-                            blk = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf8(a[0], a[1], a[2], a[3]),
-                                                                          as_bf8(xj[0], xj[1], xj[2], xj[3]), blk, 0, 0, 0);
+                            xs += bf16_to_f32(static_cast<uint16_t>(pr)) + bf16_to_f32(static_cast<uint16_t>(pr >> 16));
                     }
-                    const uint32_t gl = kb / 128u;
-                    const float xs = xon ? xsum[r16 * G + gl] : 0.0f;
+                    uint32_t a[4];
+                    u4x8_to_pairs<AF>(wv[u][j], a);
+                    if constexpr (AF == OPURE_A_F16)
+                        blkacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(a[0], a[1], a[2], a[3]),
+                                                                        as_half8(xj[0], xj[1], xj[2], xj[3]), blkacc, 0, 0, 0);
+                    else
+                        blkacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf8(a[0], a[1], a[2], a[3]),
+                                                                         as_bf8(xj[0], xj[1], xj[2], xj[3]), blkacc, 0, 0, 0);
+                }
+                // the group sum of column m over all 128 k: the four lane groups hold 32 each
+                xs += __shfl_xor(xs, 16);
+                xs += __shfl_xor(xs, 32);
+                const uint32_t g = kb / 128u;
 #pragma unroll
-                    for (int i = 0; i < 4; ++i)
-                    {
-                        const uint32_t rloc = wave * 16u + 4u * g4 + i;
-                        const float s = sz[(rloc * G + gl) * 2u], z = sz[(rloc * G + gl) * 2u + 1u];
-                        acc[i] = __fmaf_rn(s, __fsub_rn(blk[i], __fmul_rn(z, xs)), acc[i]);
-                    }
+                for (int i = 0; i < 4; ++i)
+                {
+                    const float s = sz[((4u * g4 + i) * G + g) * 2u], z = sz[((4u * g4 + i) * G + g) * 2u + 1u];
+                    acc[i] = __fmaf_rn(s, __fsub_rn(blkacc[i], __fmul_rn(z, xs)), acc[i]);
                 }
             }
         }
     }
 
-    // ---- split-K fixup: the last workgroup of the row group sums in order --
-    if (p.splits > 1)
+    // ---- combine the waves' K slices in wave order -------------------------
+    if constexpr (NW > 1)
     {
-        float* part = p.partials + ((static_cast<uint64_t>(group) * p.splits + split) * 4u + wave) * 256u + lane * 4u;
-        if (active) *reinterpret_cast<f4_t*>(part) = acc;
-        __threadfence();
+        red[wave][lane] = acc;
         __syncthreads();
-        if (threadIdx.x == 0)
-        {
-            const uint32_t prev = atomicAdd(&p.counters[group], 1u);
-            s_last = prev == p.splits - 1u ? 1u : 0u;
-        }
-        __syncthreads();
-        if (!s_last) return;
-        __threadfence();
-        if (active)
-        {
-            const float* base = p.partials + (static_cast<uint64_t>(group) * p.splits * 4u + wave) * 256u + lane * 4u;
-            acc = __builtin_nontemporal_load(reinterpret_cast<const f4_t*>(base));
-            for (uint32_t s = 1; s < p.splits; ++s)
-                acc += __builtin_nontemporal_load(reinterpret_cast<const f4_t*>(base + static_cast<uint64_t>(s) * 4u * 256u));
-        }
-        if (threadIdx.x == 0) p.counters[group] = 0u;
+        if (wave != 0) return;
+        acc = red[0][lane];
+#pragma unroll
+        for (int w = 1; w < NW; ++w) acc += red[w][lane];
     }
 
     // ---- epilogue: lane holds D rows 4*g4 + i for column m = r16 -----------
@@ -289,16 +240,14 @@ __global__ __launch_bounds__(256) void k_gemv(KParams p)
     {
         v[i] = acc[i];
         if constexpr (WF == OPURE_W_I8PC)
-        {
-            if (active) v[i] = __fmul_rn(v[i], f16_to_f32(static_cast<const uint16_t*>(p.scale)[weight_row(EPI, tile, 4u * g4 + i, p.out)]));
-        }
+            v[i] = __fmul_rn(v[i], f16_to_f32(static_cast<const uint16_t*>(p.scale)[weight_row(EPI, tile, 4u * g4 + i, p.out)]));
     }
     if constexpr (EPI == opure_hip::EPI_LOGITS)
     {
         // logits, then the best (value, lowest index) of this tile for column m
         float bv = -__builtin_huge_valf();
         int32_t bi = 0x7FFFFFFF;
-        if (active && m < M)
+        if (m < M)
         {
 #pragma unroll
             for (int i = 0; i < 4; ++i)
@@ -316,14 +265,14 @@ __global__ __launch_bounds__(256) void k_gemv(KParams p)
             const int32_t oi = __shfl_xor(bi, off);
             if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
         }
-        if (active && m < M && g4 == 0)
+        if (m < M && g4 == 0)
         {
             p.lg.am_val[static_cast<uint64_t>(tile) * M + m] = bv;
             p.lg.am_idx[static_cast<uint64_t>(tile) * M + m] = bi;
         }
         return;
     }
-    if (!active || m >= M) return;
+    if (m >= M) return;
     if constexpr (EPI == opure_hip::EPI_STORE)
     {
 #pragma unroll
@@ -384,31 +333,43 @@ __global__ __launch_bounds__(256) void k_gemv(KParams p)
     }
 }
 
-template <int WF, int AF, int EPI>
-int launch_t(opure_dev* dev, const KParams& kp, uint32_t groups, uint32_t splits, uint32_t lds)
+template <int WF, int AF, int EPI, int NW>
+int launch_t(opure_dev* dev, const KParams& kp, uint32_t lds)
 {
     static bool configured = false;
     if (!configured)
     {
-        OPURE_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemv<WF, AF, EPI>),
-                                          hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024));
+        OPURE_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemv<WF, AF, EPI, NW>),
+                                          hipFuncAttributeMaxDynamicSharedMemorySize, 64 * 1024));
         configured = true;
     }
-    hipLaunchKernelGGL((k_gemv<WF, AF, EPI>), dim3(groups, splits), dim3(256), lds, dev->stream, kp);
+    hipLaunchKernelGGL((k_gemv<WF, AF, EPI, NW>), dim3(kp.tiles), dim3(NW * 64), lds, dev->stream, kp);
     OPURE_LAUNCH_CHECK("k_gemv");
     return OPURE_OK;
 }
 
+template <int WF, int AF, int EPI>
+int launch_nw(opure_dev* dev, const KParams& kp, uint32_t nw, uint32_t lds)
+{
+    switch (nw)
+    {
+    case 4: return launch_t<WF, AF, EPI, 4>(dev, kp, lds);
+    case 8: return launch_t<WF, AF, EPI, 8>(dev, kp, lds);
+    case 16: return launch_t<WF, AF, EPI, 16>(dev, kp, lds);
+    }
+    return opure_hip::set_error(OPURE_E_INVALID, "gemv: bad wave count %u", nw);
+}
+
 template <int WF, int AF>
-int launch_epi(opure_dev* dev, uint32_t epi, const KParams& kp, uint32_t groups, uint32_t splits, uint32_t lds)
+int launch_epi(opure_dev* dev, uint32_t epi, const KParams& kp, uint32_t nw, uint32_t lds)
 {
     switch (epi)
     {
-    case opure_hip::EPI_STORE: return launch_t<WF, AF, opure_hip::EPI_STORE>(dev, kp, groups, splits, lds);
-    case opure_hip::EPI_RESIDUAL: return launch_t<WF, AF, opure_hip::EPI_RESIDUAL>(dev, kp, groups, splits, lds);
-    case opure_hip::EPI_SWIGLU: return launch_t<WF, AF, opure_hip::EPI_SWIGLU>(dev, kp, groups, splits, lds);
-    case opure_hip::EPI_QKV: return launch_t<WF, AF, opure_hip::EPI_QKV>(dev, kp, groups, splits, lds);
-    case opure_hip::EPI_LOGITS: return launch_t<WF, AF, opure_hip::EPI_LOGITS>(dev, kp, groups, splits, lds);
+    case opure_hip::EPI_STORE: return launch_nw<WF, AF, opure_hip::EPI_STORE>(dev, kp, nw, lds);
+    case opure_hip::EPI_RESIDUAL: return launch_nw<WF, AF, opure_hip::EPI_RESIDUAL>(dev, kp, nw, lds);
+    case opure_hip::EPI_SWIGLU: return launch_nw<WF, AF, opure_hip::EPI_SWIGLU>(dev, kp, nw, lds);
+    case opure_hip::EPI_QKV: return launch_nw<WF, AF, opure_hip::EPI_QKV>(dev, kp, nw, lds);
+    case opure_hip::EPI_LOGITS: return launch_nw<WF, AF, opure_hip::EPI_LOGITS>(dev, kp, nw, lds);
     }
     return opure_hip::set_error(OPURE_E_INVALID, "gemv: unknown epilogue %u", epi);
 }
@@ -419,30 +380,17 @@ uint32_t kb_of(uint32_t wfmt) { return wfmt == OPURE_W_F32 ? 16u : (wfmt == OPUR
 
 namespace opure_hip {
 
+// One workgroup per 16-row tile; its NW waves split K and are combined in wave
+// order.  NW grows while the grid has fewer than 2048 waves and every wave keeps
+// at least two 64-byte blocks per row.  Depends on the shape only, never on M.
 GemvShape gemv_shape(uint32_t wfmt, uint32_t out, uint32_t in)
 {
     GemvShape s;
-    const uint32_t KB = kb_of(wfmt);
-    const uint32_t kr_min = wfmt == OPURE_W_I4G128 ? 512u : 256u;
-    const uint32_t kr_max = wfmt == OPURE_W_F32 ? 1024u : 2048u;
     s.tiles = out / 16u;
-    s.groups = (s.tiles + 3u) / 4u;
-    const uint32_t target = 512u;
-    uint32_t S = (target + s.groups - 1u) / s.groups;
-    if (S < 1u) S = 1u;
-    uint32_t kr = (in + S - 1u) / S;
-    kr = (kr + KB - 1u) / KB * KB;
-    if (kr < kr_min) kr = kr_min;
-    if (kr > kr_max) kr = kr_max;
-    if (kr > in) kr = in;
-    s.kr = kr;
-    s.splits = (in + kr - 1u) / kr;
+    s.blocks = in / kb_of(wfmt);
+    s.nw = 4u;
+    while (s.nw < 16u && s.tiles * s.nw < 2048u && s.blocks >= 4u * s.nw) s.nw *= 2u;
     return s;
-}
-
-uint64_t gemv_partial_bytes(const GemvShape& s)
-{
-    return s.splits > 1 ? static_cast<uint64_t>(s.groups) * s.splits * 4u * 256u * 4u : 0u;
 }
 
 int gemv_validate(const GemvCall& c)
@@ -480,7 +428,7 @@ int gemv_validate(const GemvCall& c)
     return OPURE_OK;
 }
 
-int gemv_launch(opure_dev* dev, const GemvCall& c, float* partials, uint32_t* counters)
+int gemv_launch(opure_dev* dev, const GemvCall& c)
 {
     const GemvShape s = gemv_shape(c.wfmt, c.W.out, c.W.in);
     KParams kp;
@@ -494,20 +442,14 @@ int gemv_launch(opure_dev* dev, const GemvCall& c, float* partials, uint32_t* co
     kp.y = c.y;
     kp.yfmt = c.yfmt;
     kp.tiles = s.tiles;
-    kp.splits = s.splits;
-    kp.kr = s.kr;
-    kp.partials = partials;
-    kp.counters = counters;
     kp.qkv = c.qkv;
     kp.lg = c.logits;
-    if (s.splits > 1) OPURE_REQUIRE(partials && counters, OPURE_E_INVALID, "gemv: split-K needs a workspace");
-    const uint32_t ebx = act_bytes(c.xfmt);
-    uint32_t lds = c.M * (s.kr * ebx + 16u);
-    if (c.wfmt == OPURE_W_I4G128) lds += 16u * (s.kr / 128u) * 4u + 64u * (s.kr / 128u) * 8u;
-    if (c.wfmt == OPURE_W_F32) return launch_epi<OPURE_W_F32, OPURE_A_F32>(dev, c.epi, kp, s.groups, s.splits, lds);
-    if (c.wfmt == OPURE_W_I8PC) return launch_epi<OPURE_W_I8PC, OPURE_A_F16>(dev, c.epi, kp, s.groups, s.splits, lds);
-    if (c.xfmt == OPURE_A_F16) return launch_epi<OPURE_W_I4G128, OPURE_A_F16>(dev, c.epi, kp, s.groups, s.splits, lds);
-    return launch_epi<OPURE_W_I4G128, OPURE_A_BF16>(dev, c.epi, kp, s.groups, s.splits, lds);
+    const uint32_t lds = c.wfmt == OPURE_W_I4G128 ? 16u * (c.W.in / 128u) * 8u : 0u;
+    OPURE_REQUIRE(lds <= 64u * 1024u, OPURE_E_UNSUPPORTED, "gemv: in=%u too long for the group-scale stage", c.W.in);
+    if (c.wfmt == OPURE_W_F32) return launch_epi<OPURE_W_F32, OPURE_A_F32>(dev, c.epi, kp, s.nw, lds);
+    if (c.wfmt == OPURE_W_I8PC) return launch_epi<OPURE_W_I8PC, OPURE_A_F16>(dev, c.epi, kp, s.nw, lds);
+    if (c.xfmt == OPURE_A_F16) return launch_epi<OPURE_W_I4G128, OPURE_A_F16>(dev, c.epi, kp, s.nw, lds);
+    return launch_epi<OPURE_W_I4G128, OPURE_A_BF16>(dev, c.epi, kp, s.nw, lds);
 }
 
 }  // namespace opure_hip
@@ -527,12 +469,9 @@ static int gemv_public(opure_dev* dev, const opure_gemv_args* a, uint32_t wfmt)
     c.y = a->y;
     c.yfmt = a->yfmt;
     c.epi = a->epilogue;
-    int rc = gemv_validate(c);
+    const int rc = gemv_validate(c);
     if (rc) return rc;
-    const GemvShape s = gemv_shape(wfmt, c.W.out, c.W.in);
-    rc = ensure_workspace(dev, gemv_partial_bytes(s), s.groups);
-    if (rc) return rc;
-    return gemv_launch(dev, c, static_cast<float*>(dev->ws), dev->counters);
+    return gemv_launch(dev, c);
 }
 
 extern "C" {

@@ -100,17 +100,14 @@ struct GemvCall {
 };
 
 struct GemvShape {
-    uint32_t tiles = 0;     // 16-row output tiles
-    uint32_t groups = 0;    // workgroups along the rows (4 tiles each)
-    uint32_t splits = 0;    // workgroups along K
-    uint32_t kr = 0;        // K elements per split
+    uint32_t tiles = 0;     // 16-row output tiles = workgroups
+    uint32_t blocks = 0;    // 64-byte blocks per weight row
+    uint32_t nw = 0;        // waves per workgroup splitting K
 };
 
 GemvShape gemv_shape(uint32_t wfmt, uint32_t out, uint32_t in);
-uint64_t  gemv_partial_bytes(const GemvShape& s);
 int       gemv_validate(const GemvCall& c);
-// `partials` and `counters` must hold gemv_partial_bytes(shape) and shape.groups words.
-int       gemv_launch(opure_dev* dev, const GemvCall& c, float* partials, uint32_t* counters);
+int       gemv_launch(opure_dev* dev, const GemvCall& c);
 
 // ---- attention (attention.hip) ---------------------------------------------
 uint32_t attn_chunk(uint32_t head_dim);
@@ -123,11 +120,11 @@ int      attn_launch(opure_dev* dev, const opure_model* m, const opure_kv* kv, u
 uint32_t argmax_parts(uint32_t vocab);
 uint64_t accept_ws_bytes(uint32_t batch, uint32_t k, uint32_t vocab, uint32_t mode);
 int      accept_validate(const opure_accept_args* a, bool rejection);
+// `rb` (may be null): run that rollback inside the acceptance kernel
 int      greedy_from_partials(opure_dev* dev, const float* am_val, const int32_t* am_idx, uint32_t parts,
                               uint32_t batch, uint32_t K, const int32_t* drafts, uint32_t stride, int32_t* out_tokens,
-                              int32_t* accepted, const int32_t* seq_len, int32_t* new_seq_len);
-int      accept_greedy_launch(opure_dev* dev, const opure_accept_args* a, void* ws, const int32_t* seq_len,
-                              int32_t* new_seq_len);
+                              int32_t* accepted, const opure_rollback_args* rb);
+int      accept_greedy_launch(opure_dev* dev, const opure_accept_args* a, void* ws);
 int      accept_rejection_launch(opure_dev* dev, const opure_accept_args* a, void* ws, uint32_t* counters,
                                  const int32_t* seq_len, int32_t* new_seq_len);
 int      rollback_validate(const opure_rollback_args* a);

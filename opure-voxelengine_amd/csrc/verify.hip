@@ -84,9 +84,8 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const float* x, const float* g,
 namespace opure_hip {
 
 struct VerifyPlan {
-    uint64_t x = 0, xn = 0, q = 0, att = 0, h = 0, am_val = 0, am_idx = 0, attn = 0, gemv = 0, rej = 0, total = 0;
+    uint64_t x = 0, xn = 0, q = 0, att = 0, h = 0, am_val = 0, am_idx = 0, attn = 0, rej = 0, total = 0;
     uint64_t counters = 0;
-    uint32_t gemv_groups = 0;
     uint32_t lm_tiles = 0;
 };
 
@@ -107,21 +106,9 @@ static VerifyPlan make_plan(const opure_model* m, uint32_t B, uint32_t R, uint32
     p.am_val = take(static_cast<uint64_t>(p.lm_tiles) * MR * 4u);
     p.am_idx = take(static_cast<uint64_t>(p.lm_tiles) * MR * 4u);
     p.attn = take(attn_partial_bytes(B, m->n_kv_heads, m->n_heads / m->n_kv_heads, R, m->head_dim, max_ctx));
-    uint64_t gp = 0;
-    uint32_t gg = 0;
-    const uint32_t shapes[5][2] = {{qdim + 2u * kvdim, m->hidden}, {m->hidden, qdim}, {2u * m->ffn, m->hidden},
-                                   {m->hidden, m->ffn}, {m->vocab, m->hidden}};
-    for (const auto& s : shapes)
-    {
-        const GemvShape gs = gemv_shape(m->wfmt, s[0], s[1]);
-        if (gemv_partial_bytes(gs) > gp) gp = gemv_partial_bytes(gs);
-        if (gs.groups > gg) gg = gs.groups;
-    }
-    p.gemv = take(gp);
     p.rej = take(accept_ws_bytes(B, R - 1u, m->vocab, OPURE_ACCEPT_REJECTION));
     p.total = off;
-    p.gemv_groups = gg;
-    p.counters = static_cast<uint64_t>(gg) + B;
+    p.counters = B;
     return p;
 }
 
@@ -232,8 +219,6 @@ int opure_verify_step(opure_dev* dev, const opure_verify_args* a)
     void* q = ws + P.q;
     void* att = ws + P.att;
     void* hbuf = ws + P.h;
-    float* gpart = reinterpret_cast<float*>(ws + P.gemv);
-    uint32_t* gcnt = dev->counters;
     const uint32_t qdim = m->n_heads * m->head_dim, kvdim = m->n_kv_heads * m->head_dim;
 
     hipLaunchKernelGGL(k_embed, dim3(MR), dim3(256), 0, dev->stream, a->tokens, m->embed, m->wfmt, m->hidden, m->vocab, x);
@@ -269,7 +254,7 @@ int opure_verify_step(opure_dev* dev, const opure_verify_args* a)
         c.qkv.max_pages = kv->max_pages_per_seq;
         c.qkv.n_pages = kv->n_pages;
         c.qkv.layer = L;
-        if ((rc = gemv_validate(c)) || (rc = gemv_launch(dev, c, gpart, gcnt))) return rc;
+        if ((rc = gemv_validate(c)) || (rc = gemv_launch(dev, c))) return rc;
 
         if ((rc = attn_launch(dev, m, kv, L, B, R, a->seq_len, a->max_ctx, q, att,
                               reinterpret_cast<float*>(ws + P.attn))))
@@ -280,7 +265,7 @@ int opure_verify_step(opure_dev* dev, const opure_verify_args* a)
         c.y = x;
         c.yfmt = OPURE_A_F32;
         c.epi = EPI_RESIDUAL;
-        if ((rc = gemv_validate(c)) || (rc = gemv_launch(dev, c, gpart, gcnt))) return rc;
+        if ((rc = gemv_validate(c)) || (rc = gemv_launch(dev, c))) return rc;
 
         hipLaunchKernelGGL(k_rmsnorm, dim3(MR), dim3(256), 0, dev->stream, x, W.mlp_norm, m->hidden, m->rms_eps, xn,
                            m->afmt);
@@ -291,14 +276,14 @@ int opure_verify_step(opure_dev* dev, const opure_verify_args* a)
         c.y = hbuf;
         c.yfmt = m->afmt;
         c.epi = EPI_SWIGLU;
-        if ((rc = gemv_validate(c)) || (rc = gemv_launch(dev, c, gpart, gcnt))) return rc;
+        if ((rc = gemv_validate(c)) || (rc = gemv_launch(dev, c))) return rc;
 
         c.W = W.down;
         c.x = hbuf;
         c.y = x;
         c.yfmt = OPURE_A_F32;
         c.epi = EPI_RESIDUAL;
-        if ((rc = gemv_validate(c)) || (rc = gemv_launch(dev, c, gpart, gcnt))) return rc;
+        if ((rc = gemv_validate(c)) || (rc = gemv_launch(dev, c))) return rc;
     }
 
     hipLaunchKernelGGL(k_rmsnorm, dim3(MR), dim3(256), 0, dev->stream, x, m->final_norm, m->hidden, m->rms_eps, xn,
@@ -311,12 +296,30 @@ int opure_verify_step(opure_dev* dev, const opure_verify_args* a)
     c.epi = EPI_LOGITS;
     c.logits.am_val = reinterpret_cast<float*>(ws + P.am_val);
     c.logits.am_idx = reinterpret_cast<int32_t*>(ws + P.am_idx);
-    if ((rc = gemv_validate(c)) || (rc = gemv_launch(dev, c, gpart, gcnt))) return rc;
+    if ((rc = gemv_validate(c)) || (rc = gemv_launch(dev, c))) return rc;
 
+    opure_rollback_args rb{};
+    if (a->rollback)
+    {
+        rb.model = m;
+        rb.kv = kv;
+        rb.batch = B;
+        rb.k = R - 1u;
+        rb.seq_len = a->seq_len;
+        rb.accepted = a->accepted;
+        rb.new_seq_len = a->new_seq_len;
+        rb.freed = a->freed;
+        rb.freed_stride = a->freed_stride;
+        rb.n_freed = a->n_freed;
+        rb.poison = a->poison;
+        rb.poison_bits = a->poison_bits;
+        if ((rc = rollback_validate(&rb))) return rc;
+    }
     if (a->accept_mode == OPURE_ACCEPT_GREEDY)
     {
+        // greedy acceptance and the rollback run in one kernel
         rc = greedy_from_partials(dev, c.logits.am_val, c.logits.am_idx, P.lm_tiles, B, R - 1u, a->tokens + 1, R,
-                                  a->out_tokens, a->accepted, nullptr, nullptr);
+                                  a->out_tokens, a->accepted, a->rollback ? &rb : nullptr);
         if (rc) return rc;
     }
     else if (a->accept_mode == OPURE_ACCEPT_REJECTION)
@@ -335,25 +338,9 @@ int opure_verify_step(opure_dev* dev, const opure_verify_args* a)
         aa.out_tokens = a->out_tokens;
         aa.accepted = a->accepted;
         aa.dist_out = a->dist_out;
-        rc = accept_rejection_launch(dev, &aa, ws + P.rej, dev->counters + P.gemv_groups, nullptr, nullptr);
+        rc = accept_rejection_launch(dev, &aa, ws + P.rej, dev->counters, nullptr, nullptr);
         if (rc) return rc;
-    }
-    if (a->rollback)
-    {
-        opure_rollback_args rb{};
-        rb.model = m;
-        rb.kv = kv;
-        rb.batch = B;
-        rb.k = R - 1u;
-        rb.seq_len = a->seq_len;
-        rb.accepted = a->accepted;
-        rb.new_seq_len = a->new_seq_len;
-        rb.freed = a->freed;
-        rb.freed_stride = a->freed_stride;
-        rb.n_freed = a->n_freed;
-        rb.poison = a->poison;
-        rb.poison_bits = a->poison_bits;
-        if ((rc = rollback_validate(&rb)) || (rc = rollback_launch(dev, &rb))) return rc;
+        if (a->rollback && (rc = rollback_launch(dev, &rb))) return rc;
     }
     return OPURE_OK;
 }

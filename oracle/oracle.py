@@ -259,6 +259,20 @@ class HostModel:
         self.rope_cos, self.rope_sin = rope_table(theta, head_dim, max_pos, rope_mode)
         self._build()
 
+    @classmethod
+    def from_arrays(cls, cfg: dict, w: dict) -> "HostModel":
+        """Wraps host arrays (e.g. downloaded from the device) as an oracle model."""
+        self = cls.__new__(cls)
+        keys = ("n_layers", "hidden", "n_heads", "n_kv_heads", "head_dim", "ffn", "vocab", "wfmt", "afmt",
+                "rms_eps", "attn_scale")
+        self.cfg = {k: cfg[k] for k in keys}
+        self.cfg["max_pos"] = w["rope_cos"].shape[0]
+        self.cfg["tied"] = w["lm_head"] is w["embed"]
+        self.embed, self.lm_head, self.final_norm = w["embed"], w["lm_head"], w["final_norm"]
+        self.layers, self.rope_cos, self.rope_sin = w["layers"], w["rope_cos"], w["rope_sin"]
+        self._build()
+        return self
+
     def _build(self):
         c = self.cfg
 

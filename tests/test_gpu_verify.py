@@ -181,6 +181,19 @@ def test_verify_with_rollback_matches_oracle(dev):
     assert diff[keep].max() <= 2e-2
 
 
+def logit_tolerance(want, afmt):
+    """max_abs bar on logits: 1e-4 for fp32 activations, 2e-2 for fp16; for bf16
+    activations the larger of 2e-2 and one bf16 ulp of the largest logit, since a
+    bf16 model rounds its activations to 8 significant bits at every stage and
+    the two sides' rounding decisions diverge through that chain."""
+    if afmt == O.A_F32:
+        return 1e-4
+    if afmt == O.A_F16:
+        return 2e-2
+    top = float(np.abs(want).max())
+    return max(2e-2, 2.0 ** (np.floor(np.log2(top)) - 7))
+
+
 def _full_width(wfmt, afmt, shape, n_layers, vocab, seed, attn_scale):
     h, nh, nkv, hd, ff = shape
     return O.HostModel(n_layers=n_layers, hidden=h, n_heads=nh, n_kv_heads=nkv, head_dim=hd, ffn=ff, vocab=vocab,
@@ -222,12 +235,13 @@ def test_full_width_two_layers(dev, cfg):
     got = run.get_logits()
     err = np.abs(got - want).max()
     gap = top2_gap(want).min()
-    say(name, "max_abs", err, "min top2 gap", gap)
-    assert err <= 2e-2
+    tol = logit_tolerance(want, afmt)
+    say(name, "max_abs", err, "tolerance", tol, "min top2 gap", gap)
+    assert err <= tol
     out, acc = run.get_accept()
     w_out, w_acc = O.accept_greedy(got, tokens[:, 1:])
     assert np.array_equal(out, w_out) and np.array_equal(acc, w_acc)
-    if gap > 2e-2:
+    if gap > tol:
         o_out, o_acc = O.accept_greedy(want, tokens[:, 1:])
         assert np.array_equal(out, o_out) and np.array_equal(acc, o_acc)
         assert acc[0] == R - 1
