@@ -1,7 +1,7 @@
 """Benchmark of the speculative-decoding verify step on one MI355X.
 
     python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--config c3|c4|c1]
-                    [--cpu-baseline auto|skip] [--no-kernel-timing]
+                    [--cpu-baseline auto|skip] [--no-kernel-timing] [--eager]
 
 One step = one verify pass over K+1 rows: embedding, every layer (fused QKV
 GEMV + RoPE + paged KV append, paged attention, o_proj + residual, gate/up
@@ -116,27 +116,39 @@ def build_workload(dev, cfg_name, seed=1234):
                 ctx=ctx, R=R, K=K, rng=rng)
 
 
-def time_graph(dev, step, tokens, ctx, warmup, steps):
+def time_graph(dev, step, tokens, ctx, warmup, steps, eager=False):
+    """Times `steps` verify steps replayed from one captured hipGraph (or, with
+    `eager`, launched one by one; profilers that do not follow graph replays
+    see the same kernels that way)."""
     step.dev.write(step.tokens, tokens)
     step.dev.write(step.seq_len, np.array([ctx], np.int32))
     a = step.args(H.ACCEPT_GREEDY)
-    dev.graph_begin()
-    H.check(H.lib().opure_verify_step(dev.h, C.byref(a)))
-    g = dev.graph_end()
+    if eager:
+        def launch():
+            H.check(H.lib().opure_verify_step(dev.h, C.byref(a)))
+        g = None
+    else:
+        dev.graph_begin()
+        H.check(H.lib().opure_verify_step(dev.h, C.byref(a)))
+        g = dev.graph_end()
+
+        def launch():
+            dev.graph_launch(g)
     for _ in range(warmup):
-        dev.graph_launch(g)
+        launch()
     dev.sync()
     t0 = time.perf_counter()
     dev.timer_begin()
     for _ in range(steps):
-        dev.graph_launch(g)
+        launch()
     dev.timer_end()
     gpu_ms = dev.timer_ms()
     dev.sync()
     wall_ms = (time.perf_counter() - t0) * 1e3
     acc = dev.download(step.accepted, np.int32, (1,))
     out = dev.download(step.out_tokens, np.int32, (1, step.R))
-    dev.graph_destroy(g)
+    if g is not None:
+        dev.graph_destroy(g)
     return dict(ms_per_step=gpu_ms / steps, wall_ms_per_step=wall_ms / steps, accepted=int(acc[0]),
                 out_tokens=out[0].tolist())
 
@@ -211,6 +223,7 @@ def main():
     ap.add_argument("--config", default="c3", choices=sorted(synth.CONFIGS))
     ap.add_argument("--cpu-baseline", default="auto", choices=["auto", "skip"])
     ap.add_argument("--no-kernel-timing", action="store_true")
+    ap.add_argument("--eager", action="store_true", help="launch each step's kernels directly instead of a hipGraph")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
@@ -221,12 +234,12 @@ def main():
     log("device", dev.name)
     w = build_workload(dev, args.config)
     cfg, ctx, R, K = w["cfg"], w["ctx"], w["R"], w["K"]
-    res = time_graph(dev, w["step"], w["tokens"], ctx, args.warmup, args.steps)
+    res = time_graph(dev, w["step"], w["tokens"], ctx, args.warmup, args.steps, args.eager)
     gpu_logits = w["step"].logits_host()
     log(f"self-drafts: {res['ms_per_step'] * 1e3:.1f} us/step, accepted {res['accepted']}/{K}")
     rnd = w["tokens"].copy()
     rnd[0, 1:] = w["rng"].integers(0, cfg["vocab"], K)
-    res_r = time_graph(dev, w["step"], rnd, ctx, args.warmup, args.steps)
+    res_r = time_graph(dev, w["step"], rnd, ctx, args.warmup, args.steps, args.eager)
     log(f"random drafts: {res_r['ms_per_step'] * 1e3:.1f} us/step, accepted {res_r['accepted']}/{K}")
     # restore the self-draft step's logits for the parity check (same cache state)
     step_bytes = synth.verify_bytes(cfg, R, ctx)
@@ -253,7 +266,7 @@ def main():
         "data": "synthetic: seeded N(0,0.02) weights quantised on device; context prefilled from random ids",
         "config": {"workload": f"{args.config}: verify step, {names[args.config]}, {cfg['n_layers']} layers, "
                                f"batch 1, K={K} ({R} rows), {ctx}-token paged context (16-token pages), greedy "
-                               "acceptance + rollback, hipGraph replay",
+                               "acceptance + rollback, " + ("eager launches" if args.eager else "hipGraph replay"),
                    "drafts": f"target's greedy continuation ({res['accepted']}/{K} accepted)",
                    "accepted_tokens_per_s_random_drafts": round((res_r["accepted"] + 1) /
                                                                 (res_r["ms_per_step"] * 1e-3), 1),

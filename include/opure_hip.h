@@ -294,7 +294,9 @@ int opure_verify_step(opure_dev* dev, const opure_verify_args* a);
  *      can read layer intermediates (run with n_layers = 1 to see layer 0).
  *      The counterpart of ReadActBank / RunLayersTraced (Opure_VoxelEngine.h:
  *      173-178, :226-227).  offsets[0..4] = byte offsets of x (fp32 residual,
- *      [rows][hidden]), xn (normed, afmt), q (afmt), att (afmt), h (afmt). */
+ *      [rows][hidden]), ss (fp32 sums of squares of x per 16-column tile,
+ *      [hidden/16][rows], feeding the fused RMSNorm), q (afmt), att (afmt),
+ *      h (afmt). */
 int opure_debug_workspace(opure_dev* dev, void** ptr, uint64_t* bytes);
 int opure_debug_verify_offsets(const opure_model* model, uint32_t batch, uint32_t rows, uint32_t max_ctx,
                                uint64_t offsets[5]);

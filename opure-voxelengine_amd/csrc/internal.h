@@ -95,13 +95,22 @@ struct GemvCall {
     void* y = nullptr;
     uint32_t yfmt = 0;
     uint32_t epi = EPI_STORE;
+    // fused rmsnorm (Opure_RMSNorm.usf:44-78) of an fp32 residual x: gain != null
+    // turns it on; ss_in holds per-16-column sums of squares [ss_tiles][M]
+    const float* gain = nullptr;
+    float eps = 0.0f;
+    const float* ss_in = nullptr;
+    uint32_t ss_tiles = 0;
+    // EPI_RESIDUAL: where to write the new residual's per-tile sums of squares
+    float* ss_out = nullptr;
     QkvEpilogue qkv{};
     LogitsEpilogue logits{};
 };
 
 struct GemvShape {
-    uint32_t tiles = 0;     // 16-row output tiles = workgroups
+    uint32_t tiles = 0;     // 16-row output tiles
     uint32_t blocks = 0;    // 64-byte blocks per weight row
+    uint32_t t = 0;         // tiles per workgroup
     uint32_t nw = 0;        // waves per workgroup splitting K
 };
 

@@ -7,14 +7,15 @@
 //
 //    embed gather (dequantised)                        x  [MR][h]  fp32 residual
 //    per layer:
-//      rmsnorm(x, attn_norm)                           xn [MR][h]  afmt
+//      rmsnorm(x, attn_norm) fused into the qkv load
 //      gemv qkv   + RoPE, q store, paged K/V append    q  [MR][nh*hd]
 //      paged attention (split-K chunks + combine)      att[MR][nh*hd]
 //      gemv o     + residual add                       x += o
-//      rmsnorm(x, mlp_norm)                            xn
+//      rmsnorm(x, mlp_norm) fused into the gate/up load
 //      gemv gate/up + SwiGLU                           h  [MR][ffn]
 //      gemv down  + residual add                       x += down
-//    rmsnorm(x, final_norm); gemv lm_head -> logits + per-tile argmax partials
+//    rmsnorm(x, final_norm) fused into the LM head; logits + per-tile argmax
+//    partials
 //    acceptance (greedy from the partials, or rejection sampling)
 //    rollback of rejected positions
 //
@@ -28,55 +29,44 @@ using namespace opure_dev_math;
 
 namespace {
 
+// Dequantised embedding rows into the fp32 residual, plus each 16-column
+// tile's sum of squares for the first layer's fused RMSNorm.  One thread per
+// 16-column tile.
 __global__ __launch_bounds__(256) void k_embed(const int32_t* tokens, opure_linear E, uint32_t wfmt, uint32_t h,
-                                               uint32_t vocab, float* x)
+                                               uint32_t vocab, uint32_t M, float* x, float* ss)
 {
     const uint32_t r = blockIdx.x;
     const int32_t t = tokens[r];
     float* xr = x + static_cast<uint64_t>(r) * h;
-    if (t < 0 || static_cast<uint32_t>(t) >= vocab)
+    const bool bad = t < 0 || static_cast<uint32_t>(t) >= vocab;
+    const uint64_t base = bad ? 0u : static_cast<uint64_t>(t) * h;
+    for (uint32_t tile = threadIdx.x; tile < h / 16u; tile += 256u)
     {
-        // an id outside the vocabulary poisons its row instead of reading out of bounds
-        for (uint32_t i = threadIdx.x; i < h; i += 256u) xr[i] = __builtin_nanf("");
-        return;
-    }
-    const uint64_t base = static_cast<uint64_t>(t) * h;
-    for (uint32_t i = threadIdx.x; i < h; i += 256u)
-    {
-        float v;
-        if (wfmt == OPURE_W_F32) v = static_cast<const float*>(E.w)[base + i];
-        else if (wfmt == OPURE_W_I8PC)
-            v = __fmul_rn(static_cast<float>(static_cast<const int8_t*>(E.w)[base + i]),
-                          f16_to_f32(static_cast<const uint16_t*>(E.scale)[t]));
-        else
+        float sq = 0.0f;
+#pragma unroll 4
+        for (uint32_t j = 0; j < 16u; ++j)
         {
-            const uint8_t byte = static_cast<const uint8_t*>(E.w)[(base + i) >> 1];
-            const uint32_t q = ((base + i) & 1u) ? (byte & 0x0Fu) : (byte >> 4);
-            const uint64_t g = static_cast<uint64_t>(t) * (h / 128u) + i / 128u;
-            v = __fmul_rn(bf16_to_f32(static_cast<const uint16_t*>(E.scale)[g]),
-                          __fsub_rn(static_cast<float>(q), bf16_to_f32(static_cast<const uint16_t*>(E.zero)[g])));
+            const uint32_t i = 16u * tile + j;
+            float v;
+            // an id outside the vocabulary poisons its row instead of reading out of bounds
+            if (bad) v = __builtin_nanf("");
+            else if (wfmt == OPURE_W_F32) v = static_cast<const float*>(E.w)[base + i];
+            else if (wfmt == OPURE_W_I8PC)
+                v = __fmul_rn(static_cast<float>(static_cast<const int8_t*>(E.w)[base + i]),
+                              f16_to_f32(static_cast<const uint16_t*>(E.scale)[t]));
+            else
+            {
+                const uint8_t byte = static_cast<const uint8_t*>(E.w)[(base + i) >> 1];
+                const uint32_t q = ((base + i) & 1u) ? (byte & 0x0Fu) : (byte >> 4);
+                const uint64_t g = static_cast<uint64_t>(t) * (h / 128u) + i / 128u;
+                v = __fmul_rn(bf16_to_f32(static_cast<const uint16_t*>(E.scale)[g]),
+                              __fsub_rn(static_cast<float>(q), bf16_to_f32(static_cast<const uint16_t*>(E.zero)[g])));
+            }
+            xr[i] = v;
+            sq = __fmaf_rn(v, v, sq);
         }
-        xr[i] = v;
+        ss[static_cast<uint64_t>(tile) * M + r] = sq;
     }
-}
-
-// x * rsqrt(mean(x^2) + eps) * g  (Opure_RMSNorm.usf:44-78), one workgroup per row
-__global__ __launch_bounds__(256) void k_rmsnorm(const float* x, const float* g, uint32_t d, float eps, void* y,
-                                                 uint32_t afmt)
-{
-    __shared__ float red[4];
-    const uint32_t r = blockIdx.x;
-    const float* xr = x + static_cast<uint64_t>(r) * d;
-    float ss = 0.0f;
-    for (uint32_t i = threadIdx.x; i < d; i += 256u) ss = __fmaf_rn(xr[i], xr[i], ss);
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
-    if ((threadIdx.x & 63u) == 0) red[threadIdx.x >> 6] = ss;
-    __syncthreads();
-    const float tot = (red[0] + red[1]) + (red[2] + red[3]);
-    const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(tot, static_cast<float>(d)), eps)));
-    for (uint32_t i = threadIdx.x; i < d; i += 256u)
-        store_act_rt(y, static_cast<uint64_t>(r) * d + i, __fmul_rn(__fmul_rn(xr[i], inv), g[i]), afmt);
 }
 
 }  // namespace
@@ -84,7 +74,7 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const float* x, const float* g,
 namespace opure_hip {
 
 struct VerifyPlan {
-    uint64_t x = 0, xn = 0, q = 0, att = 0, h = 0, am_val = 0, am_idx = 0, attn = 0, rej = 0, total = 0;
+    uint64_t x = 0, ss = 0, q = 0, att = 0, h = 0, am_val = 0, am_idx = 0, attn = 0, rej = 0, total = 0;
     uint64_t counters = 0;
     uint32_t lm_tiles = 0;
 };
@@ -98,7 +88,7 @@ static VerifyPlan make_plan(const opure_model* m, uint32_t B, uint32_t R, uint32
     uint64_t off = 0;
     auto take = [&](uint64_t bytes) { const uint64_t o = off; off += align_up(bytes ? bytes : 1, 256); return o; };
     p.x = take(MR * m->hidden * 4u);
-    p.xn = take(MR * m->hidden * eb);
+    p.ss = take(MR * (m->hidden / 16u) * 4u);
     p.q = take(MR * qdim * eb);
     p.att = take(MR * qdim * eb);
     p.h = take(MR * m->ffn * eb);
@@ -125,7 +115,8 @@ static int check_model(const opure_model* m, const opure_kv* kv, uint32_t B, uin
 {
     OPURE_REQUIRE(m && kv && m->layers && m->final_norm && m->rope_cos && m->rope_sin, OPURE_E_INVALID,
                   "verify: null model field");
-    OPURE_REQUIRE(m->n_layers >= 1 && m->hidden >= 16 && m->vocab >= 16 && m->vocab % 16 == 0 && m->ffn >= 16,
+    OPURE_REQUIRE(m->n_layers >= 1 && m->hidden >= 16 && m->hidden % 16 == 0 && m->vocab >= 16 && m->vocab % 16 == 0 &&
+                      m->ffn >= 16,
                   OPURE_E_INVALID, "verify: bad model shape");
     const bool ok = (m->wfmt == OPURE_W_F32 && m->afmt == OPURE_A_F32) ||
                     (m->wfmt == OPURE_W_I8PC && m->afmt == OPURE_A_F16) ||
@@ -181,7 +172,7 @@ int opure_debug_verify_offsets(const opure_model* model, uint32_t batch, uint32_
     OPURE_REQUIRE(model && offsets && batch && rows, OPURE_E_INVALID, "opure_debug_verify_offsets: bad argument");
     const VerifyPlan p = make_plan(model, batch, rows, max_ctx);
     offsets[0] = p.x;
-    offsets[1] = p.xn;
+    offsets[1] = p.ss;
     offsets[2] = p.q;
     offsets[3] = p.att;
     offsets[4] = p.h;
@@ -215,28 +206,33 @@ int opure_verify_step(opure_dev* dev, const opure_verify_args* a)
     if (rc) return rc;
     char* ws = static_cast<char*>(dev->ws);
     float* x = reinterpret_cast<float*>(ws + P.x);
-    void* xn = ws + P.xn;
+    float* ss = reinterpret_cast<float*>(ws + P.ss);
     void* q = ws + P.q;
     void* att = ws + P.att;
     void* hbuf = ws + P.h;
     const uint32_t qdim = m->n_heads * m->head_dim, kvdim = m->n_kv_heads * m->head_dim;
 
-    hipLaunchKernelGGL(k_embed, dim3(MR), dim3(256), 0, dev->stream, a->tokens, m->embed, m->wfmt, m->hidden, m->vocab, x);
+    hipLaunchKernelGGL(k_embed, dim3(MR), dim3(256), 0, dev->stream, a->tokens, m->embed, m->wfmt, m->hidden, m->vocab,
+                       MR, x, ss);
     OPURE_LAUNCH_CHECK("k_embed");
 
+    // Each residual producer (embed, o, down) leaves per-tile sums of squares in
+    // `ss`; the next consumer (qkv, gate/up, LM head) applies the RMSNorm while
+    // loading x.  Stream order keeps the single buffer consistent.
     GemvCall c;
     c.wfmt = m->wfmt;
     c.xfmt = m->afmt;
     c.M = MR;
+    c.eps = m->rms_eps;
+    c.ss_tiles = m->hidden / 16u;
     for (uint32_t L = 0; L < m->n_layers; ++L)
     {
         const opure_layer_weights& W = m->layers[L];
-        hipLaunchKernelGGL(k_rmsnorm, dim3(MR), dim3(256), 0, dev->stream, x, W.attn_norm, m->hidden, m->rms_eps, xn,
-                           m->afmt);
-        OPURE_LAUNCH_CHECK("k_rmsnorm");
-
         c.W = W.qkv;
-        c.x = xn;
+        c.x = x;
+        c.gain = W.attn_norm;
+        c.ss_in = ss;
+        c.ss_out = nullptr;
         c.y = q;
         c.yfmt = m->afmt;
         c.epi = EPI_QKV;
@@ -262,17 +258,17 @@ int opure_verify_step(opure_dev* dev, const opure_verify_args* a)
 
         c.W = W.o;
         c.x = att;
+        c.gain = nullptr;
+        c.ss_out = ss;
         c.y = x;
         c.yfmt = OPURE_A_F32;
         c.epi = EPI_RESIDUAL;
         if ((rc = gemv_validate(c)) || (rc = gemv_launch(dev, c))) return rc;
 
-        hipLaunchKernelGGL(k_rmsnorm, dim3(MR), dim3(256), 0, dev->stream, x, W.mlp_norm, m->hidden, m->rms_eps, xn,
-                           m->afmt);
-        OPURE_LAUNCH_CHECK("k_rmsnorm");
-
         c.W = W.gate_up;
-        c.x = xn;
+        c.x = x;
+        c.gain = W.mlp_norm;
+        c.ss_out = nullptr;
         c.y = hbuf;
         c.yfmt = m->afmt;
         c.epi = EPI_SWIGLU;
@@ -280,17 +276,18 @@ int opure_verify_step(opure_dev* dev, const opure_verify_args* a)
 
         c.W = W.down;
         c.x = hbuf;
+        c.gain = nullptr;
+        c.ss_out = ss;
         c.y = x;
         c.yfmt = OPURE_A_F32;
         c.epi = EPI_RESIDUAL;
         if ((rc = gemv_validate(c)) || (rc = gemv_launch(dev, c))) return rc;
     }
 
-    hipLaunchKernelGGL(k_rmsnorm, dim3(MR), dim3(256), 0, dev->stream, x, m->final_norm, m->hidden, m->rms_eps, xn,
-                       m->afmt);
-    OPURE_LAUNCH_CHECK("k_rmsnorm");
     c.W = m->lm_head;
-    c.x = xn;
+    c.x = x;
+    c.gain = m->final_norm;
+    c.ss_out = nullptr;
     c.y = a->logits;
     c.yfmt = OPURE_A_F32;
     c.epi = EPI_LOGITS;
