@@ -153,36 +153,54 @@ def time_graph(dev, step, tokens, ctx, warmup, steps, eager=False):
                 out_tokens=out[0].tolist())
 
 
-def time_dominant_gemv(dev, w, reps=5):
-    """Live timing of the gate/up GEMV (SwiGLU epilogue): one launch per layer,
-    rotating through the layers so the weights stream from HBM, each launch
-    bracketed by HIP events on the library's stream."""
-    m = w["model"]
-    cfg = m.cfg
-    M = w["R"]
-    eb = 2 if cfg["afmt"] != H.A_F32 else 4
-    x = dev.alloc(M * cfg["hidden"] * eb)
-    y = dev.alloc(M * cfg["ffn"] * eb)
-    H.check(H.lib().opure_convert_f32(dev.h, int(dev.upload(np.random.default_rng(0).standard_normal(
-        (M, cfg["hidden"])).astype(np.float32))), int(x), cfg["afmt"], M * cfg["hidden"]))
-    fn = {H.W_F32: H.lib().opure_gemv_batched_f32, H.W_I8PC: H.lib().opure_gemv_batched_i8pc,
-          H.W_I4G128: H.lib().opure_gemv_batched_i4g128}[cfg["wfmt"]]
-    times = []
-    for r in range(reps + 1):
-        for L in range(cfg["n_layers"]):
-            lin = synth.SynthModel._lin(m.layers[L]["gate_up"])
-            a = H.GemvArgs(lin, int(x), int(y), M, cfg["afmt"], cfg["afmt"], H.EPI_SWIGLU)
-            dev.timer_begin()
-            H.check(fn(dev.h, C.byref(a)))
-            dev.timer_end()
-            ms = dev.timer_ms()
-            if r > 0:
-                times.append(ms)
-    out, inn = 2 * cfg["ffn"], cfg["hidden"]
-    alg = synth.linear_bytes(cfg["wfmt"], out, inn) + M * inn * eb + M * cfg["ffn"] * eb
-    avg_ms = float(np.mean(times))
-    return dict(kernel=f"k_gemv<w{cfg['wfmt']},a{cfg['afmt']},swiglu> gate/up {out}x{inn}, M={M}",
-                bytes_per_launch=alg, avg_us=avg_ms * 1e3, gbs=alg / (avg_ms * 1e-3) / 1e9)
+def stage_bytes(cfg, stage, M, ctx):
+    """Algorithmic HBM bytes of one launch of a verify-step stage for M rows
+    over a ctx-token cache: the weights once, activations in and out once."""
+    h, nh, nkv, hd, ff, V = (cfg[k] for k in ("hidden", "n_heads", "n_kv_heads", "head_dim", "ffn", "vocab"))
+    w = cfg["wfmt"]
+    eb = 4 if cfg["afmt"] == H.A_F32 else 2
+    qkv_out = (nh + 2 * nkv) * hd
+    if stage == "embed":
+        return M * synth.linear_bytes(w, 1, h) + M * h * 4
+    if stage == "qkv":      # fp32 residual + gain in, q out, K/V rows appended
+        return synth.linear_bytes(w, qkv_out, h) + M * h * 4 + h * 4 + M * qkv_out * eb
+    if stage == "attention":
+        return 2 * nkv * hd * eb * (ctx + M) + 2 * M * nh * hd * eb
+    if stage == "o_proj":   # attention output in, residual read and written
+        return synth.linear_bytes(w, h, nh * hd) + M * nh * hd * eb + 2 * M * h * 4
+    if stage == "gate_up":  # residual + gain in, SwiGLU output out
+        return synth.linear_bytes(w, 2 * ff, h) + M * h * 4 + h * 4 + M * ff * eb
+    if stage == "down":
+        return synth.linear_bytes(w, h, ff) + M * ff * eb + 2 * M * h * 4
+    if stage == "lm_head":  # fp32 logits out
+        return synth.linear_bytes(w, V, h) + M * h * 4 + h * 4 + M * V * 4
+    return 0
+
+
+def time_stages(dev, step, tokens, ctx, steps):
+    """Per-stage timing of eager verify steps: each stage's launches are
+    bracketed by HIP events on the library's stream (opure_profile_*)."""
+    step.dev.write(step.tokens, tokens)
+    step.dev.write(step.seq_len, np.array([ctx], np.int32))
+    a = step.args(H.ACCEPT_GREEDY)
+    for _ in range(3):
+        H.check(H.lib().opure_verify_step(dev.h, C.byref(a)))
+    dev.sync()
+    dev.profile(True)
+    for _ in range(steps):
+        H.check(H.lib().opure_verify_step(dev.h, C.byref(a)))
+    prof = dev.profile_read()
+    dev.profile(False)
+    cfg = step.model.cfg
+    out = {}
+    for st, (n, ms) in prof.items():
+        if n == 0:
+            continue
+        avg_us = ms * 1e3 / n
+        by = stage_bytes(cfg, st, step.B * step.R, ctx)
+        out[st] = dict(launches_per_step=n / steps, avg_us=avg_us, us_per_step=ms * 1e3 / steps,
+                       bytes_per_launch=by, gbs=by / (avg_us * 1e-6) / 1e9 if by else None)
+    return out
 
 
 def cpu_baseline(dev, w, gpu_logits, gpu_accept):
@@ -244,9 +262,16 @@ def main():
     # restore the self-draft step's logits for the parity check (same cache state)
     step_bytes = synth.verify_bytes(cfg, R, ctx)
     step_gbs = step_bytes["total"] / (res["ms_per_step"] * 1e-3) / 1e9
-    kern = None if args.no_kernel_timing else time_dominant_gemv(dev, w)
-    if kern:
-        log(f"dominant kernel {kern['kernel']}: {kern['avg_us']:.1f} us, {kern['gbs']:.0f} GB/s")
+    stages = None if args.no_kernel_timing else time_stages(dev, w["step"], w["tokens"], ctx, 10)
+    kern = None
+    if stages:
+        for st, d in stages.items():
+            log(f"stage {st:10s} x{d['launches_per_step']:4.0f}/step  {d['avg_us']:8.2f} us/launch  "
+                f"{d['us_per_step']:8.1f} us/step" + (f"  {d['gbs']:6.0f} GB/s" if d["gbs"] else ""))
+        # the dominant single-kernel stage (attention is two kernels: chunks + combine)
+        gemv_stages = [st for st in ("qkv", "o_proj", "gate_up", "down", "lm_head") if st in stages]
+        dom = max(gemv_stages, key=lambda st: stages[st]["us_per_step"])
+        kern = dict(stages[dom], stage=dom)
     cpu, parity = None, None
     if args.cpu_baseline == "auto":
         cpu, parity = cpu_baseline(dev, w, gpu_logits, res)
@@ -278,8 +303,9 @@ def main():
     if kern:
         line["roofline"] = {"bound": "hbm", "achieved": round(kern["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                             "frac": round(kern["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
-                            "kernel": kern["kernel"], "bytes_per_launch": kern["bytes_per_launch"],
-                            "avg_us": round(kern["avg_us"], 2)}
+                            "kernel": f"k_gemv ({kern['stage']} stage of the verify step)",
+                            "bytes_per_launch": kern["bytes_per_launch"], "avg_us": round(kern["avg_us"], 2)}
+        line["stages_us_per_step"] = {st: round(d["us_per_step"], 1) for st, d in stages.items()}
     if cpu:
         line["cpu_baseline"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in cpu.items()}
         line["parity"] = parity

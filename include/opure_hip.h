@@ -290,6 +290,25 @@ int opure_verify_reserve(opure_dev* dev, const opure_model* model, uint32_t batc
                          uint32_t max_ctx);
 int opure_verify_step(opure_dev* dev, const opure_verify_args* a);
 
+/* ---- stage timing of eager verify steps.  With profiling on, every stage of
+ *      opure_verify_step is bracketed by HIP events on the device's stream
+ *      (skipped while a graph is being captured).  opure_profile_read waits
+ *      for the stream, returns per stage the number of bracketed launches and
+ *      their summed milliseconds since the last read, and starts over.  The
+ *      counterpart of the per-layer timings of MetricsSnapshot
+ *      (src/engine/Opure_Metrics.h:42-43). */
+#define OPURE_STAGE_EMBED    0u   /* embedding gather                          */
+#define OPURE_STAGE_QKV      1u   /* rmsnorm + qkv GEMV + RoPE + K/V append    */
+#define OPURE_STAGE_ATTN     2u   /* paged attention (chunks + combine)        */
+#define OPURE_STAGE_O        3u   /* o_proj GEMV + residual                    */
+#define OPURE_STAGE_GATE_UP  4u   /* rmsnorm + gate/up GEMV + SwiGLU           */
+#define OPURE_STAGE_DOWN     5u   /* down GEMV + residual                      */
+#define OPURE_STAGE_LM_HEAD  6u   /* final rmsnorm + LM head + argmax partials */
+#define OPURE_STAGE_ACCEPT   7u   /* acceptance and KV rollback                */
+#define OPURE_STAGE_COUNT    8u
+int opure_profile_enable(opure_dev* dev, int on);
+int opure_profile_read(opure_dev* dev, uint32_t counts[OPURE_STAGE_COUNT], double ms[OPURE_STAGE_COUNT]);
+
 /* ---- diagnostics: the device workspace of the last verify step, so a test
  *      can read layer intermediates (run with n_layers = 1 to see layer 0).
  *      The counterpart of ReadActBank / RunLayersTraced (Opure_VoxelEngine.h:

@@ -7,6 +7,7 @@
 #include <stdint.h>
 
 #include <string>
+#include <vector>
 
 #include "../../include/opure_hip.h"
 
@@ -27,6 +28,11 @@ struct opure_dev {
     uint64_t    ws_bytes = 0;
     uint32_t*   counters = nullptr;     // zero between launches
     uint64_t    counter_words = 0;
+    // stage timing of eager verify steps: event pairs and the stage of each pair
+    bool                   prof_on = false;
+    std::vector<hipEvent_t> prof_ev;
+    std::vector<uint32_t>  prof_stage;
+    uint32_t               prof_used = 0;    // events recorded since the last read
 };
 
 struct opure_graph {
@@ -40,6 +46,9 @@ int set_error(int code, const char* fmt, ...);
 int hip_fail(hipError_t e, const char* what);
 const char* afmt_name(uint32_t afmt);
 int  ensure_workspace(opure_dev* dev, uint64_t bytes, uint64_t counter_words);
+// bracket one stage's launches with events (no-op unless profiling, or while capturing)
+int  prof_begin(opure_dev* dev, uint32_t stage);
+int  prof_end(opure_dev* dev);
 inline uint64_t align_up(uint64_t v, uint64_t a) { return (v + a - 1) / a * a; }
 inline uint32_t act_bytes(uint32_t afmt) { return afmt == OPURE_A_F32 ? 4u : 2u; }
 

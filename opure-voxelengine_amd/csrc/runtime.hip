@@ -85,6 +85,33 @@ int ensure_workspace(opure_dev* dev, uint64_t bytes, uint64_t counter_words)
 using namespace opure_hip;
 
 // ---------------------------------------------------------------------------
+namespace opure_hip {
+
+int prof_begin(opure_dev* dev, uint32_t stage)
+{
+    if (!dev->prof_on || dev->capturing) return OPURE_OK;
+    while (dev->prof_ev.size() < dev->prof_used + 2u)
+    {
+        hipEvent_t e;
+        OPURE_HIP_TRY(hipEventCreate(&e));
+        dev->prof_ev.push_back(e);
+    }
+    if (dev->prof_stage.size() < dev->prof_ev.size() / 2u) dev->prof_stage.resize(dev->prof_ev.size() / 2u);
+    dev->prof_stage[dev->prof_used / 2u] = stage;
+    OPURE_HIP_TRY(hipEventRecord(dev->prof_ev[dev->prof_used], dev->stream));
+    return OPURE_OK;
+}
+
+int prof_end(opure_dev* dev)
+{
+    if (!dev->prof_on || dev->capturing) return OPURE_OK;
+    OPURE_HIP_TRY(hipEventRecord(dev->prof_ev[dev->prof_used + 1u], dev->stream));
+    dev->prof_used += 2u;
+    return OPURE_OK;
+}
+
+}  // namespace opure_hip
+
 extern "C" {
 
 const char* opure_last_error(void) { return g_err; }
@@ -125,6 +152,7 @@ int opure_dev_destroy(opure_dev* dev)
     hipStreamSynchronize(dev->stream);
     if (dev->ws) hipFree(dev->ws);
     if (dev->counters) hipFree(dev->counters);
+    for (hipEvent_t e : dev->prof_ev) hipEventDestroy(e);
     if (dev->ev_begin) hipEventDestroy(dev->ev_begin);
     if (dev->ev_end) hipEventDestroy(dev->ev_end);
     if (dev->stream) hipStreamDestroy(dev->stream);
@@ -261,6 +289,32 @@ int opure_graph_destroy(opure_graph* g)
     if (g->exec) hipGraphExecDestroy(g->exec);
     if (g->graph) hipGraphDestroy(g->graph);
     delete g;
+    return OPURE_OK;
+}
+
+
+int opure_profile_enable(opure_dev* dev, int on)
+{
+    OPURE_REQUIRE(dev, OPURE_E_INVALID, "opure_profile_enable: null device");
+    dev->prof_on = on != 0;
+    dev->prof_used = 0;
+    return OPURE_OK;
+}
+
+int opure_profile_read(opure_dev* dev, uint32_t counts[OPURE_STAGE_COUNT], double ms[OPURE_STAGE_COUNT])
+{
+    OPURE_REQUIRE(dev && counts && ms, OPURE_E_INVALID, "opure_profile_read: null argument");
+    for (uint32_t i = 0; i < OPURE_STAGE_COUNT; ++i) { counts[i] = 0; ms[i] = 0.0; }
+    OPURE_HIP_TRY(hipStreamSynchronize(dev->stream));
+    for (uint32_t k = 0; k + 1u < dev->prof_used; k += 2u)
+    {
+        float t = 0.0f;
+        OPURE_HIP_TRY(hipEventElapsedTime(&t, dev->prof_ev[k], dev->prof_ev[k + 1u]));
+        const uint32_t st = dev->prof_stage[k / 2u];
+        counts[st] += 1u;
+        ms[st] += t;
+    }
+    dev->prof_used = 0;
     return OPURE_OK;
 }
 

@@ -212,9 +212,11 @@ int opure_verify_step(opure_dev* dev, const opure_verify_args* a)
     void* hbuf = ws + P.h;
     const uint32_t qdim = m->n_heads * m->head_dim, kvdim = m->n_kv_heads * m->head_dim;
 
+    if ((rc = prof_begin(dev, OPURE_STAGE_EMBED))) return rc;
     hipLaunchKernelGGL(k_embed, dim3(MR), dim3(256), 0, dev->stream, a->tokens, m->embed, m->wfmt, m->hidden, m->vocab,
                        MR, x, ss);
     OPURE_LAUNCH_CHECK("k_embed");
+    if ((rc = prof_end(dev))) return rc;
 
     // Each residual producer (embed, o, down) leaves per-tile sums of squares in
     // `ss`; the next consumer (qkv, gate/up, LM head) applies the RMSNorm while
@@ -250,10 +252,14 @@ int opure_verify_step(opure_dev* dev, const opure_verify_args* a)
         c.qkv.max_pages = kv->max_pages_per_seq;
         c.qkv.n_pages = kv->n_pages;
         c.qkv.layer = L;
-        if ((rc = gemv_validate(c)) || (rc = gemv_launch(dev, c))) return rc;
+        if ((rc = gemv_validate(c)) || (rc = prof_begin(dev, OPURE_STAGE_QKV)) || (rc = gemv_launch(dev, c)) ||
+            (rc = prof_end(dev)))
+            return rc;
 
-        if ((rc = attn_launch(dev, m, kv, L, B, R, a->seq_len, a->max_ctx, q, att,
-                              reinterpret_cast<float*>(ws + P.attn))))
+        if ((rc = prof_begin(dev, OPURE_STAGE_ATTN)) ||
+            (rc = attn_launch(dev, m, kv, L, B, R, a->seq_len, a->max_ctx, q, att,
+                              reinterpret_cast<float*>(ws + P.attn))) ||
+            (rc = prof_end(dev)))
             return rc;
 
         c.W = W.o;
@@ -263,7 +269,9 @@ int opure_verify_step(opure_dev* dev, const opure_verify_args* a)
         c.y = x;
         c.yfmt = OPURE_A_F32;
         c.epi = EPI_RESIDUAL;
-        if ((rc = gemv_validate(c)) || (rc = gemv_launch(dev, c))) return rc;
+        if ((rc = gemv_validate(c)) || (rc = prof_begin(dev, OPURE_STAGE_O)) || (rc = gemv_launch(dev, c)) ||
+            (rc = prof_end(dev)))
+            return rc;
 
         c.W = W.gate_up;
         c.x = x;
@@ -272,7 +280,9 @@ int opure_verify_step(opure_dev* dev, const opure_verify_args* a)
         c.y = hbuf;
         c.yfmt = m->afmt;
         c.epi = EPI_SWIGLU;
-        if ((rc = gemv_validate(c)) || (rc = gemv_launch(dev, c))) return rc;
+        if ((rc = gemv_validate(c)) || (rc = prof_begin(dev, OPURE_STAGE_GATE_UP)) || (rc = gemv_launch(dev, c)) ||
+            (rc = prof_end(dev)))
+            return rc;
 
         c.W = W.down;
         c.x = hbuf;
@@ -281,7 +291,9 @@ int opure_verify_step(opure_dev* dev, const opure_verify_args* a)
         c.y = x;
         c.yfmt = OPURE_A_F32;
         c.epi = EPI_RESIDUAL;
-        if ((rc = gemv_validate(c)) || (rc = gemv_launch(dev, c))) return rc;
+        if ((rc = gemv_validate(c)) || (rc = prof_begin(dev, OPURE_STAGE_DOWN)) || (rc = gemv_launch(dev, c)) ||
+            (rc = prof_end(dev)))
+            return rc;
     }
 
     c.W = m->lm_head;
@@ -293,7 +305,9 @@ int opure_verify_step(opure_dev* dev, const opure_verify_args* a)
     c.epi = EPI_LOGITS;
     c.logits.am_val = reinterpret_cast<float*>(ws + P.am_val);
     c.logits.am_idx = reinterpret_cast<int32_t*>(ws + P.am_idx);
-    if ((rc = gemv_validate(c)) || (rc = gemv_launch(dev, c))) return rc;
+    if ((rc = gemv_validate(c)) || (rc = prof_begin(dev, OPURE_STAGE_LM_HEAD)) || (rc = gemv_launch(dev, c)) ||
+        (rc = prof_end(dev)))
+        return rc;
 
     opure_rollback_args rb{};
     if (a->rollback)
@@ -312,6 +326,7 @@ int opure_verify_step(opure_dev* dev, const opure_verify_args* a)
         rb.poison_bits = a->poison_bits;
         if ((rc = rollback_validate(&rb))) return rc;
     }
+    if (a->accept_mode != OPURE_ACCEPT_NONE && (rc = prof_begin(dev, OPURE_STAGE_ACCEPT))) return rc;
     if (a->accept_mode == OPURE_ACCEPT_GREEDY)
     {
         // greedy acceptance and the rollback run in one kernel
@@ -339,6 +354,7 @@ int opure_verify_step(opure_dev* dev, const opure_verify_args* a)
         if (rc) return rc;
         if (a->rollback && (rc = rollback_launch(dev, &rb))) return rc;
     }
+    if (a->accept_mode != OPURE_ACCEPT_NONE && (rc = prof_end(dev))) return rc;
     return OPURE_OK;
 }
 

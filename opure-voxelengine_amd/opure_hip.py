@@ -21,6 +21,7 @@ W_F32, W_I8PC, W_I4G128 = 0, 1, 2
 A_F32, A_F16, A_BF16 = 0, 1, 2
 ROPE_GPU, ROPE_CPUREF = 0, 1
 EPI_STORE, EPI_RESIDUAL, EPI_SWIGLU = 0, 1, 2
+STAGES = ("embed", "qkv", "attention", "o_proj", "gate_up", "down", "lm_head", "accept")
 ACCEPT_NONE, ACCEPT_GREEDY, ACCEPT_REJECTION = 0, 1, 2
 
 
@@ -139,6 +140,8 @@ def _declare(L):
         "opure_verify_step": ([vp, C.POINTER(VerifyArgs)], i),
         "opure_debug_workspace": ([vp, C.POINTER(vp), C.POINTER(u64)], i),
         "opure_debug_verify_offsets": ([C.POINTER(Model), u32, u32, u32, C.POINTER(u64)], i),
+        "opure_profile_enable": ([vp, C.c_int], i),
+        "opure_profile_read": ([vp, C.POINTER(u32), C.POINTER(C.c_double)], i),
         "opure_synth_normal_f32": ([vp, vp, u64, u64, u32, f32, f32], i),
         "opure_quantize_i8pc": ([vp, vp, u32, u32, vp, vp], i),
         "opure_quantize_i4g128": ([vp, vp, u32, u32, vp, vp, vp], i),
@@ -232,6 +235,16 @@ class Dev:
         ms = C.c_float()
         check(lib().opure_timer_ms(self.h, C.byref(ms)))
         return float(ms.value)
+
+    def profile(self, on: bool):
+        check(lib().opure_profile_enable(self.h, 1 if on else 0))
+
+    def profile_read(self) -> dict:
+        """{stage: (launches, total ms)} since the last read."""
+        n = len(STAGES)
+        counts, ms = (C.c_uint32 * n)(), (C.c_double * n)()
+        check(lib().opure_profile_read(self.h, counts, ms))
+        return {STAGES[i]: (int(counts[i]), float(ms[i])) for i in range(n)}
 
     def graph_begin(self):
         check(lib().opure_graph_begin(self.h))
