@@ -17,7 +17,8 @@
  *     Uploads and downloads are synchronous, like UploadToBuffer /
  *     ReadbackFromBuffer (Opure_Dx12.h:230-244).
  *
- * Data layouts (all row-major)
+ * Data layouts (row-major interchange; the kernels read weights in the tiled
+ * layout made by opure_tile_linear, see opure_linear below)
  *   linear (OPURE_W_F32)     w: float[out][in]
  *   linear (OPURE_W_I8PC)    w: int8[out][in], scale: fp16[out]; y = scale[o] * sum_i w*x
  *   linear (OPURE_W_I4G128)  w: uint8[out][in/2], element 2i in the high nibble
@@ -107,20 +108,51 @@ int opure_rope_table(double theta, uint32_t head_dim, uint32_t max_pos, uint32_t
                      float* cos_out, float* sin_out);
 
 /* ---- model description ------------------------------------------------ */
+/* Weight layouts.  ROWMAJOR is the interchange format above (what loaders and
+ * the quantisers produce).  Every compute entry point reads the TILED layout
+ * made by opure_tile_linear:
+ *   16-row tiles (out/16), each weight row cut into 64-byte blocks (16 f32,
+ *   64 int8 or 128 uint4 values); tile t, block b is one 1 KB piece at
+ *   (t * (in_bytes/64) + b) * 1024, and lane l = 16*g + r of a wave reads its
+ *   16 bytes [16g, 16g+16) of row r's block at offset 16*l -- one contiguous
+ *   1 KB load per wave, already in MFMA operand order.
+ *   int8 is stored offset-binary (q ^ 0x80); uint4 nibbles are reordered
+ *   inside each 32-bit word so that byte masks and permutes yield element
+ *   pairs in k order; scales follow the tiles: int8 fp16[tile][16], uint4
+ *   uint32 (bf16 scale | bf16 zero << 16)[tile][in/128][16]; zero is unused.
+ * TILED_SWIGLU additionally interleaves the rows of a [gate; up] linear
+ * (out = 2F): tile t holds gate rows 8t..8t+7 and up rows 8t..8t+7 alternately,
+ * so the SwiGLU epilogue finds each (gate, up) pair in one lane. */
+#define OPURE_LAYOUT_ROWMAJOR      0u
+#define OPURE_LAYOUT_TILED         1u
+#define OPURE_LAYOUT_TILED_SWIGLU  2u
+
 typedef struct opure_linear {
     const void* w;
-    const void* scale;      /* I8PC: fp16[out]; I4G128: bf16[out][in/128] */
-    const void* zero;       /* I4G128: bf16[out][in/128] */
+    const void* scale;      /* ROWMAJOR I8PC: fp16[out]; I4G128: bf16[out][in/128]; TILED: see above */
+    const void* zero;       /* ROWMAJOR I4G128: bf16[out][in/128]; TILED: unused */
     uint32_t    out, in;
+    uint32_t    layout;     /* OPURE_LAYOUT_* */
 } opure_linear;
+
+/* Bytes of the tiled copy of an out x in linear. */
+int opure_tiled_bytes(uint32_t wfmt, uint32_t out, uint32_t in, uint64_t* w_bytes, uint64_t* scale_bytes);
+/* Rewrites the ROWMAJOR linear `src` into w_dst / scale_dst (device buffers of
+ * opure_tiled_bytes) in layout OPURE_LAYOUT_TILED or _TILED_SWIGLU, and fills
+ * *dst to describe it.  A pure permutation (plus the int8 sign flip): the
+ * values the kernels compute with are exactly the row-major ones.  The
+ * counterpart of the weight upload (Opure_Graph.cpp:500-528), done once at
+ * load time. */
+int opure_tile_linear(opure_dev* dev, uint32_t wfmt, uint32_t layout, const opure_linear* src, void* w_dst,
+                      void* scale_dst, opure_linear* dst);
 
 typedef struct opure_layer_weights {
     const float* attn_norm;   /* [hidden] fp32 */
     const float* mlp_norm;    /* [hidden] fp32 */
-    opure_linear qkv;         /* rows [q; k; v] = (n_heads + 2 n_kv_heads) * head_dim */
-    opure_linear o;           /* hidden x n_heads*head_dim */
-    opure_linear gate_up;     /* rows [gate; up] = 2 ffn */
-    opure_linear down;        /* hidden x ffn */
+    opure_linear qkv;         /* rows [q; k; v] = (n_heads + 2 n_kv_heads) * head_dim, TILED */
+    opure_linear o;           /* hidden x n_heads*head_dim, TILED */
+    opure_linear gate_up;     /* rows [gate; up] = 2 ffn, TILED_SWIGLU */
+    opure_linear down;        /* hidden x ffn, TILED */
 } opure_layer_weights;
 
 typedef struct opure_model {
@@ -132,8 +164,8 @@ typedef struct opure_model {
     const float* rope_cos;    /* device [rope_max_pos][head_dim/2] */
     const float* rope_sin;
     uint32_t rope_max_pos;
-    opure_linear embed;       /* [vocab][hidden] */
-    opure_linear lm_head;     /* [vocab][hidden] (same pointers as embed when tied) */
+    opure_linear embed;       /* [vocab][hidden], TILED (rows are gathered from the tiles) */
+    opure_linear lm_head;     /* [vocab][hidden], TILED (same pointers as embed when tied) */
     const float* final_norm;  /* [hidden] */
     const opure_layer_weights* layers;   /* HOST array [n_layers] of device pointers */
 } opure_model;
@@ -154,7 +186,7 @@ typedef struct opure_kv {
  *        SWIGLU:   W rows = [gate; up] (out = 2F); y[m][f] = silu(g) * u  (y in yfmt)
  *      Weight/activation pairs built: F32/F32, I8PC/F16, I4G128/F16, I4G128/BF16. */
 typedef struct opure_gemv_args {
-    opure_linear W;
+    opure_linear W;           /* TILED (TILED_SWIGLU for the SwiGLU epilogue) */
     const void*  x;           /* [M][W.in] in xfmt */
     void*        y;
     uint32_t     M;

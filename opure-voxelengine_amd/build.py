@@ -24,7 +24,8 @@ HIP_LIB = os.path.join(LIB, "libopure_hip.so")
 ENGINE_LIB = os.path.join(LIB, "libopure_engine.so")
 
 ARCH = "gfx950"
-HIP_SOURCES = ["runtime.hip", "gemv.hip", "attention.hip", "accept.hip", "verify.hip"]
+HIP_SOURCES = ["runtime.hip", "gemv.hip", "gemv_f32.hip", "gemv_i8.hip", "gemv_i4h.hip", "gemv_i4b.hip",
+               "attention.hip", "accept.hip", "verify.hip"]
 # -ffp-contract=off: every float expression rounds as written (fmas are
 # explicit __fmaf_rn), like the CPU oracle.  Packed-fp32 instructions stay
 # off: they are emitted only from plain float

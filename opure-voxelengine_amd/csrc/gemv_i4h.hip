@@ -1,0 +1,13 @@
+// gemv_i4h.hip -- instantiations of the K+1-row GEMV kernel (gemv_kernel.h)
+// for W_I4G128 weights with A_F16 activations.
+#include "gemv_kernel.h"
+
+namespace opure_gemv {
+
+int launch_i4_f16(opure_dev* dev, uint32_t epi, bool norm, bool staged, const KParams& kp, const Recipe& r, uint32_t grid,
+        uint32_t lds)
+{
+    return launch_format<OPURE_W_I4G128, OPURE_A_F16>(dev, epi, norm, staged, kp, r, grid, lds);
+}
+
+}  // namespace opure_gemv

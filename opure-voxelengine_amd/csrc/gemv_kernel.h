@@ -1,0 +1,674 @@
+// ============================================================================
+//  gemv_kernel.h -- the K+1-row GEMV kernel for gfx950 matrix cores, included
+//  by gemv_f32.hip / gemv_i8.hip / gemv_i4.hip (one weight format each, so the
+//  instantiations compile in parallel).
+//
+//  Replaces GEMVMain / GEMVQuantMain (shaders/Opure_GEMV.usf:40-89,
+//  shaders/Opure_GEMV_Quant.usf:39-95), which read the whole weight matrix once
+//  per activation row.  Here every weight byte is read once for all M <= 16
+//  rows (the K+1 draft positions of one or more sequences).
+//
+//  Mapping.  y^T[o][m] = sum_k W[o][k] X[m][k] is one 16 x 16 MFMA tile per 16
+//  weight rows: A = 16 weight rows x 32 k, B = 32 k x 16 columns of X (columns
+//  >= M compute on a copy of column M-1 and are never stored).  Weights are in
+//  the tiled layout (opure_tile_linear): tile t, block b is 1 KB and lane l of
+//  a wave loads bytes [16l, 16l+16) of it -- row l%16, k-slice l/16 -- so one
+//  wave instruction reads 1 KB of contiguous memory.  Widening in registers:
+//    f32   -> v_mfma_f32_16x16x4_f32, 4 MFMAs per block
+//    int8  -> offset-binary bytes into fp16 1024+u via byte permutes, minus
+//             1152 (exact), 2 x v_mfma_f32_16x16x32_f16 per block
+//    uint4 -> nibbles pre-ordered so two masks and four byte permutes give
+//             MAGIC|q pairs in k order, 4 MFMAs per 128-k group; the group's
+//             scale and zero point are applied to the fresh group accumulator
+//             through the column's group sum of X
+//
+//  Work split.  A workgroup of NW waves owns T tiles at a time ("a group");
+//  its waves take interleaved blocks of K (U per wave per pass) and are
+//  combined through LDS in wave order, then wave t runs the epilogue of tile t.
+//  With STAGED, X is staged once into LDS for the whole K (rmsnorm applied
+//  there for consumers of the residual) and the workgroup loops over groups
+//  (persistent); otherwise X fragments are loaded from global memory with the
+//  weights.  Weights (and X fragments) of the next pass are always in flight
+//  while the current pass computes.  No workgroup talks to another, and every
+//  sum has a fixed order that depends on the shape only, so results are
+//  reproducible and independent of M and of the path taken.
+// ============================================================================
+#pragma once
+
+#include "internal.h"
+
+namespace opure_gemv {
+
+using namespace opure_dev_math;
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u4_t __attribute__((ext_vector_type(4)));
+
+struct KParams {
+    const uint8_t* w;          // tiled weights
+    const void* sc;            // tiled scales: int8 fp16[tiles][16]; uint4 u32[tiles][G][16]
+    uint32_t out, in, tiles, nblk, groups;
+    const uint8_t* x;          // X [M][in] in the activation format, or the fp32 residual with NORM
+    uint32_t M;
+    void* y;
+    uint32_t yfmt;
+    const float* gain;         // NORM: rmsnorm gain [in]
+    float eps;
+    const float* ss_in;        // NORM: producer's per-16-column sums of squares [ss_tiles][M]
+    uint32_t ss_tiles;
+    float* ss_out;             // RESIDUAL: this GEMV's per-tile sums of squares [tiles][M] (may be null)
+    uint32_t x_stride;         // STAGED: LDS bytes per staged X row
+    uint32_t off_xsum;         // STAGED uint4: LDS offset of the group sums [M][in/128]
+    uint32_t off_red;          // LDS offset of the wave reduction [NW][T][64] f4
+    opure_hip::QkvEpilogue qkv;
+    opure_hip::LogitsEpilogue lg;
+};
+
+template <int WF> struct Fmt;
+// KB: k values per 64-byte block of a row; N: X dwords per lane per block
+template <> struct Fmt<OPURE_W_F32>    { static constexpr uint32_t KB = 16, N = 4; };
+template <> struct Fmt<OPURE_W_I8PC>   { static constexpr uint32_t KB = 64, N = 8; };
+template <> struct Fmt<OPURE_W_I4G128> { static constexpr uint32_t KB = 128, N = 16; };
+
+__device__ __forceinline__ half8_t as_half8(uint32_t a, uint32_t b, uint32_t c, uint32_t d)
+{
+    u4_t v = {a, b, c, d};
+    return __builtin_bit_cast(half8_t, v);
+}
+
+__device__ __forceinline__ bf16x8_t as_bf8(uint32_t a, uint32_t b, uint32_t c, uint32_t d)
+{
+    u4_t v = {a, b, c, d};
+    return __builtin_bit_cast(bf16x8_t, v);
+}
+
+// 4 offset-binary bytes u = q + 128 -> fp16 pairs (q0, q1), (q2, q3), exactly:
+// 0x64uu is 1024 + u, minus 1152
+__device__ __forceinline__ void u8x4_to_f16(uint32_t u, uint32_t& lo, uint32_t& hi)
+{
+    const uint32_t a = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);
+    const uint32_t b = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);
+    const half2_t bias = {static_cast<_Float16>(-1152.0f), static_cast<_Float16>(-1152.0f)};
+    lo = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, a) + bias);
+    hi = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, b) + bias);
+}
+
+// A tiled uint4 word holds elements e0..e7 at nibbles 0,4,1,5,2,6,3,7, so
+// the low nibbles of its bytes are (e0,e4,e1,e5) and the high nibbles
+// (e2,e6,e3,e7); byte permutes against MAGIC then give MAGIC|q pairs in k
+// order.  fp16 MAGIC 0x64 (1024 + q, minus 1024 exactly); bf16 0x43 (128 + q,
+// the 128 is taken out with the zero point).
+template <int AF>
+__device__ __forceinline__ void u4x8_pairs(uint32_t d, uint32_t (&o)[4])
+{
+    constexpr uint32_t MAGIC = AF == OPURE_A_F16 ? 0x64646464u : 0x43434343u;
+    const uint32_t lo = d & 0x0F0F0F0Fu;
+    const uint32_t hi = (d >> 4) & 0x0F0F0F0Fu;
+    o[0] = __builtin_amdgcn_perm(MAGIC, lo, 0x04020400u);   // e0 e1
+    o[1] = __builtin_amdgcn_perm(MAGIC, hi, 0x04020400u);   // e2 e3
+    o[2] = __builtin_amdgcn_perm(MAGIC, lo, 0x04030401u);   // e4 e5
+    o[3] = __builtin_amdgcn_perm(MAGIC, hi, 0x04030401u);   // e6 e7
+    if constexpr (AF == OPURE_A_F16)
+    {
+        const half2_t bias = {static_cast<_Float16>(-1024.0f), static_cast<_Float16>(-1024.0f)};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o[j] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, o[j]) + bias);
+    }
+}
+
+// sum of 8 rounded activations (4 pairs): packed dot products with (1, 1)
+template <int AF>
+__device__ __forceinline__ float unit_sum(uint32_t d0, uint32_t d1, uint32_t d2, uint32_t d3)
+{
+    const uint32_t d[4] = {d0, d1, d2, d3};
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+    {
+        if constexpr (AF == OPURE_A_F16)
+            s = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, d[j]), __builtin_bit_cast(half2_t, 0x3C003C00u), s,
+                                       false);
+        else
+            s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, d[j]),
+                                                __builtin_bit_cast(bf16x2_t, 0x3F803F80u), s, false);
+    }
+    return s;
+}
+
+template <int AF>
+__device__ __forceinline__ uint32_t pack2(float a, float b)
+{
+    if constexpr (AF == OPURE_A_F16)
+        return f32_to_f16(a) | (static_cast<uint32_t>(f32_to_f16(b)) << 16);
+    else
+        return f32_to_bf16(a) | (static_cast<uint32_t>(f32_to_bf16(b)) << 16);
+}
+
+// 1 / rms of column m from the producer's per-16-column sums of squares, in
+// a fixed order (lanes g4 take tiles g4, g4+4, ...; then a 2-level butterfly)
+__device__ __forceinline__ float inv_rms(const KParams& p, uint32_t mc, uint32_t g4)
+{
+    float ssum = 0.0f;
+#pragma unroll 8
+    for (uint32_t t = g4; t < p.ss_tiles; t += 4u) ssum += p.ss_in[static_cast<uint64_t>(t) * p.M + mc];
+    ssum += __shfl_xor(ssum, 16);
+    ssum += __shfl_xor(ssum, 32);
+    return __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(ssum, static_cast<float>(p.in)), p.eps)));
+}
+
+// 8 consecutive activations of row m at k, as 8 fp32 words (AF f32) or 4
+// pairs; with NORM rmsnorm'd from the fp32 residual: round(x*inv*g)
+// (Opure_RMSNorm.usf:44-78)
+template <int AF, bool NORM>
+__device__ __forceinline__ void load8(const KParams& p, uint32_t m, uint32_t k, float inv, uint32_t (&o)[8])
+{
+    if constexpr (!NORM)
+    {
+        if constexpr (AF == OPURE_A_F32)
+        {
+            const u4_t* src = reinterpret_cast<const u4_t*>(p.x + (static_cast<uint64_t>(m) * p.in + k) * 4u);
+            const u4_t a = src[0], b = src[1];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) { o[e] = a[e]; o[4 + e] = b[e]; }
+        }
+        else
+        {
+            const u4_t a = *reinterpret_cast<const u4_t*>(p.x + (static_cast<uint64_t>(m) * p.in + k) * 2u);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o[e] = a[e];
+        }
+    }
+    else
+    {
+        const f4_t* xr = reinterpret_cast<const f4_t*>(reinterpret_cast<const float*>(p.x) + static_cast<uint64_t>(m) * p.in + k);
+        const f4_t* gr = reinterpret_cast<const f4_t*>(p.gain + k);
+        const f4_t x0 = xr[0], x1 = xr[1], g0 = gr[0], g1 = gr[1];
+        float yv[8];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+        {
+            yv[e] = __fmul_rn(__fmul_rn(x0[e], inv), g0[e]);
+            yv[4 + e] = __fmul_rn(__fmul_rn(x1[e], inv), g1[e]);
+        }
+        if constexpr (AF == OPURE_A_F32)
+        {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[e] = __float_as_uint(yv[e]);
+        }
+        else
+        {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) o[j] = pack2<AF>(yv[2 * j], yv[2 * j + 1]);
+        }
+    }
+}
+
+// Stage X rows 0..M-1 (whole K) into LDS rows of x_stride bytes, natural k
+// order; uint4 also writes each 128-k group's sum to xsum[m][g].  Threads take
+// 8-value units; the 16 units of a group sit in 16 aligned lanes of one wave.
+template <int WF, int AF, bool NORM, int NTH>
+__device__ __forceinline__ void stage_x(const KParams& p, uint8_t* lds, float inv_lane)
+{
+    constexpr uint32_t EB = AF == OPURE_A_F32 ? 4u : 2u;
+    const uint32_t n8 = p.in / 8u;
+    const uint32_t lane = threadIdx.x & 63u;
+    float* xsum = reinterpret_cast<float*>(lds + p.off_xsum);
+    for (uint32_t m = 0; m < p.M; ++m)
+    {
+        float inv = 1.0f;
+        if constexpr (NORM) inv = __shfl(inv_lane, static_cast<int>(m), 64);     // whole wave active here
+        uint8_t* row = lds + static_cast<uint64_t>(m) * p.x_stride;
+        for (uint32_t j = threadIdx.x; j < n8; j += NTH)
+        {
+            uint32_t o[8];
+            load8<AF, NORM>(p, m, 8u * j, inv, o);
+            uint8_t* dst = row + 8u * j * EB;
+            if constexpr (AF == OPURE_A_F32)
+            {
+                reinterpret_cast<u4_t*>(dst)[0] = u4_t{o[0], o[1], o[2], o[3]};
+                reinterpret_cast<u4_t*>(dst)[1] = u4_t{o[4], o[5], o[6], o[7]};
+            }
+            else
+            {
+                *reinterpret_cast<u4_t*>(dst) = u4_t{o[0], o[1], o[2], o[3]};
+                if constexpr (WF == OPURE_W_I4G128)
+                {
+                    // n8 and NTH are multiples of 16: a group's 16 lanes are all active
+                    float u = unit_sum<AF>(o[0], o[1], o[2], o[3]);
+                    u += __shfl_xor(u, 1);
+                    u += __shfl_xor(u, 2);
+                    u += __shfl_xor(u, 4);
+                    u += __shfl_xor(u, 8);
+                    if ((lane & 15u) == 0) xsum[m * (p.in / 128u) + j / 16u] = u;
+                }
+            }
+        }
+    }
+}
+
+// Epilogue of one tile: lane holds D rows 4*g4 + i of column m (v[i]).
+template <int WF, int EPI>
+__device__ __forceinline__ void epilogue(const KParams& p, uint32_t tile, uint32_t m, uint32_t g4, f4_t tot)
+{
+    const uint32_t M = p.M;
+    float v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+    {
+        v[i] = tot[i];
+        if constexpr (WF == OPURE_W_I8PC)
+            v[i] = __fmul_rn(v[i], f16_to_f32(static_cast<const uint16_t*>(p.sc)[tile * 16u + 4u * g4 + i]));
+    }
+    if constexpr (EPI == opure_hip::EPI_LOGITS)
+    {
+        // logits, then the best (value, lowest index) of this tile for column m
+        float bv = -__builtin_huge_valf();
+        int32_t bi = 0x7FFFFFFF;
+        if (m < M)
+        {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+            {
+                const uint32_t o = 16u * tile + 4u * g4 + i;
+                static_cast<float*>(p.y)[static_cast<uint64_t>(m) * p.out + o] = v[i];
+                const float c = v[i] != v[i] ? -__builtin_huge_valf() : v[i];
+                if (c > bv || (c == bv && static_cast<int32_t>(o) < bi)) { bv = c; bi = static_cast<int32_t>(o); }
+            }
+        }
+#pragma unroll
+        for (int off = 16; off <= 32; off <<= 1)
+        {
+            const float ov = __shfl_xor(bv, off);
+            const int32_t oi = __shfl_xor(bi, off);
+            if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+        }
+        if (m < M && g4 == 0)
+        {
+            p.lg.am_val[static_cast<uint64_t>(tile) * M + m] = bv;
+            p.lg.am_idx[static_cast<uint64_t>(tile) * M + m] = bi;
+        }
+        return;
+    }
+    if constexpr (EPI == opure_hip::EPI_RESIDUAL)
+    {
+        // x += y, and this tile's sum of squares of the new x for the next rmsnorm
+        float sq = 0.0f;
+        if (m < M)
+        {
+            float* y = static_cast<float*>(p.y) + static_cast<uint64_t>(m) * p.out + 16u * tile + 4u * g4;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+            {
+                const float nv = __fadd_rn(y[i], v[i]);
+                y[i] = nv;
+                sq = __fmaf_rn(nv, nv, sq);
+            }
+        }
+        sq += __shfl_xor(sq, 16);
+        sq += __shfl_xor(sq, 32);
+        if (p.ss_out && m < M && g4 == 0) p.ss_out[static_cast<uint64_t>(tile) * M + m] = sq;
+        return;
+    }
+    if (m >= M) return;
+    if constexpr (EPI == opure_hip::EPI_STORE)
+    {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            store_act_rt(p.y, static_cast<uint64_t>(m) * p.out + 16u * tile + 4u * g4 + i, v[i], p.yfmt);
+    }
+    else if constexpr (EPI == opure_hip::EPI_SWIGLU)
+    {
+        // tile rows alternate gate / up: (v0, v1) and (v2, v3) are (gate, up) pairs
+        const uint32_t F = p.out >> 1;
+        const uint32_t f = 8u * tile + 2u * g4;
+        store_act_rt(p.y, static_cast<uint64_t>(m) * F + f, swiglu(v[0], v[1]), p.yfmt);
+        store_act_rt(p.y, static_cast<uint64_t>(m) * F + f + 1u, swiglu(v[2], v[3]), p.yfmt);
+    }
+    else if constexpr (EPI == opure_hip::EPI_QKV)
+    {
+        const opure_hip::QkvEpilogue& e = p.qkv;
+        const uint32_t b = m / e.rows_per_seq, j = m - b * e.rows_per_seq;
+        const uint32_t pos = static_cast<uint32_t>(e.seq_len[b]) + j;
+        if (pos >= e.rope_max_pos || pos / OPURE_PAGE_SIZE >= e.max_pages) return;   // past the tables: drop
+        const uint32_t o0 = 16u * tile + 4u * g4;   // even; o0..o0+3 lie in one head
+        const uint32_t hd = e.head_dim, half = hd >> 1;
+        if (o0 < e.qdim + e.kvdim)
+        {
+            // rotate the two interleaved pairs (Opure_RoPE.usf:7-10)
+#pragma unroll
+            for (int pr = 0; pr < 2; ++pr)
+            {
+                const uint32_t o = o0 + 2u * pr;
+                const uint32_t d = (o < e.qdim ? o : o - e.qdim) % hd;
+                const float c = e.rope_cos[static_cast<uint64_t>(pos) * half + d / 2u];
+                const float s = e.rope_sin[static_cast<uint64_t>(pos) * half + d / 2u];
+                const float e0 = v[2 * pr], e1 = v[2 * pr + 1];
+                v[2 * pr] = __fsub_rn(__fmul_rn(e0, c), __fmul_rn(e1, s));
+                v[2 * pr + 1] = __fadd_rn(__fmul_rn(e0, s), __fmul_rn(e1, c));
+            }
+        }
+        if (o0 < e.qdim)
+        {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) store_act_rt(p.y, static_cast<uint64_t>(m) * e.qdim + o0 + i, v[i], p.yfmt);
+            return;
+        }
+        const uint32_t kvsel = o0 < e.qdim + e.kvdim ? 0u : 1u;
+        const uint32_t ok = o0 - e.qdim - kvsel * e.kvdim;
+        const uint32_t kh = ok / hd, d0 = ok - kh * hd;
+        const int32_t page = e.page_table[static_cast<uint64_t>(b) * e.max_pages + pos / OPURE_PAGE_SIZE];
+        if (page < 0 || static_cast<uint32_t>(page) >= e.n_pages) return;
+        const uint64_t base = ((((static_cast<uint64_t>(e.layer) * e.n_pages + static_cast<uint32_t>(page)) * 2u + kvsel) *
+                                e.n_kv_heads + kh) * OPURE_PAGE_SIZE + pos % OPURE_PAGE_SIZE) * hd + d0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) store_act_rt(e.kv_pool, base + i, v[i], p.yfmt);
+    }
+}
+
+template <int WF, int AF, int T, int U, bool STAGED>
+struct Payload {
+    u4_t w[T][U];
+    u4_t s[T][U];                                        // uint4 scales of the block (rows 4*g4..+3)
+    u4_t x[STAGED ? 1 : U][Fmt<WF>::N / 4u];             // direct X fragments
+};
+
+template <int WF, int AF, int EPI, int NW, int T, int U, bool NORM, bool STAGED>
+__global__ __launch_bounds__(NW * 64) void k_gemv(KParams p)
+{
+    constexpr uint32_t KB = Fmt<WF>::KB, N = Fmt<WF>::N;
+    constexpr uint32_t EB = AF == OPURE_A_F32 ? 4u : 2u;
+    constexpr uint32_t VALS = KB / 4u;                   // k values per lane per block
+    constexpr uint32_t PB = U * NW;                      // blocks per pass
+    static_assert(STAGED || !NORM, "the fused rmsnorm needs the staged X");
+    extern __shared__ __align__(16) uint8_t lds[];
+    f4_t* red = reinterpret_cast<f4_t*>(lds + p.off_red);
+    const float* xsum = reinterpret_cast<const float*>(lds + p.off_xsum);
+
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    const uint32_t g4 = lane >> 4, r16 = lane & 15u;
+    const uint32_t M = p.M;
+    const uint32_t mc = r16 < M ? r16 : M - 1u;         // columns >= M compute on a copy of column M-1
+    const uint32_t nblk = p.nblk;
+    const uint32_t npass = (nblk + PB - 1u) / PB;
+    const uint32_t G = p.in / 128u;
+    // groups of this workgroup: blockIdx.x, blockIdx.x + gridDim.x, ...  (grid <= groups)
+    const uint32_t S = (p.groups - blockIdx.x + gridDim.x - 1u) / gridDim.x * npass;
+
+    using PL = Payload<WF, AF, T, U, STAGED>;
+    auto load = [&](PL& b, uint32_t s) {
+        const uint32_t gi = s / npass, ps = s - gi * npass;
+        const uint32_t grp = blockIdx.x + gi * gridDim.x;
+#pragma unroll
+        for (int t = 0; t < T; ++t)
+        {
+            const uint32_t tile = min(grp * T + t, p.tiles - 1u);
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+            {
+                const uint32_t blk = min(ps * PB + u * NW + wave, nblk - 1u);
+                b.w[t][u] = __builtin_nontemporal_load(
+                    reinterpret_cast<const u4_t*>(p.w + ((static_cast<uint64_t>(tile) * nblk + blk) << 10) + (lane << 4)));
+                if constexpr (WF == OPURE_W_I4G128)
+                    b.s[t][u] = *reinterpret_cast<const u4_t*>(static_cast<const uint32_t*>(p.sc) +
+                                                               (static_cast<uint64_t>(tile) * G + blk) * 16u + 4u * g4);
+            }
+        }
+        if constexpr (!STAGED)
+        {
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+            {
+                const uint32_t blk = min(ps * PB + u * NW + wave, nblk - 1u);
+                const u4_t* src = reinterpret_cast<const u4_t*>(
+                    p.x + (static_cast<uint64_t>(mc) * p.in + blk * KB + VALS * g4) * EB);
+#pragma unroll
+                for (uint32_t i = 0; i < N / 4u; ++i) b.x[u][i] = src[i];
+            }
+        }
+    };
+
+    PL A, B;
+    load(A, 0);
+    if (S > 1u) load(B, 1);
+
+    float inv = 1.0f;
+    if constexpr (NORM) inv = inv_rms(p, mc, g4);
+    if constexpr (STAGED)
+    {
+        stage_x<WF, AF, NORM, NW * 64>(p, lds, inv);
+        __syncthreads();
+    }
+
+    f4_t acc[T];
+    auto run = [&](const PL& b, uint32_t s) {
+        const uint32_t gi = s / npass, ps = s - gi * npass;
+        if (ps == 0)
+        {
+#pragma unroll
+            for (int t = 0; t < T; ++t) acc[t] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+        {
+            const uint32_t blk = ps * PB + u * NW + wave;
+            if (blk >= nblk) continue;
+            uint32_t xd[N];
+            float xs = 0.0f;
+            if constexpr (STAGED)
+            {
+                const u4_t* src = reinterpret_cast<const u4_t*>(lds + mc * p.x_stride + (blk * KB + VALS * g4) * EB);
+#pragma unroll
+                for (uint32_t i = 0; i < N / 4u; ++i)
+                {
+                    const u4_t v = src[i];
+                    xd[4 * i] = v[0]; xd[4 * i + 1] = v[1]; xd[4 * i + 2] = v[2]; xd[4 * i + 3] = v[3];
+                }
+                if constexpr (WF == OPURE_W_I4G128) xs = xsum[mc * G + blk];
+            }
+            else
+            {
+#pragma unroll
+                for (uint32_t i = 0; i < N / 4u; ++i)
+                {
+                    xd[4 * i] = b.x[u][i][0]; xd[4 * i + 1] = b.x[u][i][1];
+                    xd[4 * i + 2] = b.x[u][i][2]; xd[4 * i + 3] = b.x[u][i][3];
+                }
+                if constexpr (WF == OPURE_W_I4G128)
+                {
+                    // the same sum tree as the staged group sums
+                    const float u0 = unit_sum<AF>(xd[0], xd[1], xd[2], xd[3]);
+                    const float u1 = unit_sum<AF>(xd[4], xd[5], xd[6], xd[7]);
+                    const float u2 = unit_sum<AF>(xd[8], xd[9], xd[10], xd[11]);
+                    const float u3 = unit_sum<AF>(xd[12], xd[13], xd[14], xd[15]);
+                    xs = (u0 + u1) + (u2 + u3);
+                    xs += __shfl_xor(xs, 16);
+                    xs += __shfl_xor(xs, 32);
+                }
+            }
+            if constexpr (WF == OPURE_W_F32)
+            {
+#pragma unroll
+                for (int t = 0; t < T; ++t)
+                {
+                    const f4_t wf = __builtin_bit_cast(f4_t, b.w[t][u]);
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+                        acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(wf[q], __uint_as_float(xd[q]), acc[t], 0, 0, 0);
+                }
+            }
+            else if constexpr (WF == OPURE_W_I8PC)
+            {
+                const half8_t b1 = as_half8(xd[0], xd[1], xd[2], xd[3]);
+                const half8_t b2 = as_half8(xd[4], xd[5], xd[6], xd[7]);
+#pragma unroll
+                for (int t = 0; t < T; ++t)
+                {
+                    uint32_t a[8];
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) u8x4_to_f16(b.w[t][u][j], a[2 * j], a[2 * j + 1]);
+                    acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(a[0], a[1], a[2], a[3]), b1, acc[t], 0, 0, 0);
+                    acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(a[4], a[5], a[6], a[7]), b2, acc[t], 0, 0, 0);
+                }
+            }
+            else
+            {
+                // one 128-k group per block: a fresh accumulator per tile, then
+                // acc += s * (bacc - (z + off) * xs), off = 128 for bf16 (MAGIC)
+                const float xoff = AF == OPURE_A_BF16 ? __fmul_rn(xs, 128.0f) : 0.0f;
+#pragma unroll
+                for (int t = 0; t < T; ++t)
+                {
+                    f4_t bacc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                    {
+                        uint32_t a[4];
+                        u4x8_pairs<AF>(b.w[t][u][j], a);
+                        if constexpr (AF == OPURE_A_F16)
+                            bacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                                as_half8(a[0], a[1], a[2], a[3]),
+                                as_half8(xd[4 * j], xd[4 * j + 1], xd[4 * j + 2], xd[4 * j + 3]), bacc, 0, 0, 0);
+                        else
+                            bacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                                as_bf8(a[0], a[1], a[2], a[3]),
+                                as_bf8(xd[4 * j], xd[4 * j + 1], xd[4 * j + 2], xd[4 * j + 3]), bacc, 0, 0, 0);
+                    }
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                    {
+                        const uint32_t sz = b.s[t][u][i];
+                        const float sc = __uint_as_float(sz << 16), z = __uint_as_float(sz & 0xFFFF0000u);
+                        const float yv = __fmaf_rn(-z, xs, __fsub_rn(bacc[i], xoff));
+                        acc[t][i] = __fmaf_rn(sc, yv, acc[t][i]);
+                    }
+                }
+            }
+        }
+        if (ps + 1u == npass)
+        {
+            // combine the waves' K slices in wave order; wave t finishes tile t
+            const uint32_t grp = blockIdx.x + gi * gridDim.x;
+            __syncthreads();                               // the previous group's sums are read
+#pragma unroll
+            for (int t = 0; t < T; ++t) red[(wave * T + t) * 64u + lane] = acc[t];
+            __syncthreads();
+            const uint32_t tile = grp * T + wave;
+            if (wave < static_cast<uint32_t>(T) && tile < p.tiles)
+            {
+                f4_t tot = red[wave * 64u + lane];
+#pragma unroll
+                for (int w = 1; w < NW; ++w) tot += red[(w * T + wave) * 64u + lane];
+                epilogue<WF, EPI>(p, tile, r16, g4, tot);
+            }
+        }
+    };
+
+    // software pipeline over the steps (group, pass): step s computes while
+    // s+1 is in flight.  Loads are issued only for steps that exist, on
+    // straight-line paths, so each wait covers exactly the buffer consumed.
+    uint32_t s = 0;
+    while (S - s >= 4u)
+    {
+        run(A, s);
+        load(A, s + 2u);
+        run(B, s + 1u);
+        load(B, s + 3u);
+        s += 2u;
+    }
+    const uint32_t rest = S - s;
+    if (rest == 3u)
+    {
+        run(A, s);
+        load(A, s + 2u);
+        run(B, s + 1u);
+        run(A, s + 2u);
+    }
+    else if (rest == 2u)
+    {
+        run(A, s);
+        run(B, s + 1u);
+    }
+    else if (rest == 1u)
+    {
+        run(A, s);
+    }
+}
+
+// Launch one instantiation.  grid = workgroups; lds = dynamic LDS bytes.
+template <int WF, int AF, int EPI, int NW, int T, int U, bool NORM, bool STAGED>
+int launch(opure_dev* dev, const KParams& kp, uint32_t grid, uint32_t lds)
+{
+    static bool configured = false;
+    if (!configured)
+    {
+        OPURE_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemv<WF, AF, EPI, NW, T, U, NORM, STAGED>),
+                                          hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+        configured = true;
+    }
+    hipLaunchKernelGGL((k_gemv<WF, AF, EPI, NW, T, U, NORM, STAGED>), dim3(grid), dim3(NW * 64), lds, dev->stream, kp);
+    OPURE_LAUNCH_CHECK("k_gemv");
+    return OPURE_OK;
+}
+
+// The shape recipes the host chooses from (waves, tiles per workgroup, blocks
+// per wave per pass of the staged kernel)
+struct Recipe { uint32_t nw, t, u; };
+constexpr Recipe R_WIDE{4, 2, 2};     // many tiles: persistent, 2 tiles share X
+constexpr Recipe R_MID{8, 1, 2};
+constexpr Recipe R_NARROW{16, 1, 2};  // few tiles: 16 waves split K
+
+// Blocks go to waves by index (wave w takes w, w+NW, ...) whatever U is, so
+// U may differ between the staged and direct kernels of a recipe without
+// changing any sum; direct 16-wave kernels carry X fragments and keep U = 1
+// to stay within 128 VGPRs.
+template <int WF, int AF, int EPI, bool NORM, bool STAGED>
+int launch_recipe(opure_dev* dev, const KParams& kp, const Recipe& r, uint32_t grid, uint32_t lds)
+{
+    if (r.nw == 4) return launch<WF, AF, EPI, 4, 2, 2, NORM, STAGED>(dev, kp, grid, lds);
+    if (r.nw == 8) return launch<WF, AF, EPI, 8, 1, 2, NORM, STAGED>(dev, kp, grid, lds);
+    return launch<WF, AF, EPI, 16, 1, STAGED ? 2 : 1, NORM, STAGED>(dev, kp, grid, lds);
+}
+
+// every (epilogue, norm, staged) combination the host may ask for
+template <int WF, int AF>
+int launch_format(opure_dev* dev, uint32_t epi, bool norm, bool staged, const KParams& kp, const Recipe& r,
+                  uint32_t grid, uint32_t lds)
+{
+    using namespace opure_hip;
+    if (norm)
+    {
+        switch (epi)
+        {
+        case EPI_SWIGLU: return launch_recipe<WF, AF, EPI_SWIGLU, true, true>(dev, kp, r, grid, lds);
+        case EPI_QKV: return launch_recipe<WF, AF, EPI_QKV, true, true>(dev, kp, r, grid, lds);
+        case EPI_LOGITS: return launch_recipe<WF, AF, EPI_LOGITS, true, true>(dev, kp, r, grid, lds);
+        }
+    }
+    else if (staged)
+    {
+        switch (epi)
+        {
+        case EPI_STORE: return launch_recipe<WF, AF, EPI_STORE, false, true>(dev, kp, r, grid, lds);
+        case EPI_RESIDUAL: return launch_recipe<WF, AF, EPI_RESIDUAL, false, true>(dev, kp, r, grid, lds);
+        case EPI_SWIGLU: return launch_recipe<WF, AF, EPI_SWIGLU, false, true>(dev, kp, r, grid, lds);
+        }
+    }
+    else
+    {
+        switch (epi)
+        {
+        case EPI_STORE: return launch_recipe<WF, AF, EPI_STORE, false, false>(dev, kp, r, grid, lds);
+        case EPI_RESIDUAL: return launch_recipe<WF, AF, EPI_RESIDUAL, false, false>(dev, kp, r, grid, lds);
+        case EPI_SWIGLU: return launch_recipe<WF, AF, EPI_SWIGLU, false, false>(dev, kp, r, grid, lds);
+        case EPI_QKV: return launch_recipe<WF, AF, EPI_QKV, false, false>(dev, kp, r, grid, lds);
+        case EPI_LOGITS: return launch_recipe<WF, AF, EPI_LOGITS, false, false>(dev, kp, r, grid, lds);
+        }
+    }
+    return set_error(OPURE_E_INVALID, "gemv: epilogue %u (norm %d, staged %d) is not built", epi, norm, staged);
+}
+
+}  // namespace opure_gemv

@@ -112,20 +112,17 @@ struct GemvCall {
     uint32_t ss_tiles = 0;
     // EPI_RESIDUAL: where to write the new residual's per-tile sums of squares
     float* ss_out = nullptr;
+    // fused rmsnorm whose X does not fit in LDS: [M][in] activations, written
+    // by a normalisation pre-pass that the GEMV then reads
+    void* xn_scratch = nullptr;
     QkvEpilogue qkv{};
     LogitsEpilogue logits{};
 };
 
-struct GemvShape {
-    uint32_t tiles = 0;     // 16-row output tiles
-    uint32_t blocks = 0;    // 64-byte blocks per weight row
-    uint32_t t = 0;         // tiles per workgroup
-    uint32_t nw = 0;        // waves per workgroup splitting K
-};
-
-GemvShape gemv_shape(uint32_t wfmt, uint32_t out, uint32_t in);
-int       gemv_validate(const GemvCall& c);
-int       gemv_launch(opure_dev* dev, const GemvCall& c);
+int gemv_validate(const GemvCall& c);
+int gemv_launch(opure_dev* dev, const GemvCall& c);
+// device-side tiled-layout helpers shared with the embedding gather
+uint32_t tiled_block_k(uint32_t wfmt);      // k values per 64-byte block
 
 // ---- attention (attention.hip) ---------------------------------------------
 uint32_t attn_chunk(uint32_t head_dim);

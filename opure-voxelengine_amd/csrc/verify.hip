@@ -29,17 +29,44 @@ using namespace opure_dev_math;
 
 namespace {
 
+// Element i of row `row` of a tiled linear (opure_tile_linear layout),
+// dequantised.  Tile t = row / 16 holds the row as lane r = row % 16 of its
+// 1 KB blocks.
+__device__ __forceinline__ float tiled_elem(const opure_linear& E, uint32_t wfmt, uint32_t row, uint32_t i, uint32_t nblk,
+                                            uint32_t KB)
+{
+    const uint32_t t = row >> 4, r = row & 15u;
+    const uint32_t b = i / KB, k = i - b * KB;
+    const uint32_t vals = KB / 4u, g = k / vals, kk = k - g * vals;
+    const uint8_t* piece = static_cast<const uint8_t*>(E.w) + ((static_cast<uint64_t>(t) * nblk + b) << 10) +
+                           ((16u * g + r) << 4);
+    if (wfmt == OPURE_W_F32) return reinterpret_cast<const float*>(piece)[kk];
+    if (wfmt == OPURE_W_I8PC)
+    {
+        const int8_t q = static_cast<int8_t>(piece[kk] ^ 0x80u);
+        return __fmul_rn(static_cast<float>(q), f16_to_f32(static_cast<const uint16_t*>(E.scale)[t * 16u + r]));
+    }
+    // uint4: element e of word kk/8 sits at nibble {0,4,1,5,2,6,3,7}[e]
+    const uint32_t word = reinterpret_cast<const uint32_t*>(piece)[kk >> 3];
+    const uint32_t e = kk & 7u;
+    const uint32_t pos = (e >> 1) | ((e & 1u) << 2);
+    const uint32_t q = (word >> (4u * pos)) & 0x0Fu;
+    const uint32_t sz = static_cast<const uint32_t*>(E.scale)[(static_cast<uint64_t>(t) * nblk + b) * 16u + r];
+    const float s = __uint_as_float(sz << 16), z = __uint_as_float(sz & 0xFFFF0000u);
+    return __fmul_rn(s, __fsub_rn(static_cast<float>(q), z));
+}
+
 // Dequantised embedding rows into the fp32 residual, plus each 16-column
 // tile's sum of squares for the first layer's fused RMSNorm.  One thread per
 // 16-column tile.
 __global__ __launch_bounds__(256) void k_embed(const int32_t* tokens, opure_linear E, uint32_t wfmt, uint32_t h,
-                                               uint32_t vocab, uint32_t M, float* x, float* ss)
+                                               uint32_t vocab, uint32_t M, uint32_t KB, float* x, float* ss)
 {
     const uint32_t r = blockIdx.x;
     const int32_t t = tokens[r];
     float* xr = x + static_cast<uint64_t>(r) * h;
     const bool bad = t < 0 || static_cast<uint32_t>(t) >= vocab;
-    const uint64_t base = bad ? 0u : static_cast<uint64_t>(t) * h;
+    const uint32_t nblk = h / KB;
     for (uint32_t tile = threadIdx.x; tile < h / 16u; tile += 256u)
     {
         float sq = 0.0f;
@@ -47,21 +74,8 @@ __global__ __launch_bounds__(256) void k_embed(const int32_t* tokens, opure_line
         for (uint32_t j = 0; j < 16u; ++j)
         {
             const uint32_t i = 16u * tile + j;
-            float v;
             // an id outside the vocabulary poisons its row instead of reading out of bounds
-            if (bad) v = __builtin_nanf("");
-            else if (wfmt == OPURE_W_F32) v = static_cast<const float*>(E.w)[base + i];
-            else if (wfmt == OPURE_W_I8PC)
-                v = __fmul_rn(static_cast<float>(static_cast<const int8_t*>(E.w)[base + i]),
-                              f16_to_f32(static_cast<const uint16_t*>(E.scale)[t]));
-            else
-            {
-                const uint8_t byte = static_cast<const uint8_t*>(E.w)[(base + i) >> 1];
-                const uint32_t q = ((base + i) & 1u) ? (byte & 0x0Fu) : (byte >> 4);
-                const uint64_t g = static_cast<uint64_t>(t) * (h / 128u) + i / 128u;
-                v = __fmul_rn(bf16_to_f32(static_cast<const uint16_t*>(E.scale)[g]),
-                              __fsub_rn(static_cast<float>(q), bf16_to_f32(static_cast<const uint16_t*>(E.zero)[g])));
-            }
+            const float v = bad ? __builtin_nanf("") : tiled_elem(E, wfmt, static_cast<uint32_t>(t), i, nblk, KB);
             xr[i] = v;
             sq = __fmaf_rn(v, v, sq);
         }
@@ -74,7 +88,7 @@ __global__ __launch_bounds__(256) void k_embed(const int32_t* tokens, opure_line
 namespace opure_hip {
 
 struct VerifyPlan {
-    uint64_t x = 0, ss = 0, q = 0, att = 0, h = 0, am_val = 0, am_idx = 0, attn = 0, rej = 0, total = 0;
+    uint64_t x = 0, ss = 0, xn = 0, q = 0, att = 0, h = 0, am_val = 0, am_idx = 0, attn = 0, rej = 0, total = 0;
     uint64_t counters = 0;
     uint32_t lm_tiles = 0;
 };
@@ -89,6 +103,7 @@ static VerifyPlan make_plan(const opure_model* m, uint32_t B, uint32_t R, uint32
     auto take = [&](uint64_t bytes) { const uint64_t o = off; off += align_up(bytes ? bytes : 1, 256); return o; };
     p.x = take(MR * m->hidden * 4u);
     p.ss = take(MR * (m->hidden / 16u) * 4u);
+    p.xn = take(MR * m->hidden * eb);
     p.q = take(MR * qdim * eb);
     p.att = take(MR * qdim * eb);
     p.h = take(MR * m->ffn * eb);
@@ -102,12 +117,14 @@ static VerifyPlan make_plan(const opure_model* m, uint32_t B, uint32_t R, uint32
     return p;
 }
 
-static int check_linear(const opure_linear& L, uint32_t out, uint32_t in, const char* what, uint32_t wfmt)
+static int check_linear(const opure_linear& L, uint32_t out, uint32_t in, const char* what, uint32_t wfmt,
+                        uint32_t layout = OPURE_LAYOUT_TILED)
 {
     OPURE_REQUIRE(L.w && L.out == out && L.in == in, OPURE_E_INVALID, "verify: %s is %ux%u (w=%p), expected %ux%u", what,
                   L.out, L.in, L.w, out, in);
-    if (wfmt == OPURE_W_I8PC) OPURE_REQUIRE(L.scale, OPURE_E_INVALID, "verify: %s has no scales", what);
-    if (wfmt == OPURE_W_I4G128) OPURE_REQUIRE(L.scale && L.zero, OPURE_E_INVALID, "verify: %s has no scale/zero", what);
+    OPURE_REQUIRE(L.layout == layout, OPURE_E_INVALID, "verify: %s must be in layout %u (opure_tile_linear), got %u",
+                  what, layout, L.layout);
+    if (wfmt != OPURE_W_F32) OPURE_REQUIRE(L.scale, OPURE_E_INVALID, "verify: %s has no scales", what);
     return OPURE_OK;
 }
 
@@ -137,7 +154,8 @@ static int check_model(const opure_model* m, const opure_kv* kv, uint32_t B, uin
         OPURE_REQUIRE(W.attn_norm && W.mlp_norm, OPURE_E_INVALID, "verify: layer %u norm gains missing", L);
         if ((rc = check_linear(W.qkv, qdim + 2u * kvdim, m->hidden, "qkv", m->wfmt))) return rc;
         if ((rc = check_linear(W.o, m->hidden, qdim, "o_proj", m->wfmt))) return rc;
-        if ((rc = check_linear(W.gate_up, 2u * m->ffn, m->hidden, "gate_up", m->wfmt))) return rc;
+        if ((rc = check_linear(W.gate_up, 2u * m->ffn, m->hidden, "gate_up", m->wfmt, OPURE_LAYOUT_TILED_SWIGLU)))
+            return rc;
         if ((rc = check_linear(W.down, m->hidden, m->ffn, "down", m->wfmt))) return rc;
     }
     return OPURE_OK;
@@ -214,7 +232,7 @@ int opure_verify_step(opure_dev* dev, const opure_verify_args* a)
 
     if ((rc = prof_begin(dev, OPURE_STAGE_EMBED))) return rc;
     hipLaunchKernelGGL(k_embed, dim3(MR), dim3(256), 0, dev->stream, a->tokens, m->embed, m->wfmt, m->hidden, m->vocab,
-                       MR, x, ss);
+                       MR, tiled_block_k(m->wfmt), x, ss);
     OPURE_LAUNCH_CHECK("k_embed");
     if ((rc = prof_end(dev))) return rc;
 
@@ -227,6 +245,7 @@ int opure_verify_step(opure_dev* dev, const opure_verify_args* a)
     c.M = MR;
     c.eps = m->rms_eps;
     c.ss_tiles = m->hidden / 16u;
+    c.xn_scratch = ws + P.xn;
     for (uint32_t L = 0; L < m->n_layers; ++L)
     {
         const opure_layer_weights& W = m->layers[L];

@@ -31,9 +31,12 @@ class OpureError(RuntimeError):
         self.code = code
 
 
+LAYOUT_ROWMAJOR, LAYOUT_TILED, LAYOUT_TILED_SWIGLU = 0, 1, 2
+
+
 class Linear(C.Structure):
     _fields_ = [("w", C.c_void_p), ("scale", C.c_void_p), ("zero", C.c_void_p),
-                ("out", C.c_uint32), ("in_", C.c_uint32)]
+                ("out", C.c_uint32), ("in_", C.c_uint32), ("layout", C.c_uint32)]
 
 
 class LayerWeights(C.Structure):
@@ -140,6 +143,8 @@ def _declare(L):
         "opure_verify_step": ([vp, C.POINTER(VerifyArgs)], i),
         "opure_debug_workspace": ([vp, C.POINTER(vp), C.POINTER(u64)], i),
         "opure_debug_verify_offsets": ([C.POINTER(Model), u32, u32, u32, C.POINTER(u64)], i),
+        "opure_tiled_bytes": ([u32, u32, u32, C.POINTER(u64), C.POINTER(u64)], i),
+        "opure_tile_linear": ([vp, u32, u32, C.POINTER(Linear), vp, vp, C.POINTER(Linear)], i),
         "opure_profile_enable": ([vp, C.c_int], i),
         "opure_profile_read": ([vp, C.POINTER(u32), C.POINTER(C.c_double)], i),
         "opure_synth_normal_f32": ([vp, vp, u64, u64, u32, f32, f32], i),
@@ -236,6 +241,16 @@ class Dev:
         check(lib().opure_timer_ms(self.h, C.byref(ms)))
         return float(ms.value)
 
+    def tile(self, wfmt: int, src: "Linear", layout: int = LAYOUT_TILED):
+        """Tiled copy of a row-major device linear: (Linear, [buffers to keep alive])."""
+        wb, sb = C.c_uint64(), C.c_uint64()
+        check(lib().opure_tiled_bytes(wfmt, src.out, src.in_, C.byref(wb), C.byref(sb)))
+        w = self.alloc(wb.value)
+        s = self.alloc(sb.value) if sb.value else None
+        dst = Linear()
+        check(lib().opure_tile_linear(self.h, wfmt, layout, C.byref(src), int(w), int(s) if s else None, C.byref(dst)))
+        return dst, [w, s]
+
     def profile(self, on: bool):
         check(lib().opure_profile_enable(self.h, 1 if on else 0))
 
@@ -298,15 +313,22 @@ class DeviceModel:
                 self._cache[k] = (a, dev.upload(a))
             return self._cache[k][1]
 
-        def lin(d):
-            return Linear(int(up(d["w"])), int(up(d.get("scale"))) if d.get("scale") is not None else None,
-                          int(up(d.get("zero"))) if d.get("zero") is not None else None, d["out"], d["in"])
+        self._tiled = {}
+
+        def lin(d, layout=LAYOUT_TILED):
+            k = (id(d), layout)
+            if k not in self._tiled:
+                rm = Linear(int(up(d["w"])), int(up(d.get("scale"))) if d.get("scale") is not None else None,
+                            int(up(d.get("zero"))) if d.get("zero") is not None else None, d["out"], d["in"],
+                            LAYOUT_ROWMAJOR)
+                self._tiled[k] = dev.tile(cfg["wfmt"], rm, layout)
+            return self._tiled[k][0]
 
         n = cfg["n_layers"]
         self._layers = (LayerWeights * n)()
         for i, L in enumerate(weights["layers"]):
             self._layers[i] = LayerWeights(int(up(L["attn_norm"])), int(up(L["mlp_norm"])), lin(L["qkv"]),
-                                           lin(L["o"]), lin(L["gate_up"]), lin(L["down"]))
+                                           lin(L["o"]), lin(L["gate_up"], LAYOUT_TILED_SWIGLU), lin(L["down"]))
         self.rope_cos = up(weights["rope_cos"])
         self.rope_sin = up(weights["rope_sin"])
         self.desc = Model(n, cfg["hidden"], cfg["n_heads"], cfg["n_kv_heads"], cfg["head_dim"], cfg["ffn"],
@@ -345,7 +367,16 @@ class DeviceKV:
 
 
 def gemv(dev: Dev, wfmt: int, lin: Linear, x, y, M: int, xfmt: int, yfmt: int, epilogue: int) -> None:
+    """One batched GEMV; a row-major `lin` is tiled first (into temporaries)."""
+    keep = None
+    if lin.layout == LAYOUT_ROWMAJOR and lin.w:
+        lin, keep = dev.tile(wfmt, lin, LAYOUT_TILED_SWIGLU if epilogue == EPI_SWIGLU else LAYOUT_TILED)
     a = GemvArgs(lin, int(x), int(y), M, xfmt, yfmt, epilogue)
     fn = {W_F32: lib().opure_gemv_batched_f32, W_I8PC: lib().opure_gemv_batched_i8pc,
           W_I4G128: lib().opure_gemv_batched_i4g128}[wfmt]
     check(fn(dev.h, C.byref(a)))
+    if keep is not None:
+        dev.sync()
+        for b in keep:
+            if b is not None:
+                b.free()

@@ -75,7 +75,8 @@ class SynthModel:
         for L in range(c["n_layers"]):
             d = {"attn_norm": self._ones(h), "mlp_norm": self._ones(h)}
             for j, name in enumerate(("qkv", "o", "gate_up", "down")):
-                d[name] = self._linear(*self.shapes[name], 2 + 4 * L + j)
+                d[name] = self._linear(*self.shapes[name], 2 + 4 * L + j,
+                                       H.LAYOUT_TILED_SWIGLU if name == "gate_up" else H.LAYOUT_TILED)
             self.layers.append(d)
         self.final_norm = self._ones(h)
         cos, sin = H.rope_table(c["theta"], hd, max_pos, H.ROPE_GPU)
@@ -92,26 +93,36 @@ class SynthModel:
         self.dev.fill_u32(b, 0x3F800000, n)
         return b
 
-    def _linear(self, out, inn, tid):
+    def _linear(self, out, inn, tid, layout=H.LAYOUT_TILED):
+        """Seeded weights, quantised on the device in the row-major interchange
+        layout (kept for downloads), plus the tiled copy the kernels read."""
         dev, w = self.dev, self.cfg["wfmt"]
         L = H.lib()
         if w == H.W_F32:
             wb = dev.alloc(out * inn * 4)
             H.check(L.opure_synth_normal_f32(dev.h, int(wb), out * inn, self.seed, tid, 0.02, 0.0))
-            return {"w": wb, "scale": None, "zero": None, "out": out, "in": inn}
-        H.check(L.opure_synth_normal_f32(dev.h, int(self._tmp), out * inn, self.seed, tid, 0.02, 0.0))
-        if w == H.W_I8PC:
-            q, s = dev.alloc(out * inn), dev.alloc(out * 2)
-            H.check(L.opure_quantize_i8pc(dev.h, int(self._tmp), out, inn, int(q), int(s)))
-            return {"w": q, "scale": s, "zero": None, "out": out, "in": inn}
-        q, s, z = dev.alloc(out * inn // 2), dev.alloc(out * (inn // 128) * 2), dev.alloc(out * (inn // 128) * 2)
-        H.check(L.opure_quantize_i4g128(dev.h, int(self._tmp), out, inn, int(q), int(s), int(z)))
-        return {"w": q, "scale": s, "zero": z, "out": out, "in": inn}
+            d = {"w": wb, "scale": None, "zero": None, "out": out, "in": inn}
+        else:
+            H.check(L.opure_synth_normal_f32(dev.h, int(self._tmp), out * inn, self.seed, tid, 0.02, 0.0))
+            if w == H.W_I8PC:
+                q, s = dev.alloc(out * inn), dev.alloc(out * 2)
+                H.check(L.opure_quantize_i8pc(dev.h, int(self._tmp), out, inn, int(q), int(s)))
+                d = {"w": q, "scale": s, "zero": None, "out": out, "in": inn}
+            else:
+                q, s, z = dev.alloc(out * inn // 2), dev.alloc(out * (inn // 128) * 2), dev.alloc(out * (inn // 128) * 2)
+                H.check(L.opure_quantize_i4g128(dev.h, int(self._tmp), out, inn, int(q), int(s), int(z)))
+                d = {"w": q, "scale": s, "zero": z, "out": out, "in": inn}
+        d["tiled"], d["tiled_bufs"] = dev.tile(w, self._rowmajor(d), layout)
+        return d
+
+    @staticmethod
+    def _rowmajor(d):
+        return H.Linear(int(d["w"]), int(d["scale"]) if d["scale"] else None, int(d["zero"]) if d["zero"] else None,
+                        d["out"], d["in"], H.LAYOUT_ROWMAJOR)
 
     @staticmethod
     def _lin(d):
-        return H.Linear(int(d["w"]), int(d["scale"]) if d["scale"] else None, int(d["zero"]) if d["zero"] else None,
-                        d["out"], d["in"])
+        return d["tiled"]
 
     def _desc(self):
         c = self.cfg

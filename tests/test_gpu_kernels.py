@@ -54,6 +54,65 @@ def dev_linear(dev, lin):
     return H.Linear(int(w), int(s) if s else None, int(z) if z else None, lin["out"], lin["in"]), (w, s, z)
 
 
+def np_tiled(wfmt, lin, layout):
+    """numpy restatement of the tiled layout (opure_tile_linear): weight bytes
+    and scale words, from the row-major linear."""
+    out, inn = lin["out"], lin["in"]
+    tiles = out // 16
+    t, r = np.divmod(np.arange(out), 16)
+    if layout == H.LAYOUT_TILED_SWIGLU:
+        perm = np.where(r % 2 == 1, out // 2 + 8 * t + r // 2, 8 * t + r // 2)
+    else:
+        perm = np.arange(out)
+    wb = np.ascontiguousarray(lin["w"]).view(np.uint8).reshape(out, -1)[perm]
+    if wfmt == H.W_I8PC:
+        wb = wb ^ np.uint8(0x80)
+    elif wfmt == H.W_I4G128:
+        d = np.ascontiguousarray(wb).view(np.uint32)
+        o = np.zeros_like(d)
+        for e, pos in enumerate((0, 4, 1, 5, 2, 6, 3, 7)):
+            byte = (d >> np.uint32(8 * (e // 2))) & np.uint32(0xFF)
+            q = (byte & np.uint32(0xF)) if e % 2 else (byte >> np.uint32(4))
+            o |= q << np.uint32(4 * pos)
+        wb = o.view(np.uint8).reshape(out, -1)
+    nblk = wb.shape[1] // 64
+    tiled = wb.reshape(tiles, 16, nblk, 4, 16).transpose(0, 2, 3, 1, 4).reshape(-1)
+    if wfmt == H.W_F32:
+        return tiled, None
+    if wfmt == H.W_I8PC:
+        return tiled, lin["scale"][perm]
+    G = inn // 128
+    sc = lin["scale"][perm].reshape(tiles, 16, G).transpose(0, 2, 1).astype(np.uint32)
+    zr = lin["zero"][perm].reshape(tiles, 16, G).transpose(0, 2, 1).astype(np.uint32)
+    return tiled, (sc | (zr << np.uint32(16))).reshape(-1)
+
+
+@pytest.mark.parametrize("wfmt", [H.W_F32, H.W_I8PC, H.W_I4G128])
+@pytest.mark.parametrize("layout", [H.LAYOUT_TILED, H.LAYOUT_TILED_SWIGLU])
+def test_tile_linear_layout(dev, wfmt, layout):
+    rng = np.random.default_rng(11 + wfmt + 3 * layout)
+    out, inn = 64, 256
+    if wfmt == H.W_F32:
+        lin = {"w": rng.standard_normal((out, inn)).astype(np.float32), "out": out, "in": inn}
+    elif wfmt == H.W_I8PC:
+        lin = {"w": rng.integers(-128, 128, (out, inn), dtype=np.int8),
+               "scale": rng.integers(0, 65536, out, dtype=np.uint16), "out": out, "in": inn}
+    else:
+        lin = {"w": rng.integers(0, 256, (out, inn // 2), dtype=np.uint8),
+               "scale": rng.integers(0, 65536, (out, inn // 128), dtype=np.uint16),
+               "zero": rng.integers(0, 65536, (out, inn // 128), dtype=np.uint16), "out": out, "in": inn}
+    desc, keep = dev_linear(dev, lin)
+    tiled, bufs = dev.tile(wfmt, desc, layout)
+    dev.sync()
+    assert tiled.layout == layout and tiled.out == out and tiled.in_ == inn
+    want_w, want_s = np_tiled(wfmt, lin, layout)
+    got_w = dev.download(bufs[0], np.uint8, want_w.shape)
+    assert np.array_equal(got_w, want_w)
+    if want_s is not None:
+        got_s = dev.download(bufs[1], want_s.dtype, want_s.shape)
+        assert np.array_equal(got_s, want_s)
+
+
 def run_gemv(dev, wfmt, lin_desc, x_bits, M, xfmt, yfmt, epi, y_init=None):
     out = lin_desc.out // 2 if epi == H.EPI_SWIGLU else lin_desc.out
     eb = 4 if yfmt == H.A_F32 else 2
@@ -154,19 +213,28 @@ def test_gemv_known_answer_fixtures(dev):
 
 
 def test_gemv_rejects_bad_shapes(dev):
+    # 24 rows are not a whole number of 16-row tiles: tiling refuses them
     lin = {"w": np.zeros((24, 128), np.float32), "out": 24, "in": 128}
     desc, keep = dev_linear(dev, lin)
-    x = dev.upload(np.zeros((1, 128), np.float32))
-    y = dev.alloc(24 * 4)
+    x = dev.upload(np.zeros((17, 128), np.float32))
+    y = dev.alloc(17 * 32 * 4)
     with pytest.raises(H.OpureError) as e:
         H.gemv(dev, H.W_F32, desc, x, y, 1, H.A_F32, H.A_F32, H.EPI_STORE)
     assert e.value.code == H.E_INVALID
+    lin = {"w": np.zeros((32, 128), np.float32), "out": 32, "in": 128}
+    desc, keep = dev_linear(dev, lin)
     with pytest.raises(H.OpureError) as e:
         H.gemv(dev, H.W_F32, desc, x, y, 17, H.A_F32, H.A_F32, H.EPI_STORE)
     assert e.value.code == H.E_CAPACITY
     with pytest.raises(H.OpureError) as e:
         H.gemv(dev, H.W_I8PC, desc, x, y, 1, H.A_F32, H.A_F32, H.EPI_STORE)
-    assert e.value.code == H.E_UNSUPPORTED
+    assert e.value.code in (H.E_UNSUPPORTED, H.E_INVALID)
+    # a row-major linear handed straight to the kernel entry point is refused
+    tiled, bufs = dev.tile(H.W_F32, desc)
+    a = H.GemvArgs(desc, int(x), int(y), 1, H.A_F32, H.A_F32, H.EPI_STORE)
+    assert H.lib().opure_gemv_batched_f32(dev.h, C.byref(a)) == H.E_INVALID
+    a = H.GemvArgs(tiled, int(x), int(y), 1, H.A_F32, H.A_F32, H.EPI_SWIGLU)
+    assert H.lib().opure_gemv_batched_f32(dev.h, C.byref(a)) == H.E_INVALID    # SwiGLU needs the paired layout
 
 
 # ---------------------------------------------------------------------------
