@@ -25,8 +25,11 @@
  *                            (Opure_Streamer.cpp:403-426 nibble order, unsigned),
  *                            scale, zero: bf16[out][in/128]; w(o,i) = s*(q - z)
  *   activations              [rows][width] in OPURE_A_F32 / F16 / BF16
- *   KV pool                  [n_layers][n_pages][2 (K,V)][n_kv_heads][page_size][head_dim]
- *                            in the model's activation format; page_table
+ *   KV pool                  [n_layers][n_pages][2 (K,V)][n_kv_heads] planes of
+ *                            page_size*head_dim elements in the model's activation
+ *                            format: a K plane is token-major [page_size][head_dim],
+ *                            a V plane channel-major [head_dim][page_size] (so V^T
+ *                            tiles of 8 tokens are one 16-byte load); page_table
  *                            int32[batch][max_pages_per_seq] (-1 = none)
  *   rope table               float cos[max_pos][head_dim/2], sin[...] (interleaved
  *                            pairs (2p, 2p+1), Opure_RoPE.usf:7-10)

@@ -210,8 +210,8 @@ __device__ void rollback_seq(const RollbackParams& p, uint32_t b, uint32_t acc)
                 const uint32_t d = e % p.hd, rest = e / p.hd;
                 const uint32_t h = rest % p.n_kv, rest2 = rest / p.n_kv;
                 const uint32_t s = rest2 % 2u, L = rest2 / 2u;
-                const uint64_t idx = ((((static_cast<uint64_t>(L) * p.n_pages + static_cast<uint32_t>(page)) * 2u + s) *
-                                       p.n_kv + h) * OPURE_PAGE_SIZE + pos % OPURE_PAGE_SIZE) * p.hd + d;
+                const uint64_t idx = kv_elem(L, p.n_pages, static_cast<uint32_t>(page), s, p.n_kv, h, p.hd,
+                                             pos % OPURE_PAGE_SIZE, d);
                 if (p.afmt == OPURE_A_F32) static_cast<uint32_t*>(p.pool)[idx] = p.poison_bits;
                 else static_cast<uint16_t*>(p.pool)[idx] = static_cast<uint16_t>(p.poison_bits);
             }

@@ -5,17 +5,25 @@
 //  which ran one workgroup per query head serially over every position, and
 //  the never-dispatched SpeculativeVerifyMain{hd} (Opure_SpeculativeDecode.usf).
 //
-//  Split-K ("flash-decoding") over fixed 64-token chunks of the paged cache:
-//  one workgroup per (KV head, chunk, sequence) scores all query rows of that
-//  KV head's GQA group against the chunk (query head h reads KV head
-//  h / (n_heads / n_kv_heads), Opure_FlashAttention_Decode.usf:71-72), keeps
-//  a per-chunk (max, sum, unnormalised output), and a combine kernel merges
+//  Split-K ("flash-decoding") over fixed chunks of the paged cache: one
+//  workgroup per (KV head, chunk, sequence) scores all query rows of that KV
+//  head's GQA group against the chunk (query head h reads KV head
+//  h / (n_heads / n_kv_heads), Opure_FlashAttention_Decode.usf:71-72), keeps a
+//  per-chunk (max, sum, unnormalised output), and a combine kernel merges
 //  chunks 0..last(row) in order.  Chunk boundaries sit at fixed positions, so
 //  each row's output depends only on its own position: verifying K+1 rows
 //  gives bitwise the same rows as K+1 single-row decodes.  Row j of sequence b
 //  is at position seq_len[b] + j and sees positions 0 .. seq_len[b] + j.
 //  Scores are scaled by attn_scale (1.0 = the reference, which has no
 //  1/sqrt(head_dim): Opure_FlashAttention_Decode.usf:91-104).
+//
+//  fp16/bf16 caches with head_dim 64 or 128 run on matrix cores
+//  (k_attn_mfma): S^T = K Q^T and O^T = V^T P^T with v_mfma_f32_16x16x32, K
+//  tokens assigned to MFMA rows so that the score tile a lane holds is already
+//  its P^T operand, and V read as V^T tiles straight from the channel-major V
+//  planes of the pool.  P^T enters as a hi + lo pair of 16-bit operands
+//  (about 16 significant bits, where one bf16 operand would give 8).  fp32
+//  caches and other head sizes use VALU kernels.
 // ============================================================================
 #include "internal.h"
 
@@ -35,7 +43,27 @@ struct AttnParams {
     float* part_ml;      // [B][nkv][nch][Gq][2]
     uint32_t n_heads, n_kv, hd, rows, n_pages, max_pages, layer, nch, chunk, afmt;
     float scale;
+    uint32_t qoff;       // matrix-core path: first query row of this launch
 };
+
+// zero the elements n.. of a 16-byte piece of consecutive tokens (stale slots
+// past the cache may hold anything, even NaN poison, and meet p = 0)
+template <int AF>
+__device__ __forceinline__ u4v mask_tail(u4v v, uint32_t n)
+{
+    constexpr uint32_t PER = AF == OPURE_A_F32 ? 1u : 2u;     // elements per dword
+#pragma unroll
+    for (uint32_t i = 0; i < 4; ++i)
+    {
+        if (PER == 1u) { if (i >= n) v[i] = 0u; }
+        else
+        {
+            if (2u * i >= n) v[i] = 0u;
+            else if (2u * i + 1u >= n) v[i] &= 0x0000FFFFu;
+        }
+    }
+    return v;
+}
 
 // wave-wide reductions with a fixed butterfly order (deterministic)
 __device__ __forceinline__ float wave_max(float v)
@@ -82,9 +110,9 @@ __global__ __launch_bounds__(256) void k_attn_chunk_generic(AttnParams p)
                 // a missing page or a length past the table reads as NaN, never out of bounds
                 const int32_t page = pos / OPURE_PAGE_SIZE < p.max_pages ? pt[pos / OPURE_PAGE_SIZE] : -1;
                 if (page < 0 || static_cast<uint32_t>(page) >= p.n_pages) { T[tl * kvs + d] = __builtin_nanf(""); continue; }
-                const uint64_t idx = ((((static_cast<uint64_t>(p.layer) * p.n_pages + static_cast<uint32_t>(page)) * 2u + kvsel) *
-                                       p.n_kv + kh) * OPURE_PAGE_SIZE + pos % OPURE_PAGE_SIZE) * hd + d;
-                v = load_act_rt(p.pool, idx, p.afmt);
+                v = load_act_rt(p.pool, kv_elem(p.layer, p.n_pages, static_cast<uint32_t>(page), kvsel, p.n_kv, kh, hd,
+                                                pos % OPURE_PAGE_SIZE, d),
+                                p.afmt);
             }
             T[tl * kvs + d] = v;
         }
@@ -150,8 +178,9 @@ __global__ __launch_bounds__(256) void k_attn_chunk(AttnParams p)
     constexpr uint32_t CH = 64, EB = AF == OPURE_A_F32 ? 4u : 2u;
     constexpr uint32_t ROWB = HD * EB + 16u;              // padded LDS row (bank spread)
     constexpr uint32_t DPL = (HD + 63u) / 64u;             // V channels per lane
+    constexpr uint32_t VROWB = CH * EB + 16u;              // padded LDS V column (channel-major)
     __shared__ __align__(16) uint8_t kt[CH * ROWB];
-    __shared__ __align__(16) uint8_t vt[CH * ROWB];
+    __shared__ __align__(16) uint8_t vt[HD * VROWB];
     __shared__ __align__(16) float pbuf[4][CH];
     extern __shared__ __align__(16) float qs[];            // [Gq][HD]
 
@@ -170,30 +199,39 @@ __global__ __launch_bounds__(256) void k_attn_chunk(AttnParams p)
         const uint32_t j = qi / group, head = kh * group + (qi - j * group);
         qs[e] = load_act_rt(p.q, (static_cast<uint64_t>(b * R + j) * p.n_heads + head) * HD + d, AF);
     }
-    // stage K and V rows: 16-byte pieces, a page's 16 tokens of this head are contiguous
-    constexpr uint32_t PIECES = HD * EB / 16u;
-    for (uint32_t e = threadIdx.x; e < 2u * CH * PIECES; e += 256u)
+    // stage K rows (token-major) and V columns (channel-major, as stored):
+    // 16-byte pieces; a page's 16 tokens of this head are contiguous in both planes
+    constexpr uint32_t KP = HD * EB / 16u;                 // pieces per K row
+    constexpr uint32_t VP = CH * EB / 16u;                 // pieces per V column of the chunk
+    constexpr uint32_t TPP = 16u / EB;                     // tokens per V piece
+    const uint32_t nan = AF == OPURE_A_F32 ? 0x7FC00000u : (AF == OPURE_A_F16 ? 0x7E007E00u : 0x7FC07FC0u);
+    for (uint32_t e = threadIdx.x; e < CH * KP + HD * VP; e += 256u)
     {
-        const uint32_t kvsel = e / (CH * PIECES), rem = e - kvsel * CH * PIECES;
-        const uint32_t tl = rem / PIECES, pc = rem - tl * PIECES, pos = t0 + tl;
+        const bool isk = e < CH * KP;
+        const uint32_t r = isk ? e : e - CH * KP;
+        const uint32_t row = isk ? r / KP : r / VP, pc = isk ? r - row * KP : r - row * VP;   // row: token or channel
+        const uint32_t pos = isk ? t0 + row : t0 + pc * TPP;
         u4v val = {0u, 0u, 0u, 0u};
         if (pos < total)
         {
             const int32_t page = pos / OPURE_PAGE_SIZE < p.max_pages ? pt[pos / OPURE_PAGE_SIZE] : -1;
             if (page >= 0 && static_cast<uint32_t>(page) < p.n_pages)
             {
-                const uint64_t idx = ((((static_cast<uint64_t>(p.layer) * p.n_pages + static_cast<uint32_t>(page)) * 2u + kvsel) *
-                                       p.n_kv + kh) * OPURE_PAGE_SIZE + pos % OPURE_PAGE_SIZE) * HD;
-                val = *reinterpret_cast<const u4v*>(static_cast<const uint8_t*>(p.pool) + idx * EB + pc * 16u);
+                const uint64_t idx = isk ? kv_elem(p.layer, p.n_pages, static_cast<uint32_t>(page), 0u, p.n_kv, kh, HD,
+                                                   pos % OPURE_PAGE_SIZE, pc * (16u / EB))
+                                         : kv_elem(p.layer, p.n_pages, static_cast<uint32_t>(page), 1u, p.n_kv, kh, HD,
+                                                   pos % OPURE_PAGE_SIZE, row);
+                val = *reinterpret_cast<const u4v*>(static_cast<const uint8_t*>(p.pool) + idx * EB);
+                if (!isk && pos + TPP > total) val = mask_tail<AF>(val, total - pos);   // slots past the cache read 0
             }
             else
             {
                 // a missing page or a length past the table reads as NaN, never out of bounds
-                const uint32_t nan = AF == OPURE_A_F32 ? 0x7FC00000u : (AF == OPURE_A_F16 ? 0x7E007E00u : 0x7FC07FC0u);
                 val = {nan, nan, nan, nan};
             }
         }
-        *reinterpret_cast<u4v*>((kvsel ? vt : kt) + tl * ROWB + pc * 16u) = val;
+        if (isk) *reinterpret_cast<u4v*>(kt + row * ROWB + pc * 16u) = val;
+        else *reinterpret_cast<u4v*>(vt + row * VROWB + pc * 16u) = val;
     }
     __syncthreads();
 
@@ -213,7 +251,7 @@ __global__ __launch_bounds__(256) void k_attn_chunk(AttnParams p)
         const uint32_t d = lane + 64u * i;
 #pragma unroll
         for (uint32_t t = 0; t < CH; ++t)
-            vc[i][t] = d < HD ? load_act_rt(vt + t * ROWB, d, AF) : 0.0f;
+            vc[i][t] = d < HD ? load_act_rt(vt + d * VROWB, t, AF) : 0.0f;
     }
     const uint64_t pbase = ((static_cast<uint64_t>(b) * p.n_kv + kh) * p.nch + c) * Gq;
     const uint32_t pos = t0 + lane;
@@ -249,51 +287,324 @@ __global__ __launch_bounds__(256) void k_attn_chunk(AttnParams p)
     }
 }
 
-// one workgroup of hd threads per (row, query head): merge chunks 0..last in
-// order; the loads of each group of 16 chunks are independent and issued together
-__global__ void k_attn_combine(AttnParams p)
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f4_t __attribute__((ext_vector_type(4)));
+
+template <int AF>
+__device__ __forceinline__ f4_t mfma32(u4v a, u4v b, f4_t c)
 {
-    const uint32_t head = blockIdx.x, r = blockIdx.y;     // r = b * R + j
-    const uint32_t R = p.rows, b = r / R, j = r - b * R;
+    if constexpr (AF == OPURE_A_F16)
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, a), __builtin_bit_cast(half8_t, b), c, 0,
+                                                      0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), c,
+                                                       0, 0, 0);
+}
+
+template <int AF>
+__device__ __forceinline__ float unpack_lo(uint32_t v)
+{
+    return AF == OPURE_A_F16 ? f16_to_f32(static_cast<uint16_t>(v)) : bf16_to_f32(static_cast<uint16_t>(v));
+}
+
+template <int AF>
+__device__ __forceinline__ float unpack_hi(uint32_t v)
+{
+    return AF == OPURE_A_F16 ? f16_to_f32(static_cast<uint16_t>(v >> 16)) : bf16_to_f32(static_cast<uint16_t>(v >> 16));
+}
+
+template <int AF>
+__device__ __forceinline__ uint32_t pack_pair(float a, float b)
+{
+    if constexpr (AF == OPURE_A_F16) return f32_to_f16(a) | (static_cast<uint32_t>(f32_to_f16(b)) << 16);
+    else return f32_to_bf16(a) | (static_cast<uint32_t>(f32_to_bf16(b)) << 16);
+}
+
+// Matrix-core flash-decoding for fp16/bf16 caches, head_dim HD in {64, 128}.
+// One workgroup per (KV head, chunk of 4*32*KK tokens, sequence); wave w scores
+// tokens [t0 + 32*KK*w, +32*KK) against query rows qoff .. qoff+16*NT-1 of the
+// KV head's Gq = group*rows rows:
+//   S^T = K Q^T   A = K, lane l = (r, g): token tb + 8(r/4) + r%4 (+4 in the
+//                 second tile), channels 32s + 8g..;  B = Q^T, column = query row
+//   so the score tile a lane holds -- query row r, tokens tb + 8g .. 8g+7 --
+//   is exactly its B operand of
+//   O^T = V^T P^T A = V^T tile (channel r, tokens tb + 8g..8g+7: 16 contiguous
+//                 bytes of a channel-major V plane)
+// All K and V loads are issued before the first MFMA.  The four waves'
+// (max, sum, output) are merged in LDS in wave order and the chunk's partial
+// is written for the combine kernel.
+template <int HD, int AF, int NT, int KK>
+__global__ __launch_bounds__(256) void k_attn_mfma(AttnParams p)
+{
+    constexpr uint32_t KS = HD / 32u, DT = HD / 16u, EB = 2u, TPW = 32u * KK;
+    __shared__ f4_t cacc[3][DT][NT][64];
+    __shared__ float cml[3][NT][16][2];
+    const uint32_t kh = blockIdx.x, c = blockIdx.y, b = blockIdx.z;
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u, g = lane >> 4, r = lane & 15u;
+    const uint32_t group = p.n_heads / p.n_kv, R = p.rows, Gq = group * R;
+    const uint32_t ctx = static_cast<uint32_t>(p.seq_len[b]);
+    const uint32_t total = ctx + R;
+    const uint32_t t0 = c * 4u * TPW;
+    if (t0 >= total) return;                          // whole workgroup: no row reaches this chunk
+    const uint32_t tw = t0 + TPW * wave;
+    const int32_t* pt = p.page_table + static_cast<uint64_t>(b) * p.max_pages;
+    const uint8_t* pool = static_cast<const uint8_t*>(p.pool);
+    const uint32_t nan2 = AF == OPURE_A_F16 ? 0x7E007E00u : 0x7FC07FC0u;
+    const bool active = tw < total;
+
+    // page of a token, -1 if missing (read as NaN) or past the table
+    auto page_of = [&](uint32_t tok) -> int32_t {
+        if (tok / OPURE_PAGE_SIZE >= p.max_pages) return -1;
+        const int32_t pg = pt[tok / OPURE_PAGE_SIZE];
+        return (pg >= 0 && static_cast<uint32_t>(pg) < p.n_pages) ? pg : -1;
+    };
+
+    // ---- every load first: Q^T, K (both score tiles of each k-step), V^T ----
+    u4v qop[NT][KS];
+    uint32_t lim[NT];
+#pragma unroll
+    for (int n = 0; n < NT; ++n)
+    {
+        const uint32_t qi = min(p.qoff + 16u * n + r, Gq - 1u);
+        const uint32_t j = qi / group, head = kh * group + (qi - j * group);
+        lim[n] = ctx + j;
+        const uint8_t* qrow = static_cast<const uint8_t*>(p.q) + ((static_cast<uint64_t>(b * R + j) * p.n_heads + head) * HD) * EB;
+#pragma unroll
+        for (uint32_t s = 0; s < KS; ++s) qop[n][s] = *reinterpret_cast<const u4v*>(qrow + (32u * s + 8u * g) * EB);
+    }
+    u4v kop[KK][2][KS], vop[KK][DT];
+#pragma unroll
+    for (uint32_t kk = 0; kk < KK; ++kk)
+    {
+        const uint32_t tb = tw + 32u * kk;
+#pragma unroll
+        for (uint32_t T = 0; T < 2; ++T)
+        {
+            const uint32_t tok = tb + 8u * (r >> 2) + (r & 3u) + 4u * T;
+            const int32_t pg = active && tok < total ? page_of(tok) : -1;
+            const uint32_t f = active && tok < total ? nan2 : 0u;
+#pragma unroll
+            for (uint32_t s = 0; s < KS; ++s)
+                kop[kk][T][s] = pg >= 0 ? *reinterpret_cast<const u4v*>(
+                                              pool + kv_elem(p.layer, p.n_pages, static_cast<uint32_t>(pg), 0u, p.n_kv, kh,
+                                                             HD, tok % OPURE_PAGE_SIZE, 32u * s + 8u * g) * EB)
+                                        : u4v{f, f, f, f};
+        }
+        const uint32_t tok = tb + 8u * g;             // 8 tokens of one page
+        const int32_t pg = active && tok < total ? page_of(tok) : -1;
+        const uint32_t f = active && tok < total ? nan2 : 0u;
+#pragma unroll
+        for (uint32_t dt = 0; dt < DT; ++dt)
+        {
+            if (pg >= 0)
+            {
+                vop[kk][dt] = *reinterpret_cast<const u4v*>(pool + kv_elem(p.layer, p.n_pages, static_cast<uint32_t>(pg), 1u,
+                                                                           p.n_kv, kh, HD, tok % OPURE_PAGE_SIZE,
+                                                                           16u * dt + r) * EB);
+                if (tok + 8u > total) vop[kk][dt] = mask_tail<AF>(vop[kk][dt], total - tok);   // stale slots read 0
+            }
+            else
+            {
+                vop[kk][dt] = u4v{f, f, f, f};
+            }
+        }
+    }
+
+    // ---- scores, masked past each row's position --------------------------
+    float sc[KK][2][NT][4];
+#pragma unroll
+    for (uint32_t kk = 0; kk < KK; ++kk)
+    {
+        const uint32_t tb = tw + 32u * kk;
+#pragma unroll
+        for (uint32_t T = 0; T < 2; ++T)
+#pragma unroll
+            for (int n = 0; n < NT; ++n)
+            {
+                f4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (uint32_t s = 0; s < KS; ++s) acc = mfma32<AF>(kop[kk][T][s], qop[n][s], acc);
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                {
+                    const uint32_t tok = tb + 8u * g + 4u * T + i;
+                    sc[kk][T][n][i] = active && tok <= lim[n] ? __fmul_rn(acc[i], p.scale) : -__builtin_huge_valf();
+                }
+            }
+    }
+
+    // ---- softmax statistics of each query row over this wave's tokens -----
+    float mrow[NT], lrow[NT];
+    u4v pop[KK][NT], plo[KK][NT];   // P^T = hi + lo, both in the 16-bit format: ~16 significant bits
+#pragma unroll
+    for (int n = 0; n < NT; ++n)
+    {
+        float mx = -__builtin_huge_valf();
+#pragma unroll
+        for (uint32_t kk = 0; kk < KK; ++kk)
+#pragma unroll
+            for (uint32_t T = 0; T < 2; ++T)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sc[kk][T][n][i]);
+        mx = fmaxf(mx, __shfl_xor(mx, 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        float sum = 0.0f;
+#pragma unroll
+        for (uint32_t kk = 0; kk < KK; ++kk)
+        {
+            float e[8];
+#pragma unroll
+            for (uint32_t T = 0; T < 2; ++T)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                {
+                    const float v = sc[kk][T][n][i];
+                    e[4 * T + i] = v == -__builtin_huge_valf() ? 0.0f : expf_ref(__fsub_rn(v, mx));
+                    sum += e[4 * T + i];
+                }
+            pop[kk][n] = u4v{pack_pair<AF>(e[0], e[1]), pack_pair<AF>(e[2], e[3]), pack_pair<AF>(e[4], e[5]),
+                             pack_pair<AF>(e[6], e[7])};
+            float lo[8];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+            {
+                const uint32_t pr = pop[kk][n][i];
+                lo[2 * i] = __fsub_rn(e[2 * i], unpack_lo<AF>(pr));
+                lo[2 * i + 1] = __fsub_rn(e[2 * i + 1], unpack_hi<AF>(pr));
+            }
+            plo[kk][n] = u4v{pack_pair<AF>(lo[0], lo[1]), pack_pair<AF>(lo[2], lo[3]), pack_pair<AF>(lo[4], lo[5]),
+                             pack_pair<AF>(lo[6], lo[7])};
+        }
+        sum += __shfl_xor(sum, 16);
+        sum += __shfl_xor(sum, 32);
+        mrow[n] = mx;
+        lrow[n] = sum;
+    }
+
+    // ---- O^T = V^T P^T ------------------------------------------------------
+    f4_t o[DT][NT];
+#pragma unroll
+    for (uint32_t dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int n = 0; n < NT; ++n)
+        {
+            o[dt][n] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (uint32_t kk = 0; kk < KK; ++kk)
+            {
+                o[dt][n] = mfma32<AF>(vop[kk][dt], plo[kk][n], o[dt][n]);
+                o[dt][n] = mfma32<AF>(vop[kk][dt], pop[kk][n], o[dt][n]);
+            }
+        }
+
+    // ---- merge the four waves in wave order: m = max, weights exp(m_w - m) -
+    if (wave > 0)
+    {
+#pragma unroll
+        for (uint32_t dt = 0; dt < DT; ++dt)
+#pragma unroll
+            for (int n = 0; n < NT; ++n) cacc[wave - 1][dt][n][lane] = o[dt][n];
+        if (g == 0)
+        {
+#pragma unroll
+            for (int n = 0; n < NT; ++n)
+            {
+                cml[wave - 1][n][r][0] = mrow[n];
+                cml[wave - 1][n][r][1] = lrow[n];
+            }
+        }
+    }
+    __syncthreads();
+    if (wave != 0) return;
+    const uint64_t pbase = ((static_cast<uint64_t>(b) * p.n_kv + kh) * p.nch + c) * Gq;
+#pragma unroll
+    for (int n = 0; n < NT; ++n)
+    {
+        float mw[4], lw[4];
+        mw[0] = mrow[n];
+        lw[0] = lrow[n];
+#pragma unroll
+        for (int w = 1; w < 4; ++w)
+        {
+            mw[w] = cml[w - 1][n][r][0];
+            lw[w] = cml[w - 1][n][r][1];
+        }
+        const float M = fmaxf(fmaxf(mw[0], mw[1]), fmaxf(mw[2], mw[3]));
+        float ew[4];
+#pragma unroll
+        for (int w = 0; w < 4; ++w)
+            ew[w] = mw[w] == -__builtin_huge_valf() ? 0.0f : expf_ref(__fsub_rn(mw[w], M));
+        float L = __fmul_rn(ew[0], lw[0]);
+#pragma unroll
+        for (int w = 1; w < 4; ++w) L = __fmaf_rn(ew[w], lw[w], L);
+        const uint32_t qi = p.qoff + 16u * n + r;
+        if (qi >= Gq) continue;
+        if (g == 0)
+        {
+            p.part_ml[(pbase + qi) * 2u] = M;
+            p.part_ml[(pbase + qi) * 2u + 1u] = L;
+        }
+#pragma unroll
+        for (uint32_t dt = 0; dt < DT; ++dt)
+        {
+            f4_t a = o[dt][n] * ew[0];
+#pragma unroll
+            for (int w = 1; w < 4; ++w)
+            {
+                const f4_t v = cacc[w - 1][dt][n][lane];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) a[i] = __fmaf_rn(ew[w], v[i], a[i]);
+            }
+            *reinterpret_cast<f4_t*>(p.part_acc + (pbase + qi) * HD + 16u * dt + 4u * g) = a;
+        }
+    }
+}
+
+// One wave per (row, query head): merge that row's chunks 0..last in order.
+// Lanes first take chunks (max, then weights and the denominator with a fixed
+// butterfly), then channels, summing the chunks' outputs in chunk order.
+__global__ __launch_bounds__(64) void k_attn_combine(AttnParams p)
+{
+    __shared__ float wsh[1024];
+    const uint32_t head = blockIdx.x, rr = blockIdx.y;    // rr = b * R + j
+    const uint32_t R = p.rows, b = rr / R, j = rr - b * R;
     const uint32_t group = p.n_heads / p.n_kv, kh = head / group, qi = j * group + (head - kh * group);
-    const uint32_t Gq = group * R, hd = p.hd, d = threadIdx.x;
+    const uint32_t Gq = group * R, hd = p.hd, lane = threadIdx.x;
     uint32_t last = (static_cast<uint32_t>(p.seq_len[b]) + j) / p.chunk;
     if (last >= p.nch) last = p.nch - 1u;          // length beyond the launch bound: clamp, never overrun
     const uint64_t base = (static_cast<uint64_t>(b) * p.n_kv + kh) * p.nch;
-    constexpr uint32_t G = 16;
     float mx = -__builtin_huge_valf();
-    for (uint32_t c0 = 0; c0 <= last; c0 += G)
+    for (uint32_t c = lane; c <= last; c += 64u) mx = fmaxf(mx, p.part_ml[((base + c) * Gq + qi) * 2u]);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    float den = 0.0f;
+    for (uint32_t c = lane; c <= last; c += 64u)
     {
-        float m[G];
-#pragma unroll
-        for (uint32_t i = 0; i < G; ++i)
-            m[i] = c0 + i <= last ? p.part_ml[((base + c0 + i) * Gq + qi) * 2u] : -__builtin_huge_valf();
-#pragma unroll
-        for (uint32_t i = 0; i < G; ++i) mx = fmaxf(mx, m[i]);
+        const float m = p.part_ml[((base + c) * Gq + qi) * 2u];
+        const float w = m == -__builtin_huge_valf() ? 0.0f : expf_ref(__fsub_rn(m, mx));
+        wsh[c] = w;
+        den = __fmaf_rn(w, p.part_ml[((base + c) * Gq + qi) * 2u + 1u], den);
     }
-    float num = 0.0f, den = 0.0f;
-    for (uint32_t c0 = 0; c0 <= last; c0 += G)
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) den += __shfl_xor(den, o);
+    __syncthreads();
+    const float dd = den > 0.0f ? den : 1.0f;
+    for (uint32_t d = lane; d < hd; d += 64u)
     {
-        float m[G], l[G], a[G];
-#pragma unroll
-        for (uint32_t i = 0; i < G; ++i)
-        {
-            const bool on = c0 + i <= last;
-            const uint64_t k = (base + c0 + i) * Gq + qi;
-            m[i] = on ? p.part_ml[k * 2u] : -__builtin_huge_valf();
-            l[i] = on ? p.part_ml[k * 2u + 1u] : 0.0f;
-            a[i] = on ? p.part_acc[k * hd + d] : 0.0f;
-        }
-#pragma unroll
-        for (uint32_t i = 0; i < G; ++i)
-        {
-            const float w = m[i] == -__builtin_huge_valf() ? 0.0f : expf_ref(__fsub_rn(m[i], mx));
-            den = __fmaf_rn(w, l[i], den);
-            num = __fmaf_rn(w, a[i], num);
-        }
+        float num = 0.0f;
+#pragma unroll 8
+        for (uint32_t c = 0; c <= last; ++c) num = __fmaf_rn(wsh[c], p.part_acc[((base + c) * Gq + qi) * hd + d], num);
+        store_act_rt(p.out, (static_cast<uint64_t>(rr) * p.n_heads + head) * hd + d, __fdiv_rn(num, dd), p.afmt);
     }
-    const float o = __fdiv_rn(num, den > 0.0f ? den : 1.0f);
-    store_act_rt(p.out, (static_cast<uint64_t>(r) * p.n_heads + head) * hd + d, o, p.afmt);
+}
+
+template <int HD, int AF, int NT, int KK>
+int launch_mfma(opure_dev* dev, dim3 grid, const AttnParams& p)
+{
+    hipLaunchKernelGGL((k_attn_mfma<HD, AF, NT, KK>), grid, dim3(256), 0, dev->stream, p);
+    OPURE_LAUNCH_CHECK("k_attn_mfma");
+    return OPURE_OK;
 }
 
 template <int HD, int AF>
@@ -315,11 +626,29 @@ int launch_fast(opure_dev* dev, dim3 grid, uint32_t lds, const AttnParams& p)
 
 namespace opure_hip {
 
-uint32_t attn_chunk(uint32_t hd) { return hd <= 128u ? 64u : 32u; }
-
-uint64_t attn_partial_bytes(uint32_t batch, uint32_t n_kv, uint32_t group, uint32_t rows, uint32_t hd, uint32_t max_ctx)
+// Chunk length of the kernel that runs a shape: 256 for the matrix-core path
+// (fp16/bf16, head_dim 64/128, <= 64 query rows per KV head), 64 for the VALU
+// fast path, 32 for the generic kernel.
+static bool use_mfma(uint32_t hd, uint32_t afmt, uint32_t)
 {
-    const uint32_t nch = (max_ctx + attn_chunk(hd) - 1u) / attn_chunk(hd);
+    return (hd == 64u || hd == 128u) && afmt != OPURE_A_F32;
+}
+
+// Chunk length of the kernel that runs a shape: matrix-core path 128 tokens
+// (head_dim 64) or 256 (head_dim 128), VALU fast path 64, generic kernel 32.
+// It depends on the head size and format only, so a row's chunks never
+// depend on how many rows are scored with it.
+uint32_t attn_chunk(uint32_t hd, uint32_t afmt, uint32_t gq)
+{
+    if (use_mfma(hd, afmt, gq)) return hd == 64u ? 128u : 256u;
+    return hd <= 128u ? 64u : 32u;
+}
+
+uint64_t attn_partial_bytes(uint32_t batch, uint32_t n_kv, uint32_t group, uint32_t rows, uint32_t hd, uint32_t afmt,
+                            uint32_t max_ctx)
+{
+    const uint32_t ch = attn_chunk(hd, afmt, group * rows);
+    const uint32_t nch = (max_ctx + ch - 1u) / ch;
     const uint64_t q = static_cast<uint64_t>(batch) * n_kv * nch * group * rows;
     return align_up(q * hd * 4u, 256) + align_up(q * 2u * 4u, 256);
 }
@@ -339,17 +668,28 @@ int attn_validate(const opure_model* m, const opure_kv* kv, uint32_t batch, uint
                   "attention: max_ctx %u beyond the page-table capacity %u", max_ctx,
                   kv->max_pages_per_seq * OPURE_PAGE_SIZE);
     OPURE_REQUIRE(m->afmt <= OPURE_A_BF16, OPURE_E_INVALID, "attention: bad activation format");
-    const uint32_t group = m->n_heads / m->n_kv_heads, CH = attn_chunk(m->head_dim);
-    const uint64_t lds = (static_cast<uint64_t>(group) * rows * m->head_dim + static_cast<uint64_t>(group) * rows * CH +
-                          static_cast<uint64_t>(CH) * (m->head_dim + 1)) * 4u;
-    OPURE_REQUIRE(lds <= 160u * 1024u, OPURE_E_CAPACITY, "attention: %u query rows per KV head exceed LDS", group * rows);
+    const uint32_t group = m->n_heads / m->n_kv_heads, CH = attn_chunk(m->head_dim, m->afmt, group * rows);
+    OPURE_REQUIRE((max_ctx + CH - 1u) / CH <= 1024u, OPURE_E_CAPACITY, "attention: max_ctx %u has more than 1024 chunks",
+                  max_ctx);
+    if (!use_mfma(m->head_dim, m->afmt, group * rows))
+    {
+        // VALU kernels hold the query rows (and, generic, the scores and K/V) in LDS
+        const uint64_t eb = act_bytes(m->afmt), hd = m->head_dim;
+        const uint64_t lds = CH == 64u ? static_cast<uint64_t>(group) * rows * hd * 4u + 64u * (hd * eb + 16u) +
+                                             hd * (64u * eb + 16u) + 1024u
+                                       : (static_cast<uint64_t>(group) * rows * m->head_dim +
+                                          static_cast<uint64_t>(group) * rows * CH +
+                                          static_cast<uint64_t>(CH) * (m->head_dim + 1)) * 4u;
+        OPURE_REQUIRE(lds <= 160u * 1024u, OPURE_E_CAPACITY, "attention: %u query rows per KV head exceed LDS",
+                      group * rows);
+    }
     return OPURE_OK;
 }
 
 int attn_launch(opure_dev* dev, const opure_model* m, const opure_kv* kv, uint32_t layer, uint32_t batch,
                 uint32_t rows, const int32_t* seq_len, uint32_t max_ctx, const void* q, void* out, float* part)
 {
-    AttnParams p;
+    AttnParams p{};
     p.q = q;
     p.out = out;
     p.pool = kv->pool;
@@ -362,17 +702,37 @@ int attn_launch(opure_dev* dev, const opure_model* m, const opure_kv* kv, uint32
     p.n_pages = kv->n_pages;
     p.max_pages = kv->max_pages_per_seq;
     p.layer = layer;
-    p.chunk = attn_chunk(m->head_dim);
+    const uint32_t group = m->n_heads / m->n_kv_heads, Gq = group * rows;
+    p.chunk = attn_chunk(m->head_dim, m->afmt, Gq);
     p.nch = (max_ctx + p.chunk - 1u) / p.chunk;
     p.afmt = m->afmt;
     p.scale = m->attn_scale;
-    const uint32_t group = m->n_heads / m->n_kv_heads, Gq = group * rows;
     const uint64_t q_elems = static_cast<uint64_t>(batch) * p.n_kv * p.nch * Gq;
     p.part_acc = part;
     p.part_ml = part + align_up(q_elems * p.hd * 4u, 256) / 4u;
     const dim3 grid(p.n_kv, p.nch, batch);
     const uint32_t hd = p.hd;
-    if (p.chunk == 64u && (hd == 64u || hd == 128u))
+    if (use_mfma(hd, p.afmt, Gq))
+    {
+        // query rows in launches of up to 2 tiles of 16 (each row's result is the same in any launch)
+        for (uint32_t q0 = 0; q0 < Gq; q0 += 32u)
+        {
+            AttnParams pq = p;
+            pq.qoff = q0;
+            const bool one = Gq - q0 <= 16u;
+            int rc;
+            if (hd == 64u && p.afmt == OPURE_A_F16)
+                rc = one ? launch_mfma<64, OPURE_A_F16, 1, 1>(dev, grid, pq) : launch_mfma<64, OPURE_A_F16, 2, 1>(dev, grid, pq);
+            else if (hd == 64u)
+                rc = one ? launch_mfma<64, OPURE_A_BF16, 1, 1>(dev, grid, pq) : launch_mfma<64, OPURE_A_BF16, 2, 1>(dev, grid, pq);
+            else if (p.afmt == OPURE_A_F16)
+                rc = one ? launch_mfma<128, OPURE_A_F16, 1, 2>(dev, grid, pq) : launch_mfma<128, OPURE_A_F16, 2, 2>(dev, grid, pq);
+            else
+                rc = one ? launch_mfma<128, OPURE_A_BF16, 1, 2>(dev, grid, pq) : launch_mfma<128, OPURE_A_BF16, 2, 2>(dev, grid, pq);
+            if (rc) return rc;
+        }
+    }
+    else if (p.chunk == 64u && (hd == 64u || hd == 128u))
     {
         const uint32_t lds = Gq * hd * 4u;
         int rc;
@@ -397,7 +757,7 @@ int attn_launch(opure_dev* dev, const opure_model* m, const opure_kv* kv, uint32
         hipLaunchKernelGGL(k_attn_chunk_generic, grid, dim3(256), lds, dev->stream, p);
         OPURE_LAUNCH_CHECK("k_attn_chunk_generic");
     }
-    hipLaunchKernelGGL(k_attn_combine, dim3(p.n_heads, batch * rows), dim3(p.hd), 0, dev->stream, p);
+    hipLaunchKernelGGL(k_attn_combine, dim3(p.n_heads, batch * rows), dim3(64), 0, dev->stream, p);
     OPURE_LAUNCH_CHECK("k_attn_combine");
     return OPURE_OK;
 }
@@ -416,7 +776,7 @@ extern "C" int opure_attn_decode_paged(opure_dev* dev, const opure_attn_args* a)
                   a->layer);
     const uint32_t group = a->model->n_heads / a->model->n_kv_heads;
     rc = ensure_workspace(dev, attn_partial_bytes(a->batch, a->model->n_kv_heads, group, a->rows, a->model->head_dim,
-                                                  a->max_ctx), 0);
+                                                  a->model->afmt, a->max_ctx), 0);
     if (rc) return rc;
     return attn_launch(dev, a->model, a->kv, a->layer, a->batch, a->rows, a->seq_len, a->max_ctx, a->q, a->out,
                        static_cast<float*>(dev->ws));

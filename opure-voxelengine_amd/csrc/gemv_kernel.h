@@ -362,10 +362,12 @@ __device__ __forceinline__ void epilogue(const KParams& p, uint32_t tile, uint32
         const uint32_t kh = ok / hd, d0 = ok - kh * hd;
         const int32_t page = e.page_table[static_cast<uint64_t>(b) * e.max_pages + pos / OPURE_PAGE_SIZE];
         if (page < 0 || static_cast<uint32_t>(page) >= e.n_pages) return;
-        const uint64_t base = ((((static_cast<uint64_t>(e.layer) * e.n_pages + static_cast<uint32_t>(page)) * 2u + kvsel) *
-                                e.n_kv_heads + kh) * OPURE_PAGE_SIZE + pos % OPURE_PAGE_SIZE) * hd + d0;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) store_act_rt(e.kv_pool, base + i, v[i], p.yfmt);
+        for (int i = 0; i < 4; ++i)
+            store_act_rt(e.kv_pool,
+                         kv_elem(e.layer, e.n_pages, static_cast<uint32_t>(page), kvsel, e.n_kv_heads, kh, hd,
+                                 pos % OPURE_PAGE_SIZE, d0 + i),
+                         v[i], p.yfmt);
     }
 }
 

@@ -125,8 +125,9 @@ int gemv_launch(opure_dev* dev, const GemvCall& c);
 uint32_t tiled_block_k(uint32_t wfmt);      // k values per 64-byte block
 
 // ---- attention (attention.hip) ---------------------------------------------
-uint32_t attn_chunk(uint32_t head_dim);
-uint64_t attn_partial_bytes(uint32_t batch, uint32_t n_kv, uint32_t group, uint32_t rows, uint32_t hd, uint32_t max_ctx);
+uint32_t attn_chunk(uint32_t head_dim, uint32_t afmt, uint32_t query_rows_per_kv_head);
+uint64_t attn_partial_bytes(uint32_t batch, uint32_t n_kv, uint32_t group, uint32_t rows, uint32_t hd, uint32_t afmt,
+                            uint32_t max_ctx);
 int      attn_validate(const opure_model* m, const opure_kv* kv, uint32_t batch, uint32_t rows, uint32_t max_ctx);
 int      attn_launch(opure_dev* dev, const opure_model* m, const opure_kv* kv, uint32_t layer, uint32_t batch,
                      uint32_t rows, const int32_t* seq_len, uint32_t max_ctx, const void* q, void* out, float* part);
@@ -246,6 +247,17 @@ __device__ __forceinline__ float round_act_rt(float v, uint32_t af)
     if (af == OPURE_A_F16) return f16_to_f32(f32_to_f16(v));
     if (af == OPURE_A_BF16) return bf16_to_f32(f32_to_bf16(v));
     return v;
+}
+
+// Element (slot, d) of the K (kvsel 0) or V (kvsel 1) plane of a cache page.
+// K planes are token-major [16][hd]; V planes channel-major [hd][16], so a
+// V^T tile of 8 consecutive tokens of one channel is 16 contiguous bytes.
+__device__ __forceinline__ uint64_t kv_elem(uint32_t layer, uint32_t n_pages, uint32_t page, uint32_t kvsel,
+                                            uint32_t n_kv, uint32_t head, uint32_t hd, uint32_t slot, uint32_t d)
+{
+    const uint64_t plane = ((((static_cast<uint64_t>(layer) * n_pages + page) * 2u + kvsel) * n_kv + head) *
+                            OPURE_PAGE_SIZE) * hd;
+    return kvsel == 0u ? plane + static_cast<uint64_t>(slot) * hd + d : plane + static_cast<uint64_t>(d) * OPURE_PAGE_SIZE + slot;
 }
 
 // silu(g) * u in the order of Opure_CpuReference.cpp:195-196

@@ -110,7 +110,7 @@ static VerifyPlan make_plan(const opure_model* m, uint32_t B, uint32_t R, uint32
     p.lm_tiles = m->vocab / 16u;
     p.am_val = take(static_cast<uint64_t>(p.lm_tiles) * MR * 4u);
     p.am_idx = take(static_cast<uint64_t>(p.lm_tiles) * MR * 4u);
-    p.attn = take(attn_partial_bytes(B, m->n_kv_heads, m->n_heads / m->n_kv_heads, R, m->head_dim, max_ctx));
+    p.attn = take(attn_partial_bytes(B, m->n_kv_heads, m->n_heads / m->n_kv_heads, R, m->head_dim, m->afmt, max_ctx));
     p.rej = take(accept_ws_bytes(B, R - 1u, m->vocab, OPURE_ACCEPT_REJECTION));
     p.total = off;
     p.counters = B;

@@ -364,11 +364,16 @@ void orc_swiglu(const float* g, const float* u, float* h, uint64_t n)
     }
 }
 
-static inline uint64_t kv_index(const orc_model* m, const orc_kv* kv, uint32_t layer,
-                                int32_t page, uint32_t kvsel, uint32_t head, uint32_t slot)
+// Element (slot, d) of a page's K or V plane.  K planes are token-major
+// [page_size][head_dim]; V planes are channel-major [head_dim][page_size], so
+// the GPU reads V^T tiles of 8 tokens with one 16-byte load (see opure_hip.h).
+static inline uint64_t kv_elem(const orc_model* m, const orc_kv* kv, uint32_t layer, int32_t page,
+                               uint32_t kvsel, uint32_t head, uint32_t slot, uint32_t d)
 {
-    return ((((static_cast<uint64_t>(layer) * kv->n_pages + static_cast<uint32_t>(page)) * 2 + kvsel) *
-             m->n_kv_heads + head) * kv->page_size + slot) * m->head_dim;
+    const uint64_t plane = (((static_cast<uint64_t>(layer) * kv->n_pages + static_cast<uint32_t>(page)) * 2 + kvsel) *
+                            m->n_kv_heads + head) * kv->page_size * m->head_dim;
+    return kvsel == 0 ? plane + static_cast<uint64_t>(slot) * m->head_dim + d
+                      : plane + static_cast<uint64_t>(d) * kv->page_size + slot;
 }
 
 void orc_attention_paged(const orc_model* m, const orc_kv* kv, uint32_t layer,
@@ -389,9 +394,11 @@ void orc_attention_paged(const orc_model* m, const orc_kv* kv, uint32_t layer,
             double mx = -1e300;
             for (uint32_t s = 0; s < seqLen; ++s)
             {
-                const uint64_t base = kv_index(m, kv, layer, pt[s / kv->page_size], 0, kvh, s % kv->page_size);
+                const int32_t pg = pt[s / kv->page_size];
                 double sc = 0.0;
-                for (uint32_t d = 0; d < hd; ++d) sc += double(qRow[d]) * double(load_act(kv->pool, base + d, m->afmt));
+                for (uint32_t d = 0; d < hd; ++d)
+                    sc += double(qRow[d]) *
+                          double(load_act(kv->pool, kv_elem(m, kv, layer, pg, 0, kvh, s % kv->page_size, d), m->afmt));
                 sc *= double(m->attn_scale);
                 scores[s] = sc;
                 if (sc > mx) mx = sc;
@@ -406,9 +413,10 @@ void orc_attention_paged(const orc_model* m, const orc_kv* kv, uint32_t layer,
             std::fill(o.begin(), o.end(), 0.0);
             for (uint32_t s = 0; s < seqLen; ++s)
             {
-                const uint64_t base = kv_index(m, kv, layer, pt[s / kv->page_size], 1, kvh, s % kv->page_size);
+                const int32_t pg = pt[s / kv->page_size];
                 const double w = scores[s];
-                for (uint32_t d = 0; d < hd; ++d) o[d] += w * double(load_act(kv->pool, base + d, m->afmt));
+                for (uint32_t d = 0; d < hd; ++d)
+                    o[d] += w * double(load_act(kv->pool, kv_elem(m, kv, layer, pg, 1, kvh, s % kv->page_size, d), m->afmt));
             }
             const double invSum = 1.0 / (sum > 0.0 ? sum : 1.0);
             float* oRow = out + (static_cast<uint64_t>(j) * nh + hq) * hd;
@@ -506,12 +514,12 @@ static int verify_impl(const orc_model* m, orc_kv* kv, uint32_t B, uint32_t R,
                 const int32_t pg = kv->page_table[static_cast<uint64_t>(b) * kv->max_pages_per_seq + pos / kv->page_size];
                 for (uint32_t kh = 0; kh < nkv; ++kh)
                 {
-                    const uint64_t kb = kv_index(m, kv, L, pg, 0, kh, pos % kv->page_size);
-                    const uint64_t vb = kv_index(m, kv, L, pg, 1, kh, pos % kv->page_size);
                     for (uint32_t d = 0; d < hd; ++d)
                     {
-                        store_act(kv->pool, kb + d, row[qdim + kh * hd + d], m->afmt);
-                        store_act(kv->pool, vb + d, row[qdim + kvdim + kh * hd + d], m->afmt);
+                        store_act(kv->pool, kv_elem(m, kv, L, pg, 0, kh, pos % kv->page_size, d), row[qdim + kh * hd + d],
+                                  m->afmt);
+                        store_act(kv->pool, kv_elem(m, kv, L, pg, 1, kh, pos % kv->page_size, d),
+                                  row[qdim + kvdim + kh * hd + d], m->afmt);
                     }
                 }
             }
@@ -744,11 +752,11 @@ void orc_kv_rollback(orc_kv* kv, const orc_model* m, uint32_t B, uint32_t K,
                     for (uint32_t s = 0; s < 2; ++s)
                         for (uint32_t h = 0; h < m->n_kv_heads; ++h)
                         {
-                            const uint64_t base = kv_index(m, kv, L, pg, s, h, pos % ps);
                             for (uint32_t d = 0; d < m->head_dim; ++d)
                             {
-                                if (m->afmt == ORC_A_F32) static_cast<uint32_t*>(kv->pool)[base + d] = poison_bits;
-                                else static_cast<uint16_t*>(kv->pool)[base + d] = static_cast<uint16_t>(poison_bits);
+                                const uint64_t e = kv_elem(m, kv, L, pg, s, h, pos % ps, d);
+                                if (m->afmt == ORC_A_F32) static_cast<uint32_t*>(kv->pool)[e] = poison_bits;
+                                else static_cast<uint16_t*>(kv->pool)[e] = static_cast<uint16_t>(poison_bits);
                             }
                         }
             }

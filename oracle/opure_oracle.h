@@ -69,7 +69,9 @@ typedef struct orc_model {
 } orc_model;
 
 typedef struct orc_kv {
-    void*    pool;            /* [n_layers][n_pages][2][n_kv][page_size][hd] afmt elements */
+    void*    pool;            /* [n_layers][n_pages][2][n_kv] planes of page_size*hd afmt elements:
+                                 K plane [page_size][hd] (token-major), V plane [hd][page_size]
+                                 (channel-major) */
     uint32_t n_pages;
     uint32_t page_size;
     const int32_t* page_table;/* [batch][max_pages_per_seq] */

@@ -294,6 +294,16 @@ def act_np_dtype(afmt: int):
     return np.float32 if afmt == A_F32 else np.uint16
 
 
+def kv_planes(pool):
+    """Logical (K, V) views [layers][pages][kv_heads][page_size][head_dim] of a
+    paged pool.  K planes are stored token-major, V planes channel-major
+    ([head_dim][page_size]), so V is a transposed view; both are writable."""
+    K = pool[:, :, 0]
+    L, P, nkv, ps, hd = K.shape
+    V = pool[:, :, 1].reshape(L, P, nkv, hd, ps).swapaxes(-1, -2)
+    return K, V
+
+
 class HostKV:
     """Paged cache [n_layers][n_pages][2][n_kv][page][hd] with per-sequence page tables."""
 

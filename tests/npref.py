@@ -49,6 +49,7 @@ def forward(model, pool, page_table, tokens, seq_len):
     B, R = tokens.shape
     h, nh, nkv, hd, ff = c["hidden"], c["n_heads"], c["n_kv_heads"], c["head_dim"], c["ffn"]
     ps = pool.shape[4]
+    Kp, Vp = O.kv_planes(pool)
     grp = nh // nkv
     deq = {}
 
@@ -91,14 +92,14 @@ def forward(model, pool, page_table, tokens, seq_len):
             for j in range(R):
                 p = pos[b, j]
                 pg = page_table[b, p // ps]
-                pool[L, pg, 0, :, p % ps] = f32_to_act(k[b, j], afmt)
-                pool[L, pg, 1, :, p % ps] = f32_to_act(v[b, j], afmt)
+                Kp[L, pg, :, p % ps] = f32_to_act(k[b, j], afmt)
+                Vp[L, pg, :, p % ps] = f32_to_act(v[b, j], afmt)
         att = np.zeros((B, R, nh, hd), dtype=np.float32)
         for b in range(B):
             n = int(seq_len[b]) + R
             pages = page_table[b, :(n + ps - 1) // ps]
-            Kc = act_to_f32(pool[L, pages, 0], afmt).transpose(1, 0, 2, 3).reshape(nkv, -1, hd)[:, :n]
-            Vc = act_to_f32(pool[L, pages, 1], afmt).transpose(1, 0, 2, 3).reshape(nkv, -1, hd)[:, :n]
+            Kc = act_to_f32(Kp[L, pages], afmt).transpose(1, 0, 2, 3).reshape(nkv, -1, hd)[:, :n]
+            Vc = act_to_f32(Vp[L, pages], afmt).transpose(1, 0, 2, 3).reshape(nkv, -1, hd)[:, :n]
             Kq = np.repeat(Kc, grp, axis=0).astype(np.float64)
             Vq = np.repeat(Vc, grp, axis=0).astype(np.float64)
             s = np.einsum("jhd,hnd->jhn", q[b].astype(np.float64), Kq) * float(np.float32(c["attn_scale"]))

@@ -265,8 +265,9 @@ def run_attn(dev, m, pool_bits, pt, seq_len, R, q_bits, layer=0):
 def test_attention_known_answers(dev, hd):
     g = np.load(os.path.join(GOLD, f"attention_hd{hd}.npz"))
     pool = np.zeros((1, 1, 2, 2, 16, hd), np.float32)
-    pool[0, 0, 0, :, :7] = g["K"]
-    pool[0, 0, 1, :, :7] = g["V"]
+    Kp, Vp = O.kv_planes(pool)
+    Kp[0, 0, :, :7] = g["K"]
+    Vp[0, 0, :, :7] = g["V"]
     out = run_attn(dev, attn_model(4, 2, hd, H.A_F32), pool, np.zeros((1, 1)), [6], 1,
                    np.ascontiguousarray(g["Q"].reshape(1, -1)))
     rms = np.sqrt(np.mean((out.ravel().astype(np.float64) - g["ref"].ravel()) ** 2))

@@ -156,7 +156,9 @@ def test_rollback_bookkeeping_and_poison():
     assert list(new_len) == [16, 15]
     # seq 0: positions 16..19 rolled back, page 1 (positions 16..31) released
     assert nf[0] == 1 and freed[0, 0] == 1 and kv.page_table[0, 1] == -1
-    assert np.isnan(kv.pool[:, 1, :, :, 0:4]).all()
+    Kp, Vp = O.kv_planes(kv.pool)
+    assert np.isnan(Kp[:, 1, :, 0:4]).all() and np.isnan(Vp[:, 1, :, 0:4]).all()
+    assert not np.isnan(Kp[:, 1, :, 4:]).any() and not np.isnan(Vp[:, 1, :, 4:]).any()
     assert not np.isnan(kv.pool[:, 5]).any()
     assert nf[1] == 0 and kv.page_table[1, 0] == 0
 

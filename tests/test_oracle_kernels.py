@@ -143,9 +143,10 @@ def _paged(K, V, page_size, perm):
     n_kv, seq, hd = K.shape
     n_pages = max(perm) + 1 if len(perm) else 1
     pool = np.zeros((1, n_pages, 2, n_kv, page_size, hd), dtype=np.float32)
+    Kp, Vp = O.kv_planes(pool)
     for s in range(seq):
-        pool[0, perm[s // page_size], 0, :, s % page_size] = K[:, s]
-        pool[0, perm[s // page_size], 1, :, s % page_size] = V[:, s]
+        Kp[0, perm[s // page_size], :, s % page_size] = K[:, s]
+        Vp[0, perm[s // page_size], :, s % page_size] = V[:, s]
     pt = np.array([perm], dtype=np.int32)
     return pool, pt
 
