@@ -205,7 +205,7 @@ __device__ void rollback_seq(const RollbackParams& p, uint32_t b, uint32_t acc)
             if (pos / OPURE_PAGE_SIZE >= p.max_pages) break;
             const int32_t page = pt[pos / OPURE_PAGE_SIZE];
             if (page < 0 || static_cast<uint32_t>(page) >= p.n_pages) continue;
-            for (uint32_t e = threadIdx.x; e < per_pos; e += NT)
+            for (uint32_t e = threadIdx.x; e < per_pos; e += blockDim.x)
             {
                 const uint32_t d = e % p.hd, rest = e / p.hd;
                 const uint32_t h = rest % p.n_kv, rest2 = rest / p.n_kv;
@@ -255,14 +255,18 @@ struct GreedyParams {
     RollbackParams rb;
 };
 
-// One workgroup per sequence.  Each thread scans every row's partials at once
-// (16 rows per pass), then each row is reduced across the workgroup in a fixed
-// order: (greater value, then lower index) wins.
-__global__ __launch_bounds__(256) void k_accept_greedy(GreedyParams p)
+// One workgroup of GNT threads per sequence.  Each thread scans its share of
+// the LM head's per-tile partials for 8 rows at a time, four partials' loads
+// in flight together, then each row is reduced across the workgroup.  The
+// winner (greater value, then lower index) is a total order, so the result
+// does not depend on the reduction order.
+constexpr uint32_t GNT = 1024;
+
+__global__ __launch_bounds__(GNT) void k_accept_greedy(GreedyParams p)
 {
-    constexpr uint32_t RB = 16;
-    __shared__ float sv[4][RB];
-    __shared__ int32_t si[4][RB];
+    constexpr uint32_t RB = 8, UP = 4, NWV = GNT / 64u;
+    __shared__ float sv[NWV][RB];
+    __shared__ int32_t si[NWV][RB];
     __shared__ int32_t am[64];
     __shared__ uint32_t s_n;
     const uint32_t b = blockIdx.x, R = p.K + 1u;
@@ -274,17 +278,28 @@ __global__ __launch_bounds__(256) void k_accept_greedy(GreedyParams p)
         int32_t bi[RB];
 #pragma unroll
         for (uint32_t i = 0; i < RB; ++i) { bv[i] = -__builtin_huge_valf(); bi[i] = 0x7FFFFFFF; }
-        for (uint32_t part = threadIdx.x; part < p.parts; part += NT)
+        for (uint32_t part = threadIdx.x; part < p.parts; part += GNT * UP)
         {
-            const uint64_t base = static_cast<uint64_t>(part) * p.rows_total + b * R + r0;
+            float v[UP][RB];
+            int32_t x[UP][RB];
 #pragma unroll
-            for (uint32_t i = 0; i < RB; ++i)
+            for (uint32_t u = 0; u < UP; ++u)
             {
-                if (i >= nr) break;
-                const float v = p.am_val[base + i];
-                const int32_t x = p.am_idx[base + i];
-                if (v > bv[i] || (v == bv[i] && x < bi[i])) { bv[i] = v; bi[i] = x; }
+                const uint32_t pp = part + u * GNT;
+                const uint64_t base = static_cast<uint64_t>(pp) * p.rows_total + b * R + r0;
+#pragma unroll
+                for (uint32_t i = 0; i < RB; ++i)
+                {
+                    const bool on = pp < p.parts && i < nr;
+                    v[u][i] = on ? p.am_val[base + i] : -__builtin_huge_valf();
+                    x[u][i] = on ? p.am_idx[base + i] : 0x7FFFFFFF;
+                }
             }
+#pragma unroll
+            for (uint32_t u = 0; u < UP; ++u)
+#pragma unroll
+                for (uint32_t i = 0; i < RB; ++i)
+                    if (v[u][i] > bv[i] || (v[u][i] == bv[i] && x[u][i] < bi[i])) { bv[i] = v[u][i]; bi[i] = x[u][i]; }
         }
 #pragma unroll
         for (uint32_t i = 0; i < RB; ++i)
@@ -308,7 +323,7 @@ __global__ __launch_bounds__(256) void k_accept_greedy(GreedyParams p)
             const uint32_t i = threadIdx.x;
             float v = sv[0][i];
             int32_t x = si[0][i];
-            for (int w = 1; w < 4; ++w)
+            for (uint32_t w = 1; w < NWV; ++w)
                 if (sv[w][i] > v || (sv[w][i] == v && si[w][i] < x)) { v = sv[w][i]; x = si[w][i]; }
             am[r0 + i] = x == 0x7FFFFFFF ? 0 : x;
         }
@@ -549,7 +564,7 @@ int greedy_from_partials(opure_dev* dev, const float* am_val, const int32_t* am_
     g.accepted = accepted;
     g.rollback = rb ? 1u : 0u;
     if (rb) g.rb = rollback_params(rb);
-    hipLaunchKernelGGL(k_accept_greedy, dim3(batch), dim3(NT), 0, dev->stream, g);
+    hipLaunchKernelGGL(k_accept_greedy, dim3(batch), dim3(GNT), 0, dev->stream, g);
     OPURE_LAUNCH_CHECK("k_accept_greedy");
     return OPURE_OK;
 }

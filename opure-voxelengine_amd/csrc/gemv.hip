@@ -100,9 +100,7 @@ __global__ __launch_bounds__(64) void k_prenorm(opure_gemv::KParams p, void* xn)
 {
     constexpr uint32_t EB = AF == OPURE_A_F32 ? 4u : 2u;
     const uint32_t m = blockIdx.x, lane = threadIdx.x;
-    const uint32_t r16 = lane & 15u, mc = r16 < p.M ? r16 : p.M - 1u;
-    const float inv_lane = opure_gemv::inv_rms(p, mc, lane >> 4);
-    const float inv = __shfl(inv_lane, static_cast<int>(m), 64);
+    const float inv = opure_gemv::inv_rms_wave(p, m, lane);
     uint8_t* row = static_cast<uint8_t*>(xn) + static_cast<uint64_t>(m) * p.in * EB;
     for (uint32_t j = lane; j < p.in / 8u; j += 64u)
     {

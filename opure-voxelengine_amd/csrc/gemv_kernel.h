@@ -148,15 +148,15 @@ __device__ __forceinline__ uint32_t pack2(float a, float b)
         return f32_to_bf16(a) | (static_cast<uint32_t>(f32_to_bf16(b)) << 16);
 }
 
-// 1 / rms of column m from the producer's per-16-column sums of squares, in
-// a fixed order (lanes g4 take tiles g4, g4+4, ...; then a 2-level butterfly)
-__device__ __forceinline__ float inv_rms(const KParams& p, uint32_t mc, uint32_t g4)
+// 1 / rms of column m from the producer's per-16-column sums of squares, by
+// one wave in a fixed order (lane l takes tiles l, l+64, ..., then a 6-level
+// butterfly) that depends on neither M nor the kernel shape
+__device__ __forceinline__ float inv_rms_wave(const KParams& p, uint32_t m, uint32_t lane)
 {
     float ssum = 0.0f;
-#pragma unroll 8
-    for (uint32_t t = g4; t < p.ss_tiles; t += 4u) ssum += p.ss_in[static_cast<uint64_t>(t) * p.M + mc];
-    ssum += __shfl_xor(ssum, 16);
-    ssum += __shfl_xor(ssum, 32);
+    for (uint32_t t = lane; t < p.ss_tiles; t += 64u) ssum += p.ss_in[static_cast<uint64_t>(t) * p.M + m];
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) ssum += __shfl_xor(ssum, o);
     return __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(ssum, static_cast<float>(p.in)), p.eps)));
 }
 
@@ -211,7 +211,7 @@ __device__ __forceinline__ void load8(const KParams& p, uint32_t m, uint32_t k, 
 // order; uint4 also writes each 128-k group's sum to xsum[m][g].  Threads take
 // 8-value units; the 16 units of a group sit in 16 aligned lanes of one wave.
 template <int WF, int AF, bool NORM, int NTH>
-__device__ __forceinline__ void stage_x(const KParams& p, uint8_t* lds, float inv_lane)
+__device__ __forceinline__ void stage_x(const KParams& p, uint8_t* lds, const float* sinv)
 {
     constexpr uint32_t EB = AF == OPURE_A_F32 ? 4u : 2u;
     const uint32_t n8 = p.in / 8u;
@@ -220,7 +220,7 @@ __device__ __forceinline__ void stage_x(const KParams& p, uint8_t* lds, float in
     for (uint32_t m = 0; m < p.M; ++m)
     {
         float inv = 1.0f;
-        if constexpr (NORM) inv = __shfl(inv_lane, static_cast<int>(m), 64);     // whole wave active here
+        if constexpr (NORM) inv = sinv[m];
         uint8_t* row = lds + static_cast<uint64_t>(m) * p.x_stride;
         for (uint32_t j = threadIdx.x; j < n8; j += NTH)
         {
@@ -437,11 +437,20 @@ __global__ __launch_bounds__(NW * 64) void k_gemv(KParams p)
     load(A, 0);
     if (S > 1u) load(B, 1);
 
-    float inv = 1.0f;
-    if constexpr (NORM) inv = inv_rms(p, mc, g4);
     if constexpr (STAGED)
     {
-        stage_x<WF, AF, NORM, NW * 64>(p, lds, inv);
+        __shared__ float sinv[OPURE_MAX_ROWS];
+        if constexpr (NORM)
+        {
+            // one wave per column: a single round of loads whatever M is
+            for (uint32_t m = wave; m < M; m += NW)
+            {
+                const float v = inv_rms_wave(p, m, lane);
+                if (lane == 0) sinv[m] = v;
+            }
+            __syncthreads();
+        }
+        stage_x<WF, AF, NORM, NW * 64>(p, lds, sinv);
         __syncthreads();
     }
 
@@ -608,7 +617,7 @@ int launch(opure_dev* dev, const KParams& kp, uint32_t grid, uint32_t lds)
     if (!configured)
     {
         OPURE_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemv<WF, AF, EPI, NW, T, U, NORM, STAGED>),
-                                          hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+                                          hipFuncAttributeMaxDynamicSharedMemorySize, 159 * 1024));
         configured = true;
     }
     hipLaunchKernelGGL((k_gemv<WF, AF, EPI, NW, T, U, NORM, STAGED>), dim3(grid), dim3(NW * 64), lds, dev->stream, kp);

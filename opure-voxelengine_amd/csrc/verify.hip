@@ -29,57 +29,74 @@ using namespace opure_dev_math;
 
 namespace {
 
-// Element i of row `row` of a tiled linear (opure_tile_linear layout),
-// dequantised.  Tile t = row / 16 holds the row as lane r = row % 16 of its
-// 1 KB blocks.
-__device__ __forceinline__ float tiled_elem(const opure_linear& E, uint32_t wfmt, uint32_t row, uint32_t i, uint32_t nblk,
-                                            uint32_t KB)
-{
-    const uint32_t t = row >> 4, r = row & 15u;
-    const uint32_t b = i / KB, k = i - b * KB;
-    const uint32_t vals = KB / 4u, g = k / vals, kk = k - g * vals;
-    const uint8_t* piece = static_cast<const uint8_t*>(E.w) + ((static_cast<uint64_t>(t) * nblk + b) << 10) +
-                           ((16u * g + r) << 4);
-    if (wfmt == OPURE_W_F32) return reinterpret_cast<const float*>(piece)[kk];
-    if (wfmt == OPURE_W_I8PC)
-    {
-        const int8_t q = static_cast<int8_t>(piece[kk] ^ 0x80u);
-        return __fmul_rn(static_cast<float>(q), f16_to_f32(static_cast<const uint16_t*>(E.scale)[t * 16u + r]));
-    }
-    // uint4: element e of word kk/8 sits at nibble {0,4,1,5,2,6,3,7}[e]
-    const uint32_t word = reinterpret_cast<const uint32_t*>(piece)[kk >> 3];
-    const uint32_t e = kk & 7u;
-    const uint32_t pos = (e >> 1) | ((e & 1u) << 2);
-    const uint32_t q = (word >> (4u * pos)) & 0x0Fu;
-    const uint32_t sz = static_cast<const uint32_t*>(E.scale)[(static_cast<uint64_t>(t) * nblk + b) * 16u + r];
-    const float s = __uint_as_float(sz << 16), z = __uint_as_float(sz & 0xFFFF0000u);
-    return __fmul_rn(s, __fsub_rn(static_cast<float>(q), z));
-}
-
 // Dequantised embedding rows into the fp32 residual, plus each 16-column
 // tile's sum of squares for the first layer's fused RMSNorm.  One thread per
-// 16-column tile.
+// 16-column tile: its columns are one 16-byte piece (int8), half a piece
+// (uint4) or four pieces (fp32) of the tiled layout, loaded at once.
 __global__ __launch_bounds__(256) void k_embed(const int32_t* tokens, opure_linear E, uint32_t wfmt, uint32_t h,
                                                uint32_t vocab, uint32_t M, uint32_t KB, float* x, float* ss)
 {
+    typedef uint32_t u4v __attribute__((ext_vector_type(4)));
     const uint32_t r = blockIdx.x;
     const int32_t t = tokens[r];
     float* xr = x + static_cast<uint64_t>(r) * h;
     const bool bad = t < 0 || static_cast<uint32_t>(t) >= vocab;
     const uint32_t nblk = h / KB;
-    for (uint32_t tile = threadIdx.x; tile < h / 16u; tile += 256u)
+    const uint32_t row = bad ? 0u : static_cast<uint32_t>(t), tile = row >> 4, rr = row & 15u;
+    const uint8_t* w = static_cast<const uint8_t*>(E.w);
+    for (uint32_t c16 = threadIdx.x; c16 < h / 16u; c16 += 256u)
     {
-        float sq = 0.0f;
-#pragma unroll 4
-        for (uint32_t j = 0; j < 16u; ++j)
+        float v[16];
+        const uint32_t k0 = 16u * c16, b = k0 / KB, kk = k0 - b * KB;
+        const uint64_t blk = (static_cast<uint64_t>(tile) * nblk + b) << 10;
+        if (wfmt == OPURE_W_F32)
         {
-            const uint32_t i = 16u * tile + j;
-            // an id outside the vocabulary poisons its row instead of reading out of bounds
-            const float v = bad ? __builtin_nanf("") : tiled_elem(E, wfmt, static_cast<uint32_t>(t), i, nblk, KB);
-            xr[i] = v;
-            sq = __fmaf_rn(v, v, sq);
+#pragma unroll
+            for (uint32_t gq = 0; gq < 4; ++gq)
+            {
+                const u4v q = *reinterpret_cast<const u4v*>(w + blk + ((16u * gq + rr) << 4));
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[4 * gq + e] = __uint_as_float(q[e]);
+            }
         }
-        ss[static_cast<uint64_t>(tile) * M + r] = sq;
+        else if (wfmt == OPURE_W_I8PC)
+        {
+            const u4v q = *reinterpret_cast<const u4v*>(w + blk + ((16u * (kk / 16u) + rr) << 4));
+            const float sc = f16_to_f32(static_cast<const uint16_t*>(E.scale)[tile * 16u + rr]);
+#pragma unroll
+            for (int e = 0; e < 16; ++e)
+            {
+                const int8_t qi = static_cast<int8_t>(((q[e >> 2] >> (8 * (e & 3))) & 0xFFu) ^ 0x80u);
+                v[e] = __fmul_rn(static_cast<float>(qi), sc);
+            }
+        }
+        else
+        {
+            // 16 columns = words 2*half, 2*half+1 of lane g's piece; element e of a
+            // word sits at nibble {0,4,1,5,2,6,3,7}[e]
+            const uint32_t g = kk / 32u, half = (kk % 32u) / 16u;
+            const uint32_t* wd = reinterpret_cast<const uint32_t*>(w + blk + ((16u * g + rr) << 4)) + 2u * half;
+            const uint32_t w0 = wd[0], w1 = wd[1];
+            const uint32_t sz = static_cast<const uint32_t*>(E.scale)[(static_cast<uint64_t>(tile) * nblk + b) * 16u + rr];
+            const float s = __uint_as_float(sz << 16), z = __uint_as_float(sz & 0xFFFF0000u);
+#pragma unroll
+            for (int e = 0; e < 16; ++e)
+            {
+                const uint32_t word = e < 8 ? w0 : w1, el = e & 7;
+                const uint32_t q = (word >> (4u * ((el >> 1) | ((el & 1u) << 2)))) & 0x0Fu;
+                v[e] = __fmul_rn(s, __fsub_rn(static_cast<float>(q), z));
+            }
+        }
+        float sq = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+        {
+            // an id outside the vocabulary poisons its row instead of reading out of bounds
+            const float val = bad ? __builtin_nanf("") : v[e];
+            xr[k0 + e] = val;
+            sq = __fmaf_rn(val, val, sq);
+        }
+        ss[static_cast<uint64_t>(c16) * M + r] = sq;
     }
 }
 
