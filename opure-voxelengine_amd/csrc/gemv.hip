@@ -162,6 +162,11 @@ namespace opure_hip {
 
 uint32_t tiled_block_k(uint32_t wfmt) { return kb_of(wfmt); }
 
+uint32_t gemv_grid(const opure_dev* dev, const GemvCall& c)
+{
+    return make_plan(dev, c.wfmt, c.xfmt, c.W.out, c.W.in, c.M).grid;
+}
+
 int gemv_validate(const GemvCall& c)
 {
     const uint32_t wf = c.wfmt, af = c.xfmt;

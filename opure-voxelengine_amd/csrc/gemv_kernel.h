@@ -251,8 +251,11 @@ __device__ __forceinline__ void stage_x(const KParams& p, uint8_t* lds, const fl
 }
 
 // Epilogue of one tile: lane holds D rows 4*g4 + i of column m (v[i]).
+// EPI_LOGITS keeps the best (value, lowest index) of column m seen so far in
+// (best_v, best_i); the workgroup writes one partial per column at its end.
 template <int WF, int EPI>
-__device__ __forceinline__ void epilogue(const KParams& p, uint32_t tile, uint32_t m, uint32_t g4, f4_t tot)
+__device__ __forceinline__ void epilogue(const KParams& p, uint32_t tile, uint32_t m, uint32_t g4, f4_t tot,
+                                         float& best_v, int32_t& best_i)
 {
     const uint32_t M = p.M;
     float v[4];
@@ -286,11 +289,7 @@ __device__ __forceinline__ void epilogue(const KParams& p, uint32_t tile, uint32
             const int32_t oi = __shfl_xor(bi, off);
             if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
         }
-        if (m < M && g4 == 0)
-        {
-            p.lg.am_val[static_cast<uint64_t>(tile) * M + m] = bv;
-            p.lg.am_idx[static_cast<uint64_t>(tile) * M + m] = bi;
-        }
+        if (bv > best_v || (bv == best_v && bi < best_i)) { best_v = bv; best_i = bi; }
         return;
     }
     if constexpr (EPI == opure_hip::EPI_RESIDUAL)
@@ -455,6 +454,8 @@ __global__ __launch_bounds__(NW * 64) void k_gemv(KParams p)
     }
 
     f4_t acc[T];
+    float best_v = -__builtin_huge_valf();
+    int32_t best_i = 0x7FFFFFFF;
     auto run = [&](const PL& b, uint32_t s) {
         const uint32_t gi = s / npass, ps = s - gi * npass;
         if (ps == 0)
@@ -573,7 +574,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemv(KParams p)
                 f4_t tot = red[wave * 64u + lane];
 #pragma unroll
                 for (int w = 1; w < NW; ++w) tot += red[(w * T + wave) * 64u + lane];
-                epilogue<WF, EPI>(p, tile, r16, g4, tot);
+                epilogue<WF, EPI>(p, tile, r16, g4, tot, best_v, best_i);
             }
         }
     };
@@ -606,6 +607,27 @@ __global__ __launch_bounds__(NW * 64) void k_gemv(KParams p)
     else if (rest == 1u)
     {
         run(A, s);
+    }
+    if constexpr (EPI == opure_hip::EPI_LOGITS)
+    {
+        // one argmax partial per column for the whole workgroup: waves t < T
+        // hold the best of the tiles they finished (a total order, so any
+        // merge order gives the same winner)
+        __syncthreads();
+        float* sv = reinterpret_cast<float*>(red);
+        int32_t* si = reinterpret_cast<int32_t*>(sv + T * 16);
+        if (wave < static_cast<uint32_t>(T) && g4 == 0) { sv[wave * 16u + r16] = best_v; si[wave * 16u + r16] = best_i; }
+        __syncthreads();
+        if (wave == 0 && g4 == 0 && r16 < M)
+        {
+            float v = sv[r16];
+            int32_t i = si[r16];
+#pragma unroll
+            for (int t = 1; t < T; ++t)
+                if (sv[t * 16 + r16] > v || (sv[t * 16 + r16] == v && si[t * 16 + r16] < i)) { v = sv[t * 16 + r16]; i = si[t * 16 + r16]; }
+            p.lg.am_val[static_cast<uint64_t>(blockIdx.x) * M + r16] = v;
+            p.lg.am_idx[static_cast<uint64_t>(blockIdx.x) * M + r16] = i;
+        }
     }
 }
 

@@ -91,8 +91,8 @@ struct QkvEpilogue {
 };
 
 struct LogitsEpilogue {
-    float*   am_val = nullptr;   // [n_tiles][M]
-    int32_t* am_idx = nullptr;
+    float*   am_val = nullptr;   // [workgroups][M]: best logit of each column per workgroup
+    int32_t* am_idx = nullptr;   // its vocabulary index (lowest on ties)
 };
 
 struct GemvCall {
@@ -121,6 +121,9 @@ struct GemvCall {
 
 int gemv_validate(const GemvCall& c);
 int gemv_launch(opure_dev* dev, const GemvCall& c);
+// workgroups gemv_launch runs for this call (EPI_LOGITS writes one argmax
+// partial per workgroup and column)
+uint32_t gemv_grid(const opure_dev* dev, const GemvCall& c);
 // device-side tiled-layout helpers shared with the embedding gather
 uint32_t tiled_block_k(uint32_t wfmt);      // k values per 64-byte block
 

@@ -366,7 +366,7 @@ int opure_verify_step(opure_dev* dev, const opure_verify_args* a)
     if (a->accept_mode == OPURE_ACCEPT_GREEDY)
     {
         // greedy acceptance and the rollback run in one kernel
-        rc = greedy_from_partials(dev, c.logits.am_val, c.logits.am_idx, P.lm_tiles, B, R - 1u, a->tokens + 1, R,
+        rc = greedy_from_partials(dev, c.logits.am_val, c.logits.am_idx, gemv_grid(dev, c), B, R - 1u, a->tokens + 1, R,
                                   a->out_tokens, a->accepted, a->rollback ? &rb : nullptr);
         if (rc) return rc;
     }
