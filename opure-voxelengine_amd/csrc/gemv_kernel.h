@@ -209,36 +209,49 @@ __device__ __forceinline__ void load8(const KParams& p, uint32_t m, uint32_t k, 
 
 // Stage X rows 0..M-1 (whole K) into LDS rows of x_stride bytes, natural k
 // order; uint4 also writes each 128-k group's sum to xsum[m][g].  Threads take
-// 8-value units; the 16 units of a group sit in 16 aligned lanes of one wave.
+// 8-value units of the flattened (row, unit) space, eight units' loads in
+// flight before any store; the 16 units of a group sit in 16 aligned lanes of
+// one wave (n8 and NTH are multiples of 16), so the group sum is a fixed
+// butterfly.
 template <int WF, int AF, bool NORM, int NTH>
 __device__ __forceinline__ void stage_x(const KParams& p, uint8_t* lds, const float* sinv)
 {
-    constexpr uint32_t EB = AF == OPURE_A_F32 ? 4u : 2u;
+    constexpr uint32_t EB = AF == OPURE_A_F32 ? 4u : 2u, KU = 8u;
     const uint32_t n8 = p.in / 8u;
+    const uint32_t total = p.M * n8;
     const uint32_t lane = threadIdx.x & 63u;
     float* xsum = reinterpret_cast<float*>(lds + p.off_xsum);
-    for (uint32_t m = 0; m < p.M; ++m)
+    for (uint32_t base = 0; base < total; base += NTH * KU)
     {
-        float inv = 1.0f;
-        if constexpr (NORM) inv = sinv[m];
-        uint8_t* row = lds + static_cast<uint64_t>(m) * p.x_stride;
-        for (uint32_t j = threadIdx.x; j < n8; j += NTH)
+        uint32_t o[KU][8];
+#pragma unroll
+        for (uint32_t k = 0; k < KU; ++k)
         {
-            uint32_t o[8];
-            load8<AF, NORM>(p, m, 8u * j, inv, o);
-            uint8_t* dst = row + 8u * j * EB;
+            const uint32_t idx = base + k * NTH + threadIdx.x;
+            if (idx < total)
+            {
+                const uint32_t m = idx / n8, j = idx - m * n8;
+                load8<AF, NORM>(p, m, 8u * j, NORM ? sinv[m] : 1.0f, o[k]);
+            }
+        }
+#pragma unroll
+        for (uint32_t k = 0; k < KU; ++k)
+        {
+            const uint32_t idx = base + k * NTH + threadIdx.x;
+            if (idx >= total) continue;
+            const uint32_t m = idx / n8, j = idx - m * n8;
+            uint8_t* dst = lds + static_cast<uint64_t>(m) * p.x_stride + 8u * j * EB;
             if constexpr (AF == OPURE_A_F32)
             {
-                reinterpret_cast<u4_t*>(dst)[0] = u4_t{o[0], o[1], o[2], o[3]};
-                reinterpret_cast<u4_t*>(dst)[1] = u4_t{o[4], o[5], o[6], o[7]};
+                reinterpret_cast<u4_t*>(dst)[0] = u4_t{o[k][0], o[k][1], o[k][2], o[k][3]};
+                reinterpret_cast<u4_t*>(dst)[1] = u4_t{o[k][4], o[k][5], o[k][6], o[k][7]};
             }
             else
             {
-                *reinterpret_cast<u4_t*>(dst) = u4_t{o[0], o[1], o[2], o[3]};
+                *reinterpret_cast<u4_t*>(dst) = u4_t{o[k][0], o[k][1], o[k][2], o[k][3]};
                 if constexpr (WF == OPURE_W_I4G128)
                 {
-                    // n8 and NTH are multiples of 16: a group's 16 lanes are all active
-                    float u = unit_sum<AF>(o[0], o[1], o[2], o[3]);
+                    float u = unit_sum<AF>(o[k][0], o[k][1], o[k][2], o[k][3]);
                     u += __shfl_xor(u, 1);
                     u += __shfl_xor(u, 2);
                     u += __shfl_xor(u, 4);
@@ -250,7 +263,6 @@ __device__ __forceinline__ void stage_x(const KParams& p, uint8_t* lds, const fl
     }
 }
 
-// Epilogue of one tile: lane holds D rows 4*g4 + i of column m (v[i]).
 // EPI_LOGITS keeps the best (value, lowest index) of column m seen so far in
 // (best_v, best_i); the workgroup writes one partial per column at its end.
 template <int WF, int EPI>
