@@ -139,13 +139,17 @@ __device__ __forceinline__ float unit_sum(uint32_t d0, uint32_t d1, uint32_t d2,
     return s;
 }
 
+// two floats rounded to nearest even into one packed pair (v_cvt_pk_f16_f32 /
+// v_cvt_pk_bf16_f32)
 template <int AF>
 __device__ __forceinline__ uint32_t pack2(float a, float b)
 {
+    typedef float f2_t __attribute__((ext_vector_type(2)));
+    const f2_t v = {a, b};
     if constexpr (AF == OPURE_A_F16)
-        return f32_to_f16(a) | (static_cast<uint32_t>(f32_to_f16(b)) << 16);
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, half2_t));
     else
-        return f32_to_bf16(a) | (static_cast<uint32_t>(f32_to_bf16(b)) << 16);
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
 }
 
 // 1 / rms of column m from the producer's per-16-column sums of squares, by
@@ -209,30 +213,31 @@ __device__ __forceinline__ void load8(const KParams& p, uint32_t m, uint32_t k, 
 
 // Stage X rows 0..M-1 (whole K) into LDS rows of x_stride bytes, natural k
 // order; uint4 also writes each 128-k group's sum to xsum[m][g].  Threads take
-// 8-value units of the flattened (row, unit) space, eight units' loads in
-// flight before any store; the 16 units of a group sit in 16 aligned lanes of
+// 8-value units of the flattened (row, unit) space, up to eight units' loads
+// in flight before any store; the 16 units of a group sit in 16 aligned lanes of
 // one wave (n8 and NTH are multiples of 16), so the group sum is a fixed
 // butterfly.
 template <int WF, int AF, bool NORM, int NTH>
 __device__ __forceinline__ void stage_x(const KParams& p, uint8_t* lds, const float* sinv)
 {
-    constexpr uint32_t EB = AF == OPURE_A_F32 ? 4u : 2u, KU = 8u;
+    // units in flight per thread: 16-wave workgroups have 128 VGPRs a lane,
+    // and a rmsnorm'd unit holds 16 words (x and gain) until it is converted
+    constexpr uint32_t EB = AF == OPURE_A_F32 ? 4u : 2u, KU = NTH < 1024 ? 8u : (NORM ? 2u : 4u);
     const uint32_t n8 = p.in / 8u;
     const uint32_t total = p.M * n8;
     const uint32_t lane = threadIdx.x & 63u;
     float* xsum = reinterpret_cast<float*>(lds + p.off_xsum);
     for (uint32_t base = 0; base < total; base += NTH * KU)
     {
+        // every thread loads all KU units (past the end: the last unit again),
+        // so the loads are issued back to back before the first use
         uint32_t o[KU][8];
 #pragma unroll
         for (uint32_t k = 0; k < KU; ++k)
         {
-            const uint32_t idx = base + k * NTH + threadIdx.x;
-            if (idx < total)
-            {
-                const uint32_t m = idx / n8, j = idx - m * n8;
-                load8<AF, NORM>(p, m, 8u * j, NORM ? sinv[m] : 1.0f, o[k]);
-            }
+            const uint32_t idx = min(base + k * NTH + threadIdx.x, total - 1u);
+            const uint32_t m = idx / n8, j = idx - m * n8;
+            load8<AF, NORM>(p, m, 8u * j, NORM ? sinv[m] : 1.0f, o[k]);
         }
 #pragma unroll
         for (uint32_t k = 0; k < KU; ++k)

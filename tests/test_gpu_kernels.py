@@ -87,6 +87,38 @@ def np_tiled(wfmt, lin, layout):
     return tiled, (sc | (zr << np.uint32(16))).reshape(-1)
 
 
+def _rounding_cases():
+    """f32 values that pin round-to-nearest-even narrowing: random bit patterns
+    over the whole finite range, exact ties (even and odd) for both formats,
+    subnormal results, overflow to infinity, signed zeros and infinities."""
+    rng = np.random.default_rng(5)
+    bits = [rng.integers(0, 0x7F800000, 200000, dtype=np.uint32)]
+    hi = rng.integers(0x3000, 0x4780, 20000, dtype=np.uint32) << np.uint32(16)
+    bits += [hi | np.uint32(0x8000), hi | np.uint32(0x7FFF), hi | np.uint32(0x8001)]   # bf16 ties and neighbours
+    f16e = rng.integers(0x33000000, 0x47800000, 20000, dtype=np.uint32) & np.uint32(0xFFFFE000)
+    bits += [f16e | np.uint32(0x1000), f16e | np.uint32(0x0FFF)]                       # f16 ties
+    bits += [np.array([0, 0x7F800000, 0x477FF000, 0x477FEFFF, 0x47800000, 0x33000000, 0x33000001,
+                       0x00000001, 0x007FFFFF, 0x7F7FFFFF], np.uint32)]
+    b = np.concatenate(bits)
+    return np.concatenate([b, b | np.uint32(0x80000000)]).view(np.float32)
+
+
+@pytest.mark.parametrize("afmt", [H.A_F16, H.A_BF16], ids=["f16", "bf16"])
+def test_narrowing_rounds_to_nearest_even(dev, afmt):
+    """The device's f32 -> f16/bf16 narrowing (hardware conversions used by
+    every kernel that stores activations) equals the oracle's round-to-
+    nearest-even, bit for bit, on every non-NaN input."""
+    x = _rounding_cases()
+    src = dev.upload(x)
+    dst = dev.alloc(2 * x.size)
+    H.check(H.lib().opure_convert_f32(dev.h, int(src), int(dst), afmt, x.size))
+    dev.sync()
+    got = dev.download(dst, np.uint16, x.shape)
+    want = O.f32_to_f16_bits(x) if afmt == H.A_F16 else O.f32_to_bf16_bits(x)
+    bad = np.flatnonzero(got != want)
+    assert bad.size == 0, [(hex(int(x.view(np.uint32)[i])), hex(int(got[i])), hex(int(want[i]))) for i in bad[:8]]
+
+
 @pytest.mark.parametrize("wfmt", [H.W_F32, H.W_I8PC, H.W_I4G128])
 @pytest.mark.parametrize("layout", [H.LAYOUT_TILED, H.LAYOUT_TILED_SWIGLU])
 def test_tile_linear_layout(dev, wfmt, layout):
