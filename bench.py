@@ -233,12 +233,101 @@ def cpu_baseline(dev, w, gpu_logits, gpu_accept):
         tokens_equal=bool(out[0].tolist() == gpu_accept["out_tokens"]))
 
 
+def bench_c2(args):
+    """The isolated acceptance stage: rejection sampling over target logits
+    [64][9][49152] and draft logits [64][8][49152] (fp32, N(0,3) from Philox),
+    drafts sampled from the draft softmax at temperature 1 (Philox stream 0),
+    accept uniforms on stream 1, residual / bonus draws on stream 2.  Three
+    input sets (226 MB each) rotate so the 256 MB last-level cache cannot
+    serve a set twice in a row.  One step = one opure_accept_rejection call
+    that also writes the [64][49152] distribution of each final draw."""
+    B, K, V, tau, seed = 64, 8, 49152, 1.0, 2024
+    dev = H.Dev(0)
+    log("device", dev.name)
+    L = H.lib()
+    sets = []
+    for i in range(3):
+        t = dev.alloc(B * (K + 1) * V * 4)
+        q = dev.alloc(B * K * V * 4)
+        H.check(L.opure_synth_normal_f32(dev.h, int(t), B * (K + 1) * V, seed + i, 0, 3.0, 0.0))
+        H.check(L.opure_synth_normal_f32(dev.h, int(q), B * K * V, seed + i, 1, 3.0, 0.0))
+        pos = dev.upload(np.tile(np.arange(K, dtype=np.uint32), B))
+        seq = dev.upload(np.repeat(np.arange(B, dtype=np.uint32), K))
+        d = dev.alloc(B * K * 4)
+        sa = H.SampleArgs(B * K, V, int(q), tau, seed + i, int(pos), int(seq), 0, int(d))
+        H.check(L.opure_sample_rows(dev.h, C.byref(sa)))
+        pb = dev.upload(np.full(B, 0, np.uint32))
+        ot, ac, di = dev.alloc(B * (K + 1) * 4), dev.alloc(B * 4), dev.alloc(B * V * 4)
+        a = H.AcceptArgs(B, K, V, int(t), int(q), int(d), K, tau, seed + i, int(pb), int(ot), int(ac), int(di))
+        sets.append(dict(t=t, q=q, d=d, pos=pos, seq=seq, pb=pb, ot=ot, ac=ac, di=di, a=a))
+    dev.sync()
+
+    def launch(i):
+        H.check(L.opure_accept_rejection(dev.h, C.byref(sets[i % 3]["a"])))
+
+    for i in range(args.warmup):
+        launch(i)
+    dev.sync()
+    t0 = time.perf_counter()
+    dev.timer_begin()
+    for i in range(args.steps):
+        launch(i)
+    dev.timer_end()
+    ms = dev.timer_ms() / args.steps
+    dev.sync()
+    wall = (time.perf_counter() - t0) * 1e3 / args.steps
+    accs = [dev.download(st["ac"], np.int32, (B,)) for st in sets]
+    tokens = float(np.mean([a.sum() + B for a in accs]))     # accepted drafts + the final token, per sequence
+    value = tokens / (ms * 1e-3)
+    read = B * (2 * K + 1) * V * 4
+    written = B * V * 4 + B * (K + 2) * 4
+    gbs = (read + written) / (ms * 1e-3) / 1e9
+    log(f"accept_rejection: {ms * 1e3:.2f} us/step, {gbs:.0f} GB/s, mean accepted {np.mean(accs):.3f}")
+    line = {
+        "metric": "accepted tokens/s of the rejection-sampling acceptance stage (B=64, K=8, V=49152)",
+        "value": round(value, 1), "unit": "accepted tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32 logits, u64 fixed-point partition sums, u32 Philox",
+        "data": "synthetic: logits N(0,3) from Philox (seeds 2024..2026), drafts sampled from the draft softmax",
+        "config": {"workload": "c2: opure_accept_rejection, batch 64, K=8, vocab 49152, temperature 1.0, "
+                               "residual distributions written, 3 rotating 226 MB input sets",
+                   "mean_accepted": round(float(np.mean(accs)), 4), "wall_ms_per_step": round(wall, 5)},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "opure_accept_rejection (k_rej_rowstat + k_rej_slice + k_rej_draw), whole stage",
+                     "bytes_per_launch": read + written, "avg_us": round(ms * 1e3, 2)},
+    }
+    if args.cpu_baseline == "auto":
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import oracle as O
+        st = sets[0]
+        t = dev.download(st["t"], np.float32, (B, K + 1, V))
+        q = dev.download(st["q"], np.float32, (B, K, V))
+        d = dev.download(st["d"], np.int32, (B, K))
+        O.set_threads(1)
+        t0 = time.perf_counter()
+        w_out, w_acc, w_dist = O.accept_rejection(t, q, d, tau, seed, np.zeros(B, np.uint32))
+        dt = time.perf_counter() - t0
+        got_out = dev.download(st["ot"], np.int32, (B, K + 1))
+        got_dist = dev.download(st["di"], np.float32, (B, V))
+        w_tokens = float(w_acc.sum() + B)
+        line["cpu_baseline"] = {"value": round(w_tokens / dt, 1), "unit": "accepted tokens/s", "cores": 1,
+                                "kind": "port", "sample": f"one full acceptance stage (64 sequences) of input set 0 "
+                                                          f"through the scalar oracle: {dt:.2f}s"}
+        line["parity"] = {"accepted_equal": bool(np.array_equal(w_acc, accs[0])),
+                          "tokens_equal": bool(np.array_equal(w_out, got_out)),
+                          "dist_max_abs": float(np.abs(got_dist - w_dist).max())}
+        log("cpu baseline", line["cpu_baseline"], "parity", line["parity"])
+    print(json.dumps(line), flush=True)
+    dev.close()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--config", default="c3", choices=sorted(synth.CONFIGS))
+    ap.add_argument("--config", default="c3", choices=sorted(synth.CONFIGS) + ["c2"])
     ap.add_argument("--cpu-baseline", default="auto", choices=["auto", "skip"])
     ap.add_argument("--no-kernel-timing", action="store_true")
     ap.add_argument("--eager", action="store_true", help="launch each step's kernels directly instead of a hipGraph")
@@ -247,6 +336,8 @@ def main():
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
               "multi-GPU sharding is a design note, not a measured path", file=sys.stderr)
         sys.exit(2)
+    if args.config == "c2":
+        return bench_c2(args)
 
     dev = H.Dev(0)
     log("device", dev.name)

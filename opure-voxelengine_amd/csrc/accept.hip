@@ -24,9 +24,8 @@
 //      p_v = (float)(e_v * (2^32 / S)) , r_v = max(0, p_v - q_v), R_v = fixed(r_v)
 //      draw: smallest v whose inclusive prefix of W exceeds floor(U * sum W / 2^32)
 //
-//  One kernel does the whole rejection stage: a workgroup per (row, sequence)
-//  computes its row's statistics and accept bit, and the last workgroup of a
-//  sequence to finish (atomic counter, reset afterwards) draws the final token.
+//  The rejection stage runs as three launches (row statistics, per-slice draw
+//  weights, per-slice draw), described at k_rej_rowstat.
 // ============================================================================
 #include "internal.h"
 
@@ -36,9 +35,29 @@ namespace {
 
 constexpr uint32_t NT = 256;
 
+// the same value as a double, for sums of probabilities: for a float v in
+// [0, 2^20) the fma v * 2^32 + 1/2 is exact in double, so its floor is
+// fixed(v); with v <= 1 every term is at most 2^32 and sums of fewer than 2^20
+// terms stay exact integers.  NaN and v <= 0 give 0.
+__device__ __forceinline__ double fixed_d(float v)
+{
+    const double d = __builtin_floor(__fma_rn(static_cast<double>(v), 4294967296.0, 0.5));
+    return d > 0.0 ? d : 0.0;
+}
+
+__device__ __forceinline__ uint64_t fixed_sum_u64(double s) { return static_cast<uint64_t>(s); }
+
+// floor(v * 2^32 + 1/2) for v in [0, 2^31) (0 for v <= 0 and NaN), from the
+// float's fields: v * 2^32 = m * 2^(e - 118) exactly, rounded half up
 __device__ __forceinline__ uint64_t to_fixed(float v)
 {
-    return v > 0.0f ? static_cast<uint64_t>(__dadd_rn(__dmul_rn(static_cast<double>(v), 4294967296.0), 0.5)) : 0ull;
+    if (!(v > 0.0f)) return 0ull;
+    const uint32_t b = f_bits(v);
+    const int32_t sh = static_cast<int32_t>(b >> 23) - 118;
+    const uint64_t m = (b & 0x7FFFFFu) | 0x800000u;
+    if (sh >= 0) return m << sh;
+    const uint32_t rs = static_cast<uint32_t>(-sh);
+    return rs >= 25u ? 0ull : (m + (1ull << (rs - 1u))) >> rs;
 }
 
 __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int o)
@@ -343,124 +362,421 @@ __global__ __launch_bounds__(GNT) void k_accept_greedy(GreedyParams p)
 }
 
 // ---------------------------------------------------------------------------
-struct RejRow { float mp, mq; uint64_t Sp, Sq; uint32_t accept, pad; };
+// Rejection sampling in three launches, all rows and slices in parallel:
+//   k_rej_rowstat  one 1024-thread workgroup per logit row (K+1 target rows
+//                  and K draft rows of each sequence): m = max l, S = sum of
+//                  fixed(e_v), and e(x) of the row's draft token
+//   k_rej_slice    per (slice, sequence): n from the accept tests, then the
+//                  draw weights of row n for the slice (residual max(0,p-q),
+//                  or p_K after K accepts) into a [B][V] buffer, and the
+//                  slice's exact sums of fixed(residual) and fixed(p)
+//   k_rej_draw     per (slice, sequence): the inverse-CDF threshold against
+//                  the slices' exact prefix; the slice holding it finds the
+//                  token, every slice writes its part of the distribution
+// Every sum is an exact u64 sum of fixed-point weights, so the parallel
+// decomposition gives the bits of the sequential definition above.
+struct RowStat { float m, ex; uint64_t S; };
+struct SlicePart { uint64_t R, P; };
+
+constexpr uint32_t RNT = 1024;                 // k_rej_rowstat threads
+constexpr uint32_t RVEC = 12;                  // float4s of logits held per thread by k_rej_rowstat<true>
+constexpr uint32_t SLICE = 4096;               // elements per slice of k_rej_slice / k_rej_draw
 
 struct RejectParams {
     const float* target;      // [B][K+1][V]
     const float* draft;       // [B][K][V]
     const int32_t* drafts;
     uint32_t drafts_stride;
-    uint32_t K, V;
+    uint32_t K, V, slices;
     float tau;
     uint64_t seed;
     const uint32_t* pos_base;
     int32_t* out_tokens;
     int32_t* accepted;
-    float* dist;
-    RejRow* ws;               // [B][K+1]
-    uint32_t* counters;       // [B]
+    float* dist;              // [B][V] or null
+    RowStat* stats;           // [B][2K+1]: target rows 0..K, then draft rows
+    SlicePart* parts;         // [B][slices]
+    float* wbuf;              // [B][V] draw weights of row n
     const int32_t* seq_len;   // optional new_seq_len = seq_len + n + 1
     int32_t* new_seq_len;
 };
 
-__global__ __launch_bounds__(256) void k_accept_rejection(RejectParams p)
+template <uint32_t NTH>
+__device__ float block_max_n(float v, float* red)
 {
-    __shared__ float fred[4];
-    __shared__ uint64_t ured[4];
-    __shared__ uint64_t scan[NT];
-    __shared__ int32_t s_tok;
-    __shared__ uint32_t s_last;
-    const uint32_t j = blockIdx.x, b = blockIdx.y, K = p.K, V = p.V;
-    const float tau = p.tau;
-    const uint32_t pb = p.pos_base ? p.pos_base[b] : 0u;
-    const float* trow = p.target + (static_cast<uint64_t>(b) * (K + 1u) + j) * V;
-    const Stat P = row_stats(trow, V, tau, fred, ured);
-    RejRow rr{P.m, 0.0f, P.S, 0ull, 0u, 0u};
-    if (j < K)
-    {
-        const float* qrow = p.draft + (static_cast<uint64_t>(b) * K + j) * V;
-        const Stat Q = row_stats(qrow, V, tau, fred, ured);
-        rr.mq = Q.m;
-        rr.Sq = Q.S;
-        const int32_t x = p.drafts[static_cast<uint64_t>(b) * p.drafts_stride + j];
-        if (x >= 0 && static_cast<uint32_t>(x) < V)
-        {
-            const float ep = e_of(trow, static_cast<uint32_t>(x), tau, P.m);
-            const float eq = e_of(qrow, static_cast<uint32_t>(x), tau, Q.m);
-            const float u = uniform24(philox_u32(p.seed, pb + j, b, 1u));
-            const double lhs = __dmul_rn(__dmul_rn(static_cast<double>(u), static_cast<double>(eq)), static_cast<double>(P.S));
-            const double rhs = __dmul_rn(static_cast<double>(ep), static_cast<double>(Q.S));
-            rr.accept = lhs < rhs ? 1u : 0u;
-        }
-    }
-    if (threadIdx.x == 0) p.ws[static_cast<uint64_t>(b) * (K + 1u) + j] = rr;
-    __threadfence();
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
     __syncthreads();
-    if (threadIdx.x == 0) s_last = atomicAdd(&p.counters[b], 1u) == K ? 1u : 0u;
+    if ((threadIdx.x & 63u) == 0) red[threadIdx.x >> 6] = v;
     __syncthreads();
-    if (!s_last) return;
-    __threadfence();
+    float r = red[0];
+#pragma unroll
+    for (uint32_t w = 1; w < NTH / 64u; ++w) r = fmaxf(r, red[w]);
+    return r;
+}
 
-    // ---- last workgroup of sequence b: find n, draw the final token --------
-    const RejRow* rows = p.ws + static_cast<uint64_t>(b) * (K + 1u);
-    uint32_t n = K;
-    for (uint32_t i = 0; i < K; ++i)
-        if (!__builtin_nontemporal_load(&rows[i].accept)) { n = i; break; }
-    const uint32_t U = philox_u32(p.seed, pb + n, b, 2u);
-    float* dist = p.dist ? p.dist + static_cast<uint64_t>(b) * V : nullptr;
-    const float* tn = p.target + (static_cast<uint64_t>(b) * (K + 1u) + n) * V;
-    const float mp = __builtin_nontemporal_load(&rows[n].mp);
-    const uint64_t Sp = __builtin_nontemporal_load(&rows[n].Sp);
-    const double invP = __ddiv_rn(4294967296.0, static_cast<double>(Sp));
-    int32_t tok;
-    if (n < K)
+template <uint32_t NTH>
+__device__ uint64_t block_sum_u64_n(uint64_t v, uint64_t* red)
+{
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += shfl_xor_u64(v, o);
+    __syncthreads();
+    if ((threadIdx.x & 63u) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    uint64_t r = 0;
+#pragma unroll
+    for (uint32_t w = 0; w < NTH / 64u; ++w) r += red[w];
+    return r;
+}
+
+// logit / tau; DIV is false exactly when tau == 1 (x / 1 == x)
+template <bool DIV>
+__device__ __forceinline__ float scaled_logit(float x, float tau) { return DIV ? __fdiv_rn(x, tau) : x; }
+
+// logit row r of sequence b: target rows 0..K, draft rows K+1..2K
+__device__ __forceinline__ const float* rej_row(const RejectParams& p, uint32_t b, uint32_t r)
+{
+    return r <= p.K ? p.target + (static_cast<uint64_t>(b) * (p.K + 1u) + r) * p.V
+                    : p.draft + (static_cast<uint64_t>(b) * p.K + (r - p.K - 1u)) * p.V;
+}
+
+// REG: the row is read once, as float4s held in registers (V % 4 == 0,
+// V <= 4 * RNT * RVEC, 16-byte aligned rows); otherwise it is read twice.
+template <bool REG, bool DIV>
+__global__ __launch_bounds__(RNT) void k_rej_rowstat(RejectParams p)
+{
+    typedef float f4v __attribute__((ext_vector_type(4)));
+    __shared__ float fred[RNT / 64];
+    __shared__ uint64_t ured[RNT / 64];
+    const uint32_t r = blockIdx.x, b = blockIdx.y, V = p.V, K = p.K;
+    const float tau = p.tau;
+    const float* row = rej_row(p, b, r);
+    float mx = -__builtin_huge_valf();
+    f4v vals[REG ? RVEC : 1];
+    const uint32_t nv = V / 4u;
+    if constexpr (REG)
     {
-        const float* qn = p.draft + (static_cast<uint64_t>(b) * K + n) * V;
-        const float mq = __builtin_nontemporal_load(&rows[n].mq);
-        const uint64_t Sq = __builtin_nontemporal_load(&rows[n].Sq);
-        const double invQ = __ddiv_rn(4294967296.0, static_cast<double>(Sq));
-        auto rfn = [&](uint32_t v) -> float {
-            const float pf = static_cast<float>(__dmul_rn(static_cast<double>(e_of(tn, v, tau, mp)), invP));
-            const float qf = static_cast<float>(__dmul_rn(static_cast<double>(e_of(qn, v, tau, mq)), invQ));
-            const float d = __fsub_rn(pf, qf);
-            return d > 0.0f ? d : 0.0f;
-        };
-        uint64_t mine = 0;
-        for (uint32_t v = threadIdx.x; v < V; v += NT) mine += to_fixed(rfn(v));
-        const uint64_t Rs = block_sum_u64(mine, ured);
-        if (Rs > 0)
+        const f4v* row4 = reinterpret_cast<const f4v*>(row);
+#pragma unroll
+        for (uint32_t i = 0; i < RVEC; ++i)
         {
-            tok = draw(V, U, [&](uint32_t v) { return to_fixed(rfn(v)); }, ured, scan, &s_tok);
-            if (dist)
+            const uint32_t q = threadIdx.x + i * RNT;
+            vals[i] = q < nv ? row4[q] : f4v{-__builtin_huge_valf(), -__builtin_huge_valf(), -__builtin_huge_valf(),
+                                             -__builtin_huge_valf()};
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
             {
-                const double invR = __ddiv_rn(4294967296.0, static_cast<double>(Rs));
-                for (uint32_t v = threadIdx.x; v < V; v += NT)
-                    dist[v] = static_cast<float>(__dmul_rn(static_cast<double>(rfn(v)), invR));
+                vals[i][e] = scaled_logit<DIV>(vals[i][e], tau);
+                mx = fmaxf(mx, vals[i][e]);
             }
-        }
-        else
-        {
-            tok = draw(V, U, [&](uint32_t v) { return to_fixed(e_of(tn, v, tau, mp)); }, ured, scan, &s_tok);
-            if (dist)
-                for (uint32_t v = threadIdx.x; v < V; v += NT)
-                    dist[v] = static_cast<float>(__dmul_rn(static_cast<double>(e_of(tn, v, tau, mp)), invP));
         }
     }
     else
     {
-        tok = draw(V, U, [&](uint32_t v) { return to_fixed(e_of(tn, v, tau, mp)); }, ured, scan, &s_tok);
-        if (dist)
-            for (uint32_t v = threadIdx.x; v < V; v += NT)
-                dist[v] = static_cast<float>(__dmul_rn(static_cast<double>(e_of(tn, v, tau, mp)), invP));
+        for (uint32_t v = threadIdx.x; v < V; v += RNT) mx = fmaxf(mx, scaled_logit<DIV>(row[v], tau));
     }
+    mx = block_max_n<RNT>(mx, fred);
+    double sd = 0.0;
+    if constexpr (REG)
+    {
+        // padding lanes hold -inf: exp gives 0, fixed 0
+#pragma unroll
+        for (uint32_t i = 0; i < RVEC; ++i)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) sd += fixed_d(expf_ref_nonpos(__fsub_rn(vals[i][e], mx)));
+    }
+    else
+    {
+        for (uint32_t v = threadIdx.x; v < V; v += RNT)
+            sd += fixed_d(expf_ref_nonpos(__fsub_rn(scaled_logit<DIV>(row[v], tau), mx)));
+    }
+    const uint64_t s = block_sum_u64_n<RNT>(fixed_sum_u64(sd), ured);
     if (threadIdx.x == 0)
+    {
+        float ex = 0.0f;
+        const uint32_t j = r <= K ? r : r - K - 1u;
+        if (r != K)
+        {
+            const int32_t x = p.drafts[static_cast<uint64_t>(b) * p.drafts_stride + j];
+            if (x >= 0 && static_cast<uint32_t>(x) < V) ex = expf_ref(__fsub_rn(scaled_logit<DIV>(row[x], tau), mx));
+        }
+        p.stats[static_cast<uint64_t>(b) * (2u * K + 1u) + r] = RowStat{mx, ex, s};
+    }
+}
+
+constexpr uint32_t REJ_MAX_K = 63;              // drafts per sequence (k + 1 <= 64)
+constexpr uint32_t REJ_MAX_SLICES = 64;         // vocab <= 64 * SLICE
+
+// Sequence b's row statistics, drafts and slice sums, staged in LDS by one
+// round of loads of the whole workgroup.
+struct SeqShared {
+    RowStat st[2 * REJ_MAX_K + 1];
+    int32_t dr[REJ_MAX_K];
+    SlicePart parts[REJ_MAX_SLICES];
+};
+
+__device__ __forceinline__ void rej_stage(const RejectParams& p, uint32_t b, bool with_parts, SeqShared& sh)
+{
+    const uint32_t K = p.K, nrow = 2u * K + 1u;
+    for (uint32_t i = threadIdx.x; i < nrow; i += NT) sh.st[i] = p.stats[static_cast<uint64_t>(b) * nrow + i];
+    for (uint32_t i = threadIdx.x; i < K; i += NT) sh.dr[i] = p.drafts[static_cast<uint64_t>(b) * p.drafts_stride + i];
+    if (with_parts)
+        for (uint32_t i = threadIdx.x; i < p.slices; i += NT) sh.parts[i] = p.parts[static_cast<uint64_t>(b) * p.slices + i];
+}
+
+// n = index of the first rejected draft of sequence b (K if all are
+// accepted), from the staged statistics
+__device__ uint32_t rej_first_reject(const RejectParams& p, uint32_t b, uint32_t pb, const SeqShared& sh)
+{
+    for (uint32_t j = 0; j < p.K; ++j)
+    {
+        const int32_t x = sh.dr[j];
+        bool acc = false;
+        if (x >= 0 && static_cast<uint32_t>(x) < p.V)
+        {
+            const RowStat P = sh.st[j], Q = sh.st[p.K + 1u + j];
+            const float u = uniform24(philox_u32(p.seed, pb + j, b, 1u));
+            const double lhs = __dmul_rn(__dmul_rn(static_cast<double>(u), static_cast<double>(Q.ex)), static_cast<double>(P.S));
+            const double rhs = __dmul_rn(static_cast<double>(P.ex), static_cast<double>(Q.S));
+            acc = lhs < rhs;
+        }
+        if (!acc) return j;
+    }
+    return p.K;
+}
+
+template <bool DIV>
+__global__ __launch_bounds__(NT) void k_rej_slice(RejectParams p)
+{
+    __shared__ uint64_t ured[NT / 64];
+    __shared__ SeqShared sh;
+    const uint32_t sl = blockIdx.x, b = blockIdx.y, K = p.K, V = p.V;
+    const float tau = p.tau;
+    const uint32_t pb = p.pos_base ? p.pos_base[b] : 0u;
+    rej_stage(p, b, false, sh);
+    __syncthreads();
+    const uint32_t n = rej_first_reject(p, b, pb, sh);
+    const RowStat* st = sh.st;
+    const float* tn = rej_row(p, b, n);
+    const RowStat P = st[n];
+    const double invP = __ddiv_rn(4294967296.0, static_cast<double>(P.S));
+    float* w = p.wbuf + static_cast<uint64_t>(b) * V;
+    const uint32_t v0 = sl * SLICE;
+    constexpr uint32_t PER = SLICE / NT;
+    // every load of the slice is issued before the first use
+    float tl[PER], ql[PER];
+#pragma unroll
+    for (uint32_t i = 0; i < PER; ++i)
+    {
+        const uint32_t v = min(v0 + i * NT + threadIdx.x, V - 1u);
+        tl[i] = tn[v];
+    }
+    double rs = 0.0, ps = 0.0;
+    if (n < K)
+    {
+        const float* qn = rej_row(p, b, K + 1u + n);
+        const RowStat Q = st[K + 1u + n];
+        const double invQ = __ddiv_rn(4294967296.0, static_cast<double>(Q.S));
+#pragma unroll
+        for (uint32_t i = 0; i < PER; ++i) ql[i] = qn[min(v0 + i * NT + threadIdx.x, V - 1u)];
+#pragma unroll
+        for (uint32_t i = 0; i < PER; ++i)
+        {
+            const uint32_t v = v0 + i * NT + threadIdx.x;
+            if (v >= V) continue;
+            const float ep = expf_ref_nonpos(__fsub_rn(scaled_logit<DIV>(tl[i], tau), P.m));
+            const float eq = expf_ref_nonpos(__fsub_rn(scaled_logit<DIV>(ql[i], tau), Q.m));
+            const float pf = static_cast<float>(__dmul_rn(static_cast<double>(ep), invP));
+            const float qf = static_cast<float>(__dmul_rn(static_cast<double>(eq), invQ));
+            const float d = __fsub_rn(pf, qf);
+            const float r = d > 0.0f ? d : 0.0f;
+            w[v] = r;
+            rs += fixed_d(r);
+            ps += fixed_d(ep);
+        }
+    }
+    else
+    {
+#pragma unroll
+        for (uint32_t i = 0; i < PER; ++i)
+        {
+            const uint32_t v = v0 + i * NT + threadIdx.x;
+            if (v >= V) continue;
+            const float ep = expf_ref_nonpos(__fsub_rn(scaled_logit<DIV>(tl[i], tau), P.m));
+            w[v] = ep;
+            ps += fixed_d(ep);
+        }
+    }
+    const uint64_t rsum = block_sum_u64_n<NT>(fixed_sum_u64(rs), ured);
+    const uint64_t psum = block_sum_u64_n<NT>(fixed_sum_u64(ps), ured);
+    if (threadIdx.x == 0) p.parts[static_cast<uint64_t>(b) * p.slices + sl] = SlicePart{rsum, psum};
+}
+
+// inclusive prefix of one u64 per thread over the 256 threads
+__device__ uint64_t block_inclusive_scan_u64(uint64_t v, uint64_t* wsum)
+{
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1)
+    {
+        const uint32_t lo = __shfl_up(static_cast<uint32_t>(v), o);
+        const uint32_t hi = __shfl_up(static_cast<uint32_t>(v >> 32), o);
+        if (lane >= static_cast<uint32_t>(o)) v += (static_cast<uint64_t>(hi) << 32) | lo;
+    }
+    __syncthreads();
+    if (lane == 63u) wsum[wave] = v;
+    __syncthreads();
+    for (uint32_t w = 0; w < wave; ++w) v += wsum[w];
+    return v;
+}
+
+constexpr uint32_t PER = SLICE / NT;             // elements of a slice per thread
+
+// exclusive prefix of one u64 per thread over the 256 threads
+__device__ uint64_t block_exclusive_scan_u64_fast(uint64_t v, uint64_t* wsum)
+{
+    const uint64_t inc = block_inclusive_scan_u64(v, wsum);
+    return inc - v;
+}
+
+// The draw of sequence b within one slice.  Thread t holds the weights of the
+// contiguous elements v0 + PER*t .. +PER-1 (wl), so one scan of the threads'
+// sums locates the thread whose run holds the threshold, and that thread
+// walks its run in order.  W(v) = fixed(wl).
+__device__ __forceinline__ void rej_draw_slice(const RejectParams& p, uint32_t b, uint32_t n, uint32_t v0, uint32_t v1,
+                                               uint64_t total, uint64_t excl, uint64_t mine, uint64_t t,
+                                               const float (&wl)[PER], uint64_t* wsum, int32_t* s_tok, float* stage)
+{
+    const uint32_t K = p.K, V = p.V;
+    bool finder = mine > 0 && excl <= t && t < excl + mine;
+    int32_t tok = static_cast<int32_t>(V - 1u);
+    const uint32_t vt = v0 + PER * threadIdx.x;
+    if (finder)
+    {
+        uint64_t run = 0;
+#pragma unroll
+        for (uint32_t i = 0; i < PER; ++i) run += vt + i < v1 ? to_fixed(wl[i]) : 0ull;
+        if (threadIdx.x == 0) *s_tok = -1;
+        uint64_t pre = excl + block_exclusive_scan_u64_fast(run, wsum);
+        if (run > 0 && pre <= t && t < pre + run)
+        {
+#pragma unroll
+            for (uint32_t i = 0; i < PER; ++i)
+            {
+                const uint64_t wv = vt + i < v1 ? to_fixed(wl[i]) : 0ull;
+                pre += wv;
+                if (pre > t) { *s_tok = static_cast<int32_t>(vt + i); break; }
+            }
+        }
+        __syncthreads();
+        if (*s_tok >= 0) tok = *s_tok;
+    }
+    if (total == 0 && blockIdx.x == 0) finder = true;          // no mass anywhere: the last id, as defined
+    if (p.dist)
+    {
+        // normalised through LDS, so each store instruction writes 1 KB of
+        // consecutive elements
+        typedef float f4v __attribute__((ext_vector_type(4)));
+        const double inv = __ddiv_rn(4294967296.0, static_cast<double>(total));
+#pragma unroll
+        for (uint32_t i = 0; i < PER; ++i)
+            stage[PER * threadIdx.x + i] = static_cast<float>(__dmul_rn(static_cast<double>(wl[i]), inv));
+        __syncthreads();
+        float* d = p.dist + static_cast<uint64_t>(b) * V;
+        if (v1 - v0 == SLICE && (V & 3u) == 0)
+        {
+#pragma unroll
+            for (uint32_t j = 0; j < PER / 4u; ++j)
+            {
+                const uint32_t e = 4u * (threadIdx.x + NT * j);
+                *reinterpret_cast<f4v*>(d + v0 + e) = *reinterpret_cast<const f4v*>(stage + e);
+            }
+        }
+        else
+        {
+            for (uint32_t e = threadIdx.x; e < v1 - v0; e += NT) d[v0 + e] = stage[e];
+        }
+    }
+    if (finder && threadIdx.x == 0)
     {
         for (uint32_t i = 0; i <= K; ++i)
             p.out_tokens[b * (K + 1u) + i] =
                 i < n ? p.drafts[static_cast<uint64_t>(b) * p.drafts_stride + i] : (i == n ? tok : -1);
         p.accepted[b] = static_cast<int32_t>(n);
         if (p.new_seq_len) p.new_seq_len[b] = p.seq_len[b] + static_cast<int32_t>(n) + 1;
-        p.counters[b] = 0u;
+    }
+}
+
+template <bool DIV>
+__global__ __launch_bounds__(NT) void k_rej_draw(RejectParams p)
+{
+    __shared__ uint64_t wsum[NT / 64];
+    __shared__ int32_t s_tok;
+    __shared__ SeqShared sh;
+    __shared__ __align__(16) float stage[SLICE];
+    const uint32_t sl = blockIdx.x, b = blockIdx.y, K = p.K, V = p.V;
+    const float tau = p.tau;
+    const uint32_t pb = p.pos_base ? p.pos_base[b] : 0u;
+    const uint32_t v0 = sl * SLICE, v1 = min(V, v0 + SLICE);
+    // the stored draw weights of the slice (used unless the residual is empty),
+    // loaded together with the staged statistics
+    typedef float f4v __attribute__((ext_vector_type(4)));
+    float wl[PER];
+    const float* w = p.wbuf + static_cast<uint64_t>(b) * V;
+    const uint32_t vt = v0 + PER * threadIdx.x;
+    if (vt + PER <= V && (V & 3u) == 0)
+    {
+        const f4v* w4 = reinterpret_cast<const f4v*>(w + vt);
+#pragma unroll
+        for (uint32_t i = 0; i < PER / 4u; ++i)
+        {
+            const f4v q = w4[i];
+            wl[4 * i] = q[0]; wl[4 * i + 1] = q[1]; wl[4 * i + 2] = q[2]; wl[4 * i + 3] = q[3];
+        }
+    }
+    else
+    {
+#pragma unroll
+        for (uint32_t i = 0; i < PER; ++i) wl[i] = w[min(vt + i, V - 1u)];
+    }
+    rej_stage(p, b, true, sh);
+    __syncthreads();
+    const uint32_t n = rej_first_reject(p, b, pb, sh);
+    const RowStat P = sh.st[n];
+    const SlicePart* parts = sh.parts;
+    uint64_t Rt = 0, Pt = 0, Rx = 0, Px = 0;
+    for (uint32_t s = 0; s < p.slices; ++s)
+    {
+        const SlicePart q = parts[s];
+        Rt += q.R;
+        Pt += q.P;
+        if (s < sl) { Rx += q.R; Px += q.P; }
+    }
+    const uint32_t U = philox_u32(p.seed, pb + n, b, 2u);
+    auto threshold = [&](uint64_t total) {
+        const uint64_t hi = __umul64hi(static_cast<uint64_t>(U), total);
+        const uint64_t lo = static_cast<uint64_t>(U) * total;
+        return (hi << 32) | (lo >> 32);
+    };
+    if (n < K && Rt == 0)
+    {
+        // the residual has no mass: draw from p_n, recomputed from its logits
+        const float* tn = rej_row(p, b, n);
+#pragma unroll
+        for (uint32_t i = 0; i < PER; ++i)
+        {
+            const uint32_t v = v0 + PER * threadIdx.x + i;
+            wl[i] = v < v1 ? expf_ref_nonpos(__fsub_rn(scaled_logit<DIV>(tn[v], tau), P.m)) : 0.0f;
+        }
+        rej_draw_slice(p, b, n, v0, v1, Pt, Px, parts[sl].P, threshold(Pt), wl, wsum, &s_tok, stage);
+    }
+    else
+    {
+        // the stored weights: the residual of row n, or p_K after K accepts
+        const bool resid = n < K;
+        const uint64_t total = resid ? Rt : Pt;
+        rej_draw_slice(p, b, n, v0, v1, total, resid ? Rx : Px, resid ? parts[sl].R : parts[sl].P, threshold(total), wl,
+                       wsum, &s_tok, stage);
     }
 }
 
@@ -502,9 +818,14 @@ namespace opure_hip {
 
 uint32_t argmax_parts(uint32_t V) { return (V + 4095u) / 4096u; }
 
+uint32_t rej_slices(uint32_t V) { return (V + SLICE - 1u) / SLICE; }
+
 uint64_t accept_ws_bytes(uint32_t batch, uint32_t k, uint32_t vocab, uint32_t mode)
 {
-    if (mode == OPURE_ACCEPT_REJECTION) return align_up(static_cast<uint64_t>(batch) * (k + 1u) * sizeof(RejRow), 256);
+    if (mode == OPURE_ACCEPT_REJECTION)
+        return align_up(static_cast<uint64_t>(batch) * (2u * k + 1u) * sizeof(RowStat), 256) +
+               align_up(static_cast<uint64_t>(batch) * rej_slices(vocab) * sizeof(SlicePart), 256) +
+               align_up(static_cast<uint64_t>(batch) * vocab * 4u, 256);
     return 2u * align_up(static_cast<uint64_t>(argmax_parts(vocab)) * batch * (k + 1u) * 4u, 256);
 }
 
@@ -520,6 +841,8 @@ int accept_validate(const opure_accept_args* a, bool rejection)
         OPURE_REQUIRE(a->draft_logits || a->k == 0, OPURE_E_INVALID, "accept: rejection needs draft logits");
         OPURE_REQUIRE(a->temperature > 0.0f && a->temperature == a->temperature, OPURE_E_INVALID,
                       "accept: temperature must be > 0");
+        OPURE_REQUIRE(rej_slices(a->vocab) <= REJ_MAX_SLICES, OPURE_E_CAPACITY,
+                      "accept: rejection sampling supports vocab <= %u", REJ_MAX_SLICES * SLICE);
     }
     return OPURE_OK;
 }
@@ -586,28 +909,46 @@ int accept_greedy_launch(opure_dev* dev, const opure_accept_args* a, void* ws)
                                 a->out_tokens, a->accepted, nullptr);
 }
 
-int accept_rejection_launch(opure_dev* dev, const opure_accept_args* a, void* ws, uint32_t* counters,
-                            const int32_t* seq_len, int32_t* new_seq_len)
+int accept_rejection_launch(opure_dev* dev, const opure_accept_args* a, void* ws, const int32_t* seq_len,
+                            int32_t* new_seq_len)
 {
+    const uint32_t B = a->batch, K = a->k, V = a->vocab;
     RejectParams r;
     r.target = a->target_logits;
     r.draft = a->draft_logits;
     r.drafts = a->drafts;
     r.drafts_stride = a->drafts_stride;
-    r.K = a->k;
-    r.V = a->vocab;
+    r.K = K;
+    r.V = V;
+    r.slices = rej_slices(V);
     r.tau = a->temperature;
     r.seed = a->seed;
     r.pos_base = a->pos_base;
     r.out_tokens = a->out_tokens;
     r.accepted = a->accepted;
     r.dist = a->dist_out;
-    r.ws = static_cast<RejRow*>(ws);
-    r.counters = counters;
+    char* w = static_cast<char*>(ws);
+    r.stats = reinterpret_cast<RowStat*>(w);
+    w += align_up(static_cast<uint64_t>(B) * (2u * K + 1u) * sizeof(RowStat), 256);
+    r.parts = reinterpret_cast<SlicePart*>(w);
+    w += align_up(static_cast<uint64_t>(B) * r.slices * sizeof(SlicePart), 256);
+    r.wbuf = reinterpret_cast<float*>(w);
     r.seq_len = seq_len;
     r.new_seq_len = new_seq_len;
-    hipLaunchKernelGGL(k_accept_rejection, dim3(a->k + 1u, a->batch), dim3(NT), 0, dev->stream, r);
-    OPURE_LAUNCH_CHECK("k_accept_rejection");
+    const bool aligned = ((reinterpret_cast<uintptr_t>(a->target_logits) | reinterpret_cast<uintptr_t>(a->draft_logits)) & 15u) == 0;
+    const bool reg = V % 4u == 0 && V <= 4u * RNT * RVEC && aligned, div = r.tau != 1.0f;
+    const dim3 rows(2u * K + 1u, B), slices(r.slices, B);
+    if (reg && div) hipLaunchKernelGGL((k_rej_rowstat<true, true>), rows, dim3(RNT), 0, dev->stream, r);
+    if (reg && !div) hipLaunchKernelGGL((k_rej_rowstat<true, false>), rows, dim3(RNT), 0, dev->stream, r);
+    if (!reg && div) hipLaunchKernelGGL((k_rej_rowstat<false, true>), rows, dim3(RNT), 0, dev->stream, r);
+    if (!reg && !div) hipLaunchKernelGGL((k_rej_rowstat<false, false>), rows, dim3(RNT), 0, dev->stream, r);
+    OPURE_LAUNCH_CHECK("k_rej_rowstat");
+    if (div) hipLaunchKernelGGL(k_rej_slice<true>, slices, dim3(NT), 0, dev->stream, r);
+    else hipLaunchKernelGGL(k_rej_slice<false>, slices, dim3(NT), 0, dev->stream, r);
+    OPURE_LAUNCH_CHECK("k_rej_slice");
+    if (div) hipLaunchKernelGGL(k_rej_draw<true>, slices, dim3(NT), 0, dev->stream, r);
+    else hipLaunchKernelGGL(k_rej_draw<false>, slices, dim3(NT), 0, dev->stream, r);
+    OPURE_LAUNCH_CHECK("k_rej_draw");
     return OPURE_OK;
 }
 
@@ -639,7 +980,7 @@ int opure_accept_greedy(opure_dev* dev, const opure_accept_args* a)
     OPURE_REQUIRE(dev, OPURE_E_INVALID, "opure_accept_greedy: null device");
     int rc = accept_validate(a, false);
     if (rc) return rc;
-    rc = ensure_workspace(dev, accept_ws_bytes(a->batch, a->k, a->vocab, OPURE_ACCEPT_GREEDY), 0);
+    rc = ensure_workspace(dev, accept_ws_bytes(a->batch, a->k, a->vocab, OPURE_ACCEPT_GREEDY));
     if (rc) return rc;
     return accept_greedy_launch(dev, a, dev->ws);
 }
@@ -649,9 +990,9 @@ int opure_accept_rejection(opure_dev* dev, const opure_accept_args* a)
     OPURE_REQUIRE(dev, OPURE_E_INVALID, "opure_accept_rejection: null device");
     int rc = accept_validate(a, true);
     if (rc) return rc;
-    rc = ensure_workspace(dev, accept_ws_bytes(a->batch, a->k, a->vocab, OPURE_ACCEPT_REJECTION), a->batch);
+    rc = ensure_workspace(dev, accept_ws_bytes(a->batch, a->k, a->vocab, OPURE_ACCEPT_REJECTION));
     if (rc) return rc;
-    return accept_rejection_launch(dev, a, dev->ws, dev->counters, nullptr, nullptr);
+    return accept_rejection_launch(dev, a, dev->ws, nullptr, nullptr);
 }
 
 int opure_sample_rows(opure_dev* dev, const opure_sample_args* a)

@@ -776,7 +776,7 @@ extern "C" int opure_attn_decode_paged(opure_dev* dev, const opure_attn_args* a)
                   a->layer);
     const uint32_t group = a->model->n_heads / a->model->n_kv_heads;
     rc = ensure_workspace(dev, attn_partial_bytes(a->batch, a->model->n_kv_heads, group, a->rows, a->model->head_dim,
-                                                  a->model->afmt, a->max_ctx), 0);
+                                                  a->model->afmt, a->max_ctx));
     if (rc) return rc;
     return attn_launch(dev, a->model, a->kv, a->layer, a->batch, a->rows, a->seq_len, a->max_ctx, a->q, a->out,
                        static_cast<float*>(dev->ws));

@@ -22,12 +22,10 @@ struct opure_dev {
     uint64_t    hbm = 0;
     int         n_cu = 0;
     bool        capturing = false;
-    // Grow-only workspace used by the kernels (split-K partials, attention
-    // partials, activations of a verify step) and a zeroed counter array.
+    // Grow-only workspace used by the kernels (attention partials, acceptance
+    // statistics, activations of a verify step).
     void*       ws = nullptr;
     uint64_t    ws_bytes = 0;
-    uint32_t*   counters = nullptr;     // zero between launches
-    uint64_t    counter_words = 0;
     // stage timing of eager verify steps: event pairs and the stage of each pair
     bool                   prof_on = false;
     std::vector<hipEvent_t> prof_ev;
@@ -45,7 +43,7 @@ namespace opure_hip {
 int set_error(int code, const char* fmt, ...);
 int hip_fail(hipError_t e, const char* what);
 const char* afmt_name(uint32_t afmt);
-int  ensure_workspace(opure_dev* dev, uint64_t bytes, uint64_t counter_words);
+int  ensure_workspace(opure_dev* dev, uint64_t bytes);
 // bracket one stage's launches with events (no-op unless profiling, or while capturing)
 int  prof_begin(opure_dev* dev, uint32_t stage);
 int  prof_end(opure_dev* dev);
@@ -144,8 +142,8 @@ int      greedy_from_partials(opure_dev* dev, const float* am_val, const int32_t
                               uint32_t batch, uint32_t K, const int32_t* drafts, uint32_t stride, int32_t* out_tokens,
                               int32_t* accepted, const opure_rollback_args* rb);
 int      accept_greedy_launch(opure_dev* dev, const opure_accept_args* a, void* ws);
-int      accept_rejection_launch(opure_dev* dev, const opure_accept_args* a, void* ws, uint32_t* counters,
-                                 const int32_t* seq_len, int32_t* new_seq_len);
+int      accept_rejection_launch(opure_dev* dev, const opure_accept_args* a, void* ws, const int32_t* seq_len,
+                                 int32_t* new_seq_len);
 int      rollback_validate(const opure_rollback_args* a);
 int      rollback_launch(opure_dev* dev, const opure_rollback_args* a);
 
@@ -182,6 +180,29 @@ __device__ __forceinline__ float expf_ref(float x)
     const int k = static_cast<int>(kf);
     if (k > 127) return __fmul_rn(__fmul_rn(p, bits_f(254u << 23)), 2.0f);
     return __fmul_rn(p, bits_f(static_cast<uint32_t>(k + 127) << 23));
+}
+
+// expf_ref restricted to x <= 0 (and NaN): the same operations in the same
+// order, without the overflow paths, so the bits equal expf_ref's there
+__device__ __forceinline__ float expf_ref_nonpos(float x)
+{
+    const float LOG2E = static_cast<float>(1.4426950408889634);
+    const float LN2_HI = 0.693145751953125f;
+    const float LN2_LO = static_cast<float>(0.6931471805599453 - 0.693145751953125);
+    const float kf = __builtin_rintf(__fmul_rn(x, LOG2E));
+    float r = __fmaf_rn(-kf, LN2_HI, x);
+    r = __fmaf_rn(-kf, LN2_LO, r);
+    float p = static_cast<float>(1.0 / 5040.0);
+    p = __fmaf_rn(p, r, static_cast<float>(1.0 / 720.0));
+    p = __fmaf_rn(p, r, static_cast<float>(1.0 / 120.0));
+    p = __fmaf_rn(p, r, static_cast<float>(1.0 / 24.0));
+    p = __fmaf_rn(p, r, static_cast<float>(1.0 / 6.0));
+    p = __fmaf_rn(p, r, 0.5f);
+    p = __fmaf_rn(p, r, 1.0f);
+    p = __fmaf_rn(p, r, 1.0f);
+    const int k = x < -87.33654022216797f ? 0 : static_cast<int>(kf);
+    const float v = __fmul_rn(p, bits_f(static_cast<uint32_t>(k + 127) << 23));
+    return x != x ? x : (x < -87.33654022216797f ? 0.0f : v);
 }
 
 __device__ __forceinline__ uint32_t philox_u32(uint64_t seed, uint32_t c0, uint32_t c1, uint32_t c2)

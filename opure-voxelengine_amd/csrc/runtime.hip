@@ -44,7 +44,7 @@ __global__ void k_fill_u32(uint32_t* p, uint32_t v, uint64_t n)
         p[i] = v;
 }
 
-int ensure_workspace(opure_dev* dev, uint64_t bytes, uint64_t counter_words)
+int ensure_workspace(opure_dev* dev, uint64_t bytes)
 {
     bytes = align_up(bytes ? bytes : 256, 256);
     if (bytes > dev->ws_bytes)
@@ -59,23 +59,6 @@ int ensure_workspace(opure_dev* dev, uint64_t bytes, uint64_t counter_words)
         dev->ws_bytes = 0;
         OPURE_HIP_TRY(hipMalloc(&dev->ws, bytes));
         dev->ws_bytes = bytes;
-    }
-    if (counter_words > dev->counter_words)
-    {
-        OPURE_REQUIRE(!dev->capturing, OPURE_E_CAPACITY,
-                      "counter array too small during graph capture: call opure_verify_reserve first");
-        OPURE_HIP_TRY(hipStreamSynchronize(dev->stream));
-        if (dev->counters) OPURE_HIP_TRY(hipFree(dev->counters));
-        dev->counters = nullptr;
-        dev->counter_words = 0;
-        const uint64_t words = align_up(counter_words, 1024);
-        OPURE_HIP_TRY(hipMalloc(&dev->counters, words * 4));
-        // counters must read zero before the first kernel that uses them; each
-        // user leaves them zero again when it finishes
-        hipLaunchKernelGGL(k_fill_u32, dim3(64), dim3(256), 0, dev->stream, dev->counters, 0u, words);
-        OPURE_LAUNCH_CHECK("k_fill_u32");
-        OPURE_HIP_TRY(hipStreamSynchronize(dev->stream));
-        dev->counter_words = words;
     }
     return OPURE_OK;
 }
@@ -151,7 +134,6 @@ int opure_dev_destroy(opure_dev* dev)
     hipSetDevice(dev->ordinal);
     hipStreamSynchronize(dev->stream);
     if (dev->ws) hipFree(dev->ws);
-    if (dev->counters) hipFree(dev->counters);
     for (hipEvent_t e : dev->prof_ev) hipEventDestroy(e);
     if (dev->ev_begin) hipEventDestroy(dev->ev_begin);
     if (dev->ev_end) hipEventDestroy(dev->ev_end);

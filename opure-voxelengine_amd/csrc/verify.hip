@@ -106,7 +106,6 @@ namespace opure_hip {
 
 struct VerifyPlan {
     uint64_t x = 0, ss = 0, xn = 0, q = 0, att = 0, h = 0, am_val = 0, am_idx = 0, attn = 0, rej = 0, total = 0;
-    uint64_t counters = 0;
     uint32_t lm_tiles = 0;
 };
 
@@ -130,7 +129,6 @@ static VerifyPlan make_plan(const opure_model* m, uint32_t B, uint32_t R, uint32
     p.attn = take(attn_partial_bytes(B, m->n_kv_heads, m->n_heads / m->n_kv_heads, R, m->head_dim, m->afmt, max_ctx));
     p.rej = take(accept_ws_bytes(B, R - 1u, m->vocab, OPURE_ACCEPT_REJECTION));
     p.total = off;
-    p.counters = B;
     return p;
 }
 
@@ -190,7 +188,7 @@ int opure_verify_reserve(opure_dev* dev, const opure_model* model, uint32_t batc
     OPURE_REQUIRE(batch >= 1 && rows >= 1 && batch * rows <= OPURE_MAX_ROWS, OPURE_E_CAPACITY,
                   "opure_verify_reserve: batch*rows = %u exceeds %d", batch * rows, OPURE_MAX_ROWS);
     const VerifyPlan p = make_plan(model, batch, rows, max_ctx);
-    return ensure_workspace(dev, p.total, p.counters);
+    return ensure_workspace(dev, p.total);
 }
 
 int opure_debug_workspace(opure_dev* dev, void** ptr, uint64_t* bytes)
@@ -237,7 +235,7 @@ int opure_verify_step(opure_dev* dev, const opure_verify_args* a)
                       "verify: rollback needs acceptance and new_seq_len");
 
     const VerifyPlan P = make_plan(m, B, R, a->max_ctx);
-    rc = ensure_workspace(dev, P.total, P.counters);
+    rc = ensure_workspace(dev, P.total);
     if (rc) return rc;
     char* ws = static_cast<char*>(dev->ws);
     float* x = reinterpret_cast<float*>(ws + P.x);
@@ -386,7 +384,7 @@ int opure_verify_step(opure_dev* dev, const opure_verify_args* a)
         aa.out_tokens = a->out_tokens;
         aa.accepted = a->accepted;
         aa.dist_out = a->dist_out;
-        rc = accept_rejection_launch(dev, &aa, ws + P.rej, dev->counters, nullptr, nullptr);
+        rc = accept_rejection_launch(dev, &aa, ws + P.rej, nullptr, nullptr);
         if (rc) return rc;
         if (a->rollback && (rc = rollback_launch(dev, &rb))) return rc;
     }
