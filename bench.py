@@ -233,6 +233,79 @@ def cpu_baseline(dev, w, gpu_logits, gpu_accept):
         tokens_equal=bool(out[0].tolist() == gpu_accept["out_tokens"]))
 
 
+def bench_c1(args):
+    """Greedy speculative generation through the native engine
+    (libopure_engine.so): SmolLM-135M-shaped fp32 target (30 layers) and a
+    2-layer draft of the same width, both seeded N(0,0.02), a 32-token random
+    prompt, K=4 drafts per verify step, 64 new tokens.  A step is one whole
+    generation of 64 tokens (prefill excluded); value = new tokens / s."""
+    import opure_engine as E
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import spec_loop
+    cfg = synth.CONFIGS["c1"]
+    n_new, K, P = 64, 4, 32
+    dev = H.Dev(0)
+    log("device", dev.name)
+    max_pos = P + n_new + 2 * K + 16
+    tgt = synth.SynthModel(dev, cfg, seed=1234, max_pos=max_pos)
+    drf = synth.SynthModel(dev, dict(cfg, n_layers=2), seed=4321, max_pos=max_pos)
+    prompt = np.random.default_rng(7).integers(0, cfg["vocab"], P).astype(np.int32)
+    eng = E.Engine(dev, tgt.desc, drf.desc, max_positions=max_pos, draft_tokens=K)
+    for _ in range(max(1, args.warmup // 5)):
+        eng.generate_speculative(prompt, n_new)
+        eng.generate(prompt, n_new)
+    runs = max(1, args.steps // 10)
+    spec_ms, greedy_ms, hist = [], [], None
+    for _ in range(runs):
+        out, hist, st = eng.generate_speculative(prompt, n_new)
+        spec_ms.append(st.ms_generate)
+        g, gst = eng.generate(prompt, n_new)
+        greedy_ms.append(gst.ms_generate)
+    ms = float(np.median(spec_ms))
+    gms = float(np.median(greedy_ms))
+    value = n_new / (ms * 1e-3)
+    log(f"speculative: {ms:.2f} ms for {n_new} tokens ({st.verify_steps} verify + {st.draft_steps} draft steps, "
+        f"accepted per step {hist.tolist()}); greedy: {gms:.2f} ms")
+    wbytes = synth.verify_bytes(cfg, 1, P + n_new // 2)["weights"]
+    line = {
+        "metric": "new tokens/s of greedy speculative generation (SmolLM-135M-shape fp32 + 2-layer draft, K=4)",
+        "value": round(value, 1), "unit": "tokens/s", "n_gpus": 1, "steps": runs, "warmup": args.warmup,
+        "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic: seeded N(0,0.02) target and draft, uniform random 32-token prompt",
+        "config": {"workload": "c1: native engine GenerateSpeculative, 30-layer target + 2-layer draft, 32-token "
+                               "prompt, K=4, 64 new tokens, one step = the whole generation (prefill excluded)",
+                   "accepted_per_verify_step": hist.tolist(), "verify_steps": int(st.verify_steps),
+                   "draft_steps": int(st.draft_steps), "greedy_ms": round(gms, 4),
+                   "greedy_tokens_per_s": round(n_new / (gms * 1e-3), 1),
+                   "target_weight_bytes": int(wbytes)},
+    }
+    if args.cpu_baseline == "auto":
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import oracle as O
+        hm = O.HostModel.from_arrays(tgt.cfg, tgt.download())
+        npg = (max_pos + 15) // 16
+        kv = O.HostKV(hm, n_pages=npg, batch=1, max_pages_per_seq=npg)
+        kv.page_table[0] = np.arange(npg)
+        O.set_threads(1)
+        n_cpu = 4
+
+        def step(_k, toks, ctx):
+            return O.verify_forward(hm, kv, toks, np.array([ctx], np.int32))
+
+        t0 = time.perf_counter()
+        want, _ = spec_loop.greedy(step, list(prompt), n_cpu)
+        dt = time.perf_counter() - t0
+        line["cpu_baseline"] = {"value": round(n_cpu / dt, 3), "unit": "tokens/s", "cores": 1, "kind": "port",
+                                "sample": f"greedy decoding of {n_cpu} tokens after the 32-token prompt through the "
+                                          f"scalar oracle (prefill included): {dt:.1f}s"}
+        line["parity"] = {"speculative_equals_greedy": bool(np.array_equal(out, g)),
+                          "first_tokens_equal_oracle": bool(g[:n_cpu].tolist() == want)}
+        log("cpu baseline", line["cpu_baseline"], "parity", line["parity"])
+    print(json.dumps(line), flush=True)
+    eng.close()
+    dev.close()
+
+
 def bench_c2(args):
     """The isolated acceptance stage: rejection sampling over target logits
     [64][9][49152] and draft logits [64][8][49152] (fp32, N(0,3) from Philox),
@@ -338,6 +411,8 @@ def main():
         sys.exit(2)
     if args.config == "c2":
         return bench_c2(args)
+    if args.config == "c1":
+        return bench_c1(args)
 
     dev = H.Dev(0)
     log("device", dev.name)

@@ -224,10 +224,11 @@ int opure_verify_step(opure_dev* dev, const opure_verify_args* a)
     OPURE_REQUIRE(a->accept_mode <= OPURE_ACCEPT_REJECTION, OPURE_E_INVALID, "verify: accept_mode %u", a->accept_mode);
     if (a->accept_mode != OPURE_ACCEPT_NONE)
     {
-        OPURE_REQUIRE(R >= 2 && a->out_tokens && a->accepted, OPURE_E_INVALID,
-                      "verify: acceptance needs rows >= 2, out_tokens and accepted");
+        // one row and no drafts is a plain decode step: out_tokens[0] is the
+        // argmax (greedy) or a sample at the temperature (rejection)
+        OPURE_REQUIRE(a->out_tokens && a->accepted, OPURE_E_INVALID, "verify: acceptance needs out_tokens and accepted");
         if (a->accept_mode == OPURE_ACCEPT_REJECTION)
-            OPURE_REQUIRE(a->draft_logits && a->temperature > 0.0f, OPURE_E_INVALID,
+            OPURE_REQUIRE((a->draft_logits || R == 1) && a->temperature > 0.0f, OPURE_E_INVALID,
                           "verify: rejection needs draft_logits and temperature > 0");
     }
     if (a->rollback)

@@ -1,0 +1,109 @@
+// ============================================================================
+//  voxel_engine.h -- the native generation engine over the verify path.
+//
+//  Keeps the shape of the reference's VoxelEngine (Initialize / Shutdown /
+//  IsReady / Prefill / DecodeStep / Generate, src/engine/Opure_VoxelEngine.h:
+//  127-200) with the D3D12 command lists replaced by opure_verify_step
+//  launches, and adds GenerateSpeculative: a small draft model proposes K
+//  tokens one at a time, the target scores all K+1 rows in one verify step,
+//  greedy acceptance keeps the longest agreeing prefix plus the target's own
+//  next token, and the target cache is rolled back past it.  The emitted ids
+//  are exactly the target's greedy ids whatever the draft proposes.
+//
+//  One iteration of the speculative loop is one captured hipGraph: the draft
+//  steps feed each other's argmax on the device (out_tokens -> next tokens
+//  by a device copy) and the verify step reads the drafts from the same
+//  buffer, so the host writes one small input block and reads back
+//  accepted + out_tokens once per iteration.
+// ============================================================================
+#pragma once
+
+#include <cstdint>
+#include <memory>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "opure_hip.h"
+
+namespace opure::engine {
+
+// A failed library call, carrying opure_last_error()'s message (the role of
+// opure::Error / ThrowError, src/core/Opure_Platform.h:53, :72-84).
+class Error : public std::runtime_error {
+public:
+    Error(int code, const std::string& what) : std::runtime_error(what), code_(code) {}
+    int Code() const { return code_; }
+
+private:
+    int code_;
+};
+
+void Check(int rc, const char* what);
+
+struct EngineOptions {
+    uint32_t maxPositions = 4096;   // cache capacity per model (prompt + generated + K + 1)
+    uint32_t draftTokens = 4;       // K
+    bool     useGraphs = true;      // replay captured hipGraphs for the fixed-shape steps
+    int32_t  stopToken = -1;        // < 0: none
+};
+
+struct GenerateResult {
+    std::vector<uint32_t> promptTokens;
+    std::vector<uint32_t> generated;
+    std::vector<uint32_t> acceptedPerStep;   // speculative only
+    bool     hitStop = false;
+    uint32_t verifySteps = 0;
+    uint32_t draftSteps = 0;
+    double   msPrefill = 0.0;
+    double   msGenerate = 0.0;
+    double   msPerToken = 0.0;
+};
+
+class VoxelEngine {
+public:
+    VoxelEngine();
+    ~VoxelEngine();
+    VoxelEngine(const VoxelEngine&) = delete;
+    VoxelEngine& operator=(const VoxelEngine&) = delete;
+
+    // `dev`, `target` and `draft` (may be null) are borrowed: their device
+    // buffers and host layer arrays must outlive the engine.  Allocates the
+    // KV pools and step buffers; throws Error on failure.
+    void Initialize(opure_dev* dev, const opure_model& target, const opure_model* draft, const EngineOptions& opts);
+    void Shutdown();
+    [[nodiscard]] bool IsReady() const { return ready_; }
+
+    // Greedy decoding of the target, one token per step.
+    [[nodiscard]] GenerateResult Generate(const std::vector<uint32_t>& prompt, uint32_t nNew);
+    // Greedy speculative decoding with the draft model.
+    [[nodiscard]] GenerateResult GenerateSpeculative(const std::vector<uint32_t>& prompt, uint32_t nNew);
+
+    // Writes `tokens` at positions [start, start + n) of the target (draft:
+    // `draft` true) cache; with `wantNext` returns the argmax after the last.
+    uint32_t Prefill(bool draft, const std::vector<uint32_t>& tokens, uint32_t start, bool wantNext);
+    // Appends `token` at `position` of the target cache; returns the argmax.
+    uint32_t DecodeStep(uint32_t token, uint32_t position);
+
+private:
+    struct ModelState;
+    struct Step;
+
+    void RunStep(Step& s);
+    uint32_t SpecIteration(uint32_t pendingLen, uint32_t nxt, uint32_t ctx, uint32_t dctx, const uint32_t* pending,
+                           std::vector<int32_t>& outTokens);
+
+    opure_dev* dev_ = nullptr;
+    EngineOptions opts_{};
+    bool ready_ = false;
+    std::unique_ptr<ModelState> target_, draft_;
+    // one speculative iteration's inputs (one upload) and outputs (one download)
+    void* io_ = nullptr;            // int32 [dseq K+1 | dtok K+1 | vseq | vtok K+1]
+    std::vector<std::unique_ptr<Step>> draftSteps_;   // K+1 single-row draft slots
+    std::unique_ptr<Step> verify_;                    // K+1 rows of the target
+    std::unique_ptr<Step> decode_;                    // one row of the target
+    opure_graph* iterGraph_[2] = {nullptr, nullptr};  // pending length 1 or 2
+    opure_graph* decodeGraph_ = nullptr;
+};
+
+}  // namespace opure::engine

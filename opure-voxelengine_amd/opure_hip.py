@@ -275,7 +275,15 @@ class Dev:
     def graph_destroy(self, g):
         check(lib().opure_graph_destroy(g))
 
+    def on_close(self, fn) -> None:
+        """Registers a callback run first by close() (objects that hold device
+        resources and must be released before the device)."""
+        self.__dict__.setdefault("_closers", []).append(fn)
+
     def close(self):
+        for fn in reversed(self.__dict__.get("_closers", [])):
+            fn()
+        self.__dict__["_closers"] = []
         for b in self._bufs:
             if b.ptr:
                 lib().opure_buf_free(self.h, b.ptr)

@@ -85,3 +85,53 @@ def test_struct_layouts_match_header(tmp_path):
         assert got[(cname, "size")] == C.sizeof(cls), cname
         for fname, _ in cls._fields_:
             assert got[(cname, fname)] == getattr(cls, fname).offset, (cname, fname)
+
+
+# ---- the native engine (include/opure_engine.h, libopure_engine.so) -------
+def engine_symbols():
+    text = open(os.path.join(ROOT, "include", "opure_engine.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(opure_engine_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_engine_library_exports_every_declared_symbol():
+    import opure_engine as E
+    L = E.lib()
+    names = engine_symbols()
+    assert len(names) >= 5
+    assert not [n for n in names if not hasattr(L, n)]
+
+
+def test_engine_struct_layouts_match_header(tmp_path):
+    import subprocess
+    import opure_engine as E
+    structs = {"opure_engine_options": E.Options, "opure_engine_stats": E.Stats}
+    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "opure_engine.h"', "int main(void){"]
+    for cname, cls in structs.items():
+        lines.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')
+        for fname, _ in cls._fields_:
+            lines.append(f'printf("{cname} {fname} %zu\\n", offsetof({cname}, {fname}));')
+    lines.append("return 0;}")
+    src = tmp_path / "probe.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "probe"
+    subprocess.run(["gcc", "-I", os.path.join(ROOT, "include"), str(src), "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split("\n")
+    for ln in out:
+        if not ln:
+            continue
+        cname, field, val = ln.split()
+        cls = structs[cname]
+        want = C.sizeof(cls) if field == "size" else getattr(cls, field).offset
+        assert int(val) == want, (cname, field, val, want)
+
+
+def test_engine_error_paths_without_device():
+    import opure_engine as E
+    L = E.lib()
+    h = C.c_void_p()
+    assert L.opure_engine_create(None, None, None, None, C.byref(h)) == H.E_INVALID
+    assert b"null argument" in L.opure_engine_last_error()
+    assert L.opure_engine_generate(None, None, 0, 0, None, None) == H.E_INVALID
+    assert L.opure_engine_generate_speculative(None, None, 0, 0, None, None, 0, None) == H.E_INVALID
+    assert L.opure_engine_destroy(None) == H.OK
