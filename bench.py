@@ -233,6 +233,178 @@ def cpu_baseline(dev, w, gpu_logits, gpu_accept):
         tokens_equal=bool(out[0].tolist() == gpu_accept["out_tokens"]))
 
 
+def bench_c5(args):
+    """Batched stochastic verify at the 1B int8 shape: 32 sequences with ragged
+    contexts ~U[512, 8192] (16-token pages scattered over one pool), K=6 drafts
+    each (7 rows, 224 rows in all), drafts sampled at temperature 0.8 from
+    synthetic draft logits, rejection sampling at temperature 0.8 with Philox
+    keyed by (seed, sequence, position), per-sequence rollback.  The cache
+    holds seeded random K/V (the verify work does not depend on its values).
+    One step = one verify step of all 32 sequences, replayed from a hipGraph."""
+    cfg = dict(synth.CONFIGS["c3"])
+    B, K, tau, seed = 32, 6, 0.8, 2025
+    R = K + 1
+    V, L, nkv, hd = cfg["vocab"], cfg["n_layers"], cfg["n_kv_heads"], cfg["head_dim"]
+    dev = H.Dev(0)
+    log("device", dev.name)
+    rng = np.random.default_rng(seed)
+    ctx = rng.integers(512, 8193, size=B).astype(np.int32)
+    need = (ctx + R + 15) // 16
+    n_pages = int(need.sum()) + 64
+    maxp = int(need.max()) + 1
+    max_ctx = int(ctx.max()) + R
+    model = synth.SynthModel(dev, cfg, seed=1234, max_pos=max_ctx + 64)
+    kv = H.DeviceKV(dev, cfg, n_pages, B, maxp)
+    perm = rng.permutation(n_pages).astype(np.int32)
+    pt = np.full((B, maxp), -1, np.int32)
+    o = 0
+    for b in range(B):
+        pt[b, :need[b]] = perm[o:o + need[b]]
+        o += need[b]
+    kv.set_page_table(pt)
+    # seeded random K/V in 64M-element pieces (fp32 staging, converted to fp16)
+    L_ = H.lib()
+    total = L * n_pages * 2 * nkv * 16 * hd
+    piece = 64 << 20
+    tmp = dev.alloc(piece * 4)
+    for i, off in enumerate(range(0, total, piece)):
+        n = min(piece, total - off)
+        H.check(L_.opure_synth_normal_f32(dev.h, int(tmp), n, seed, 1000 + i, 1.0, 0.0))
+        H.check(L_.opure_convert_f32(dev.h, int(tmp), int(kv.pool) + off * 2, cfg["afmt"], n))
+    tmp.free()
+    log(f"{B} sequences, contexts {ctx.min()}..{ctx.max()} (sum {int(ctx.sum())}), {n_pages} pages of 16 tokens")
+    step = Verify(dev, model, kv.desc, B, R, max_ctx)
+    draft = dev.alloc(B * K * V * 4)
+    H.check(L_.opure_synth_normal_f32(dev.h, int(draft), B * K * V, seed, 7, 2.0, 0.0))
+    pos = dev.upload((ctx[:, None] + np.arange(K)[None]).astype(np.uint32).ravel())
+    seqs = dev.upload(np.repeat(np.arange(B, dtype=np.uint32), K))
+    dtok = dev.alloc(B * K * 4)
+    sa = H.SampleArgs(B * K, V, int(draft), tau, seed, int(pos), int(seqs), 0, int(dtok))
+    H.check(L_.opure_sample_rows(dev.h, C.byref(sa)))
+    last = rng.integers(0, V, size=B).astype(np.int32)
+    drafts = dev.download(dtok, np.int32, (B, K))
+    tokens = np.concatenate([last[:, None], drafts], axis=1).astype(np.int32)
+    pos_base = dev.upload(ctx.astype(np.uint32))
+    dev.write(step.tokens, tokens)
+    dev.write(step.seq_len, ctx)
+    a = step.args(H.ACCEPT_REJECTION)
+    a.draft_logits = int(draft)
+    a.temperature = tau
+    a.seed = seed
+    a.pos_base = int(pos_base)
+    H.check(L_.opure_verify_reserve(dev.h, C.byref(model.desc), B, R, max_ctx))
+
+    def launch():
+        H.check(L_.opure_verify_step(dev.h, C.byref(a)))
+
+    launch()
+    dev.sync()
+    if args.eager:
+        g = None
+        run = launch
+    else:
+        dev.graph_begin()
+        launch()
+        g = dev.graph_end()
+
+        def run():
+            dev.graph_launch(g)
+    for _ in range(args.warmup):
+        run()
+    dev.sync()
+    t0 = time.perf_counter()
+    dev.timer_begin()
+    for _ in range(args.steps):
+        run()
+    dev.timer_end()
+    ms = dev.timer_ms() / args.steps
+    dev.sync()
+    wall = (time.perf_counter() - t0) * 1e3 / args.steps
+    acc = dev.download(step.accepted, np.int32, (B,))
+    value = float(acc.sum() + B) / (ms * 1e-3)
+    wbytes = synth.verify_bytes(cfg, B * R, 0)["weights"]
+    kvbytes = int(sum(synth.verify_bytes(cfg, R, int(c))["kv"] for c in ctx))
+    lbytes = B * R * V * 4 + B * K * V * 4
+    step_bytes = wbytes + kvbytes + lbytes
+    log(f"c5 verify step {ms * 1e3:.1f} us, accepted {acc.tolist()}, {step_bytes / (ms * 1e-3) / 1e9:.0f} GB/s")
+    stages = None
+    if not args.no_kernel_timing:
+        for _ in range(2):
+            launch()
+        dev.sync()
+        dev.profile(True)
+        for _ in range(5):
+            launch()
+        prof = dev.profile_read()
+        dev.profile(False)
+        stages = {st: dict(avg_us=msx * 1e3 / n, us_per_step=msx * 1e3 / 5, launches_per_step=n / 5)
+                  for st, (n, msx) in prof.items() if n}
+        att = stages.get("attention")
+        if att:
+            att_bytes = kvbytes / L
+            att["gbs"] = att_bytes / (att["avg_us"] * 1e-6) / 1e9
+            att["bytes_per_launch"] = int(att_bytes)
+        for st, d in stages.items():
+            log(f"stage {st:10s} x{d['launches_per_step']:4.0f}/step  {d['avg_us']:8.2f} us/launch  "
+                f"{d['us_per_step']:8.1f} us/step")
+    line = {
+        "metric": "accepted tokens/s of the batched stochastic verify step (1B int8, batch 32, K=6)",
+        "value": round(value, 1), "unit": "accepted tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "int8 weights, f16 activations, f32 accumulate",
+        "data": "synthetic: seeded N(0,0.02) int8 weights, seeded random K/V, N(0,2) draft logits",
+        "config": {"workload": f"c5: verify step of 32 sequences x 7 rows (224 rows), Llama-3.2-1B-shape int8/fp16, "
+                               f"contexts {int(ctx.min())}..{int(ctx.max())} (sum {int(ctx.sum())}), pages scattered "
+                               "over one pool, drafts at T=0.8, rejection sampling at T=0.8 + rollback, "
+                               + ("eager launches" if args.eager else "hipGraph replay"),
+                   "accepted": acc.tolist(), "step_bytes": int(step_bytes),
+                   "step_GBps": round(step_bytes / (ms * 1e-3) / 1e9, 1),
+                   "step_frac_of_hbm_peak": round(step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                   "wall_ms_per_step": round(wall, 4)},
+    }
+    if stages and "attention" in stages:
+        att = stages["attention"]
+        line["roofline"] = {"bound": "hbm", "achieved": round(att["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                            "frac": round(att["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                            "kernel": "paged attention (k_attn_mfma + k_attn_combine) of one layer, K/V bytes",
+                            "bytes_per_launch": att["bytes_per_launch"], "avg_us": round(att["avg_us"], 2)}
+        line["stages_us_per_step"] = {st: round(d["us_per_step"], 1) for st, d in stages.items()}
+    if args.cpu_baseline == "auto":
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import oracle as O
+        got = step.logits_host()
+        host = model.download()
+        hm = O.HostModel.from_arrays(cfg, host)
+        # sequence 0 alone through the oracle: its pages copied into a small host pool
+        n0 = int(need[0])
+        kvh = O.HostKV(hm, n_pages=n0, batch=1, max_pages_per_seq=n0)
+        page_bytes = 2 * nkv * 16 * hd * 2
+        for layer in range(L):
+            for i in range(n0):
+                src = (layer * n_pages + int(pt[0, i])) * page_bytes
+                kvh.pool[layer, i] = dev.download(kv.pool, np.uint16, (2, nkv, 16, hd), offset=src)
+        kvh.page_table[0] = np.arange(n0)
+        O.set_threads(1)
+        t0 = time.perf_counter()
+        want0 = O.verify_forward(hm, kvh, tokens[:1], ctx[:1])
+        dt = time.perf_counter() - t0
+        q = dev.download(draft, np.float32, (B, K, V))
+        w_out, w_acc, _ = O.accept_rejection(got, q, tokens[:, 1:], tau, seed, ctx.astype(np.uint32))
+        out = dev.download(step.out_tokens, np.int32, (B, R))
+        line["cpu_baseline"] = {"value": round((int(w_acc[0]) + 1) / dt, 4), "unit": "accepted tokens/s", "cores": 1,
+                                "kind": "port",
+                                "sample": f"sequence 0 alone ({R} rows over its {int(ctx[0])}-token context) through the "
+                                          f"scalar oracle: {dt:.1f}s"}
+        line["parity"] = {"seq0_logits_max_abs": float(np.abs(got[0] - want0[0]).max()),
+                          "accepted_equal": bool(np.array_equal(w_acc, acc)),
+                          "tokens_equal": bool(np.array_equal(w_out, out))}
+        log("cpu baseline", line["cpu_baseline"], "parity", line["parity"])
+    print(json.dumps(line), flush=True)
+    if g is not None:
+        dev.graph_destroy(g)
+    dev.close()
+
+
 def bench_c1(args):
     """Greedy speculative generation through the native engine
     (libopure_engine.so): SmolLM-135M-shaped fp32 target (30 layers) and a
@@ -400,7 +572,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--config", default="c3", choices=sorted(synth.CONFIGS) + ["c2"])
+    ap.add_argument("--config", default="c3", choices=sorted(synth.CONFIGS) + ["c2", "c5"])
     ap.add_argument("--cpu-baseline", default="auto", choices=["auto", "skip"])
     ap.add_argument("--no-kernel-timing", action="store_true")
     ap.add_argument("--eager", action="store_true", help="launch each step's kernels directly instead of a hipGraph")
@@ -413,6 +585,8 @@ def main():
         return bench_c2(args)
     if args.config == "c1":
         return bench_c1(args)
+    if args.config == "c5":
+        return bench_c5(args)
 
     dev = H.Dev(0)
     log("device", dev.name)

@@ -52,7 +52,9 @@ extern "C" {
 #define OPURE_E_UNSUPPORTED  -5   /* weight/activation combination not built */
 #define OPURE_E_CAPACITY     -6   /* rows > OPURE_MAX_ROWS, ctx past capacity, pages missing */
 
-#define OPURE_MAX_ROWS       16   /* verify rows per launch (batch * (K+1)) */
+#define OPURE_MAX_ROWS       16   /* rows of one sequence's verify step (K+1); GEMV rows scored by the K+1-row kernel */
+#define OPURE_MAX_BATCH_ROWS 256  /* rows of one verify step or GEMV (batch * (K+1)); above OPURE_MAX_ROWS the
+                                   * GEMV runs as a thin GEMM (16-bit activations, quantised weights) */
 #define OPURE_PAGE_SIZE      16   /* KV tokens per page */
 
 enum { OPURE_W_F32 = 0, OPURE_W_I8PC = 1, OPURE_W_I4G128 = 2 };

@@ -892,20 +892,30 @@ int greedy_from_partials(opure_dev* dev, const float* am_val, const int32_t* am_
     return OPURE_OK;
 }
 
+int argmax_partials_launch(opure_dev* dev, const float* logits, uint32_t rows, uint32_t V, float* am_val,
+                           int32_t* am_idx)
+{
+    ArgmaxParams ap;
+    ap.logits = logits;
+    ap.rows = rows;
+    ap.V = V;
+    ap.chunk = 4096u;
+    ap.parts = argmax_parts(V);
+    ap.am_val = am_val;
+    ap.am_idx = am_idx;
+    hipLaunchKernelGGL(k_argmax_partial, dim3(ap.parts, rows), dim3(NT), 0, dev->stream, ap);
+    OPURE_LAUNCH_CHECK("k_argmax_partial");
+    return OPURE_OK;
+}
+
 int accept_greedy_launch(opure_dev* dev, const opure_accept_args* a, void* ws)
 {
     const uint32_t rows = a->batch * (a->k + 1u), parts = argmax_parts(a->vocab);
-    ArgmaxParams ap;
-    ap.logits = a->target_logits;
-    ap.rows = rows;
-    ap.V = a->vocab;
-    ap.chunk = 4096u;
-    ap.parts = parts;
-    ap.am_val = static_cast<float*>(ws);
-    ap.am_idx = reinterpret_cast<int32_t*>(static_cast<char*>(ws) + align_up(static_cast<uint64_t>(parts) * rows * 4u, 256));
-    hipLaunchKernelGGL(k_argmax_partial, dim3(parts, rows), dim3(NT), 0, dev->stream, ap);
-    OPURE_LAUNCH_CHECK("k_argmax_partial");
-    return greedy_from_partials(dev, ap.am_val, ap.am_idx, parts, a->batch, a->k, a->drafts, a->drafts_stride,
+    float* am_val = static_cast<float*>(ws);
+    int32_t* am_idx = reinterpret_cast<int32_t*>(static_cast<char*>(ws) + align_up(static_cast<uint64_t>(parts) * rows * 4u, 256));
+    const int rc = argmax_partials_launch(dev, a->target_logits, rows, a->vocab, am_val, am_idx);
+    if (rc) return rc;
+    return greedy_from_partials(dev, am_val, am_idx, parts, a->batch, a->k, a->drafts, a->drafts_stride,
                                 a->out_tokens, a->accepted, nullptr);
 }
 

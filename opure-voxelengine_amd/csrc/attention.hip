@@ -662,8 +662,9 @@ int attn_validate(const opure_model* m, const opure_kv* kv, uint32_t batch, uint
                   "attention: head_dim %u not in 16..256 step 16", m->head_dim);
     OPURE_REQUIRE(kv->page_size == OPURE_PAGE_SIZE, OPURE_E_UNSUPPORTED, "attention: page_size must be %d",
                   OPURE_PAGE_SIZE);
-    OPURE_REQUIRE(batch >= 1 && rows >= 1 && batch * rows <= OPURE_MAX_ROWS, OPURE_E_CAPACITY,
-                  "attention: batch*rows = %u exceeds %d", batch * rows, OPURE_MAX_ROWS);
+    OPURE_REQUIRE(batch >= 1 && rows >= 1 && rows <= OPURE_MAX_ROWS && batch * rows <= OPURE_MAX_BATCH_ROWS,
+                  OPURE_E_CAPACITY, "attention: %u rows per sequence x batch %u beyond %d / %d", rows, batch,
+                  OPURE_MAX_ROWS, OPURE_MAX_BATCH_ROWS);
     OPURE_REQUIRE(max_ctx >= rows && max_ctx <= kv->max_pages_per_seq * OPURE_PAGE_SIZE, OPURE_E_CAPACITY,
                   "attention: max_ctx %u beyond the page-table capacity %u", max_ctx,
                   kv->max_pages_per_seq * OPURE_PAGE_SIZE);

@@ -4,7 +4,7 @@
 //  kernel itself is gemv_kernel.h, instantiated per weight format in
 //  gemv_f32.hip, gemv_i8.hip, gemv_i4h.hip and gemv_i4b.hip.
 // ============================================================================
-#include "gemv_kernel.h"
+#include "gemm_wide.h"
 
 #include <algorithm>
 
@@ -16,6 +16,9 @@ int launch_f32(opure_dev*, uint32_t, bool, bool, const KParams&, const Recipe&, 
 int launch_i8(opure_dev*, uint32_t, bool, bool, const KParams&, const Recipe&, uint32_t, uint32_t);
 int launch_i4_f16(opure_dev*, uint32_t, bool, bool, const KParams&, const Recipe&, uint32_t, uint32_t);
 int launch_i4_bf16(opure_dev*, uint32_t, bool, bool, const KParams&, const Recipe&, uint32_t, uint32_t);
+int launch_wide_i8(opure_dev*, uint32_t, const WParams&, uint32_t);
+int launch_wide_i4_f16(opure_dev*, uint32_t, const WParams&, uint32_t);
+int launch_wide_i4_bf16(opure_dev*, uint32_t, const WParams&, uint32_t);
 
 }  // namespace opure_gemv
 
@@ -156,11 +159,63 @@ Plan make_plan(const opure_dev* dev, uint32_t wfmt, uint32_t xfmt, uint32_t out,
     return pl;
 }
 
+// Shape plan of the GEMV over more than OPURE_MAX_ROWS rows: K splits so that
+// every CU gets a workgroup (at least 4 blocks per split), and the largest X
+// chunk whose LDS footprint fits.
+struct WidePlan {
+    uint32_t tiles = 0, nblk = 0, mt = 0, ckb = 0, splits = 1, bps = 0, lds = 0;
+    uint32_t x_stride = 0, off_xsum = 0, off_a = 0, off_s = 0;
+    uint64_t part_bytes = 0;
+};
+
+WidePlan wide_plan(const opure_dev* dev, uint32_t wfmt, uint32_t out, uint32_t in, uint32_t M)
+{
+    using namespace opure_gemv;
+    WidePlan w;
+    const uint32_t KB = kb_of(wfmt);
+    w.tiles = out / 16u;
+    w.nblk = in / KB;
+    w.mt = (M + 15u) / 16u;
+    const uint32_t groups = (w.tiles + WIDE_TO - 1u) / WIDE_TO;
+    const uint32_t n_cu = dev && dev->n_cu > 0 ? static_cast<uint32_t>(dev->n_cu) : 256u;
+    if (groups < n_cu) w.splits = std::min((n_cu + groups - 1u) / groups, std::max(1u, w.nblk / 4u));
+    w.bps = (w.nblk + w.splits - 1u) / w.splits;
+    w.splits = (w.nblk + w.bps - 1u) / w.bps;
+    const uint32_t aq = KB / 32u;
+    const uint32_t abytes = 2u * WIDE_TO * aq * 64u * 16u, sbytes = 2u * WIDE_TO * 16u * 4u;
+    for (uint32_t ckb : {8u, 4u, 2u, 1u})
+    {
+        if (ckb > w.bps && ckb > 1u) continue;
+        const uint32_t stride = ckb * KB * 2u + 16u;
+        const uint32_t xb = static_cast<uint32_t>(opure_hip::align_up(16ull * w.mt * stride, 16));
+        const uint32_t xs = wfmt == OPURE_W_I4G128 ? static_cast<uint32_t>(opure_hip::align_up(16ull * w.mt * ckb * 4u, 16)) : 0u;
+        const uint32_t total = xb + xs + abytes + sbytes;
+        if (total <= 159u * 1024u || ckb == 1u)
+        {
+            w.ckb = ckb;
+            w.x_stride = stride;
+            w.off_xsum = xb;
+            w.off_a = xb + xs;
+            w.off_s = xb + xs + abytes;
+            w.lds = total;
+            break;
+        }
+    }
+    w.part_bytes = w.splits > 1u ? static_cast<uint64_t>(w.splits) * w.tiles * w.mt * 64u * 16u : 0u;
+    return w;
+}
+
 }  // namespace
 
 namespace opure_hip {
 
 uint32_t tiled_block_k(uint32_t wfmt) { return kb_of(wfmt); }
+
+uint64_t gemv_scratch_bytes(const opure_dev* dev, uint32_t wfmt, uint32_t out, uint32_t in, uint32_t M)
+{
+    if (M <= OPURE_MAX_ROWS || wfmt == OPURE_W_F32 || out % 16u || in % kb_of(wfmt)) return 0;
+    return wide_plan(dev, wfmt, out, in, M).part_bytes;
+}
 
 uint32_t gemv_grid(const opure_dev* dev, const GemvCall& c)
 {
@@ -178,7 +233,16 @@ int gemv_validate(const GemvCall& c)
     const uint32_t want = c.epi == EPI_SWIGLU ? OPURE_LAYOUT_TILED_SWIGLU : OPURE_LAYOUT_TILED;
     OPURE_REQUIRE(c.W.layout == want, OPURE_E_INVALID,
                   "gemv: weights must be in layout %u (opure_tile_linear), got %u", want, c.W.layout);
-    OPURE_REQUIRE(c.M >= 1 && c.M <= OPURE_MAX_ROWS, OPURE_E_CAPACITY, "gemv: M=%u outside 1..%d", c.M, OPURE_MAX_ROWS);
+    OPURE_REQUIRE(c.M >= 1 && c.M <= OPURE_MAX_BATCH_ROWS, OPURE_E_CAPACITY, "gemv: M=%u outside 1..%d", c.M,
+                  OPURE_MAX_BATCH_ROWS);
+    if (c.M > OPURE_MAX_ROWS)
+    {
+        OPURE_REQUIRE(wf != OPURE_W_F32 && af != OPURE_A_F32, OPURE_E_UNSUPPORTED,
+                      "gemv: more than %d rows needs quantised weights and 16-bit activations", OPURE_MAX_ROWS);
+        OPURE_REQUIRE(c.epi != EPI_LOGITS, OPURE_E_UNSUPPORTED,
+                      "gemv: argmax partials are built for at most %d rows (store the logits instead)", OPURE_MAX_ROWS);
+        OPURE_REQUIRE(!c.gain || c.xn_scratch, OPURE_E_INVALID, "gemv: rmsnorm over %u rows needs xn_scratch", c.M);
+    }
     OPURE_REQUIRE(c.W.out >= 16 && c.W.out % 16 == 0, OPURE_E_INVALID, "gemv: out=%u must be a positive multiple of 16",
                   c.W.out);
     const uint32_t KB = kb_of(wf);
@@ -195,7 +259,7 @@ int gemv_validate(const GemvCall& c)
     if (c.epi == EPI_LOGITS) OPURE_REQUIRE(c.logits.am_val && c.logits.am_idx, OPURE_E_INVALID, "gemv: argmax partials");
     if (c.gain)
         OPURE_REQUIRE(c.ss_in && c.ss_tiles >= 1 && (reinterpret_cast<uintptr_t>(c.gain) & 15u) == 0 &&
-                          (c.epi == EPI_SWIGLU || c.epi == EPI_QKV || c.epi == EPI_LOGITS),
+                          (c.epi == EPI_SWIGLU || c.epi == EPI_QKV || c.epi == EPI_LOGITS || c.M > OPURE_MAX_ROWS),
                       OPURE_E_INVALID, "gemv: fused rmsnorm needs sums of squares, an aligned gain and a consumer epilogue");
     if (c.epi == EPI_QKV)
     {
@@ -210,9 +274,59 @@ int gemv_validate(const GemvCall& c)
     return OPURE_OK;
 }
 
+static int gemv_launch_wide(opure_dev* dev, const GemvCall& c)
+{
+    using namespace opure_gemv;
+    const WidePlan w = wide_plan(dev, c.wfmt, c.W.out, c.W.in, c.M);
+    OPURE_REQUIRE(w.splits == 1u || c.part_scratch, OPURE_E_INVALID, "gemv: %u x %u over %u rows needs part_scratch",
+                  c.W.out, c.W.in, c.M);
+    WParams wp{};
+    KParams& kp = wp.p;
+    kp.w = static_cast<const uint8_t*>(c.W.w);
+    kp.sc = c.W.scale;
+    kp.out = c.W.out;
+    kp.in = c.W.in;
+    kp.tiles = w.tiles;
+    kp.nblk = w.nblk;
+    kp.x = static_cast<const uint8_t*>(c.x);
+    kp.M = c.M;
+    kp.y = c.y;
+    kp.yfmt = c.yfmt;
+    kp.ss_out = c.ss_out;
+    kp.x_stride = w.x_stride;
+    kp.off_xsum = w.off_xsum;
+    kp.qkv = c.qkv;
+    wp.mt = w.mt;
+    wp.ckb = w.ckb;
+    wp.splits = w.splits;
+    wp.bps = w.bps;
+    wp.off_a = w.off_a;
+    wp.off_s = w.off_s;
+    wp.part = static_cast<f4_t*>(c.part_scratch);
+    if (c.gain)
+    {
+        // rmsnorm into the scratch rows first, then the GEMV reads them
+        kp.gain = c.gain;
+        kp.eps = c.eps;
+        kp.ss_in = c.ss_in;
+        kp.ss_tiles = c.ss_tiles;
+        if (c.xfmt == OPURE_A_F16)
+            hipLaunchKernelGGL(k_prenorm<OPURE_A_F16>, dim3(c.M), dim3(64), 0, dev->stream, kp, c.xn_scratch);
+        else
+            hipLaunchKernelGGL(k_prenorm<OPURE_A_BF16>, dim3(c.M), dim3(64), 0, dev->stream, kp, c.xn_scratch);
+        OPURE_LAUNCH_CHECK("k_prenorm");
+        kp.x = static_cast<const uint8_t*>(c.xn_scratch);
+        kp.gain = nullptr;
+    }
+    if (c.wfmt == OPURE_W_I8PC) return launch_wide_i8(dev, c.epi, wp, w.lds);
+    if (c.xfmt == OPURE_A_F16) return launch_wide_i4_f16(dev, c.epi, wp, w.lds);
+    return launch_wide_i4_bf16(dev, c.epi, wp, w.lds);
+}
+
 int gemv_launch(opure_dev* dev, const GemvCall& c)
 {
     using namespace opure_gemv;
+    if (c.M > OPURE_MAX_ROWS) return gemv_launch_wide(dev, c);
     const bool norm = c.gain != nullptr;
     Plan pl = make_plan(dev, c.wfmt, c.xfmt, c.W.out, c.W.in, c.M);
     KParams kp{};
@@ -277,8 +391,14 @@ static int gemv_public(opure_dev* dev, const opure_gemv_args* a, uint32_t wfmt)
     c.y = a->y;
     c.yfmt = a->yfmt;
     c.epi = a->epilogue;
-    const int rc = gemv_validate(c);
+    int rc = gemv_validate(c);
     if (rc) return rc;
+    const uint64_t scratch = gemv_scratch_bytes(dev, wfmt, c.W.out, c.W.in, c.M);
+    if (scratch)
+    {
+        if ((rc = ensure_workspace(dev, scratch))) return rc;
+        c.part_scratch = dev->ws;
+    }
     return gemv_launch(dev, c);
 }
 

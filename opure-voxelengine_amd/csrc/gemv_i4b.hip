@@ -1,6 +1,7 @@
 // gemv_i4b.hip -- instantiations of the K+1-row GEMV kernel (gemv_kernel.h)
+// and of the GEMV over more rows (gemm_wide.h)
 // for W_I4G128 weights with A_BF16 activations.
-#include "gemv_kernel.h"
+#include "gemm_wide.h"
 
 namespace opure_gemv {
 
@@ -8,6 +9,11 @@ int launch_i4_bf16(opure_dev* dev, uint32_t epi, bool norm, bool staged, const K
         uint32_t lds)
 {
     return launch_format<OPURE_W_I4G128, OPURE_A_BF16>(dev, epi, norm, staged, kp, r, grid, lds);
+}
+
+int launch_wide_i4_bf16(opure_dev* dev, uint32_t epi, const WParams& wp, uint32_t lds)
+{
+    return launch_wide_format<OPURE_W_I4G128, OPURE_A_BF16>(dev, epi, wp, lds);
 }
 
 }  // namespace opure_gemv

@@ -1,6 +1,7 @@
 // gemv_i8.hip -- instantiations of the K+1-row GEMV kernel (gemv_kernel.h)
+// and of the GEMV over more rows (gemm_wide.h)
 // for W_I8PC weights with A_F16 activations.
-#include "gemv_kernel.h"
+#include "gemm_wide.h"
 
 namespace opure_gemv {
 
@@ -8,6 +9,11 @@ int launch_i8(opure_dev* dev, uint32_t epi, bool norm, bool staged, const KParam
         uint32_t lds)
 {
     return launch_format<OPURE_W_I8PC, OPURE_A_F16>(dev, epi, norm, staged, kp, r, grid, lds);
+}
+
+int launch_wide_i8(opure_dev* dev, uint32_t epi, const WParams& wp, uint32_t lds)
+{
+    return launch_wide_format<OPURE_W_I8PC, OPURE_A_F16>(dev, epi, wp, lds);
 }
 
 }  // namespace opure_gemv

@@ -113,11 +113,16 @@ struct GemvCall {
     // fused rmsnorm whose X does not fit in LDS: [M][in] activations, written
     // by a normalisation pre-pass that the GEMV then reads
     void* xn_scratch = nullptr;
+    // more than OPURE_MAX_ROWS rows with K split over workgroups: the splits'
+    // accumulators (gemv_scratch_bytes)
+    void* part_scratch = nullptr;
     QkvEpilogue qkv{};
     LogitsEpilogue logits{};
 };
 
 int gemv_validate(const GemvCall& c);
+// device scratch a call needs in part_scratch (0 when it needs none)
+uint64_t gemv_scratch_bytes(const opure_dev* dev, uint32_t wfmt, uint32_t out, uint32_t in, uint32_t M);
 int gemv_launch(opure_dev* dev, const GemvCall& c);
 // workgroups gemv_launch runs for this call (EPI_LOGITS writes one argmax
 // partial per workgroup and column)
@@ -142,6 +147,9 @@ int      greedy_from_partials(opure_dev* dev, const float* am_val, const int32_t
                               uint32_t batch, uint32_t K, const int32_t* drafts, uint32_t stride, int32_t* out_tokens,
                               int32_t* accepted, const opure_rollback_args* rb);
 int      accept_greedy_launch(opure_dev* dev, const opure_accept_args* a, void* ws);
+// per-4096-column (value, lowest index) argmax partials [parts][rows] of fp32 logits
+int      argmax_partials_launch(opure_dev* dev, const float* logits, uint32_t rows, uint32_t V, float* am_val,
+                                int32_t* am_idx);
 int      accept_rejection_launch(opure_dev* dev, const opure_accept_args* a, void* ws, const int32_t* seq_len,
                                  int32_t* new_seq_len);
 int      rollback_validate(const opure_rollback_args* a);

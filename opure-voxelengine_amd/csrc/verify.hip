@@ -25,6 +25,9 @@
 // ============================================================================
 #include "internal.h"
 
+#include <algorithm>
+#include <utility>
+
 using namespace opure_dev_math;
 
 namespace {
@@ -105,11 +108,11 @@ __global__ __launch_bounds__(256) void k_embed(const int32_t* tokens, opure_line
 namespace opure_hip {
 
 struct VerifyPlan {
-    uint64_t x = 0, ss = 0, xn = 0, q = 0, att = 0, h = 0, am_val = 0, am_idx = 0, attn = 0, rej = 0, total = 0;
+    uint64_t x = 0, ss = 0, xn = 0, q = 0, att = 0, h = 0, am_val = 0, am_idx = 0, attn = 0, rej = 0, part = 0, total = 0;
     uint32_t lm_tiles = 0;
 };
 
-static VerifyPlan make_plan(const opure_model* m, uint32_t B, uint32_t R, uint32_t max_ctx)
+static VerifyPlan make_plan(const opure_dev* dev, const opure_model* m, uint32_t B, uint32_t R, uint32_t max_ctx)
 {
     VerifyPlan p;
     const uint64_t MR = static_cast<uint64_t>(B) * R;
@@ -123,11 +126,20 @@ static VerifyPlan make_plan(const opure_model* m, uint32_t B, uint32_t R, uint32
     p.q = take(MR * qdim * eb);
     p.att = take(MR * qdim * eb);
     p.h = take(MR * m->ffn * eb);
+    // argmax partials: one per LM-head workgroup and row (at most one per tile),
+    // or one per 4096 logits when more than OPURE_MAX_ROWS rows store the logits
     p.lm_tiles = m->vocab / 16u;
-    p.am_val = take(static_cast<uint64_t>(p.lm_tiles) * MR * 4u);
-    p.am_idx = take(static_cast<uint64_t>(p.lm_tiles) * MR * 4u);
+    const uint64_t am = std::max<uint64_t>(p.lm_tiles, argmax_parts(m->vocab)) * MR * 4u;
+    p.am_val = take(am);
+    p.am_idx = take(am);
     p.attn = take(attn_partial_bytes(B, m->n_kv_heads, m->n_heads / m->n_kv_heads, R, m->head_dim, m->afmt, max_ctx));
     p.rej = take(accept_ws_bytes(B, R - 1u, m->vocab, OPURE_ACCEPT_REJECTION));
+    // split-K accumulators of the GEMVs over more than OPURE_MAX_ROWS rows
+    uint64_t part = 0;
+    for (const auto& s : {std::pair<uint32_t, uint32_t>{qdim + 2u * kvdim, m->hidden}, {m->hidden, qdim},
+                          {2u * m->ffn, m->hidden}, {m->hidden, m->ffn}, {m->vocab, m->hidden}})
+        part = std::max(part, gemv_scratch_bytes(dev, m->wfmt, s.first, s.second, static_cast<uint32_t>(MR)));
+    p.part = take(part);
     p.total = off;
     return p;
 }
@@ -185,9 +197,10 @@ extern "C" {
 int opure_verify_reserve(opure_dev* dev, const opure_model* model, uint32_t batch, uint32_t rows, uint32_t max_ctx)
 {
     OPURE_REQUIRE(dev && model, OPURE_E_INVALID, "opure_verify_reserve: null argument");
-    OPURE_REQUIRE(batch >= 1 && rows >= 1 && batch * rows <= OPURE_MAX_ROWS, OPURE_E_CAPACITY,
-                  "opure_verify_reserve: batch*rows = %u exceeds %d", batch * rows, OPURE_MAX_ROWS);
-    const VerifyPlan p = make_plan(model, batch, rows, max_ctx);
+    OPURE_REQUIRE(batch >= 1 && rows >= 1 && rows <= OPURE_MAX_ROWS && batch * rows <= OPURE_MAX_BATCH_ROWS,
+                  OPURE_E_CAPACITY, "opure_verify_reserve: %u rows x batch %u beyond %d / %d", rows, batch,
+                  OPURE_MAX_ROWS, OPURE_MAX_BATCH_ROWS);
+    const VerifyPlan p = make_plan(dev, model, batch, rows, max_ctx);
     return ensure_workspace(dev, p.total);
 }
 
@@ -203,7 +216,7 @@ int opure_debug_verify_offsets(const opure_model* model, uint32_t batch, uint32_
                                uint64_t offsets[5])
 {
     OPURE_REQUIRE(model && offsets && batch && rows, OPURE_E_INVALID, "opure_debug_verify_offsets: bad argument");
-    const VerifyPlan p = make_plan(model, batch, rows, max_ctx);
+    const VerifyPlan p = make_plan(nullptr, model, batch, rows, max_ctx);
     offsets[0] = p.x;
     offsets[1] = p.ss;
     offsets[2] = p.q;
@@ -235,7 +248,7 @@ int opure_verify_step(opure_dev* dev, const opure_verify_args* a)
         OPURE_REQUIRE(a->accept_mode != OPURE_ACCEPT_NONE && a->new_seq_len, OPURE_E_INVALID,
                       "verify: rollback needs acceptance and new_seq_len");
 
-    const VerifyPlan P = make_plan(m, B, R, a->max_ctx);
+    const VerifyPlan P = make_plan(dev, m, B, R, a->max_ctx);
     rc = ensure_workspace(dev, P.total);
     if (rc) return rc;
     char* ws = static_cast<char*>(dev->ws);
@@ -262,6 +275,7 @@ int opure_verify_step(opure_dev* dev, const opure_verify_args* a)
     c.eps = m->rms_eps;
     c.ss_tiles = m->hidden / 16u;
     c.xn_scratch = ws + P.xn;
+    c.part_scratch = ws + P.part;
     for (uint32_t L = 0; L < m->n_layers; ++L)
     {
         const opure_layer_weights& W = m->layers[L];
@@ -337,7 +351,10 @@ int opure_verify_step(opure_dev* dev, const opure_verify_args* a)
     c.ss_out = nullptr;
     c.y = a->logits;
     c.yfmt = OPURE_A_F32;
-    c.epi = EPI_LOGITS;
+    // up to OPURE_MAX_ROWS rows the LM head also leaves per-workgroup argmax
+    // partials; beyond, the logits are stored and reduced per 4096 columns
+    const bool wide = MR > OPURE_MAX_ROWS;
+    c.epi = wide ? EPI_STORE : EPI_LOGITS;
     c.logits.am_val = reinterpret_cast<float*>(ws + P.am_val);
     c.logits.am_idx = reinterpret_cast<int32_t*>(ws + P.am_idx);
     if ((rc = gemv_validate(c)) || (rc = prof_begin(dev, OPURE_STAGE_LM_HEAD)) || (rc = gemv_launch(dev, c)) ||
@@ -365,7 +382,17 @@ int opure_verify_step(opure_dev* dev, const opure_verify_args* a)
     if (a->accept_mode == OPURE_ACCEPT_GREEDY)
     {
         // greedy acceptance and the rollback run in one kernel
-        rc = greedy_from_partials(dev, c.logits.am_val, c.logits.am_idx, gemv_grid(dev, c), B, R - 1u, a->tokens + 1, R,
+        uint32_t parts = 0;
+        if (wide)
+        {
+            parts = argmax_parts(m->vocab);
+            if ((rc = argmax_partials_launch(dev, a->logits, MR, m->vocab, c.logits.am_val, c.logits.am_idx))) return rc;
+        }
+        else
+        {
+            parts = gemv_grid(dev, c);
+        }
+        rc = greedy_from_partials(dev, c.logits.am_val, c.logits.am_idx, parts, B, R - 1u, a->tokens + 1, R,
                                   a->out_tokens, a->accepted, a->rollback ? &rb : nullptr);
         if (rc) return rc;
     }

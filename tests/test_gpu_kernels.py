@@ -205,6 +205,66 @@ def test_gemv_store_residual_matches_oracle(dev, case):
             b.free()
 
 
+WIDE_CASES = [
+    # wfmt, afmt, out, in: one K split (many tiles) and several (few tiles, long K)
+    (H.W_I8PC, H.A_F16, 16384, 2048),
+    (H.W_I8PC, H.A_F16, 3072, 2048),
+    (H.W_I8PC, H.A_F16, 2048, 8192),
+    (H.W_I4G128, H.A_BF16, 6144, 4096),
+    (H.W_I4G128, H.A_F16, 1024, 4096),
+    (H.W_I4G128, H.A_BF16, 4096, 14336),
+]
+
+
+@pytest.mark.parametrize("case", WIDE_CASES, ids=[_ids(c) for c in WIDE_CASES])
+def test_gemv_wide_matches_reference(dev, case):
+    """More than 16 rows (a batch of sequences): the thin-GEMM path against
+    the dequantised product in float64; each row is independent of how many
+    rows share the call (bit for bit), runs are deterministic, and the
+    residual epilogue adds in fp32."""
+    wfmt, afmt, out, inn = case
+    M = 224
+    say("gemv wide", _ids(case), "M", M)
+    rng = np.random.default_rng(out * 3 + inn)
+    lin = O.make_linear(rng, out, inn, wfmt)
+    desc, keep = dev_linear(dev, lin)
+    x_bits, x_f = to_act(rng.standard_normal((M, inn)), afmt)
+    wd = O.dequant(lin, wfmt).astype(np.float64)
+    ref = x_f.astype(np.float64) @ wd.T
+    absref = np.abs(x_f).astype(np.float64) @ np.abs(wd).T
+    slack = 20.0 if (wfmt == H.W_I4G128 and afmt == H.A_BF16) else 1.0
+    y = run_gemv(dev, wfmt, desc, x_bits, M, afmt, H.A_F32, H.EPI_STORE)
+    err = np.abs(y - ref)
+    assert np.all(err <= 1e-5 * slack * absref + 1e-6), (err.max(), (err / (absref + 1e-9)).max())
+    y40 = run_gemv(dev, wfmt, desc, x_bits, 40, afmt, H.A_F32, H.EPI_STORE)
+    assert np.array_equal(y40, y[:40])
+    assert np.array_equal(run_gemv(dev, wfmt, desc, x_bits, M, afmt, H.A_F32, H.EPI_STORE), y)
+    y0 = rng.standard_normal((M, out)).astype(np.float32)
+    yr = run_gemv(dev, wfmt, desc, x_bits, 100, afmt, H.A_F32, H.EPI_RESIDUAL, y_init=y0)
+    assert np.array_equal(yr, (y0[:100] + y[:100]).astype(np.float32))
+    for b in keep:
+        if b:
+            b.free()
+
+
+def test_gemv_wide_swiglu(dev):
+    wfmt, afmt, out, inn, M = H.W_I8PC, H.A_F16, 16384, 2048, 100
+    rng = np.random.default_rng(77)
+    lin = O.make_linear(rng, out, inn, wfmt)
+    desc, keep = dev_linear(dev, lin)
+    x_bits, x_f = to_act(rng.standard_normal((M, inn)), afmt)
+    gu = (x_f.astype(np.float64) @ O.dequant(lin, wfmt).astype(np.float64).T).astype(np.float32)
+    F = out // 2
+    g, u = gu[:, :F].copy(), gu[:, F:].copy()
+    h = np.zeros_like(g)
+    O.lib().orc_swiglu(g.ctypes.data, u.ctypes.data, h.ctypes.data, g.size)
+    y = from_act(run_gemv(dev, wfmt, desc, x_bits, M, afmt, afmt, H.EPI_SWIGLU), afmt)
+    np.testing.assert_allclose(y, h, rtol=2e-3, atol=1e-4 * max(1.0, np.abs(h).max()))
+    for b in keep:
+        if b:
+            b.free()
+
+
 @pytest.mark.parametrize("case", [(H.W_F32, H.A_F32, 3072, 576), (H.W_I8PC, H.A_F16, 16384, 2048),
                                   (H.W_I4G128, H.A_BF16, 2048, 4096)], ids=["f32", "i8", "i4bf16"])
 def test_gemv_swiglu_matches_oracle(dev, case):
@@ -255,8 +315,12 @@ def test_gemv_rejects_bad_shapes(dev):
     assert e.value.code == H.E_INVALID
     lin = {"w": np.zeros((32, 128), np.float32), "out": 32, "in": 128}
     desc, keep = dev_linear(dev, lin)
+    # more than 16 rows run as a thin GEMM, built for quantised weights only
     with pytest.raises(H.OpureError) as e:
         H.gemv(dev, H.W_F32, desc, x, y, 17, H.A_F32, H.A_F32, H.EPI_STORE)
+    assert e.value.code == H.E_UNSUPPORTED
+    with pytest.raises(H.OpureError) as e:
+        H.gemv(dev, H.W_F32, desc, x, y, 257, H.A_F32, H.A_F32, H.EPI_STORE)
     assert e.value.code == H.E_CAPACITY
     with pytest.raises(H.OpureError) as e:
         H.gemv(dev, H.W_I8PC, desc, x, y, 1, H.A_F32, H.A_F32, H.EPI_STORE)

@@ -306,3 +306,73 @@ def test_c1_shape_speculative_equals_greedy(dev):
     say("oracle min gap", min(gaps))
     if min(gaps) > 1e-4:
         assert greedy_orc == greedy_gpu
+
+
+@pytest.mark.parametrize("fmt", FMTS[1:], ids=FMT_IDS[1:])
+def test_batched_verify_rejection_matches_oracle(dev, fmt):
+    """A batch of sequences with ragged contexts, more than 16 rows in all
+    (the thin-GEMM path): logits against the oracle, then rejection sampling
+    at temperature 0.8 inside the step and the per-sequence rollback, equal
+    bit for bit to the oracle's acceptance of the same GPU logits."""
+    wfmt, afmt, tol = fmt
+    m = small_model(wfmt, afmt, tied=wfmt != O.W_I4G128)
+    B, R, V = 6, 7, m.cfg["vocab"]
+    rng = np.random.default_rng(31)
+    kv = random_cache(m, B, 400, 6 * 25 + 10, seed=9)
+    seq_len = rng.integers(20, 390, size=B).astype(np.int32)
+    tokens = rng.integers(0, V, size=(B, R)).astype(np.int32)
+    say("batched verify", FMT_IDS[FMTS.index(fmt)], "seq_len", seq_len.tolist())
+    dm, dkv = device_model(dev, m), device_kv(dev, m, kv)
+    run = VerifyRunner(dev, dm, dkv, B, R, max_ctx=400)
+    kv_o = O.HostKV(m, n_pages=kv.n_pages, batch=B, max_pages_per_seq=kv.max_pages)
+    kv_o.pool[...] = kv.pool
+    kv_o.page_table[...] = kv.page_table
+    # drafts sampled from random draft logits at the same temperature
+    q = (rng.standard_normal((B, R - 1, V)) * 2).astype(np.float32)
+    pos = np.repeat(np.arange(R - 1)[None], B, 0).ravel()
+    seqs = np.repeat(np.arange(B)[:, None], R - 1, 1).ravel()
+    tokens[:, 1:] = O.sample_rows(q.reshape(-1, V), 0.8, 99, pos, seqs, 0).reshape(B, R - 1)
+    kv_o.pool[...] = kv.pool
+    want = O.verify_forward(m, kv_o, tokens, seq_len)
+    # the first half of the batch drafts with q = the target's own scores, so
+    # every draft is accepted there (u * q(x) < p(x) for any u < 1)
+    run.step(tokens, seq_len)
+    q[: B // 2] = run.get_logits()[: B // 2, : R - 1]
+    dev.write(run.draft_logits, q)
+    run.step(tokens, seq_len, accept=H.ACCEPT_REJECTION, rollback=True, temperature=0.8, seed=99)
+    got = run.get_logits()
+    err = np.abs(got - want).max()
+    say("max_abs logits", err)
+    assert err <= tol
+    out, acc = run.get_accept()
+    w_out, w_acc, _ = O.accept_rejection(got, q, tokens[:, 1:], 0.8, 99)
+    assert np.array_equal(acc, w_acc) and np.array_equal(out, w_out)
+    new_len = dev.download(run.new_len, np.int32, (B,))
+    assert np.array_equal(new_len, seq_len + acc + 1)
+    assert (acc[: B // 2] == R - 1).all()
+    say("accepted", acc.tolist())
+
+
+def test_batched_verify_greedy_matches_oracle(dev):
+    """More than 16 rows with greedy acceptance (argmax over stored logits)."""
+    m = small_model(O.W_I8PC, O.A_F16)
+    B, R = 4, 6
+    kv = random_cache(m, B, 320, 4 * 20 + 8, seed=12)
+    seq_len = np.array([300, 17, 150, 64], np.int32)
+    rng = np.random.default_rng(4)
+    tokens = rng.integers(0, m.cfg["vocab"], size=(B, R)).astype(np.int32)
+    dm, dkv = device_model(dev, m), device_kv(dev, m, kv)
+    run = VerifyRunner(dev, dm, dkv, B, R, max_ctx=320)
+    kv_o = O.HostKV(m, n_pages=kv.n_pages, batch=B, max_pages_per_seq=kv.max_pages)
+    kv_o.pool[...] = kv.pool
+    kv_o.page_table[...] = kv.page_table
+    tokens = self_drafts(m, kv_o, kv.pool.copy(), tokens, seq_len, seq=2)
+    kv_o.pool[...] = kv.pool
+    want = O.verify_forward(m, kv_o, tokens, seq_len)
+    run.step(tokens, seq_len, accept=H.ACCEPT_GREEDY, rollback=True)
+    got = run.get_logits()
+    assert np.abs(got - want).max() <= 2e-2
+    out, acc = run.get_accept()
+    w_out, w_acc = O.accept_greedy(got, tokens[:, 1:])
+    assert np.array_equal(out, w_out) and np.array_equal(acc, w_acc)
+    assert acc[2] == R - 1
