@@ -220,9 +220,12 @@ __device__ __forceinline__ void load8(const KParams& p, uint32_t m, uint32_t k, 
 template <int WF, int AF, bool NORM, int NTH>
 __device__ __forceinline__ void stage_x(const KParams& p, uint8_t* lds, const float* sinv)
 {
-    // units in flight per thread: 16-wave workgroups have 128 VGPRs a lane,
-    // and a rmsnorm'd unit holds 16 words (x and gain) until it is converted
-    constexpr uint32_t EB = AF == OPURE_A_F32 ? 4u : 2u, KU = NTH < 1024 ? 8u : (NORM ? 2u : 4u);
+    // units in flight per thread, sized so that staging does not raise the
+    // kernel's register count (a rmsnorm'd unit holds 16 words, x and gain,
+    // until it is converted): 4-wave workgroups run two per CU at up to 256
+    // VGPRs, 8-wave ones need <= 128 to do the same, 16-wave ones have 128
+    constexpr uint32_t EB = AF == OPURE_A_F32 ? 4u : 2u;
+    constexpr uint32_t KU = NTH <= 256 ? 8u : (NTH <= 512 ? (NORM ? 2u : 4u) : (NORM ? 2u : 4u));
     const uint32_t n8 = p.in / 8u;
     const uint32_t total = p.M * n8;
     const uint32_t lane = threadIdx.x & 63u;
