@@ -322,30 +322,38 @@ __device__ __forceinline__ uint32_t pack_pair(float a, float b)
 }
 
 // Matrix-core flash-decoding for fp16/bf16 caches, head_dim HD in {64, 128}.
-// One workgroup per (KV head, chunk of 4*32*KK tokens, sequence); wave w scores
-// tokens [t0 + 32*KK*w, +32*KK) against query rows qoff .. qoff+16*NT-1 of the
-// KV head's Gq = group*rows rows:
+// One workgroup of NWV waves per (KV head, chunk of NWV*32*KK tokens,
+// sequence); wave w scores tokens [t0 + 32*KK*w, +32*KK) against query rows
+// qoff .. qoff+16*NT-1 of the KV head's Gq = group*rows rows:
 //   S^T = K Q^T   A = K, lane l = (r, g): token tb + 8(r/4) + r%4 (+4 in the
 //                 second tile), channels 32s + 8g..;  B = Q^T, column = query row
 //   so the score tile a lane holds -- query row r, tokens tb + 8g .. 8g+7 --
 //   is exactly its B operand of
 //   O^T = V^T P^T A = V^T tile (channel r, tokens tb + 8g..8g+7: 16 contiguous
 //                 bytes of a channel-major V plane)
-// All K and V loads are issued before the first MFMA.  The four waves'
-// (max, sum, output) are merged in LDS in wave order and the chunk's partial
-// is written for the combine kernel.
-template <int HD, int AF, int NT, int KK>
-__global__ __launch_bounds__(256) void k_attn_mfma(AttnParams p)
+// All K and V loads are issued before the first MFMA.  The waves' (max, sum,
+// output) go to LDS; then the (channel tile, query tile) pieces of the merge
+// are shared out over the waves, each merging in wave order, and the chunk's
+// partial is written for the combine kernel.
+template <int HD, int NT, int NWV>
+constexpr uint32_t attn_mfma_lds()
+{
+    return NWV * (HD / 16u) * NT * 64u * 16u + NWV * NT * 16u * 2u * 4u;
+}
+
+template <int HD, int AF, int NT, int KK, int NWV>
+__global__ __launch_bounds__(NWV * 64) void k_attn_mfma(AttnParams p)
 {
     constexpr uint32_t KS = HD / 32u, DT = HD / 16u, EB = 2u, TPW = 32u * KK;
-    __shared__ f4_t cacc[3][DT][NT][64];
-    __shared__ float cml[3][NT][16][2];
+    extern __shared__ __align__(16) uint8_t lds_raw[];
+    f4_t (*cacc)[DT][NT][64] = reinterpret_cast<f4_t (*)[DT][NT][64]>(lds_raw);
+    float (*cml)[NT][16][2] = reinterpret_cast<float (*)[NT][16][2]>(lds_raw + NWV * DT * NT * 64u * 16u);
     const uint32_t kh = blockIdx.x, c = blockIdx.y, b = blockIdx.z;
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u, g = lane >> 4, r = lane & 15u;
     const uint32_t group = p.n_heads / p.n_kv, R = p.rows, Gq = group * R;
     const uint32_t ctx = static_cast<uint32_t>(p.seq_len[b]);
     const uint32_t total = ctx + R;
-    const uint32_t t0 = c * 4u * TPW;
+    const uint32_t t0 = c * NWV * TPW;
     if (t0 >= total) return;                          // whole workgroup: no row reaches this chunk
     const uint32_t tw = t0 + TPW * wave;
     const int32_t* pt = p.page_table + static_cast<uint64_t>(b) * p.max_pages;
@@ -498,66 +506,58 @@ __global__ __launch_bounds__(256) void k_attn_mfma(AttnParams p)
             }
         }
 
-    // ---- merge the four waves in wave order: m = max, weights exp(m_w - m) -
-    if (wave > 0)
+    // ---- merge the waves in wave order: m = max, weights exp(m_w - m) -------
+#pragma unroll
+    for (uint32_t dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int n = 0; n < NT; ++n) cacc[wave][dt][n][lane] = o[dt][n];
+    if (g == 0)
     {
 #pragma unroll
-        for (uint32_t dt = 0; dt < DT; ++dt)
-#pragma unroll
-            for (int n = 0; n < NT; ++n) cacc[wave - 1][dt][n][lane] = o[dt][n];
-        if (g == 0)
+        for (int n = 0; n < NT; ++n)
         {
-#pragma unroll
-            for (int n = 0; n < NT; ++n)
-            {
-                cml[wave - 1][n][r][0] = mrow[n];
-                cml[wave - 1][n][r][1] = lrow[n];
-            }
+            cml[wave][n][r][0] = mrow[n];
+            cml[wave][n][r][1] = lrow[n];
         }
     }
     __syncthreads();
-    if (wave != 0) return;
     const uint64_t pbase = ((static_cast<uint64_t>(b) * p.n_kv + kh) * p.nch + c) * Gq;
-#pragma unroll
-    for (int n = 0; n < NT; ++n)
+    for (uint32_t task = wave; task < DT * NT; task += NWV)
     {
-        float mw[4], lw[4];
-        mw[0] = mrow[n];
-        lw[0] = lrow[n];
-#pragma unroll
-        for (int w = 1; w < 4; ++w)
-        {
-            mw[w] = cml[w - 1][n][r][0];
-            lw[w] = cml[w - 1][n][r][1];
-        }
-        const float M = fmaxf(fmaxf(mw[0], mw[1]), fmaxf(mw[2], mw[3]));
-        float ew[4];
-#pragma unroll
-        for (int w = 0; w < 4; ++w)
-            ew[w] = mw[w] == -__builtin_huge_valf() ? 0.0f : expf_ref(__fsub_rn(mw[w], M));
-        float L = __fmul_rn(ew[0], lw[0]);
-#pragma unroll
-        for (int w = 1; w < 4; ++w) L = __fmaf_rn(ew[w], lw[w], L);
+        const uint32_t dt = task / NT, n = task - dt * NT;
         const uint32_t qi = p.qoff + 16u * n + r;
-        if (qi >= Gq) continue;
-        if (g == 0)
+        float mw[NWV], lw[NWV];
+#pragma unroll
+        for (int w = 0; w < NWV; ++w)
         {
+            mw[w] = cml[w][n][r][0];
+            lw[w] = cml[w][n][r][1];
+        }
+        float M = mw[0];
+#pragma unroll
+        for (int w = 1; w < NWV; ++w) M = fmaxf(M, mw[w]);
+        float ew[NWV];
+#pragma unroll
+        for (int w = 0; w < NWV; ++w)
+            ew[w] = mw[w] == -__builtin_huge_valf() ? 0.0f : expf_ref_nonpos(__fsub_rn(mw[w], M));
+        if (qi >= Gq) continue;
+        if (dt == 0 && g == 0)
+        {
+            float L = __fmul_rn(ew[0], lw[0]);
+#pragma unroll
+            for (int w = 1; w < NWV; ++w) L = __fmaf_rn(ew[w], lw[w], L);
             p.part_ml[(pbase + qi) * 2u] = M;
             p.part_ml[(pbase + qi) * 2u + 1u] = L;
         }
+        f4_t a = cacc[0][dt][n][lane] * ew[0];
 #pragma unroll
-        for (uint32_t dt = 0; dt < DT; ++dt)
+        for (int w = 1; w < NWV; ++w)
         {
-            f4_t a = o[dt][n] * ew[0];
+            const f4_t v = cacc[w][dt][n][lane];
 #pragma unroll
-            for (int w = 1; w < 4; ++w)
-            {
-                const f4_t v = cacc[w - 1][dt][n][lane];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) a[i] = __fmaf_rn(ew[w], v[i], a[i]);
-            }
-            *reinterpret_cast<f4_t*>(p.part_acc + (pbase + qi) * HD + 16u * dt + 4u * g) = a;
+            for (int i = 0; i < 4; ++i) a[i] = __fmaf_rn(ew[w], v[i], a[i]);
         }
+        *reinterpret_cast<f4_t*>(p.part_acc + (pbase + qi) * HD + 16u * dt + 4u * g) = a;
     }
 }
 
@@ -599,10 +599,18 @@ __global__ __launch_bounds__(64) void k_attn_combine(AttnParams p)
     }
 }
 
-template <int HD, int AF, int NT, int KK>
+template <int HD, int AF, int NT, int KK, int NWV>
 int launch_mfma(opure_dev* dev, dim3 grid, const AttnParams& p)
 {
-    hipLaunchKernelGGL((k_attn_mfma<HD, AF, NT, KK>), grid, dim3(256), 0, dev->stream, p);
+    constexpr uint32_t lds = attn_mfma_lds<HD, NT, NWV>();
+    static bool configured = false;
+    if (!configured)
+    {
+        OPURE_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_attn_mfma<HD, AF, NT, KK, NWV>),
+                                          hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
+        configured = true;
+    }
+    hipLaunchKernelGGL((k_attn_mfma<HD, AF, NT, KK, NWV>), grid, dim3(NWV * 64), lds, dev->stream, p);
     OPURE_LAUNCH_CHECK("k_attn_mfma");
     return OPURE_OK;
 }
@@ -722,14 +730,16 @@ int attn_launch(opure_dev* dev, const opure_model* m, const opure_kv* kv, uint32
             pq.qoff = q0;
             const bool one = Gq - q0 <= 16u;
             int rc;
+            // head_dim 64: 4 waves x 32 tokens; 128: 8 waves x 32 tokens (two
+            // waves a SIMD, 128 KB of merge buffers)
             if (hd == 64u && p.afmt == OPURE_A_F16)
-                rc = one ? launch_mfma<64, OPURE_A_F16, 1, 1>(dev, grid, pq) : launch_mfma<64, OPURE_A_F16, 2, 1>(dev, grid, pq);
+                rc = one ? launch_mfma<64, OPURE_A_F16, 1, 1, 4>(dev, grid, pq) : launch_mfma<64, OPURE_A_F16, 2, 1, 4>(dev, grid, pq);
             else if (hd == 64u)
-                rc = one ? launch_mfma<64, OPURE_A_BF16, 1, 1>(dev, grid, pq) : launch_mfma<64, OPURE_A_BF16, 2, 1>(dev, grid, pq);
+                rc = one ? launch_mfma<64, OPURE_A_BF16, 1, 1, 4>(dev, grid, pq) : launch_mfma<64, OPURE_A_BF16, 2, 1, 4>(dev, grid, pq);
             else if (p.afmt == OPURE_A_F16)
-                rc = one ? launch_mfma<128, OPURE_A_F16, 1, 2>(dev, grid, pq) : launch_mfma<128, OPURE_A_F16, 2, 2>(dev, grid, pq);
+                rc = one ? launch_mfma<128, OPURE_A_F16, 1, 2, 4>(dev, grid, pq) : launch_mfma<128, OPURE_A_F16, 2, 2, 4>(dev, grid, pq);
             else
-                rc = one ? launch_mfma<128, OPURE_A_BF16, 1, 2>(dev, grid, pq) : launch_mfma<128, OPURE_A_BF16, 2, 2>(dev, grid, pq);
+                rc = one ? launch_mfma<128, OPURE_A_BF16, 1, 2, 4>(dev, grid, pq) : launch_mfma<128, OPURE_A_BF16, 2, 2, 4>(dev, grid, pq);
             if (rc) return rc;
         }
     }

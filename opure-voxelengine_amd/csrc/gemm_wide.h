@@ -73,11 +73,7 @@ __device__ __forceinline__ void stage_wide_x(const WParams& wp, uint8_t* lds, ui
             if constexpr (WF == OPURE_W_I4G128)
             {
                 // the 16 units of a group sit in 16 aligned lanes (n8 and 256 are multiples of 16)
-                float s = unit_sum<AF>(val[0], val[1], val[2], val[3]);
-                s += __shfl_xor(s, 1);
-                s += __shfl_xor(s, 2);
-                s += __shfl_xor(s, 4);
-                s += __shfl_xor(s, 8);
+                const float s = row16_sum(unit_sum<AF>(val[0], val[1], val[2], val[3]));
                 if ((lane & 15u) == 0) xsum[m * wp.ckb + j / 16u] = s;
             }
         }

@@ -130,7 +130,7 @@ Plan make_plan(const opure_dev* dev, uint32_t wfmt, uint32_t xfmt, uint32_t out,
     Plan pl;
     pl.tiles = out / 16u;
     pl.nblk = in / kb_of(wfmt);
-    pl.r = pl.tiles >= 512u ? R_WIDE : (pl.tiles > 192u ? R_MID : R_NARROW);
+    pl.r = pl.tiles >= 320u ? R_WIDE : (pl.tiles > 192u ? R_MID : R_NARROW);
     pl.groups = (pl.tiles + pl.r.t - 1u) / pl.r.t;
     const uint32_t EB = opure_hip::act_bytes(xfmt);
     const uint32_t red = pl.r.nw * pl.r.t * 1024u;
@@ -152,10 +152,9 @@ Plan make_plan(const opure_dev* dev, uint32_t wfmt, uint32_t xfmt, uint32_t out,
         pl.off_red = 0;
         pl.lds = red;
     }
-    // wide shapes run persistent workgroups, two per CU when their LDS allows
+    // persistent workgroups, one per CU
     const uint32_t n_cu = dev->n_cu > 0 ? static_cast<uint32_t>(dev->n_cu) : 256u;
-    const uint32_t per_cu = pl.r.nw == 4u ? (pl.lds <= 79u * 1024u ? 2u : 1u) : 1u;
-    pl.grid = pl.r.nw == 4u ? std::min(pl.groups, n_cu * per_cu) : pl.groups;
+    pl.grid = std::min(pl.groups, n_cu);
     return pl;
 }
 

@@ -155,13 +155,19 @@ __device__ __forceinline__ uint32_t pack2(float a, float b)
 // 1 / rms of column m from the producer's per-16-column sums of squares, by
 // one wave in a fixed order (lane l takes tiles l, l+64, ..., then a 6-level
 // butterfly) that depends on neither M nor the kernel shape
+__device__ __forceinline__ float inv_rms_finish(const KParams& p, float ssum)
+{
+    ssum = row16_sum(ssum);
+    ssum += __shfl_xor(ssum, 16);
+    ssum += __shfl_xor(ssum, 32);
+    return __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(ssum, static_cast<float>(p.in)), p.eps)));
+}
+
 __device__ __forceinline__ float inv_rms_wave(const KParams& p, uint32_t m, uint32_t lane)
 {
     float ssum = 0.0f;
     for (uint32_t t = lane; t < p.ss_tiles; t += 64u) ssum += p.ss_in[static_cast<uint64_t>(t) * p.M + m];
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) ssum += __shfl_xor(ssum, o);
-    return __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(ssum, static_cast<float>(p.in)), p.eps)));
+    return inv_rms_finish(p, ssum);
 }
 
 // 8 consecutive activations of row m at k, as 8 fp32 words (AF f32) or 4
@@ -211,64 +217,149 @@ __device__ __forceinline__ void load8(const KParams& p, uint32_t m, uint32_t k, 
     }
 }
 
-// Stage X rows 0..M-1 (whole K) into LDS rows of x_stride bytes, natural k
-// order; uint4 also writes each 128-k group's sum to xsum[m][g].  Threads take
-// 8-value units of the flattened (row, unit) space, up to eight units' loads
-// in flight before any store; the 16 units of a group sit in 16 aligned lanes of
-// one wave (n8 and NTH are multiples of 16), so the group sum is a fixed
-// butterfly.
-template <int WF, int AF, bool NORM, int NTH>
-__device__ __forceinline__ void stage_x(const KParams& p, uint8_t* lds, const float* sinv)
+// Staging of X rows 0..M-1 (whole K) into LDS rows of x_stride bytes, natural
+// k order; uint4 also writes each 128-k group's sum to xsum[m][g].
+//
+// Thread t owns the 8-value unit column j = j0 + t % n8 (n8 = in/8) and the
+// rows rg, rg + RT, ... with rg = t / n8 and RT = max(1, NTH / n8) row groups,
+// so the gain of a rmsnorm'd unit is loaded once for all its rows.  A round
+// holds KR rows of one unit column in registers: stage_issue only issues the
+// loads, stage_store converts and writes them, so the kernel can issue the
+// first round, then its first weight loads, and wait for L2 alone (loads
+// retire in issue order).  n8 and NTH are multiples of 16, so the 16 units of
+// a group sit in 16 aligned lanes with the same row and the group sum is a
+// fixed butterfly.
+template <int AF, bool NORM, int KR>
+struct StageRound {
+    static constexpr int XW = (NORM || AF == OPURE_A_F32) ? 2 : 1;   // 16-byte words of a unit
+    u4_t x[KR][XW];
+    u4_t g[NORM ? 2 : 1];
+};
+
+template <int NTH>
+struct StageMap {
+    uint32_t n8, rt, j, rg;
+    bool col;                 // this thread owns a unit column
+    __device__ __forceinline__ StageMap(const KParams& p, uint32_t j0)
+    {
+        n8 = p.in / 8u;
+        rt = n8 >= NTH ? 1u : NTH / n8;
+        const uint32_t t = threadIdx.x;
+        rg = n8 >= NTH ? 0u : t / n8;
+        j = j0 + (n8 >= NTH ? t : t - rg * n8);
+        col = rg < rt && j < n8;
+    }
+};
+
+template <int AF, bool NORM, int NTH, int KR>
+__device__ __forceinline__ void stage_issue(const KParams& p, StageRound<AF, NORM, KR>& r, uint32_t j0, uint32_t i0)
 {
-    // units in flight per thread, sized so that staging does not raise the
-    // kernel's register count (a rmsnorm'd unit holds 16 words, x and gain,
-    // until it is converted): 4-wave workgroups run two per CU at up to 256
-    // VGPRs, 8-wave ones need <= 128 to do the same, 16-wave ones have 128
+    const StageMap<NTH> sm(p, j0);
+    const uint32_t j = sm.col ? sm.j : 0u;           // past the end: unit 0 of row 0 again, never stored
+    if constexpr (NORM)
+    {
+        const u4_t* gr = reinterpret_cast<const u4_t*>(p.gain + 8u * j);
+        r.g[0] = gr[0];
+        r.g[1] = gr[1];
+    }
+#pragma unroll
+    for (int i = 0; i < KR; ++i)
+    {
+        const uint32_t m = min(sm.rg + (i0 + i) * sm.rt, p.M - 1u);
+        if constexpr (NORM)
+        {
+            const u4_t* xr = reinterpret_cast<const u4_t*>(reinterpret_cast<const float*>(p.x) + static_cast<uint64_t>(m) * p.in + 8u * j);
+            r.x[i][0] = xr[0];
+            r.x[i][1] = xr[1];
+        }
+        else if constexpr (AF == OPURE_A_F32)
+        {
+            const u4_t* src = reinterpret_cast<const u4_t*>(p.x + (static_cast<uint64_t>(m) * p.in + 8u * j) * 4u);
+            r.x[i][0] = src[0];
+            r.x[i][1] = src[1];
+        }
+        else
+        {
+            r.x[i][0] = *reinterpret_cast<const u4_t*>(p.x + (static_cast<uint64_t>(m) * p.in + 8u * j) * 2u);
+        }
+    }
+}
+
+template <int WF, int AF, bool NORM, int NTH, int KR>
+__device__ __forceinline__ void stage_store(const KParams& p, const StageRound<AF, NORM, KR>& r, uint32_t j0, uint32_t i0,
+                                            uint8_t* lds, const float* sinv)
+{
     constexpr uint32_t EB = AF == OPURE_A_F32 ? 4u : 2u;
-    constexpr uint32_t KU = NTH <= 256 ? 8u : (NTH <= 512 ? (NORM ? 2u : 4u) : (NORM ? 2u : 4u));
-    const uint32_t n8 = p.in / 8u;
-    const uint32_t total = p.M * n8;
+    const StageMap<NTH> sm(p, j0);
     const uint32_t lane = threadIdx.x & 63u;
     float* xsum = reinterpret_cast<float*>(lds + p.off_xsum);
-    for (uint32_t base = 0; base < total; base += NTH * KU)
+#pragma unroll
+    for (int i = 0; i < KR; ++i)
     {
-        // every thread loads all KU units (past the end: the last unit again),
-        // so the loads are issued back to back before the first use
-        uint32_t o[KU][8];
-#pragma unroll
-        for (uint32_t k = 0; k < KU; ++k)
+        const uint32_t m = sm.rg + (i0 + i) * sm.rt;
+        const bool keep = sm.col && m < p.M;
+        uint32_t o[8];
+        if constexpr (NORM)
         {
-            const uint32_t idx = min(base + k * NTH + threadIdx.x, total - 1u);
-            const uint32_t m = idx / n8, j = idx - m * n8;
-            load8<AF, NORM>(p, m, 8u * j, NORM ? sinv[m] : 1.0f, o[k]);
-        }
+            // round(x * inv * g) (Opure_RMSNorm.usf:44-78)
+            const float inv = sinv[min(m, p.M - 1u)];
+            const f4_t x0 = __builtin_bit_cast(f4_t, r.x[i][0]), x1 = __builtin_bit_cast(f4_t, r.x[i][1]);
+            const f4_t g0 = __builtin_bit_cast(f4_t, r.g[0]), g1 = __builtin_bit_cast(f4_t, r.g[1]);
+            float yv[8];
 #pragma unroll
-        for (uint32_t k = 0; k < KU; ++k)
-        {
-            const uint32_t idx = base + k * NTH + threadIdx.x;
-            if (idx >= total) continue;
-            const uint32_t m = idx / n8, j = idx - m * n8;
-            uint8_t* dst = lds + static_cast<uint64_t>(m) * p.x_stride + 8u * j * EB;
+            for (int e = 0; e < 4; ++e)
+            {
+                yv[e] = __fmul_rn(__fmul_rn(x0[e], inv), g0[e]);
+                yv[4 + e] = __fmul_rn(__fmul_rn(x1[e], inv), g1[e]);
+            }
             if constexpr (AF == OPURE_A_F32)
             {
-                reinterpret_cast<u4_t*>(dst)[0] = u4_t{o[k][0], o[k][1], o[k][2], o[k][3]};
-                reinterpret_cast<u4_t*>(dst)[1] = u4_t{o[k][4], o[k][5], o[k][6], o[k][7]};
+#pragma unroll
+                for (int e = 0; e < 8; ++e) o[e] = __float_as_uint(yv[e]);
             }
             else
             {
-                *reinterpret_cast<u4_t*>(dst) = u4_t{o[k][0], o[k][1], o[k][2], o[k][3]};
-                if constexpr (WF == OPURE_W_I4G128)
-                {
-                    float u = unit_sum<AF>(o[k][0], o[k][1], o[k][2], o[k][3]);
-                    u += __shfl_xor(u, 1);
-                    u += __shfl_xor(u, 2);
-                    u += __shfl_xor(u, 4);
-                    u += __shfl_xor(u, 8);
-                    if ((lane & 15u) == 0) xsum[m * (p.in / 128u) + j / 16u] = u;
-                }
+#pragma unroll
+                for (int e = 0; e < 4; ++e) o[e] = pack2<AF>(yv[2 * e], yv[2 * e + 1]);
+            }
+        }
+        else
+        {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+            {
+                o[e] = r.x[i][0][e];
+                if constexpr (AF == OPURE_A_F32) o[4 + e] = r.x[i][1][e];
+            }
+        }
+        uint8_t* dst = lds + static_cast<uint64_t>(m) * p.x_stride + 8u * sm.j * EB;
+        if constexpr (AF == OPURE_A_F32)
+        {
+            if (keep)
+            {
+                reinterpret_cast<u4_t*>(dst)[0] = u4_t{o[0], o[1], o[2], o[3]};
+                reinterpret_cast<u4_t*>(dst)[1] = u4_t{o[4], o[5], o[6], o[7]};
+            }
+        }
+        else
+        {
+            if (keep) *reinterpret_cast<u4_t*>(dst) = u4_t{o[0], o[1], o[2], o[3]};
+            if constexpr (WF == OPURE_W_I4G128)
+            {
+                const float u = row16_sum(unit_sum<AF>(o[0], o[1], o[2], o[3]));
+                if (keep && (lane & 15u) == 0) xsum[m * (p.in / 128u) + sm.j / 16u] = u;
             }
         }
     }
+}
+
+// Rows a round holds per unit column (a rmsnorm'd row costs 8 registers):
+// one round for the 8 rows of a K=7 step; 16-wave workgroups have 128
+// registers, 8-wave ones 256
+template <int AF, bool NORM, int NTH>
+constexpr int stage_rows()
+{
+    return NTH >= 1024 ? 4 : 8;
 }
 
 // EPI_LOGITS keeps the best (value, lowest index) of column m seen so far in
@@ -453,24 +544,73 @@ __global__ __launch_bounds__(NW * 64) void k_gemv(KParams p)
     };
 
     PL A, B;
-    load(A, 0);
-    if (S > 1u) load(B, 1);
-
     if constexpr (STAGED)
     {
+        // Issue order: the first staging round, the rows' sums of squares, then
+        // the first two steps' weights.  Loads retire in issue order, so the
+        // staging below waits for L2 only while the weights stream from HBM.
+        constexpr uint32_t NTH = NW * 64;
+        constexpr int KR = stage_rows<AF, NORM, NTH>();
+        constexpr int RW = (OPURE_MAX_ROWS + NW - 1) / NW;  // columns whose rms a wave computes
+        constexpr int SSE = 4;                              // sums per lane issued early: in <= 4096
         __shared__ float sinv[OPURE_MAX_ROWS];
+        StageRound<AF, NORM, KR> r0;
+        stage_issue<AF, NORM, NTH, KR>(p, r0, 0u, 0u);
+        float ssp[NORM ? RW : 1][SSE];
         if constexpr (NORM)
         {
-            // one wave per column: a single round of loads whatever M is
-            for (uint32_t m = wave; m < M; m += NW)
+#pragma unroll
+            for (int i = 0; i < RW; ++i)
             {
-                const float v = inv_rms_wave(p, m, lane);
+                const uint32_t m = min(wave + i * NW, M - 1u);
+#pragma unroll
+                for (int e = 0; e < SSE; ++e)
+                {
+                    const uint32_t t = min(lane + 64u * e, p.ss_tiles - 1u);
+                    ssp[i][e] = p.ss_in[static_cast<uint64_t>(t) * M + m];
+                }
+            }
+        }
+        load(A, 0);
+        if (S > 1u) load(B, 1);
+        if constexpr (NORM)
+        {
+            // one wave per column, the sums in inv_rms_wave's order (adding the
+            // early sums of tiles past the end is skipped, not added as zero)
+#pragma unroll
+            for (int i = 0; i < RW; ++i)
+            {
+                const uint32_t m = wave + i * NW;
+                if (m >= M) break;
+                float ssum = 0.0f;
+#pragma unroll
+                for (int e = 0; e < SSE; ++e)
+                    if (lane + 64u * e < p.ss_tiles) ssum += ssp[i][e];
+                for (uint32_t t = lane + 64u * SSE; t < p.ss_tiles; t += 64u) ssum += p.ss_in[static_cast<uint64_t>(t) * M + m];
+                const float v = inv_rms_finish(p, ssum);
                 if (lane == 0) sinv[m] = v;
             }
             __syncthreads();
         }
-        stage_x<WF, AF, NORM, NW * 64>(p, lds, sinv);
+        stage_store<WF, AF, NORM, NTH, KR>(p, r0, 0u, 0u, lds, sinv);
+        // further rounds when the rows or the unit columns exceed one round
+        const uint32_t n8 = p.in / 8u;
+        const uint32_t rt = n8 >= NTH ? 1u : NTH / n8;
+        const uint32_t rows_per = (M + rt - 1u) / rt;
+        for (uint32_t j0 = 0; j0 < n8; j0 += NTH)
+            for (uint32_t i0 = 0; i0 < rows_per; i0 += KR)
+            {
+                if (j0 == 0 && i0 == 0) continue;
+                StageRound<AF, NORM, KR> r;
+                stage_issue<AF, NORM, NTH, KR>(p, r, j0, i0);
+                stage_store<WF, AF, NORM, NTH, KR>(p, r, j0, i0, lds, sinv);
+            }
         __syncthreads();
+    }
+    else
+    {
+        load(A, 0);
+        if (S > 1u) load(B, 1);
     }
 
     f4_t acc[T];
@@ -668,21 +808,25 @@ int launch(opure_dev* dev, const KParams& kp, uint32_t grid, uint32_t lds)
 }
 
 // The shape recipes the host chooses from (waves, tiles per workgroup, blocks
-// per wave per pass of the staged kernel)
+// per wave per pass of the staged kernel).  One workgroup per CU, persistent:
+// each CU stages X once, and a pass of 32 blocks per tile covers a whole
+// 4096-long row (int4) so a workgroup's first one or two groups are in flight
+// from its start.
 struct Recipe { uint32_t nw, t, u; };
-constexpr Recipe R_WIDE{4, 2, 2};     // many tiles: persistent, 2 tiles share X
-constexpr Recipe R_MID{8, 1, 2};
-constexpr Recipe R_NARROW{16, 1, 2};  // few tiles: 16 waves split K
+constexpr Recipe R_WIDE{8, 2, 4};     // many tiles: 2 tiles share each X fragment
+constexpr Recipe R_MID{8, 1, 4};      // about one tile per CU
+constexpr Recipe R_NARROW{16, 1, 2};  // fewer tiles than CUs: 16 waves split K
 
-// Blocks go to waves by index (wave w takes w, w+NW, ...) whatever U is, so
-// U may differ between the staged and direct kernels of a recipe without
-// changing any sum; direct 16-wave kernels carry X fragments and keep U = 1
-// to stay within 128 VGPRs.
+// Blocks go to waves by index (wave w takes w, w+NW, ...) whatever T and U
+// are, so the sums depend on NW alone: WIDE and MID give the same bits.
+// Direct kernels carry X fragments and keep U small (8 waves: 2, so the
+// 112 blocks of a 14336-long row fill whole passes; 16 waves: 1, to stay
+// within 128 VGPRs).
 template <int WF, int AF, int EPI, bool NORM, bool STAGED>
 int launch_recipe(opure_dev* dev, const KParams& kp, const Recipe& r, uint32_t grid, uint32_t lds)
 {
-    if (r.nw == 4) return launch<WF, AF, EPI, 4, 2, 2, NORM, STAGED>(dev, kp, grid, lds);
-    if (r.nw == 8) return launch<WF, AF, EPI, 8, 1, 2, NORM, STAGED>(dev, kp, grid, lds);
+    if (r.nw == 8 && r.t == 2) return launch<WF, AF, EPI, 8, 2, STAGED ? 4 : 2, NORM, STAGED>(dev, kp, grid, lds);
+    if (r.nw == 8) return launch<WF, AF, EPI, 8, 1, STAGED ? 4 : 2, NORM, STAGED>(dev, kp, grid, lds);
     return launch<WF, AF, EPI, 16, 1, STAGED ? 2 : 1, NORM, STAGED>(dev, kp, grid, lds);
 }
 

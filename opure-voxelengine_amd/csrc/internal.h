@@ -165,6 +165,27 @@ namespace opure_dev_math {
 __device__ __forceinline__ float bits_f(uint32_t u) { return __uint_as_float(u); }
 __device__ __forceinline__ uint32_t f_bits(float f) { return __float_as_uint(f); }
 
+// Sum over each row of 16 lanes with the tree of the xor butterfly 1, 2, 4, 8
+// (u += lane ^ o), in DPP moves instead of LDS permutes: quad_perm [1,0,3,2]
+// and [2,3,0,1] are xor 1 and 2; after them every lane of a quad holds the
+// quad's sum, so the half-row mirror (lane 7 - i) and the row mirror (lane
+// 15 - i) read the same values as xor 4 and xor 8.  Bit-identical to the
+// butterfly, one VALU each.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v)
+{
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+
+__device__ __forceinline__ float row16_sum(float u)
+{
+    u += dpp_f<0xB1>(u);    // quad_perm [1,0,3,2]
+    u += dpp_f<0x4E>(u);    // quad_perm [2,3,0,1]
+    u += dpp_f<0x141>(u);   // row_half_mirror
+    u += dpp_f<0x140>(u);   // row_mirror
+    return u;
+}
+
 // Cody-Waite reduced degree-7 Taylor exp, same operations as orc_expf.
 __device__ __forceinline__ float expf_ref(float x)
 {
