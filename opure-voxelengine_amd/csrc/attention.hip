@@ -335,6 +335,15 @@ __device__ __forceinline__ uint32_t pack_pair(float a, float b)
 // output) go to LDS; then the (channel tile, query tile) pieces of the merge
 // are shared out over the waves, each merging in wave order, and the chunk's
 // partial is written for the combine kernel.
+// exp(x) for x <= 0 as 2^(x log2 e) on the transcendental unit (v_exp_f32,
+// about 1 ulp): the probabilities are rounded to a 16-bit pair next, so the
+// softmax needs no more, and the ~15-instruction exp of the oracle was the
+// kernel's largest VALU cost
+__device__ __forceinline__ float exp_hw(float x)
+{
+    return __builtin_amdgcn_exp2f(__fmul_rn(x, 1.44269504088896341f));
+}
+
 template <int HD, int NT, int NWV>
 constexpr uint32_t attn_mfma_lds()
 {
@@ -468,7 +477,7 @@ __global__ __launch_bounds__(NWV * 64) void k_attn_mfma(AttnParams p)
                 for (int i = 0; i < 4; ++i)
                 {
                     const float v = sc[kk][T][n][i];
-                    e[4 * T + i] = v == -__builtin_huge_valf() ? 0.0f : expf_ref(__fsub_rn(v, mx));
+                    e[4 * T + i] = v == -__builtin_huge_valf() ? 0.0f : exp_hw(__fsub_rn(v, mx));
                     sum += e[4 * T + i];
                 }
             pop[kk][n] = u4v{pack_pair<AF>(e[0], e[1]), pack_pair<AF>(e[2], e[3]), pack_pair<AF>(e[4], e[5]),
@@ -563,9 +572,13 @@ __global__ __launch_bounds__(NWV * 64) void k_attn_mfma(AttnParams p)
 
 // One wave per (row, query head): merge that row's chunks 0..last in order.
 // Lanes first take chunks (max, then weights and the denominator with a fixed
-// butterfly), then channels, summing the chunks' outputs in chunk order.
+// butterfly), then channels d = lane + 64 i (i < DPL), summing the chunks'
+// outputs in chunk order.  The first CB chunks' outputs are loaded together
+// with the statistics, so a context of up to CB chunks costs one round trip.
+template <int DPL>
 __global__ __launch_bounds__(64) void k_attn_combine(AttnParams p)
 {
+    constexpr uint32_t CB = 32;
     __shared__ float wsh[1024];
     const uint32_t head = blockIdx.x, rr = blockIdx.y;    // rr = b * R + j
     const uint32_t R = p.rows, b = rr / R, j = rr - b * R;
@@ -574,28 +587,58 @@ __global__ __launch_bounds__(64) void k_attn_combine(AttnParams p)
     uint32_t last = (static_cast<uint32_t>(p.seq_len[b]) + j) / p.chunk;
     if (last >= p.nch) last = p.nch - 1u;          // length beyond the launch bound: clamp, never overrun
     const uint64_t base = (static_cast<uint64_t>(b) * p.n_kv + kh) * p.nch;
+    auto acc_at = [&](uint32_t c, int i) {
+        const uint32_t d = min(lane + 64u * i, hd - 1u);
+        return p.part_acc[((base + min(c, last)) * Gq + qi) * hd + d];
+    };
+    // statistics of chunks lane, lane + 64, ... and the first CB chunks' outputs
+    const uint32_t c0 = min(lane, last);
+    const float m0 = p.part_ml[((base + c0) * Gq + qi) * 2u], l0 = p.part_ml[((base + c0) * Gq + qi) * 2u + 1u];
+    float v[CB][DPL];
+#pragma unroll
+    for (uint32_t c = 0; c < CB; ++c)
+#pragma unroll
+        for (int i = 0; i < DPL; ++i) v[c][i] = acc_at(c, i);
     float mx = -__builtin_huge_valf();
-    for (uint32_t c = lane; c <= last; c += 64u) mx = fmaxf(mx, p.part_ml[((base + c) * Gq + qi) * 2u]);
+    if (lane <= last) mx = fmaxf(mx, m0);
+    for (uint32_t c = lane + 64u; c <= last; c += 64u) mx = fmaxf(mx, p.part_ml[((base + c) * Gq + qi) * 2u]);
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
     float den = 0.0f;
     for (uint32_t c = lane; c <= last; c += 64u)
     {
-        const float m = p.part_ml[((base + c) * Gq + qi) * 2u];
+        const float m = c == lane ? m0 : p.part_ml[((base + c) * Gq + qi) * 2u];
+        const float l = c == lane ? l0 : p.part_ml[((base + c) * Gq + qi) * 2u + 1u];
         const float w = m == -__builtin_huge_valf() ? 0.0f : expf_ref(__fsub_rn(m, mx));
         wsh[c] = w;
-        den = __fmaf_rn(w, p.part_ml[((base + c) * Gq + qi) * 2u + 1u], den);
+        den = __fmaf_rn(w, l, den);
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) den += __shfl_xor(den, o);
     __syncthreads();
     const float dd = den > 0.0f ? den : 1.0f;
-    for (uint32_t d = lane; d < hd; d += 64u)
+    float num[DPL];
+#pragma unroll
+    for (int i = 0; i < DPL; ++i) num[i] = 0.0f;
+#pragma unroll
+    for (uint32_t c = 0; c < CB; ++c)
     {
-        float num = 0.0f;
-#pragma unroll 8
-        for (uint32_t c = 0; c <= last; ++c) num = __fmaf_rn(wsh[c], p.part_acc[((base + c) * Gq + qi) * hd + d], num);
-        store_act_rt(p.out, (static_cast<uint64_t>(rr) * p.n_heads + head) * hd + d, __fdiv_rn(num, dd), p.afmt);
+        const bool in = c <= last;                  // past the last chunk: skipped, not added as zero
+        const float w = wsh[in ? c : 0u];
+#pragma unroll
+        for (int i = 0; i < DPL; ++i) num[i] = in ? __fmaf_rn(w, v[c][i], num[i]) : num[i];
+    }
+    for (uint32_t c = CB; c <= last; ++c)
+    {
+        const float w = wsh[c];
+#pragma unroll
+        for (int i = 0; i < DPL; ++i) num[i] = __fmaf_rn(w, acc_at(c, i), num[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < DPL; ++i)
+    {
+        const uint32_t d = lane + 64u * i;
+        if (d < hd) store_act_rt(p.out, (static_cast<uint64_t>(rr) * p.n_heads + head) * hd + d, __fdiv_rn(num[i], dd), p.afmt);
     }
 }
 
@@ -768,7 +811,14 @@ int attn_launch(opure_dev* dev, const opure_model* m, const opure_kv* kv, uint32
         hipLaunchKernelGGL(k_attn_chunk_generic, grid, dim3(256), lds, dev->stream, p);
         OPURE_LAUNCH_CHECK("k_attn_chunk_generic");
     }
-    hipLaunchKernelGGL(k_attn_combine, dim3(p.n_heads, batch * rows), dim3(64), 0, dev->stream, p);
+    const dim3 cgrid(p.n_heads, batch * rows);
+    switch ((p.hd + 63u) / 64u)
+    {
+    case 1: hipLaunchKernelGGL(k_attn_combine<1>, cgrid, dim3(64), 0, dev->stream, p); break;
+    case 2: hipLaunchKernelGGL(k_attn_combine<2>, cgrid, dim3(64), 0, dev->stream, p); break;
+    case 3: hipLaunchKernelGGL(k_attn_combine<3>, cgrid, dim3(64), 0, dev->stream, p); break;
+    default: hipLaunchKernelGGL(k_attn_combine<4>, cgrid, dim3(64), 0, dev->stream, p); break;
+    }
     OPURE_LAUNCH_CHECK("k_attn_combine");
     return OPURE_OK;
 }
