@@ -12,10 +12,10 @@ using namespace opure_dev_math;
 
 namespace opure_gemv {
 
-int launch_f32(opure_dev*, uint32_t, bool, bool, const KParams&, const Recipe&, uint32_t, uint32_t);
-int launch_i8(opure_dev*, uint32_t, bool, bool, const KParams&, const Recipe&, uint32_t, uint32_t);
-int launch_i4_f16(opure_dev*, uint32_t, bool, bool, const KParams&, const Recipe&, uint32_t, uint32_t);
-int launch_i4_bf16(opure_dev*, uint32_t, bool, bool, const KParams&, const Recipe&, uint32_t, uint32_t);
+int launch_f32(opure_dev*, uint32_t, uint32_t, bool, const KParams&, const Recipe&, uint32_t, uint32_t);
+int launch_i8(opure_dev*, uint32_t, uint32_t, bool, const KParams&, const Recipe&, uint32_t, uint32_t);
+int launch_i4_f16(opure_dev*, uint32_t, uint32_t, bool, const KParams&, const Recipe&, uint32_t, uint32_t);
+int launch_i4_bf16(opure_dev*, uint32_t, uint32_t, bool, const KParams&, const Recipe&, uint32_t, uint32_t);
 int launch_wide_i8(opure_dev*, uint32_t, const WParams&, uint32_t);
 int launch_wide_i4_f16(opure_dev*, uint32_t, const WParams&, uint32_t);
 int launch_wide_i4_bf16(opure_dev*, uint32_t, const WParams&, uint32_t);
@@ -25,6 +25,7 @@ int launch_wide_i4_bf16(opure_dev*, uint32_t, const WParams&, uint32_t);
 namespace {
 
 using opure_gemv::u4_t;
+using opure_gemv::f4_t;
 
 uint32_t kb_of(uint32_t wfmt) { return wfmt == OPURE_W_F32 ? 16u : (wfmt == OPURE_W_I8PC ? 64u : 128u); }
 uint64_t row_bytes(uint32_t wfmt, uint32_t in)
@@ -96,23 +97,53 @@ __global__ __launch_bounds__(256) void k_tile_s(const uint16_t* scale, const uin
     static_cast<uint32_t*>(dst)[id] = static_cast<uint32_t>(scale[si]) | (static_cast<uint32_t>(zero[si]) << 16);
 }
 
-// Normalisation pre-pass for a fused rmsnorm whose X does not fit in LDS: the
-// same inverse rms and rounding as the staged path, written to xn [M][in].
+// The rmsnorm rows pass: xn[m][k] = round(x[m][k] * inv_m * g[k]), the same
+// inverse rms (inv_rms_wave) and rounding as the staged fusion.  Workgroup
+// (c, m) takes 2048 columns of row m, 8 per thread; every wave issues its x
+// and gain loads, then computes inv_m itself, so the pass is one round trip.
 template <int AF>
-__global__ __launch_bounds__(64) void k_prenorm(opure_gemv::KParams p, void* xn)
+__global__ __launch_bounds__(256) void k_rmsnorm_rows(opure_gemv::KParams p, void* xn)
 {
     constexpr uint32_t EB = AF == OPURE_A_F32 ? 4u : 2u;
-    const uint32_t m = blockIdx.x, lane = threadIdx.x;
+    const uint32_t m = blockIdx.y, lane = threadIdx.x & 63u;
+    const uint32_t j = blockIdx.x * 256u + threadIdx.x, n8 = p.in / 8u;
+    const uint32_t jc = min(j, n8 - 1u);
+    const f4_t* xr = reinterpret_cast<const f4_t*>(reinterpret_cast<const float*>(p.x) + static_cast<uint64_t>(m) * p.in + 8u * jc);
+    const f4_t* gr = reinterpret_cast<const f4_t*>(p.gain + 8u * jc);
+    const f4_t x0 = xr[0], x1 = xr[1], g0 = gr[0], g1 = gr[1];
     const float inv = opure_gemv::inv_rms_wave(p, m, lane);
-    uint8_t* row = static_cast<uint8_t*>(xn) + static_cast<uint64_t>(m) * p.in * EB;
-    for (uint32_t j = lane; j < p.in / 8u; j += 64u)
+    if (j >= n8) return;
+    float yv[8];
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
     {
-        uint32_t o[8];
-        opure_gemv::load8<AF, true>(p, m, 8u * j, inv, o);
-        u4_t* dst = reinterpret_cast<u4_t*>(row + 8u * j * EB);
-        dst[0] = u4_t{o[0], o[1], o[2], o[3]};
-        if constexpr (AF == OPURE_A_F32) dst[1] = u4_t{o[4], o[5], o[6], o[7]};
+        yv[e] = __fmul_rn(__fmul_rn(x0[e], inv), g0[e]);
+        yv[4 + e] = __fmul_rn(__fmul_rn(x1[e], inv), g1[e]);
     }
+    uint8_t* dst = static_cast<uint8_t*>(xn) + (static_cast<uint64_t>(m) * p.in + 8u * j) * EB;
+    if constexpr (AF == OPURE_A_F32)
+    {
+        reinterpret_cast<u4_t*>(dst)[0] = __builtin_bit_cast(u4_t, f4_t{yv[0], yv[1], yv[2], yv[3]});
+        reinterpret_cast<u4_t*>(dst)[1] = __builtin_bit_cast(u4_t, f4_t{yv[4], yv[5], yv[6], yv[7]});
+    }
+    else
+    {
+        *reinterpret_cast<u4_t*>(dst) = u4_t{opure_gemv::pack2<AF>(yv[0], yv[1]), opure_gemv::pack2<AF>(yv[2], yv[3]),
+                                             opure_gemv::pack2<AF>(yv[4], yv[5]), opure_gemv::pack2<AF>(yv[6], yv[7])};
+    }
+}
+
+int rmsnorm_rows_launch(opure_dev* dev, const opure_gemv::KParams& kp, uint32_t afmt, uint32_t M, void* xn)
+{
+    const dim3 grid((kp.in / 8u + 255u) / 256u, M);
+    if (afmt == OPURE_A_F32)
+        hipLaunchKernelGGL(k_rmsnorm_rows<OPURE_A_F32>, grid, dim3(256), 0, dev->stream, kp, xn);
+    else if (afmt == OPURE_A_F16)
+        hipLaunchKernelGGL(k_rmsnorm_rows<OPURE_A_F16>, grid, dim3(256), 0, dev->stream, kp, xn);
+    else
+        hipLaunchKernelGGL(k_rmsnorm_rows<OPURE_A_BF16>, grid, dim3(256), 0, dev->stream, kp, xn);
+    OPURE_LAUNCH_CHECK("k_rmsnorm_rows");
+    return OPURE_OK;
 }
 
 struct Plan {
@@ -133,9 +164,9 @@ Plan make_plan(const opure_dev* dev, uint32_t wfmt, uint32_t xfmt, uint32_t out,
     pl.r = pl.tiles >= 320u ? R_WIDE : (pl.tiles > 192u ? R_MID : R_NARROW);
     pl.groups = (pl.tiles + pl.r.t - 1u) / pl.r.t;
     const uint32_t EB = opure_hip::act_bytes(xfmt);
-    const uint32_t red = pl.r.nw * pl.r.t * 1024u;
+    const uint32_t red = 2u * pl.r.nw * pl.r.t * 1024u;   // one reduction buffer per group parity
     const uint32_t stride = in * EB + 16u;
-    const uint32_t xsum = wfmt == OPURE_W_I4G128 ? M * (in / 128u) * 4u : 0u;
+    const uint32_t xsum = 0u;   // the uint4 group sums of X come from the matrix cores
     const uint32_t off_xsum = static_cast<uint32_t>(opure_hip::align_up(static_cast<uint64_t>(M) * stride, 16));
     const uint32_t off_red = static_cast<uint32_t>(opure_hip::align_up(off_xsum + xsum, 16));
     const uint32_t total = off_red + red;
@@ -260,6 +291,7 @@ int gemv_validate(const GemvCall& c)
         OPURE_REQUIRE(c.ss_in && c.ss_tiles >= 1 && (reinterpret_cast<uintptr_t>(c.gain) & 15u) == 0 &&
                           (c.epi == EPI_SWIGLU || c.epi == EPI_QKV || c.epi == EPI_LOGITS || c.M > OPURE_MAX_ROWS),
                       OPURE_E_INVALID, "gemv: fused rmsnorm needs sums of squares, an aligned gain and a consumer epilogue");
+
     if (c.epi == EPI_QKV)
     {
         const QkvEpilogue& e = c.qkv;
@@ -309,11 +341,8 @@ static int gemv_launch_wide(opure_dev* dev, const GemvCall& c)
         kp.eps = c.eps;
         kp.ss_in = c.ss_in;
         kp.ss_tiles = c.ss_tiles;
-        if (c.xfmt == OPURE_A_F16)
-            hipLaunchKernelGGL(k_prenorm<OPURE_A_F16>, dim3(c.M), dim3(64), 0, dev->stream, kp, c.xn_scratch);
-        else
-            hipLaunchKernelGGL(k_prenorm<OPURE_A_BF16>, dim3(c.M), dim3(64), 0, dev->stream, kp, c.xn_scratch);
-        OPURE_LAUNCH_CHECK("k_prenorm");
+        const int rc = rmsnorm_rows_launch(dev, kp, c.xfmt, c.M, c.xn_scratch);
+        if (rc) return rc;
         kp.x = static_cast<const uint8_t*>(c.xn_scratch);
         kp.gain = nullptr;
     }
@@ -350,27 +379,22 @@ int gemv_launch(opure_dev* dev, const GemvCall& c)
     kp.off_red = pl.off_red;
     kp.qkv = c.qkv;
     kp.lg = c.logits;
-    bool fuse = norm;
+    uint32_t nm = norm ? 1u : 0u;
     if (norm && !pl.staged)
     {
-        // X too large for LDS: normalise into the scratch rows, then a plain GEMV
+        // the rows pass into the scratch rows, then a plain GEMV
         OPURE_REQUIRE(c.xn_scratch, OPURE_E_UNSUPPORTED, "gemv: rmsnorm over %u x %u needs a scratch buffer", c.M,
                       c.W.in);
-        if (c.xfmt == OPURE_A_F32)
-            hipLaunchKernelGGL(k_prenorm<OPURE_A_F32>, dim3(c.M), dim3(64), 0, dev->stream, kp, c.xn_scratch);
-        else if (c.xfmt == OPURE_A_F16)
-            hipLaunchKernelGGL(k_prenorm<OPURE_A_F16>, dim3(c.M), dim3(64), 0, dev->stream, kp, c.xn_scratch);
-        else
-            hipLaunchKernelGGL(k_prenorm<OPURE_A_BF16>, dim3(c.M), dim3(64), 0, dev->stream, kp, c.xn_scratch);
-        OPURE_LAUNCH_CHECK("k_prenorm");
+        const int rc = rmsnorm_rows_launch(dev, kp, c.xfmt, c.M, c.xn_scratch);
+        if (rc) return rc;
         kp.x = static_cast<const uint8_t*>(c.xn_scratch);
         kp.gain = nullptr;
-        fuse = false;
+        nm = 0u;
     }
-    if (c.wfmt == OPURE_W_F32) return launch_f32(dev, c.epi, fuse, pl.staged, kp, pl.r, pl.grid, pl.lds);
-    if (c.wfmt == OPURE_W_I8PC) return launch_i8(dev, c.epi, fuse, pl.staged, kp, pl.r, pl.grid, pl.lds);
-    if (c.xfmt == OPURE_A_F16) return launch_i4_f16(dev, c.epi, fuse, pl.staged, kp, pl.r, pl.grid, pl.lds);
-    return launch_i4_bf16(dev, c.epi, fuse, pl.staged, kp, pl.r, pl.grid, pl.lds);
+    if (c.wfmt == OPURE_W_F32) return launch_f32(dev, c.epi, nm, pl.staged, kp, pl.r, pl.grid, pl.lds);
+    if (c.wfmt == OPURE_W_I8PC) return launch_i8(dev, c.epi, nm, pl.staged, kp, pl.r, pl.grid, pl.lds);
+    if (c.xfmt == OPURE_A_F16) return launch_i4_f16(dev, c.epi, nm, pl.staged, kp, pl.r, pl.grid, pl.lds);
+    return launch_i4_bf16(dev, c.epi, nm, pl.staged, kp, pl.r, pl.grid, pl.lds);
 }
 
 }  // namespace opure_hip

@@ -4,10 +4,10 @@
 
 namespace opure_gemv {
 
-int launch_f32(opure_dev* dev, uint32_t epi, bool norm, bool staged, const KParams& kp, const Recipe& r, uint32_t grid,
+int launch_f32(opure_dev* dev, uint32_t epi, uint32_t nm, bool staged, const KParams& kp, const Recipe& r, uint32_t grid,
         uint32_t lds)
 {
-    return launch_format<OPURE_W_F32, OPURE_A_F32>(dev, epi, norm, staged, kp, r, grid, lds);
+    return launch_format<OPURE_W_F32, OPURE_A_F32>(dev, epi, nm, staged, kp, r, grid, lds);
 }
 
 }  // namespace opure_gemv

@@ -5,10 +5,10 @@
 
 namespace opure_gemv {
 
-int launch_i8(opure_dev* dev, uint32_t epi, bool norm, bool staged, const KParams& kp, const Recipe& r, uint32_t grid,
+int launch_i8(opure_dev* dev, uint32_t epi, uint32_t nm, bool staged, const KParams& kp, const Recipe& r, uint32_t grid,
         uint32_t lds)
 {
-    return launch_format<OPURE_W_I8PC, OPURE_A_F16>(dev, epi, norm, staged, kp, r, grid, lds);
+    return launch_format<OPURE_W_I8PC, OPURE_A_F16>(dev, epi, nm, staged, kp, r, grid, lds);
 }
 
 int launch_wide_i8(opure_dev* dev, uint32_t epi, const WParams& wp, uint32_t lds)

@@ -218,7 +218,7 @@ __device__ __forceinline__ void load8(const KParams& p, uint32_t m, uint32_t k, 
 }
 
 // Staging of X rows 0..M-1 (whole K) into LDS rows of x_stride bytes, natural
-// k order; uint4 also writes each 128-k group's sum to xsum[m][g].
+// k order.
 //
 // Thread t owns the 8-value unit column j = j0 + t % n8 (n8 = in/8) and the
 // rows rg, rg + RT, ... with rg = t / n8 and RT = max(1, NTH / n8) row groups,
@@ -226,9 +226,7 @@ __device__ __forceinline__ void load8(const KParams& p, uint32_t m, uint32_t k, 
 // holds KR rows of one unit column in registers: stage_issue only issues the
 // loads, stage_store converts and writes them, so the kernel can issue the
 // first round, then its first weight loads, and wait for L2 alone (loads
-// retire in issue order).  n8 and NTH are multiples of 16, so the 16 units of
-// a group sit in 16 aligned lanes with the same row and the group sum is a
-// fixed butterfly.
+// retire in issue order).
 template <int AF, bool NORM, int KR>
 struct StageRound {
     static constexpr int XW = (NORM || AF == OPURE_A_F32) ? 2 : 1;   // 16-byte words of a unit
@@ -291,8 +289,6 @@ __device__ __forceinline__ void stage_store(const KParams& p, const StageRound<A
 {
     constexpr uint32_t EB = AF == OPURE_A_F32 ? 4u : 2u;
     const StageMap<NTH> sm(p, j0);
-    const uint32_t lane = threadIdx.x & 63u;
-    float* xsum = reinterpret_cast<float*>(lds + p.off_xsum);
 #pragma unroll
     for (int i = 0; i < KR; ++i)
     {
@@ -344,11 +340,6 @@ __device__ __forceinline__ void stage_store(const KParams& p, const StageRound<A
         else
         {
             if (keep) *reinterpret_cast<u4_t*>(dst) = u4_t{o[0], o[1], o[2], o[3]};
-            if constexpr (WF == OPURE_W_I4G128)
-            {
-                const float u = row16_sum(unit_sum<AF>(o[0], o[1], o[2], o[3]));
-                if (keep && (lane & 15u) == 0) xsum[m * (p.in / 128u) + sm.j / 16u] = u;
-            }
         }
     }
 }
@@ -481,10 +472,119 @@ __device__ __forceinline__ void epilogue(const KParams& p, uint32_t tile, uint32
     }
 }
 
+// Epilogue of k_gemv, one output element per thread.  The MFMAs take X as
+// the A operand, so lane (g4, r16) of a wave's accumulator holds y[m][o] for
+// the X rows m = 4*g4 + i and the weight row o = 16*tile + r16.  After the
+// waves' partial sums meet in LDS, thread e of the workgroup takes element
+// (tile t, row m, column r16) with e = 256 t + 16 m + r16 and adds the waves'
+// partials in wave order; so the 16 weight rows of a tile and row m sit in
+// the 16 lanes of a DPP row: a tile's sums of squares and argmax are DPP
+// trees, and the (gate, up) and RoPE pairs (o even, o + 1) are lanes r16 and
+// r16 ^ 1.  EPI_LOGITS keeps the best (value, lowest index) of its (t, m)
+// seen so far; the workgroup writes one partial per row at its end.
+__device__ __forceinline__ void best_merge(float& bv, int32_t& bi, float ov, int32_t oi)
+{
+    if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+}
+
+template <int CTRL>
+__device__ __forceinline__ int32_t dpp_i(int32_t v)
+{
+    return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, true);
+}
+
+template <int WF, int EPI>
+__device__ __forceinline__ void epilogue_elem(const KParams& p, uint32_t tile, uint32_t m, uint32_t r16, float v,
+                                              float& best_v, int32_t& best_i)
+{
+    const uint32_t M = p.M;
+    const uint32_t o = 16u * tile + r16;
+    const bool live = tile < p.tiles && m < M;    // uniform over the 16 lanes of the DPP row
+    if constexpr (WF == OPURE_W_I8PC) v = __fmul_rn(v, live ? f16_to_f32(static_cast<const uint16_t*>(p.sc)[o]) : 1.0f);
+    if constexpr (EPI == opure_hip::EPI_LOGITS)
+    {
+        float bv = -__builtin_huge_valf();
+        int32_t bi = 0x7FFFFFFF;
+        if (live)
+        {
+            static_cast<float*>(p.y)[static_cast<uint64_t>(m) * p.out + o] = v;
+            bv = v != v ? -__builtin_huge_valf() : v;
+            bi = static_cast<int32_t>(o);
+        }
+        // a total order, so the tree's shape does not matter
+        best_merge(bv, bi, dpp_f<0xB1>(bv), dpp_i<0xB1>(bi));
+        best_merge(bv, bi, dpp_f<0x4E>(bv), dpp_i<0x4E>(bi));
+        best_merge(bv, bi, dpp_f<0x141>(bv), dpp_i<0x141>(bi));
+        best_merge(bv, bi, dpp_f<0x140>(bv), dpp_i<0x140>(bi));
+        best_merge(best_v, best_i, bv, bi);
+        return;
+    }
+    if constexpr (EPI == opure_hip::EPI_RESIDUAL)
+    {
+        // x += y, and this tile's sum of squares of the new x for the next rmsnorm
+        float nv = 0.0f;
+        if (live)
+        {
+            float* y = static_cast<float*>(p.y) + static_cast<uint64_t>(m) * p.out + o;
+            nv = __fadd_rn(*y, v);
+            *y = nv;
+        }
+        const float sq = row16_sum(__fmul_rn(nv, nv));
+        if (p.ss_out && live && r16 == 0) p.ss_out[static_cast<uint64_t>(tile) * M + m] = sq;
+        return;
+    }
+    if constexpr (EPI == opure_hip::EPI_STORE)
+    {
+        if (live) store_act_rt(p.y, static_cast<uint64_t>(m) * p.out + o, v, p.yfmt);
+    }
+    else if constexpr (EPI == opure_hip::EPI_SWIGLU)
+    {
+        // tile rows alternate gate / up: lane r16 even holds a gate, r16 + 1 its up
+        const float up = dpp_f<0xB1>(v);
+        if (live && (r16 & 1u) == 0)
+            store_act_rt(p.y, static_cast<uint64_t>(m) * (p.out >> 1) + 8u * tile + (r16 >> 1), swiglu(v, up), p.yfmt);
+    }
+    else if constexpr (EPI == opure_hip::EPI_QKV)
+    {
+        const opure_hip::QkvEpilogue& e = p.qkv;
+        const float other = dpp_f<0xB1>(v);
+        if (!live) return;
+        const uint32_t b = m / e.rows_per_seq, j = m - b * e.rows_per_seq;
+        const uint32_t pos = static_cast<uint32_t>(e.seq_len[b]) + j;
+        if (pos >= e.rope_max_pos || pos / OPURE_PAGE_SIZE >= e.max_pages) return;   // past the tables: drop
+        const uint32_t hd = e.head_dim, half = hd >> 1;
+        const bool rot = o < e.qdim + e.kvdim;
+        if (rot)
+        {
+            // rotate the interleaved pair (o even, o + 1) (Opure_RoPE.usf:7-10)
+            const uint32_t d = (o < e.qdim ? o : o - e.qdim) % hd;
+            const float c = e.rope_cos[static_cast<uint64_t>(pos) * half + d / 2u];
+            const float sn = e.rope_sin[static_cast<uint64_t>(pos) * half + d / 2u];
+            const bool odd = (r16 & 1u) != 0;
+            const float e0 = odd ? other : v, e1 = odd ? v : other;
+            v = odd ? __fadd_rn(__fmul_rn(e0, sn), __fmul_rn(e1, c)) : __fsub_rn(__fmul_rn(e0, c), __fmul_rn(e1, sn));
+        }
+        if (o < e.qdim)
+        {
+            store_act_rt(p.y, static_cast<uint64_t>(m) * e.qdim + o, v, p.yfmt);
+            return;
+        }
+        const uint32_t kvsel = rot ? 0u : 1u;
+        const uint32_t ok = o - e.qdim - kvsel * e.kvdim;
+        const uint32_t kh = ok / hd, dk = ok - kh * hd;
+        const int32_t page = e.page_table[static_cast<uint64_t>(b) * e.max_pages + pos / OPURE_PAGE_SIZE];
+        if (page < 0 || static_cast<uint32_t>(page) >= e.n_pages) return;
+        store_act_rt(e.kv_pool,
+                     kv_elem(e.layer, e.n_pages, static_cast<uint32_t>(page), kvsel, e.n_kv_heads, kh, hd,
+                             pos % OPURE_PAGE_SIZE, dk),
+                     v, p.yfmt);
+    }
+}
+
 template <int WF, int AF, int T, int U, bool STAGED>
 struct Payload {
     u4_t w[T][U];
-    u4_t s[T][U];                                        // uint4 scales of the block (rows 4*g4..+3)
+    uint32_t s[T][U];                                    // uint4: scale | zero << 16 of weight row r16
     u4_t x[STAGED ? 1 : U][Fmt<WF>::N / 4u];             // direct X fragments
 };
 
@@ -496,9 +596,9 @@ __global__ __launch_bounds__(NW * 64) void k_gemv(KParams p)
     constexpr uint32_t VALS = KB / 4u;                   // k values per lane per block
     constexpr uint32_t PB = U * NW;                      // blocks per pass
     static_assert(STAGED || !NORM, "the fused rmsnorm needs the staged X");
+    __shared__ float sinv[OPURE_MAX_ROWS];
     extern __shared__ __align__(16) uint8_t lds[];
     f4_t* red = reinterpret_cast<f4_t*>(lds + p.off_red);
-    const float* xsum = reinterpret_cast<const float*>(lds + p.off_xsum);
 
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
     const uint32_t g4 = lane >> 4, r16 = lane & 15u;
@@ -525,8 +625,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemv(KParams p)
                 b.w[t][u] = __builtin_nontemporal_load(
                     reinterpret_cast<const u4_t*>(p.w + ((static_cast<uint64_t>(tile) * nblk + blk) << 10) + (lane << 4)));
                 if constexpr (WF == OPURE_W_I4G128)
-                    b.s[t][u] = *reinterpret_cast<const u4_t*>(static_cast<const uint32_t*>(p.sc) +
-                                                               (static_cast<uint64_t>(tile) * G + blk) * 16u + 4u * g4);
+                    b.s[t][u] = static_cast<const uint32_t*>(p.sc)[(static_cast<uint64_t>(tile) * G + blk) * 16u + r16];
             }
         }
         if constexpr (!STAGED)
@@ -544,6 +643,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemv(KParams p)
     };
 
     PL A, B;
+    [[maybe_unused]] PL C;
     if constexpr (STAGED)
     {
         // Issue order: the first staging round, the rows' sums of squares, then
@@ -553,7 +653,6 @@ __global__ __launch_bounds__(NW * 64) void k_gemv(KParams p)
         constexpr int KR = stage_rows<AF, NORM, NTH>();
         constexpr int RW = (OPURE_MAX_ROWS + NW - 1) / NW;  // columns whose rms a wave computes
         constexpr int SSE = 4;                              // sums per lane issued early: in <= 4096
-        __shared__ float sinv[OPURE_MAX_ROWS];
         StageRound<AF, NORM, KR> r0;
         stage_issue<AF, NORM, NTH, KR>(p, r0, 0u, 0u);
         float ssp[NORM ? RW : 1][SSE];
@@ -605,6 +704,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemv(KParams p)
                 stage_issue<AF, NORM, NTH, KR>(p, r, j0, i0);
                 stage_store<WF, AF, NORM, NTH, KR>(p, r, j0, i0, lds, sinv);
             }
+        if (S > 2u) load(C, 2);                             // the staging registers are free now
         __syncthreads();
     }
     else
@@ -628,8 +728,8 @@ __global__ __launch_bounds__(NW * 64) void k_gemv(KParams p)
         {
             const uint32_t blk = ps * PB + u * NW + wave;
             if (blk >= nblk) continue;
+            // X fragment of row mc, k-slice g4 of the block: the A operand
             uint32_t xd[N];
-            float xs = 0.0f;
             if constexpr (STAGED)
             {
                 const u4_t* src = reinterpret_cast<const u4_t*>(lds + mc * p.x_stride + (blk * KB + VALS * g4) * EB);
@@ -639,7 +739,6 @@ __global__ __launch_bounds__(NW * 64) void k_gemv(KParams p)
                     const u4_t v = src[i];
                     xd[4 * i] = v[0]; xd[4 * i + 1] = v[1]; xd[4 * i + 2] = v[2]; xd[4 * i + 3] = v[3];
                 }
-                if constexpr (WF == OPURE_W_I4G128) xs = xsum[mc * G + blk];
             }
             else
             {
@@ -648,17 +747,6 @@ __global__ __launch_bounds__(NW * 64) void k_gemv(KParams p)
                 {
                     xd[4 * i] = b.x[u][i][0]; xd[4 * i + 1] = b.x[u][i][1];
                     xd[4 * i + 2] = b.x[u][i][2]; xd[4 * i + 3] = b.x[u][i][3];
-                }
-                if constexpr (WF == OPURE_W_I4G128)
-                {
-                    // the same sum tree as the staged group sums
-                    const float u0 = unit_sum<AF>(xd[0], xd[1], xd[2], xd[3]);
-                    const float u1 = unit_sum<AF>(xd[4], xd[5], xd[6], xd[7]);
-                    const float u2 = unit_sum<AF>(xd[8], xd[9], xd[10], xd[11]);
-                    const float u3 = unit_sum<AF>(xd[12], xd[13], xd[14], xd[15]);
-                    xs = (u0 + u1) + (u2 + u3);
-                    xs += __shfl_xor(xs, 16);
-                    xs += __shfl_xor(xs, 32);
                 }
             }
             if constexpr (WF == OPURE_W_F32)
@@ -669,28 +757,42 @@ __global__ __launch_bounds__(NW * 64) void k_gemv(KParams p)
                     const f4_t wf = __builtin_bit_cast(f4_t, b.w[t][u]);
 #pragma unroll
                     for (int q = 0; q < 4; ++q)
-                        acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(wf[q], __uint_as_float(xd[q]), acc[t], 0, 0, 0);
+                        acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(xd[q]), wf[q], acc[t], 0, 0, 0);
                 }
             }
             else if constexpr (WF == OPURE_W_I8PC)
             {
-                const half8_t b1 = as_half8(xd[0], xd[1], xd[2], xd[3]);
-                const half8_t b2 = as_half8(xd[4], xd[5], xd[6], xd[7]);
+                const half8_t x1 = as_half8(xd[0], xd[1], xd[2], xd[3]);
+                const half8_t x2 = as_half8(xd[4], xd[5], xd[6], xd[7]);
 #pragma unroll
                 for (int t = 0; t < T; ++t)
                 {
                     uint32_t a[8];
 #pragma unroll
                     for (int j = 0; j < 4; ++j) u8x4_to_f16(b.w[t][u][j], a[2 * j], a[2 * j + 1]);
-                    acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(a[0], a[1], a[2], a[3]), b1, acc[t], 0, 0, 0);
-                    acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(a[4], a[5], a[6], a[7]), b2, acc[t], 0, 0, 0);
+                    acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(x1, as_half8(a[0], a[1], a[2], a[3]), acc[t], 0, 0, 0);
+                    acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(x2, as_half8(a[4], a[5], a[6], a[7]), acc[t], 0, 0, 0);
                 }
             }
             else
             {
-                // one 128-k group per block: a fresh accumulator per tile, then
-                // acc += s * (bacc - (z + off) * xs), off = 128 for bf16 (MAGIC)
-                const float xoff = AF == OPURE_A_BF16 ? __fmul_rn(xs, 128.0f) : 0.0f;
+                // one 128-k group per block.  The group sums of X rows 4*g4 + i
+                // come from the matrix core too (B = ones), then per tile a
+                // fresh accumulator of (MAGIC + q) * x and
+                //   acc += s * (bacc - (z + off) * xs),  off = 128 for bf16 (MAGIC)
+                f4_t xs = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                {
+                    if constexpr (AF == OPURE_A_F16)
+                        xs = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(xd[4 * j], xd[4 * j + 1], xd[4 * j + 2], xd[4 * j + 3]),
+                                                                    as_half8(0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u),
+                                                                    xs, 0, 0, 0);
+                    else
+                        xs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf8(xd[4 * j], xd[4 * j + 1], xd[4 * j + 2], xd[4 * j + 3]),
+                                                                     as_bf8(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u),
+                                                                     xs, 0, 0, 0);
+                }
 #pragma unroll
                 for (int t = 0; t < T; ++t)
                 {
@@ -702,91 +804,123 @@ __global__ __launch_bounds__(NW * 64) void k_gemv(KParams p)
                         u4x8_pairs<AF>(b.w[t][u][j], a);
                         if constexpr (AF == OPURE_A_F16)
                             bacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                                as_half8(a[0], a[1], a[2], a[3]),
-                                as_half8(xd[4 * j], xd[4 * j + 1], xd[4 * j + 2], xd[4 * j + 3]), bacc, 0, 0, 0);
+                                as_half8(xd[4 * j], xd[4 * j + 1], xd[4 * j + 2], xd[4 * j + 3]),
+                                as_half8(a[0], a[1], a[2], a[3]), bacc, 0, 0, 0);
                         else
                             bacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                                as_bf8(a[0], a[1], a[2], a[3]),
-                                as_bf8(xd[4 * j], xd[4 * j + 1], xd[4 * j + 2], xd[4 * j + 3]), bacc, 0, 0, 0);
+                                as_bf8(xd[4 * j], xd[4 * j + 1], xd[4 * j + 2], xd[4 * j + 3]),
+                                as_bf8(a[0], a[1], a[2], a[3]), bacc, 0, 0, 0);
                     }
+                    const uint32_t sz = b.s[t][u];
+                    const float sc = __uint_as_float(sz << 16), z = __uint_as_float(sz & 0xFFFF0000u);
+                    const float zo = AF == OPURE_A_BF16 ? __fadd_rn(z, 128.0f) : z;
 #pragma unroll
-                    for (int i = 0; i < 4; ++i)
-                    {
-                        const uint32_t sz = b.s[t][u][i];
-                        const float sc = __uint_as_float(sz << 16), z = __uint_as_float(sz & 0xFFFF0000u);
-                        const float yv = __fmaf_rn(-z, xs, __fsub_rn(bacc[i], xoff));
-                        acc[t][i] = __fmaf_rn(sc, yv, acc[t][i]);
-                    }
+                    for (int i = 0; i < 4; ++i) acc[t][i] = __fmaf_rn(sc, __fmaf_rn(-zo, xs[i], bacc[i]), acc[t][i]);
                 }
             }
         }
         if (ps + 1u == npass)
         {
-            // combine the waves' K slices in wave order; wave t finishes tile t
+            // the waves' K slices meet in LDS (one buffer per group parity, so
+            // one barrier a group: a buffer is written again only after every
+            // thread has passed the next group's barrier), then every thread
+            // adds its element's partials in wave order and runs its epilogue
             const uint32_t grp = blockIdx.x + gi * gridDim.x;
-            __syncthreads();                               // the previous group's sums are read
+            f4_t* rb = red + (gi & 1u) * (NW * T * 64u);
 #pragma unroll
-            for (int t = 0; t < T; ++t) red[(wave * T + t) * 64u + lane] = acc[t];
+            for (int t = 0; t < T; ++t) rb[(wave * T + t) * 64u + lane] = acc[t];
             __syncthreads();
-            const uint32_t tile = grp * T + wave;
-            if (wave < static_cast<uint32_t>(T) && tile < p.tiles)
-            {
-                f4_t tot = red[wave * 64u + lane];
 #pragma unroll
-                for (int w = 1; w < NW; ++w) tot += red[(w * T + wave) * 64u + lane];
-                epilogue<WF, EPI>(p, tile, r16, g4, tot, best_v, best_i);
+            for (uint32_t e0 = 0; e0 < T * 256u; e0 += NW * 64u)
+            {
+                const uint32_t e = e0 + threadIdx.x;
+                if (T * 256u % (NW * 64u) != 0 && e >= T * 256u) break;   // whole waves
+                const uint32_t t = e >> 8, m = (e >> 4) & 15u, c = e & 15u;
+                const uint32_t li = ((m >> 2) << 4) + c, i = m & 3u;
+                const float* rf = reinterpret_cast<const float*>(rb);
+                float v = rf[((0u * T + t) * 64u + li) * 4u + i];
+#pragma unroll
+                for (int w = 1; w < NW; ++w) v += rf[((w * T + t) * 64u + li) * 4u + i];
+                epilogue_elem<WF, EPI>(p, grp * T + t, m, c, v, best_v, best_i);
             }
         }
     };
 
-    // software pipeline over the steps (group, pass): step s computes while
-    // s+1 is in flight.  Loads are issued only for steps that exist, on
-    // straight-line paths, so each wait covers exactly the buffer consumed.
+    // software pipeline over the steps (group, pass): with staged X three
+    // buffers, so the two steps after the one computing are in flight; direct
+    // kernels carry X fragments too and keep two.  Loads are issued only for
+    // steps that exist, on straight-line paths, so each wait covers exactly
+    // the buffer consumed.
     uint32_t s = 0;
-    while (S - s >= 4u)
+    if constexpr (STAGED)
     {
-        run(A, s);
-        load(A, s + 2u);
-        run(B, s + 1u);
-        load(B, s + 3u);
-        s += 2u;
+        while (S - s >= 6u)
+        {
+            run(A, s);
+            load(A, s + 3u);
+            run(B, s + 1u);
+            load(B, s + 4u);
+            run(C, s + 2u);
+            load(C, s + 5u);
+            s += 3u;
+        }
+        switch (S - s)
+        {
+        case 5u:
+            run(A, s); load(A, s + 3u);
+            run(B, s + 1u); load(B, s + 4u);
+            run(C, s + 2u); run(A, s + 3u); run(B, s + 4u);
+            break;
+        case 4u:
+            run(A, s); load(A, s + 3u);
+            run(B, s + 1u); run(C, s + 2u); run(A, s + 3u);
+            break;
+        case 3u: run(A, s); run(B, s + 1u); run(C, s + 2u); break;
+        case 2u: run(A, s); run(B, s + 1u); break;
+        case 1u: run(A, s); break;
+        default: break;
+        }
     }
-    const uint32_t rest = S - s;
-    if (rest == 3u)
+    else
     {
-        run(A, s);
-        load(A, s + 2u);
-        run(B, s + 1u);
-        run(A, s + 2u);
-    }
-    else if (rest == 2u)
-    {
-        run(A, s);
-        run(B, s + 1u);
-    }
-    else if (rest == 1u)
-    {
-        run(A, s);
+        while (S - s >= 4u)
+        {
+            run(A, s);
+            load(A, s + 2u);
+            run(B, s + 1u);
+            load(B, s + 3u);
+            s += 2u;
+        }
+        switch (S - s)
+        {
+        case 3u: run(A, s); load(A, s + 2u); run(B, s + 1u); run(A, s + 2u); break;
+        case 2u: run(A, s); run(B, s + 1u); break;
+        case 1u: run(A, s); break;
+        default: break;
+        }
     }
     if constexpr (EPI == opure_hip::EPI_LOGITS)
     {
-        // one argmax partial per column for the whole workgroup: waves t < T
-        // hold the best of the tiles they finished (a total order, so any
-        // merge order gives the same winner)
+        // one argmax partial per row for the whole workgroup: thread (t, m, 0)
+        // holds the best of column t of the tiles it finished (a total order,
+        // so any merge order gives the same winner)
         __syncthreads();
         float* sv = reinterpret_cast<float*>(red);
         int32_t* si = reinterpret_cast<int32_t*>(sv + T * 16);
-        if (wave < static_cast<uint32_t>(T) && g4 == 0) { sv[wave * 16u + r16] = best_v; si[wave * 16u + r16] = best_i; }
-        __syncthreads();
-        if (wave == 0 && g4 == 0 && r16 < M)
+        if (threadIdx.x < T * 256u && (threadIdx.x & 15u) == 0)
         {
-            float v = sv[r16];
-            int32_t i = si[r16];
+            sv[threadIdx.x >> 4] = best_v;
+            si[threadIdx.x >> 4] = best_i;
+        }
+        __syncthreads();
+        if (threadIdx.x < M)
+        {
+            float v = sv[threadIdx.x];
+            int32_t i = si[threadIdx.x];
 #pragma unroll
-            for (int t = 1; t < T; ++t)
-                if (sv[t * 16 + r16] > v || (sv[t * 16 + r16] == v && si[t * 16 + r16] < i)) { v = sv[t * 16 + r16]; i = si[t * 16 + r16]; }
-            p.lg.am_val[static_cast<uint64_t>(blockIdx.x) * M + r16] = v;
-            p.lg.am_idx[static_cast<uint64_t>(blockIdx.x) * M + r16] = i;
+            for (int t = 1; t < T; ++t) best_merge(v, i, sv[t * 16 + threadIdx.x], si[t * 16 + threadIdx.x]);
+            p.lg.am_val[static_cast<uint64_t>(blockIdx.x) * M + threadIdx.x] = v;
+            p.lg.am_idx[static_cast<uint64_t>(blockIdx.x) * M + threadIdx.x] = i;
         }
     }
 }
@@ -830,13 +964,15 @@ int launch_recipe(opure_dev* dev, const KParams& kp, const Recipe& r, uint32_t g
     return launch<WF, AF, EPI, 16, 1, STAGED ? 2 : 1, NORM, STAGED>(dev, kp, grid, lds);
 }
 
-// every (epilogue, norm, staged) combination the host may ask for
+// every (epilogue, rmsnorm, staged) combination the host may ask for; nm 1:
+// the rmsnorm is fused into the staging, 0: X is used as it is (a rmsnorm'd
+// X comes from the rows pass)
 template <int WF, int AF>
-int launch_format(opure_dev* dev, uint32_t epi, bool norm, bool staged, const KParams& kp, const Recipe& r,
+int launch_format(opure_dev* dev, uint32_t epi, uint32_t nm, bool staged, const KParams& kp, const Recipe& r,
                   uint32_t grid, uint32_t lds)
 {
     using namespace opure_hip;
-    if (norm)
+    if (nm == 1)
     {
         switch (epi)
         {
@@ -852,6 +988,8 @@ int launch_format(opure_dev* dev, uint32_t epi, bool norm, bool staged, const KP
         case EPI_STORE: return launch_recipe<WF, AF, EPI_STORE, false, true>(dev, kp, r, grid, lds);
         case EPI_RESIDUAL: return launch_recipe<WF, AF, EPI_RESIDUAL, false, true>(dev, kp, r, grid, lds);
         case EPI_SWIGLU: return launch_recipe<WF, AF, EPI_SWIGLU, false, true>(dev, kp, r, grid, lds);
+        case EPI_QKV: return launch_recipe<WF, AF, EPI_QKV, false, true>(dev, kp, r, grid, lds);
+        case EPI_LOGITS: return launch_recipe<WF, AF, EPI_LOGITS, false, true>(dev, kp, r, grid, lds);
         }
     }
     else
@@ -865,7 +1003,7 @@ int launch_format(opure_dev* dev, uint32_t epi, bool norm, bool staged, const KP
         case EPI_LOGITS: return launch_recipe<WF, AF, EPI_LOGITS, false, false>(dev, kp, r, grid, lds);
         }
     }
-    return set_error(OPURE_E_INVALID, "gemv: epilogue %u (norm %d, staged %d) is not built", epi, norm, staged);
+    return set_error(OPURE_E_INVALID, "gemv: epilogue %u (rmsnorm %u, staged %d) is not built", epi, nm, staged);
 }
 
 }  // namespace opure_gemv

@@ -111,7 +111,7 @@ struct GemvCall {
     // EPI_RESIDUAL: where to write the new residual's per-tile sums of squares
     float* ss_out = nullptr;
     // fused rmsnorm whose X does not fit in LDS: [M][in] activations, written
-    // by a normalisation pre-pass that the GEMV then reads
+    // by a normalisation rows pass that the GEMV then reads
     void* xn_scratch = nullptr;
     // more than OPURE_MAX_ROWS rows with K split over workgroups: the splits'
     // accumulators (gemv_scratch_bytes)
