@@ -161,13 +161,20 @@ Plan make_plan(const opure_dev* dev, uint32_t wfmt, uint32_t xfmt, uint32_t out,
     Plan pl;
     pl.tiles = out / 16u;
     pl.nblk = in / kb_of(wfmt);
-    pl.r = pl.tiles >= 320u ? R_WIDE : (pl.tiles > 192u ? R_MID : R_NARROW);
-    pl.groups = (pl.tiles + pl.r.t - 1u) / pl.r.t;
     const uint32_t EB = opure_hip::act_bytes(xfmt);
-    const uint32_t red = 2u * pl.r.nw * pl.r.t * 1024u;   // one reduction buffer per group parity
     const uint32_t stride = in * EB + 16u;
-    const uint32_t xsum = 0u;   // the uint4 group sums of X come from the matrix cores
-    const uint32_t off_xsum = static_cast<uint32_t>(opure_hip::align_up(static_cast<uint64_t>(M) * stride, 16));
+    const uint32_t xbytes = static_cast<uint32_t>(opure_hip::align_up(static_cast<uint64_t>(M) * stride, 16));
+    // 1024 tiles and more: waves own whole tiles, if X, the group sums and a
+    // 1 KB slot per wave fit in LDS
+    const uint32_t wpt_xs = wfmt == OPURE_W_I4G128 ? (in / 128u) * 64u : 0u;
+    const bool wpt = pl.tiles >= 1024u && xbytes + wpt_xs + R_WPT.nw * 1024u <= 159u * 1024u;
+    pl.r = wpt ? R_WPT : (pl.tiles >= 320u ? R_WIDE : (pl.tiles > 192u ? R_MID : R_NARROW));
+    pl.groups = (pl.tiles + pl.r.t - 1u) / pl.r.t;
+    // the K-split kernels: one reduction buffer per group parity; the
+    // wave-per-tile kernel: a 1 KB transposition slot per wave
+    const uint32_t red = wpt ? pl.r.nw * 1024u : 2u * pl.r.nw * pl.r.t * 1024u;
+    const uint32_t xsum = wpt ? wpt_xs : 0u;
+    const uint32_t off_xsum = xbytes;
     const uint32_t off_red = static_cast<uint32_t>(opure_hip::align_up(off_xsum + xsum, 16));
     const uint32_t total = off_red + red;
     pl.staged = total <= 159u * 1024u;

@@ -218,18 +218,21 @@ __device__ __forceinline__ void load8(const KParams& p, uint32_t m, uint32_t k, 
 }
 
 // Staging of X rows 0..M-1 (whole K) into LDS rows of x_stride bytes, natural
-// k order.
-//
-// Thread t owns the 8-value unit column j = j0 + t % n8 (n8 = in/8) and the
-// rows rg, rg + RT, ... with rg = t / n8 and RT = max(1, NTH / n8) row groups,
-// so the gain of a rmsnorm'd unit is loaded once for all its rows.  A round
-// holds KR rows of one unit column in registers: stage_issue only issues the
+// k order.  A round holds KR rows in registers: stage_issue only issues the
 // loads, stage_store converts and writes them, so the kernel can issue the
 // first round, then its first weight loads, and wait for L2 alone (loads
-// retire in issue order).
+// retire in issue order).  Every load instruction reads 64 consecutive 16-byte
+// pieces (the memory pipeline takes 64 bytes a clock, so a strided piece costs
+// as much as a whole line).
+//
+// 16-bit or fp32 X: thread t owns the 8-value unit column j = j0 + t % n8
+// (n8 = in/8) and the rows rg, rg + RT, ... with rg = t / n8 and RT =
+// max(1, NTH / n8) row groups.
+// rmsnorm'd fp32 residual: thread t owns the 4-value quads q = j0 + t and
+// j0 + t + NTH of every row, and the gain quads once for all rows.
 template <int AF, bool NORM, int KR>
 struct StageRound {
-    static constexpr int XW = (NORM || AF == OPURE_A_F32) ? 2 : 1;   // 16-byte words of a unit
+    static constexpr int XW = (NORM || AF == OPURE_A_F32) ? 2 : 1;   // 16-byte words per row
     u4_t x[KR][XW];
     u4_t g[NORM ? 2 : 1];
 };
@@ -249,28 +252,39 @@ struct StageMap {
     }
 };
 
+// the rmsnorm'd path's rounds: quads j0 + t + h NTH (h < 2), KR rows at a time
+template <int NTH>
+__device__ __forceinline__ uint32_t norm_quad(uint32_t j0, int h) { return j0 + threadIdx.x + h * NTH; }
+
 template <int AF, bool NORM, int NTH, int KR>
 __device__ __forceinline__ void stage_issue(const KParams& p, StageRound<AF, NORM, KR>& r, uint32_t j0, uint32_t i0)
 {
-    const StageMap<NTH> sm(p, j0);
-    const uint32_t j = sm.col ? sm.j : 0u;           // past the end: unit 0 of row 0 again, never stored
     if constexpr (NORM)
     {
-        const u4_t* gr = reinterpret_cast<const u4_t*>(p.gain + 8u * j);
-        r.g[0] = gr[0];
-        r.g[1] = gr[1];
+        const uint32_t n4 = p.in / 4u;
+        const f4_t* xf = reinterpret_cast<const f4_t*>(p.x);
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+        {
+            if (h == 1 && j0 + NTH >= n4) break;             // uniform: the round has one quad per thread
+            const uint32_t q = min(norm_quad<NTH>(j0, h), n4 - 1u);   // past the end: the last quad again, never stored
+            r.g[h] = __builtin_bit_cast(u4_t, reinterpret_cast<const f4_t*>(p.gain)[q]);
+#pragma unroll
+            for (int i = 0; i < KR; ++i)
+            {
+                const uint32_t m = min(i0 + i, p.M - 1u);
+                r.x[i][h] = __builtin_bit_cast(u4_t, xf[static_cast<uint64_t>(m) * n4 + q]);
+            }
+        }
+        return;
     }
+    const StageMap<NTH> sm(p, j0);
+    const uint32_t j = sm.col ? sm.j : 0u;           // past the end: unit 0 of row 0 again, never stored
 #pragma unroll
     for (int i = 0; i < KR; ++i)
     {
         const uint32_t m = min(sm.rg + (i0 + i) * sm.rt, p.M - 1u);
-        if constexpr (NORM)
-        {
-            const u4_t* xr = reinterpret_cast<const u4_t*>(reinterpret_cast<const float*>(p.x) + static_cast<uint64_t>(m) * p.in + 8u * j);
-            r.x[i][0] = xr[0];
-            r.x[i][1] = xr[1];
-        }
-        else if constexpr (AF == OPURE_A_F32)
+        if constexpr (AF == OPURE_A_F32)
         {
             const u4_t* src = reinterpret_cast<const u4_t*>(p.x + (static_cast<uint64_t>(m) * p.in + 8u * j) * 4u);
             r.x[i][0] = src[0];
@@ -288,58 +302,56 @@ __device__ __forceinline__ void stage_store(const KParams& p, const StageRound<A
                                             uint8_t* lds, const float* sinv)
 {
     constexpr uint32_t EB = AF == OPURE_A_F32 ? 4u : 2u;
+    if constexpr (NORM)
+    {
+        const uint32_t n4 = p.in / 4u;
+#pragma unroll
+        for (int i = 0; i < KR; ++i)
+        {
+            const uint32_t m = i0 + i;
+            if (m >= p.M) break;                         // uniform
+            // round(x * inv * g) (Opure_RMSNorm.usf:44-78)
+            const float inv = sinv[m];
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+            {
+                if (h == 1 && j0 + NTH >= n4) break;         // uniform
+                const uint32_t q = norm_quad<NTH>(j0, h);
+                const f4_t x = __builtin_bit_cast(f4_t, r.x[i][h]), g = __builtin_bit_cast(f4_t, r.g[h]);
+                float yv[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) yv[e] = __fmul_rn(__fmul_rn(x[e], inv), g[e]);
+                uint8_t* dst = lds + static_cast<uint64_t>(m) * p.x_stride + 4u * q * EB;
+                if (q >= n4) continue;
+                if constexpr (AF == OPURE_A_F32)
+                    *reinterpret_cast<f4_t*>(dst) = f4_t{yv[0], yv[1], yv[2], yv[3]};
+                else
+                {
+                    typedef uint32_t u2_t __attribute__((ext_vector_type(2)));
+                    *reinterpret_cast<u2_t*>(dst) = u2_t{pack2<AF>(yv[0], yv[1]), pack2<AF>(yv[2], yv[3])};
+                }
+            }
+        }
+        return;
+    }
     const StageMap<NTH> sm(p, j0);
 #pragma unroll
     for (int i = 0; i < KR; ++i)
     {
         const uint32_t m = sm.rg + (i0 + i) * sm.rt;
         const bool keep = sm.col && m < p.M;
-        uint32_t o[8];
-        if constexpr (NORM)
-        {
-            // round(x * inv * g) (Opure_RMSNorm.usf:44-78)
-            const float inv = sinv[min(m, p.M - 1u)];
-            const f4_t x0 = __builtin_bit_cast(f4_t, r.x[i][0]), x1 = __builtin_bit_cast(f4_t, r.x[i][1]);
-            const f4_t g0 = __builtin_bit_cast(f4_t, r.g[0]), g1 = __builtin_bit_cast(f4_t, r.g[1]);
-            float yv[8];
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-            {
-                yv[e] = __fmul_rn(__fmul_rn(x0[e], inv), g0[e]);
-                yv[4 + e] = __fmul_rn(__fmul_rn(x1[e], inv), g1[e]);
-            }
-            if constexpr (AF == OPURE_A_F32)
-            {
-#pragma unroll
-                for (int e = 0; e < 8; ++e) o[e] = __float_as_uint(yv[e]);
-            }
-            else
-            {
-#pragma unroll
-                for (int e = 0; e < 4; ++e) o[e] = pack2<AF>(yv[2 * e], yv[2 * e + 1]);
-            }
-        }
-        else
-        {
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-            {
-                o[e] = r.x[i][0][e];
-                if constexpr (AF == OPURE_A_F32) o[4 + e] = r.x[i][1][e];
-            }
-        }
         uint8_t* dst = lds + static_cast<uint64_t>(m) * p.x_stride + 8u * sm.j * EB;
         if constexpr (AF == OPURE_A_F32)
         {
             if (keep)
             {
-                reinterpret_cast<u4_t*>(dst)[0] = u4_t{o[0], o[1], o[2], o[3]};
-                reinterpret_cast<u4_t*>(dst)[1] = u4_t{o[4], o[5], o[6], o[7]};
+                reinterpret_cast<u4_t*>(dst)[0] = r.x[i][0];
+                reinterpret_cast<u4_t*>(dst)[1] = r.x[i][1];
             }
         }
         else
         {
-            if (keep) *reinterpret_cast<u4_t*>(dst) = u4_t{o[0], o[1], o[2], o[3]};
+            if (keep) *reinterpret_cast<u4_t*>(dst) = r.x[i][0];
         }
     }
 }
@@ -581,6 +593,77 @@ __device__ __forceinline__ void epilogue_elem(const KParams& p, uint32_t tile, u
     }
 }
 
+// The staged prologue shared by the kernels.  Issue order: the first X
+// staging round, the rows' sums of squares, then `issue` (the first weight
+// loads).  Loads retire in issue order, so the staging below waits for L2
+// only while the weights stream from HBM.  Then the rows' 1 / rms (NORM), the
+// conversion into LDS and any further rounds, `late` (weight loads that may
+// use the staging registers), and a barrier.
+template <int WF, int AF, bool NORM, int NW, class Issue, class Late>
+__device__ __forceinline__ void staged_prologue(const KParams& p, uint8_t* lds, float* sinv, Issue issue, Late late)
+{
+    constexpr uint32_t NTH = NW * 64;
+    constexpr int KR = stage_rows<AF, NORM, NTH>();
+    constexpr int RW = (OPURE_MAX_ROWS + NW - 1) / NW;      // columns whose rms a wave computes
+    constexpr int SSE = 4;                                  // sums per lane issued early: in <= 4096
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    const uint32_t M = p.M;
+    StageRound<AF, NORM, KR> r0;
+    stage_issue<AF, NORM, NTH, KR>(p, r0, 0u, 0u);
+    float ssp[NORM ? RW : 1][SSE];
+    if constexpr (NORM)
+    {
+#pragma unroll
+        for (int i = 0; i < RW; ++i)
+        {
+            const uint32_t m = wave + i * NW;
+            if (m >= M) break;                               // uniform
+#pragma unroll
+            for (int e = 0; e < SSE; ++e)
+            {
+                const uint32_t t = min(lane + 64u * e, p.ss_tiles - 1u);
+                ssp[i][e] = p.ss_in[static_cast<uint64_t>(t) * M + m];
+            }
+        }
+    }
+    issue();
+    if constexpr (NORM)
+    {
+        // one wave per column, the sums in inv_rms_wave's order (adding the
+        // early sums of tiles past the end is skipped, not added as zero)
+#pragma unroll
+        for (int i = 0; i < RW; ++i)
+        {
+            const uint32_t m = wave + i * NW;
+            if (m >= M) break;
+            float ssum = 0.0f;
+#pragma unroll
+            for (int e = 0; e < SSE; ++e)
+                if (lane + 64u * e < p.ss_tiles) ssum += ssp[i][e];
+            for (uint32_t t = lane + 64u * SSE; t < p.ss_tiles; t += 64u) ssum += p.ss_in[static_cast<uint64_t>(t) * M + m];
+            const float v = inv_rms_finish(p, ssum);
+            if (lane == 0) sinv[m] = v;
+        }
+        __syncthreads();
+    }
+    stage_store<WF, AF, NORM, NTH, KR>(p, r0, 0u, 0u, lds, sinv);
+    // further rounds when the rows or the columns exceed one round
+    const uint32_t ncol = NORM ? p.in / 4u : p.in / 8u;             // quads or 8-value units
+    const uint32_t jstep = NORM ? 2u * NTH : NTH;
+    const uint32_t rt = NORM || ncol >= NTH ? 1u : NTH / ncol;
+    const uint32_t rows_per = (M + rt - 1u) / rt;
+    for (uint32_t j0 = 0; j0 < ncol; j0 += jstep)
+        for (uint32_t i0 = 0; i0 < rows_per; i0 += KR)
+        {
+            if (j0 == 0 && i0 == 0) continue;
+            StageRound<AF, NORM, KR> r;
+            stage_issue<AF, NORM, NTH, KR>(p, r, j0, i0);
+            stage_store<WF, AF, NORM, NTH, KR>(p, r, j0, i0, lds, sinv);
+        }
+    late();
+    __syncthreads();
+}
+
 template <int WF, int AF, int T, int U, bool STAGED>
 struct Payload {
     u4_t w[T][U];
@@ -646,66 +729,12 @@ __global__ __launch_bounds__(NW * 64) void k_gemv(KParams p)
     [[maybe_unused]] PL C;
     if constexpr (STAGED)
     {
-        // Issue order: the first staging round, the rows' sums of squares, then
-        // the first two steps' weights.  Loads retire in issue order, so the
-        // staging below waits for L2 only while the weights stream from HBM.
-        constexpr uint32_t NTH = NW * 64;
-        constexpr int KR = stage_rows<AF, NORM, NTH>();
-        constexpr int RW = (OPURE_MAX_ROWS + NW - 1) / NW;  // columns whose rms a wave computes
-        constexpr int SSE = 4;                              // sums per lane issued early: in <= 4096
-        StageRound<AF, NORM, KR> r0;
-        stage_issue<AF, NORM, NTH, KR>(p, r0, 0u, 0u);
-        float ssp[NORM ? RW : 1][SSE];
-        if constexpr (NORM)
-        {
-#pragma unroll
-            for (int i = 0; i < RW; ++i)
-            {
-                const uint32_t m = min(wave + i * NW, M - 1u);
-#pragma unroll
-                for (int e = 0; e < SSE; ++e)
-                {
-                    const uint32_t t = min(lane + 64u * e, p.ss_tiles - 1u);
-                    ssp[i][e] = p.ss_in[static_cast<uint64_t>(t) * M + m];
-                }
-            }
-        }
-        load(A, 0);
-        if (S > 1u) load(B, 1);
-        if constexpr (NORM)
-        {
-            // one wave per column, the sums in inv_rms_wave's order (adding the
-            // early sums of tiles past the end is skipped, not added as zero)
-#pragma unroll
-            for (int i = 0; i < RW; ++i)
-            {
-                const uint32_t m = wave + i * NW;
-                if (m >= M) break;
-                float ssum = 0.0f;
-#pragma unroll
-                for (int e = 0; e < SSE; ++e)
-                    if (lane + 64u * e < p.ss_tiles) ssum += ssp[i][e];
-                for (uint32_t t = lane + 64u * SSE; t < p.ss_tiles; t += 64u) ssum += p.ss_in[static_cast<uint64_t>(t) * M + m];
-                const float v = inv_rms_finish(p, ssum);
-                if (lane == 0) sinv[m] = v;
-            }
-            __syncthreads();
-        }
-        stage_store<WF, AF, NORM, NTH, KR>(p, r0, 0u, 0u, lds, sinv);
-        // further rounds when the rows or the unit columns exceed one round
-        const uint32_t n8 = p.in / 8u;
-        const uint32_t rt = n8 >= NTH ? 1u : NTH / n8;
-        const uint32_t rows_per = (M + rt - 1u) / rt;
-        for (uint32_t j0 = 0; j0 < n8; j0 += NTH)
-            for (uint32_t i0 = 0; i0 < rows_per; i0 += KR)
-            {
-                if (j0 == 0 && i0 == 0) continue;
-                StageRound<AF, NORM, KR> r;
-                stage_issue<AF, NORM, NTH, KR>(p, r, j0, i0);
-                stage_store<WF, AF, NORM, NTH, KR>(p, r, j0, i0, lds, sinv);
-            }
-        if (S > 2u) load(C, 2);                             // the staging registers are free now
-        __syncthreads();
+        staged_prologue<WF, AF, NORM, NW>(p, lds, sinv, [&] {
+            load(A, 0);
+            if (S > 1u) load(B, 1);
+        }, [&] {
+            if (S > 2u) load(C, 2);                         // the staging registers are free now
+        });
     }
     else
     {
@@ -925,6 +954,237 @@ __global__ __launch_bounds__(NW * 64) void k_gemv(KParams p)
     }
 }
 
+// Wave-per-tile GEMV for shapes with many tiles (1024 and more, so at least
+// four per CU): X staged in LDS as in k_gemv, but each wave owns whole tiles --
+// tile(k) = blockIdx.x + gridDim.x * (wave + NW * k) -- and runs U consecutive
+// blocks per step through a ring of three buffers, so no wave waits for
+// another between tiles.  A tile's sum is its blocks' in block order.  The
+// uint4 group sums of X are computed once per workgroup on the matrix cores
+// (the same MFMAs as in k_gemv, so the same bits) into LDS xs[G][16].  At a
+// tile's end the wave transposes its accumulator through its own 1 KB of LDS
+// and runs the element epilogue on 4 elements a lane: lane (g4, r16) takes
+// rows g4 + 4 j, so every DPP row still holds one row m.
+template <int WF, int AF, int EPI, int U, bool NORM>
+__global__ __launch_bounds__(512) void k_gemv_wpt(KParams p)
+{
+    constexpr int NW = 8;
+    constexpr uint32_t KB = Fmt<WF>::KB, N = Fmt<WF>::N;
+    constexpr uint32_t EB = AF == OPURE_A_F32 ? 4u : 2u;
+    constexpr uint32_t VALS = KB / 4u;
+    extern __shared__ __align__(16) uint8_t lds[];
+    __shared__ float sinv[OPURE_MAX_ROWS];
+    float* xsl = reinterpret_cast<float*>(lds + p.off_xsum);          // uint4: [G][16]
+    float* slot = reinterpret_cast<float*>(lds + p.off_red);          // [NW][64 lanes][4]
+
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    const uint32_t g4 = lane >> 4, r16 = lane & 15u;
+    const uint32_t M = p.M;
+    const uint32_t mc = r16 < M ? r16 : M - 1u;
+    const uint32_t nblk = p.nblk;
+    const uint32_t npass = (nblk + U - 1u) / U;
+    const uint32_t G = p.in / 128u;
+    const uint32_t first = blockIdx.x + gridDim.x * wave, stride = gridDim.x * NW;
+    const uint32_t ntile = first < p.tiles ? (p.tiles - first + stride - 1u) / stride : 0u;
+    const uint32_t S = ntile * npass;
+
+    struct PL {
+        u4_t w[U];
+        uint32_t s[U];
+    };
+    auto load = [&](PL& b, uint32_t s) {
+        const uint32_t k = s / npass, ps = s - k * npass;
+        const uint32_t tile = first + stride * k;
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+        {
+            const uint32_t blk = min(ps * U + u, nblk - 1u);
+            b.w[u] = __builtin_nontemporal_load(
+                reinterpret_cast<const u4_t*>(p.w + ((static_cast<uint64_t>(tile) * nblk + blk) << 10) + (lane << 4)));
+            if constexpr (WF == OPURE_W_I4G128)
+                b.s[u] = static_cast<const uint32_t*>(p.sc)[(static_cast<uint64_t>(tile) * G + blk) * 16u + r16];
+        }
+    };
+
+    PL A, B, C;
+    staged_prologue<WF, AF, NORM, NW>(p, lds, sinv, [&] {
+        if (S > 0u) load(A, 0);
+        if (S > 1u) load(B, 1);
+    }, [&] {
+        if (S > 2u) load(C, 2);
+    });
+    if constexpr (WF == OPURE_W_I4G128)
+    {
+        // the group sums of X rows 4*g4 + i, block by block over the waves
+        for (uint32_t blk = wave; blk < G; blk += NW)
+        {
+            const u4_t* src = reinterpret_cast<const u4_t*>(lds + mc * p.x_stride + (blk * KB + VALS * g4) * EB);
+            f4_t xs = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+            {
+                const u4_t v = src[j];
+                if constexpr (AF == OPURE_A_F16)
+                    xs = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(v[0], v[1], v[2], v[3]),
+                                                                as_half8(0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u),
+                                                                xs, 0, 0, 0);
+                else
+                    xs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf8(v[0], v[1], v[2], v[3]),
+                                                                 as_bf8(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u),
+                                                                 xs, 0, 0, 0);
+            }
+            if (r16 == 0) *reinterpret_cast<f4_t*>(xsl + blk * 16u + 4u * g4) = xs;
+        }
+        __syncthreads();
+    }
+
+    f4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    float best_v[4];
+    int32_t best_i[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) { best_v[j] = -__builtin_huge_valf(); best_i[j] = 0x7FFFFFFF; }
+    float* my = slot + wave * 256u;
+    auto run = [&](const PL& b, uint32_t s) {
+        const uint32_t k = s / npass, ps = s - k * npass;
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+        {
+            const uint32_t blk = ps * U + u;
+            if (blk >= nblk) continue;
+            uint32_t xd[N];
+            const u4_t* src = reinterpret_cast<const u4_t*>(lds + mc * p.x_stride + (blk * KB + VALS * g4) * EB);
+#pragma unroll
+            for (uint32_t i = 0; i < N / 4u; ++i)
+            {
+                const u4_t v = src[i];
+                xd[4 * i] = v[0]; xd[4 * i + 1] = v[1]; xd[4 * i + 2] = v[2]; xd[4 * i + 3] = v[3];
+            }
+            if constexpr (WF == OPURE_W_F32)
+            {
+                const f4_t wf = __builtin_bit_cast(f4_t, b.w[u]);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(xd[q]), wf[q], acc, 0, 0, 0);
+            }
+            else if constexpr (WF == OPURE_W_I8PC)
+            {
+                uint32_t a[8];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) u8x4_to_f16(b.w[u][j], a[2 * j], a[2 * j + 1]);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(xd[0], xd[1], xd[2], xd[3]), as_half8(a[0], a[1], a[2], a[3]), acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(xd[4], xd[5], xd[6], xd[7]), as_half8(a[4], a[5], a[6], a[7]), acc, 0, 0, 0);
+            }
+            else
+            {
+                const f4_t xs = *reinterpret_cast<const f4_t*>(xsl + blk * 16u + 4u * g4);
+                f4_t bacc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                {
+                    uint32_t a[4];
+                    u4x8_pairs<AF>(b.w[u][j], a);
+                    if constexpr (AF == OPURE_A_F16)
+                        bacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(xd[4 * j], xd[4 * j + 1], xd[4 * j + 2], xd[4 * j + 3]),
+                                                                      as_half8(a[0], a[1], a[2], a[3]), bacc, 0, 0, 0);
+                    else
+                        bacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf8(xd[4 * j], xd[4 * j + 1], xd[4 * j + 2], xd[4 * j + 3]),
+                                                                       as_bf8(a[0], a[1], a[2], a[3]), bacc, 0, 0, 0);
+                }
+                const uint32_t sz = b.s[u];
+                const float sc = __uint_as_float(sz << 16), z = __uint_as_float(sz & 0xFFFF0000u);
+                const float zo = AF == OPURE_A_BF16 ? __fadd_rn(z, 128.0f) : z;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[i] = __fmaf_rn(sc, __fmaf_rn(-zo, xs[i], bacc[i]), acc[i]);
+            }
+        }
+        if (ps + 1u == npass)
+        {
+            // this wave's tile is done: transpose through its own LDS slot
+            const uint32_t tile = first + stride * k;
+            *reinterpret_cast<f4_t*>(my + lane * 4u) = acc;
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+            {
+                const uint32_t m = g4 + 4u * j;
+                const float v = my[(((m >> 2) << 4) + r16) * 4u + (m & 3u)];
+                epilogue_elem<WF, EPI>(p, tile, m, r16, v, best_v[j], best_i[j]);
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            acc = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+    };
+
+    uint32_t s = 0;
+    while (S - s >= 6u)
+    {
+        run(A, s);
+        load(A, s + 3u);
+        run(B, s + 1u);
+        load(B, s + 4u);
+        run(C, s + 2u);
+        load(C, s + 5u);
+        s += 3u;
+    }
+    switch (S - s)
+    {
+    case 5u:
+        run(A, s); load(A, s + 3u);
+        run(B, s + 1u); load(B, s + 4u);
+        run(C, s + 2u); run(A, s + 3u); run(B, s + 4u);
+        break;
+    case 4u:
+        run(A, s); load(A, s + 3u);
+        run(B, s + 1u); run(C, s + 2u); run(A, s + 3u);
+        break;
+    case 3u: run(A, s); run(B, s + 1u); run(C, s + 2u); break;
+    case 2u: run(A, s); run(B, s + 1u); break;
+    case 1u: run(A, s); break;
+    default: break;
+    }
+
+    if constexpr (EPI == opure_hip::EPI_LOGITS)
+    {
+        // one argmax partial per row for the workgroup: lane (g4, 0) of every
+        // wave holds the best of rows g4 + 4 j over its tiles
+        __syncthreads();
+        float* sv = slot;
+        int32_t* si = reinterpret_cast<int32_t*>(slot + NW * 16u);
+        if (r16 == 0)
+        {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) { sv[wave * 16u + g4 + 4u * j] = best_v[j]; si[wave * 16u + g4 + 4u * j] = best_i[j]; }
+        }
+        __syncthreads();
+        if (threadIdx.x < M)
+        {
+            float v = sv[threadIdx.x];
+            int32_t i = si[threadIdx.x];
+#pragma unroll
+            for (int w = 1; w < NW; ++w) best_merge(v, i, sv[w * 16 + threadIdx.x], si[w * 16 + threadIdx.x]);
+            p.lg.am_val[static_cast<uint64_t>(blockIdx.x) * M + threadIdx.x] = v;
+            p.lg.am_idx[static_cast<uint64_t>(blockIdx.x) * M + threadIdx.x] = i;
+        }
+    }
+}
+
+template <int WF, int AF, int EPI, int U, bool NORM>
+int launch_wpt(opure_dev* dev, const KParams& kp, uint32_t grid, uint32_t lds)
+{
+    static bool configured = false;
+    if (!configured)
+    {
+        OPURE_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemv_wpt<WF, AF, EPI, U, NORM>),
+                                          hipFuncAttributeMaxDynamicSharedMemorySize, 159 * 1024));
+        configured = true;
+    }
+    hipLaunchKernelGGL((k_gemv_wpt<WF, AF, EPI, U, NORM>), dim3(grid), dim3(512), lds, dev->stream, kp);
+    OPURE_LAUNCH_CHECK("k_gemv_wpt");
+    return OPURE_OK;
+}
+
 // Launch one instantiation.  grid = workgroups; lds = dynamic LDS bytes.
 template <int WF, int AF, int EPI, int NW, int T, int U, bool NORM, bool STAGED>
 int launch(opure_dev* dev, const KParams& kp, uint32_t grid, uint32_t lds)
@@ -946,7 +1206,8 @@ int launch(opure_dev* dev, const KParams& kp, uint32_t grid, uint32_t lds)
 // each CU stages X once, and a pass of 32 blocks per tile covers a whole
 // 4096-long row (int4) so a workgroup's first one or two groups are in flight
 // from its start.
-struct Recipe { uint32_t nw, t, u; };
+struct Recipe { uint32_t nw, t, u, wpt = 0; };
+constexpr Recipe R_WPT{8, 1, 8, 1};   // at least four tiles per wave: waves own whole tiles (staged X)
 constexpr Recipe R_WIDE{8, 2, 4};     // many tiles: 2 tiles share each X fragment
 constexpr Recipe R_MID{8, 1, 4};      // about one tile per CU
 constexpr Recipe R_NARROW{16, 1, 2};  // fewer tiles than CUs: 16 waves split K
@@ -959,6 +1220,8 @@ constexpr Recipe R_NARROW{16, 1, 2};  // fewer tiles than CUs: 16 waves split K
 template <int WF, int AF, int EPI, bool NORM, bool STAGED>
 int launch_recipe(opure_dev* dev, const KParams& kp, const Recipe& r, uint32_t grid, uint32_t lds)
 {
+    if constexpr (STAGED)
+        if (r.wpt) return launch_wpt<WF, AF, EPI, 8, NORM>(dev, kp, grid, lds);
     if (r.nw == 8 && r.t == 2) return launch<WF, AF, EPI, 8, 2, STAGED ? 4 : 2, NORM, STAGED>(dev, kp, grid, lds);
     if (r.nw == 8) return launch<WF, AF, EPI, 8, 1, STAGED ? 4 : 2, NORM, STAGED>(dev, kp, grid, lds);
     return launch<WF, AF, EPI, 16, 1, STAGED ? 2 : 1, NORM, STAGED>(dev, kp, grid, lds);
