@@ -567,6 +567,33 @@ def bench_c2(args):
     dev.close()
 
 
+def copy_calibration():
+    """Five copies of 64 MiB (16 Mi fp32 read, 16 Mi fp32 written) by
+    k_convert_f32 into f32: under rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE,
+    counter KiB / 65536 is the factor that turns a counter into bytes."""
+    dev = H.Dev(0)
+    n = 16 << 20
+    src, dst = dev.alloc(n * 4), dev.alloc(n * 4)
+    L = H.lib()
+    H.check(L.opure_synth_normal_f32(dev.h, int(src), n, 1, 0, 1.0, 0.0))
+    for _ in range(5):
+        H.check(L.opure_convert_f32(dev.h, int(src), int(dst), H.A_F32, n))
+    dev.sync()
+    print(json.dumps({"copy_calibration": {"bytes_read": n * 4, "bytes_written": n * 4, "launches": 5}}), flush=True)
+    dev.close()
+
+
+def traffic_of(config, stage):
+    """Measured HBM bytes per launch of a stage's kernel (profiles/traffic.json:
+    FETCH_SIZE + WRITE_SIZE from rocprofv3 --pmc runs, each scaled by the copy
+    calibration), or None when not measured."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    if not os.path.exists(path):
+        return None
+    t = json.load(open(path)).get(config, {}).get(stage)
+    return int(t["bytes"]) if t else None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -576,7 +603,12 @@ def main():
     ap.add_argument("--cpu-baseline", default="auto", choices=["auto", "skip"])
     ap.add_argument("--no-kernel-timing", action="store_true")
     ap.add_argument("--eager", action="store_true", help="launch each step's kernels directly instead of a hipGraph")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run five 64 MiB fp32 copies (k_convert_f32 to f32): the known-size kernel that "
+                         "calibrates the FETCH_SIZE / WRITE_SIZE counters")
     args = ap.parse_args()
+    if args.copy_calibration:
+        return copy_calibration()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
               "multi-GPU sharding is a design note, not a measured path", file=sys.stderr)
@@ -642,7 +674,8 @@ def main():
     }
     if kern:
         line["roofline"] = {"bound": "hbm", "achieved": round(kern["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                            "frac": round(kern["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                            "frac": round(kern["gbs"] / HBM_PEAK_GBS, 4),
+                            "traffic": traffic_of(args.config, kern["stage"]),
                             "kernel": f"k_gemv ({kern['stage']} stage of the verify step)",
                             "bytes_per_launch": kern["bytes_per_launch"], "avg_us": round(kern["avg_us"], 2)}
         line["stages_us_per_step"] = {st: round(d["us_per_step"], 1) for st, d in stages.items()}

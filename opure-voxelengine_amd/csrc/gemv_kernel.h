@@ -964,7 +964,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemv(KParams p)
 // tile's end the wave transposes its accumulator through its own 1 KB of LDS
 // and runs the element epilogue on 4 elements a lane: lane (g4, r16) takes
 // rows g4 + 4 j, so every DPP row still holds one row m.
-template <int WF, int AF, int EPI, int U, bool NORM>
+template <int WF, int AF, int EPI, int U, bool NORM, int D>
 __global__ __launch_bounds__(512) void k_gemv_wpt(KParams p)
 {
     constexpr int NW = 8;
@@ -1005,12 +1005,14 @@ __global__ __launch_bounds__(512) void k_gemv_wpt(KParams p)
         }
     };
 
-    PL A, B, C;
+    PL buf[D];
     staged_prologue<WF, AF, NORM, NW>(p, lds, sinv, [&] {
-        if (S > 0u) load(A, 0);
-        if (S > 1u) load(B, 1);
+        if (S > 0u) load(buf[0], 0);
+        if (S > 1u) load(buf[1], 1);
     }, [&] {
-        if (S > 2u) load(C, 2);
+#pragma unroll
+        for (int d = 2; d < D; ++d)
+            if (S > static_cast<uint32_t>(d)) load(buf[d], d);   // the staging registers are free now
     });
     if constexpr (WF == OPURE_W_I4G128)
     {
@@ -1117,32 +1119,32 @@ __global__ __launch_bounds__(512) void k_gemv_wpt(KParams p)
         }
     };
 
+    // a ring of D buffers: the D - 1 steps after the one computing are in
+    // flight.  The steady loop issues every load unconditionally; only the
+    // last 2 D steps branch (uniformly) on whether a step exists.
     uint32_t s = 0;
-    while (S - s >= 6u)
+    while (S - s >= 2u * D)
     {
-        run(A, s);
-        load(A, s + 3u);
-        run(B, s + 1u);
-        load(B, s + 4u);
-        run(C, s + 2u);
-        load(C, s + 5u);
-        s += 3u;
+#pragma unroll
+        for (int d = 0; d < D; ++d)
+        {
+            run(buf[d], s + d);
+            load(buf[d], s + d + D);
+        }
+        s += D;
     }
-    switch (S - s)
+#pragma unroll
+    for (int d = 0; d < D; ++d)
     {
-    case 5u:
-        run(A, s); load(A, s + 3u);
-        run(B, s + 1u); load(B, s + 4u);
-        run(C, s + 2u); run(A, s + 3u); run(B, s + 4u);
-        break;
-    case 4u:
-        run(A, s); load(A, s + 3u);
-        run(B, s + 1u); run(C, s + 2u); run(A, s + 3u);
-        break;
-    case 3u: run(A, s); run(B, s + 1u); run(C, s + 2u); break;
-    case 2u: run(A, s); run(B, s + 1u); break;
-    case 1u: run(A, s); break;
-    default: break;
+        if (s + d >= S) break;
+        run(buf[d], s + d);
+        if (s + d + D < S) load(buf[d], s + d + D);
+    }
+#pragma unroll
+    for (int d = 0; d < D; ++d)
+    {
+        if (s + D + d >= S) break;
+        run(buf[d], s + D + d);
     }
 
     if constexpr (EPI == opure_hip::EPI_LOGITS)
@@ -1170,17 +1172,21 @@ __global__ __launch_bounds__(512) void k_gemv_wpt(KParams p)
     }
 }
 
+#ifndef OPURE_WPT_DEPTH
+#define OPURE_WPT_DEPTH 3
+#endif
 template <int WF, int AF, int EPI, int U, bool NORM>
 int launch_wpt(opure_dev* dev, const KParams& kp, uint32_t grid, uint32_t lds)
 {
+    constexpr int D = OPURE_WPT_DEPTH;
     static bool configured = false;
     if (!configured)
     {
-        OPURE_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemv_wpt<WF, AF, EPI, U, NORM>),
+        OPURE_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemv_wpt<WF, AF, EPI, U, NORM, D>),
                                           hipFuncAttributeMaxDynamicSharedMemorySize, 159 * 1024));
         configured = true;
     }
-    hipLaunchKernelGGL((k_gemv_wpt<WF, AF, EPI, U, NORM>), dim3(grid), dim3(512), lds, dev->stream, kp);
+    hipLaunchKernelGGL((k_gemv_wpt<WF, AF, EPI, U, NORM, D>), dim3(grid), dim3(512), lds, dev->stream, kp);
     OPURE_LAUNCH_CHECK("k_gemv_wpt");
     return OPURE_OK;
 }

@@ -1,6 +1,7 @@
 """Summarise a rocprofv3 kernel trace by verify step.
 
     python opure-voxelengine_amd/profsum.py <..._kernel_trace.csv> [--rows R]
+    python opure-voxelengine_amd/profsum.py <..._counter_collection.csv> --pmc KERNEL... [--last N]
 
 A verify step starts at its k_embed dispatch, whose grid holds one 256-thread
 workgroup per scored row.  Only steps scoring `--rows` rows are kept (the
@@ -39,11 +40,37 @@ def steps_of(rows, want_rows):
     return out
 
 
+def pmc(path, kernels, last):
+    """Median per-dispatch value of each counter over the last `last`
+    dispatches of each kernel whose name contains one of `kernels`
+    (rocprofv3 --pmc ... --output-format csv: *_counter_collection.csv)."""
+    per = collections.defaultdict(lambda: collections.defaultdict(float))
+    names, durs = {}, {}
+    for r in csv.DictReader(open(path)):
+        d = int(r["Dispatch_Id"])
+        per[d][r["Counter_Name"]] += float(r["Counter_Value"])
+        names[d] = r["Kernel_Name"]
+        durs[d] = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+    for k in kernels:
+        ds = sorted(d for d in per if k in names[d])[-last:]
+        if not ds:
+            print(f"{k}: no dispatch")
+            continue
+        for cn in sorted(per[ds[0]]):
+            v = statistics.median(per[d][cn] for d in ds)
+            print(f"{k:32s} {cn:12s} median {v:12.1f} KiB over {len(ds)} dispatches, "
+                  f"median duration {statistics.median(durs[d] for d in ds):.2f} us")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("trace")
     ap.add_argument("--rows", type=int, default=6)
+    ap.add_argument("--pmc", nargs="+", metavar="KERNEL", help="counter summary of these kernels instead")
+    ap.add_argument("--last", type=int, default=64, help="with --pmc: the last N dispatches of each kernel")
     a = ap.parse_args()
+    if a.pmc:
+        return pmc(a.trace, a.pmc, a.last)
     rows = [r for r in csv.DictReader(open(a.trace)) if r.get("Kind", "KERNEL_DISPATCH") == "KERNEL_DISPATCH"]
     rows.sort(key=lambda r: int(r["Start_Timestamp"]))
     steps = steps_of(rows, a.rows)
