@@ -28,7 +28,10 @@
 //  With STAGED, X is staged once into LDS for the whole K (rmsnorm applied
 //  there for consumers of the residual) and the workgroup loops over groups
 //  (persistent); otherwise X fragments are loaded from global memory with the
-//  weights.  Weights (and X fragments) of the next pass are always in flight
+//  weights -- for at most 8 rows two blocks a load (XM_PAIRED: lanes of rows
+//  0..7 take block u, lanes of rows 8..15 block u + 1, and a row rotation
+//  brings block u + 1 under rows 0..7 when it is its turn; the rows >= M of
+//  the MFMA are never read).  Weights (and X fragments) of the next pass are always in flight
 //  while the current pass computes.  No workgroup talks to another, and every
 //  sum has a fixed order that depends on the shape only, so results are
 //  reproducible and independent of M and of the path taken.
@@ -671,9 +674,15 @@ struct Payload {
     u4_t x[STAGED ? 1 : U][Fmt<WF>::N / 4u];             // direct X fragments
 };
 
-template <int WF, int AF, int EPI, int NW, int T, int U, bool NORM, bool STAGED>
+// X modes of k_gemv: fragments from global memory, staged in LDS, or from
+// global memory two blocks a load (at most 8 rows)
+constexpr int XM_DIRECT = 0, XM_STAGED = 1, XM_PAIRED = 2;
+
+template <int WF, int AF, int EPI, int NW, int T, int U, bool NORM, int XM>
 __global__ __launch_bounds__(NW * 64) void k_gemv(KParams p)
 {
+    constexpr bool STAGED = XM == XM_STAGED, PAIRED = XM == XM_PAIRED;
+    static_assert(!PAIRED || U % 2 == 0, "paired X fragments come two blocks a load");
     constexpr uint32_t KB = Fmt<WF>::KB, N = Fmt<WF>::N;
     constexpr uint32_t EB = AF == OPURE_A_F32 ? 4u : 2u;
     constexpr uint32_t VALS = KB / 4u;                   // k values per lane per block
@@ -711,7 +720,21 @@ __global__ __launch_bounds__(NW * 64) void k_gemv(KParams p)
                     b.s[t][u] = static_cast<const uint32_t*>(p.sc)[(static_cast<uint64_t>(tile) * G + blk) * 16u + r16];
             }
         }
-        if constexpr (!STAGED)
+        if constexpr (PAIRED)
+        {
+            // rows 0..7 of lanes r16 < 8 from block u, of lanes r16 >= 8 from block u + 1
+            const uint32_t row = min(r16 & 7u, M - 1u), hi = r16 >> 3;
+#pragma unroll
+            for (int u = 0; u < U; u += 2)
+            {
+                const uint32_t blk = min(ps * PB + (u + hi) * NW + wave, nblk - 1u);
+                const u4_t* src = reinterpret_cast<const u4_t*>(
+                    p.x + (static_cast<uint64_t>(row) * p.in + blk * KB + VALS * g4) * EB);
+#pragma unroll
+                for (uint32_t i = 0; i < N / 4u; ++i) b.x[u][i] = src[i];
+            }
+        }
+        else if constexpr (!STAGED)
         {
 #pragma unroll
             for (int u = 0; u < U; ++u)
@@ -768,6 +791,18 @@ __global__ __launch_bounds__(NW * 64) void k_gemv(KParams p)
                     const u4_t v = src[i];
                     xd[4 * i] = v[0]; xd[4 * i + 1] = v[1]; xd[4 * i + 2] = v[2]; xd[4 * i + 3] = v[3];
                 }
+            }
+            else if constexpr (PAIRED)
+            {
+                // even u: the lane's own words; odd u: those of lane r16 + 8 (row rotation by 8)
+#pragma unroll
+                for (uint32_t i = 0; i < N / 4u; ++i)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                    {
+                        const uint32_t w = b.x[u & ~1][i][j];
+                        xd[4 * i + j] = (u & 1) ? static_cast<uint32_t>(dpp_i<0x128>(static_cast<int32_t>(w))) : w;
+                    }
             }
             else
             {
@@ -1192,17 +1227,17 @@ int launch_wpt(opure_dev* dev, const KParams& kp, uint32_t grid, uint32_t lds)
 }
 
 // Launch one instantiation.  grid = workgroups; lds = dynamic LDS bytes.
-template <int WF, int AF, int EPI, int NW, int T, int U, bool NORM, bool STAGED>
+template <int WF, int AF, int EPI, int NW, int T, int U, bool NORM, int XM>
 int launch(opure_dev* dev, const KParams& kp, uint32_t grid, uint32_t lds)
 {
     static bool configured = false;
     if (!configured)
     {
-        OPURE_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemv<WF, AF, EPI, NW, T, U, NORM, STAGED>),
+        OPURE_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemv<WF, AF, EPI, NW, T, U, NORM, XM>),
                                           hipFuncAttributeMaxDynamicSharedMemorySize, 159 * 1024));
         configured = true;
     }
-    hipLaunchKernelGGL((k_gemv<WF, AF, EPI, NW, T, U, NORM, STAGED>), dim3(grid), dim3(NW * 64), lds, dev->stream, kp);
+    hipLaunchKernelGGL((k_gemv<WF, AF, EPI, NW, T, U, NORM, XM>), dim3(grid), dim3(NW * 64), lds, dev->stream, kp);
     OPURE_LAUNCH_CHECK("k_gemv");
     return OPURE_OK;
 }
@@ -1227,10 +1262,24 @@ template <int WF, int AF, int EPI, bool NORM, bool STAGED>
 int launch_recipe(opure_dev* dev, const KParams& kp, const Recipe& r, uint32_t grid, uint32_t lds)
 {
     if constexpr (STAGED)
+    {
         if (r.wpt) return launch_wpt<WF, AF, EPI, 8, NORM>(dev, kp, grid, lds);
-    if (r.nw == 8 && r.t == 2) return launch<WF, AF, EPI, 8, 2, STAGED ? 4 : 2, NORM, STAGED>(dev, kp, grid, lds);
-    if (r.nw == 8) return launch<WF, AF, EPI, 8, 1, STAGED ? 4 : 2, NORM, STAGED>(dev, kp, grid, lds);
-    return launch<WF, AF, EPI, 16, 1, STAGED ? 2 : 1, NORM, STAGED>(dev, kp, grid, lds);
+        if (r.nw == 8 && r.t == 2) return launch<WF, AF, EPI, 8, 2, 4, NORM, XM_STAGED>(dev, kp, grid, lds);
+        if (r.nw == 8) return launch<WF, AF, EPI, 8, 1, 4, NORM, XM_STAGED>(dev, kp, grid, lds);
+        return launch<WF, AF, EPI, 16, 1, 2, NORM, XM_STAGED>(dev, kp, grid, lds);
+    }
+    else
+    {
+        // same blocks per wave, so the same sums, paired or not
+        const bool paired = kp.M <= 8u;
+        if (r.nw == 8 && r.t == 2)
+            return paired ? launch<WF, AF, EPI, 8, 2, 2, NORM, XM_PAIRED>(dev, kp, grid, lds)
+                          : launch<WF, AF, EPI, 8, 2, 2, NORM, XM_DIRECT>(dev, kp, grid, lds);
+        if (r.nw == 8)
+            return paired ? launch<WF, AF, EPI, 8, 1, 2, NORM, XM_PAIRED>(dev, kp, grid, lds)
+                          : launch<WF, AF, EPI, 8, 1, 2, NORM, XM_DIRECT>(dev, kp, grid, lds);
+        return launch<WF, AF, EPI, 16, 1, 1, NORM, XM_DIRECT>(dev, kp, grid, lds);
+    }
 }
 
 // every (epilogue, rmsnorm, staged) combination the host may ask for; nm 1:
