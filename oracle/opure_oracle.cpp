@@ -381,14 +381,18 @@ void orc_attention_paged(const orc_model* m, const orc_kv* kv, uint32_t layer,
 {
     const uint32_t hd = m->head_dim, nh = m->n_heads, group = nh / m->n_kv_heads;
     const int32_t* pt = kv->page_table + static_cast<uint64_t>(seq) * kv->max_pages_per_seq;
-    std::vector<double> scores;
-    std::vector<double> o(hd);
+    // (row, query head) pairs are independent: split over threads, each pair
+    // computed exactly as on one thread
+#ifdef _OPENMP
+#pragma omp parallel for collapse(2) schedule(dynamic) num_threads(g_threads) if (g_threads > 1)
+#endif
     for (uint32_t j = 0; j < R; ++j)
     {
-        const uint32_t seqLen = ctx + j + 1;
-        scores.assign(seqLen, 0.0);
         for (uint32_t hq = 0; hq < nh; ++hq)
         {
+            const uint32_t seqLen = ctx + j + 1;
+            std::vector<double> scores(seqLen, 0.0);
+            std::vector<double> o(hd);
             const uint32_t kvh = hq / group;
             const float* qRow = q + (static_cast<uint64_t>(j) * nh + hq) * hd;
             double mx = -1e300;

@@ -62,6 +62,24 @@ def test_rows_equal_sequential_decode(case):
         assert np.array_equal(one[0, 0], multi[0, j])
 
 
+def test_threads_give_the_same_bits():
+    """The oracle's GEMVs (over output rows) and attention (over row, head
+    pairs) split over threads compute every output as one thread does."""
+    m = tiny(O.W_I4G128, O.A_BF16)
+    kv, seq_len = make_kv(m)
+    pool0 = kv.pool.copy()
+    tokens = np.random.default_rng(6).integers(0, 512, size=(2, 4)).astype(np.int32)
+    try:
+        O.set_threads(1)
+        one = O.verify_forward(m, kv, tokens, seq_len)
+        kv.pool[...] = pool0
+        O.set_threads(4)
+        four = O.verify_forward(m, kv, tokens, seq_len)
+    finally:
+        O.set_threads(1)
+    assert np.array_equal(one, four)
+
+
 def test_page_placement_invariance():
     m = tiny(O.W_I8PC, O.A_F16)
     kv, seq_len = make_kv(m, B=1)
