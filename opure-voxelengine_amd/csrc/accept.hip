@@ -70,8 +70,7 @@ __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int o)
 // block reductions over 256 threads (4 waves), fixed order
 __device__ float block_max(float v, float* red)
 {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    v = wave_max64(v);
     __syncthreads();
     if ((threadIdx.x & 63u) == 0) red[threadIdx.x >> 6] = v;
     __syncthreads();
@@ -404,8 +403,7 @@ struct RejectParams {
 template <uint32_t NTH>
 __device__ float block_max_n(float v, float* red)
 {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    v = wave_max64(v);
     __syncthreads();
     if ((threadIdx.x & 63u) == 0) red[threadIdx.x >> 6] = v;
     __syncthreads();

@@ -68,15 +68,11 @@ __device__ __forceinline__ u4v mask_tail(u4v v, uint32_t n)
 // wave-wide reductions with a fixed butterfly order (deterministic)
 __device__ __forceinline__ float wave_max(float v)
 {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-    return v;
+    return wave_max64(v);
 }
 __device__ __forceinline__ float wave_sum(float v)
 {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-    return v;
+    return wave_sum64(v);
 }
 
 __global__ __launch_bounds__(256) void k_attn_chunk_generic(AttnParams p)
@@ -464,8 +460,7 @@ __global__ __launch_bounds__(NWV * 64) void k_attn_mfma(AttnParams p)
             for (uint32_t T = 0; T < 2; ++T)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sc[kk][T][n][i]);
-        mx = fmaxf(mx, __shfl_xor(mx, 16));
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        mx = max_xor32(max_xor16(mx));
         float sum = 0.0f;
 #pragma unroll
         for (uint32_t kk = 0; kk < KK; ++kk)
@@ -493,8 +488,7 @@ __global__ __launch_bounds__(NWV * 64) void k_attn_mfma(AttnParams p)
             plo[kk][n] = u4v{pack_pair<AF>(lo[0], lo[1]), pack_pair<AF>(lo[2], lo[3]), pack_pair<AF>(lo[4], lo[5]),
                              pack_pair<AF>(lo[6], lo[7])};
         }
-        sum += __shfl_xor(sum, 16);
-        sum += __shfl_xor(sum, 32);
+        sum = add_xor32(add_xor16(sum));
         mrow[n] = mx;
         lrow[n] = sum;
     }
@@ -602,8 +596,7 @@ __global__ __launch_bounds__(64) void k_attn_combine(AttnParams p)
     float mx = -__builtin_huge_valf();
     if (lane <= last) mx = fmaxf(mx, m0);
     for (uint32_t c = lane + 64u; c <= last; c += 64u) mx = fmaxf(mx, p.part_ml[((base + c) * Gq + qi) * 2u]);
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    mx = wave_max64(mx);
     float den = 0.0f;
     for (uint32_t c = lane; c <= last; c += 64u)
     {
@@ -613,8 +606,7 @@ __global__ __launch_bounds__(64) void k_attn_combine(AttnParams p)
         wsh[c] = w;
         den = __fmaf_rn(w, l, den);
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) den += __shfl_xor(den, o);
+    den = wave_sum64(den);
     __syncthreads();
     const float dd = den > 0.0f ? den : 1.0f;
     float num[DPL];

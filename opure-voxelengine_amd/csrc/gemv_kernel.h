@@ -161,8 +161,7 @@ __device__ __forceinline__ uint32_t pack2(float a, float b)
 __device__ __forceinline__ float inv_rms_finish(const KParams& p, float ssum)
 {
     ssum = row16_sum(ssum);
-    ssum += __shfl_xor(ssum, 16);
-    ssum += __shfl_xor(ssum, 32);
+    ssum = add_xor32(add_xor16(ssum));
     return __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(ssum, static_cast<float>(p.in)), p.eps)));
 }
 
@@ -424,8 +423,7 @@ __device__ __forceinline__ void epilogue(const KParams& p, uint32_t tile, uint32
                 sq = __fmaf_rn(nv, nv, sq);
             }
         }
-        sq += __shfl_xor(sq, 16);
-        sq += __shfl_xor(sq, 32);
+        sq = add_xor32(add_xor16(sq));
         if (p.ss_out && m < M && g4 == 0) p.ss_out[static_cast<uint64_t>(tile) * M + m] = sq;
         return;
     }

@@ -177,6 +177,55 @@ __device__ __forceinline__ float dpp_f(float v)
     return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, true));
 }
 
+// Partner lanes l ^ 32 and l ^ 16 on the VALU: v_permlane32_swap and
+// v_permlane16_swap with both operands = v leave every lane its own value in one
+// result and its partner's in the other, so r[0] op r[1] is v op partner (op
+// commutative: the bits equal those of reading the partner through LDS).
+__device__ __forceinline__ float add_xor32(float v)
+{
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float max_xor32(float v)
+{
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float add_xor16(float v)
+{
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float max_xor16(float v)
+{
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+// 64-lane butterflies in the order xor 32, 16, 8, 4, 2, 1, with no LDS
+// traffic: the swaps above, then row rotations by 8 (exactly lane l ^ 8 in a
+// 16-lane row) and by 4 (after the xor-8 step the values repeat every 8 lanes,
+// so lane l + 4 holds lane l ^ 4's value), then the quad permutations xor 2
+// and xor 1.  Same partners and order as the __shfl_xor butterfly, same bits.
+__device__ __forceinline__ float wave_max64(float v)
+{
+    v = max_xor32(v);
+    v = max_xor16(v);
+    v = fmaxf(v, dpp_f<0x128>(v));   // row_ror:8
+    v = fmaxf(v, dpp_f<0x124>(v));   // row_ror:4
+    v = fmaxf(v, dpp_f<0x4E>(v));    // quad_perm [2,3,0,1]
+    return fmaxf(v, dpp_f<0xB1>(v));  // quad_perm [1,0,3,2]
+}
+__device__ __forceinline__ float wave_sum64(float v)
+{
+    v = add_xor32(v);
+    v = add_xor16(v);
+    v += dpp_f<0x128>(v);
+    v += dpp_f<0x124>(v);
+    v += dpp_f<0x4E>(v);
+    return v + dpp_f<0xB1>(v);
+}
+
 __device__ __forceinline__ float row16_sum(float u)
 {
     u += dpp_f<0xB1>(u);    // quad_perm [1,0,3,2]
