@@ -612,6 +612,15 @@ def copy_calibration():
     dev.close()
 
 
+def kernel_of(config, stage):
+    """The GEMV kernel a verify-step stage runs at these shapes: loader waves
+    for the 8B gate/up (7 tiles a CU), waves owning whole tiles for 1024 tiles
+    and more, the K-split kernel below."""
+    if stage == "gate_up" and config == "c4":
+        return "k_gemv_pc"
+    return "k_gemv_wpt" if stage in ("gate_up", "lm_head") else "k_gemv"
+
+
 def traffic_of(config, stage):
     """Measured HBM bytes per launch of a stage's kernel (profiles/traffic.json:
     FETCH_SIZE + WRITE_SIZE from rocprofv3 --pmc runs, each scaled by the copy
@@ -705,8 +714,7 @@ def main():
         line["roofline"] = {"bound": "hbm", "achieved": round(kern["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                             "frac": round(kern["gbs"] / HBM_PEAK_GBS, 4),
                             "traffic": traffic_of(args.config, kern["stage"]),
-                            "kernel": f"{'k_gemv_wpt' if kern['stage'] in ('gate_up', 'lm_head') else 'k_gemv'} "
-                                      f"({kern['stage']} stage of the verify step)",
+                            "kernel": f"{kernel_of(args.config, kern['stage'])} ({kern['stage']} stage of the verify step)",
                             "bytes_per_launch": kern["bytes_per_launch"], "avg_us": round(kern["avg_us"], 2)}
         line["stages_us_per_step"] = {st: round(d["us_per_step"], 1) for st, d in stages.items()}
     if cpu:

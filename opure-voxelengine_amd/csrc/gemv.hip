@@ -150,7 +150,7 @@ struct Plan {
     opure_gemv::Recipe r{};
     uint32_t tiles = 0, nblk = 0, groups = 0, grid = 0, lds = 0;
     bool staged = false;
-    uint32_t x_stride = 0, off_xsum = 0, off_red = 0;
+    uint32_t x_stride = 0, off_xsum = 0, off_red = 0, off_ring = 0, ring = 0;
 };
 
 // The recipe depends on the shape only (so a row's result never depends on the
@@ -189,6 +189,31 @@ Plan make_plan(const opure_dev* dev, uint32_t wfmt, uint32_t xfmt, uint32_t out,
     {
         pl.off_red = 0;
         pl.lds = red;
+    }
+    // wave-per-tile shapes of quantised weights and 16-bit X where most of the
+    // 8 compute waves of a CU own one tile (6 to 8 tiles a CU: the 8B gate/up):
+    // loader waves feed them through LDS rings, 3 slots each if they fit, else
+    // 2.  Longer streams (the LM head) keep the wave-per-tile kernel, whose
+    // waves keep more loads in flight, and so do fewer tiles (the 1B gate/up,
+    // 4 a CU, measured slower in graph replay with loader waves).
+    const uint32_t n_cu_pc = dev->n_cu > 0 ? static_cast<uint32_t>(dev->n_cu) : 256u;
+    if (wpt && pl.staged && wfmt != OPURE_W_F32 && xfmt != OPURE_A_F32 && pl.nblk % PC_SB == 0 &&
+        pl.tiles >= static_cast<uint32_t>(PC_NC - 2) * n_cu_pc && pl.tiles <= static_cast<uint32_t>(PC_NC) * n_cu_pc)
+    {
+        const uint32_t slot = wfmt == OPURE_W_I4G128 ? pc_slot_bytes<OPURE_W_I4G128>() : pc_slot_bytes<OPURE_W_I8PC>();
+        const uint32_t off_ring = static_cast<uint32_t>(opure_hip::align_up(total, 16));
+        for (uint32_t ring : {3u, 2u})
+        {
+            const uint32_t pc_total = off_ring + static_cast<uint32_t>(PC_NC) * ring * slot + 2u * PC_NC * 4u;
+            if (pc_total <= 159u * 1024u)
+            {
+                pl.r.wpt = 2;
+                pl.ring = ring;
+                pl.off_ring = off_ring;
+                pl.lds = pc_total;
+                break;
+            }
+        }
     }
     // persistent workgroups, one per CU
     const uint32_t n_cu = dev->n_cu > 0 ? static_cast<uint32_t>(dev->n_cu) : 256u;
@@ -384,6 +409,8 @@ int gemv_launch(opure_dev* dev, const GemvCall& c)
     kp.x_stride = pl.x_stride;
     kp.off_xsum = pl.off_xsum;
     kp.off_red = pl.off_red;
+    kp.off_ring = pl.off_ring;
+    kp.ring = pl.ring;
     kp.qkv = c.qkv;
     kp.lg = c.logits;
     uint32_t nm = norm ? 1u : 0u;

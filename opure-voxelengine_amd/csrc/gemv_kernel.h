@@ -67,6 +67,7 @@ struct KParams {
     uint32_t x_stride;         // STAGED: LDS bytes per staged X row
     uint32_t off_xsum;         // STAGED uint4: LDS offset of the group sums [M][in/128]
     uint32_t off_red;          // LDS offset of the wave reduction [NW][T][64] f4
+    uint32_t off_ring, ring;   // loader-wave kernel: LDS offset of the slot rings, slots per compute wave
     opure_hip::QkvEpilogue qkv;
     opure_hip::LogitsEpilogue lg;
 };
@@ -1205,6 +1206,309 @@ __global__ __launch_bounds__(512) void k_gemv_wpt(KParams p)
     }
 }
 
+
+// Wave-per-tile GEMV with loader waves.  Waves 0..7 compute exactly as in
+// k_gemv_wpt -- the same tiles, blocks and order of sums, so the same bits --
+// but take their weight blocks from LDS.  Waves 8..11 only load: each fills
+// a ring of `ring` slots of PC_SB blocks (and their uint4 scale words) for
+// two compute waves with global_load_lds_dwordx4, so the weight stream runs
+// from the first cycle, across the X staging and while the compute waves
+// dequantise; no compute wave ever waits to issue a load.  Hand-off per
+// compute wave: an LDS count of its steps filled (written by its loader once
+// those steps' loads have landed: loads retire in issue order, s_waitcnt
+// vmcnt) and of its steps consumed (written once the compute wave holds the
+// slot's words in registers).  Every wait is a bounded sleep loop; a wave
+// that gives up stops waiting (its results are then wrong) but still reaches
+// every barrier, so the grid always drains.
+constexpr int PC_NC = 8, PC_NL = 4;                   // compute and loader waves
+constexpr uint32_t PC_SB = 4;                          // blocks a slot
+constexpr uint32_t PC_SPIN = 1u << 22;                 // sleeps before a wait gives up
+
+template <int WF>
+constexpr uint32_t pc_slot_bytes() { return PC_SB * 1024u + (WF == OPURE_W_I4G128 ? 256u : 0u); }
+
+// the hand-off counts, as LDS pointers (ds_read / ds_write: a flat access
+// would count in vmcnt and make every poll wait for the loader's loads)
+typedef __attribute__((address_space(3))) volatile uint32_t lds_u32;
+
+// wait until *f >= want (a count another wave raises); false if given up
+__device__ __forceinline__ bool pc_wait(const lds_u32* f, uint32_t want, bool& bail)
+{
+    if (bail) return false;
+    // every lane reads the same count: take lane 0's, so the loop is scalar
+    for (uint32_t n = 0; static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(*f))) < want; ++n)
+    {
+        if (n >= PC_SPIN)
+        {
+            bail = true;
+            return false;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+    return true;
+}
+
+template <int WF, int AF, int EPI, bool NORM>
+__global__ __launch_bounds__((PC_NC + PC_NL) * 64) void k_gemv_pc(KParams p)
+{
+    constexpr int NW = PC_NC;
+    constexpr uint32_t KB = Fmt<WF>::KB, N = Fmt<WF>::N, SB = PC_SB, SLOT = pc_slot_bytes<WF>();
+    constexpr uint32_t EB = AF == OPURE_A_F32 ? 4u : 2u;
+    constexpr uint32_t VALS = KB / 4u;
+    constexpr int NBAR = (NORM ? 1 : 0) + 1 + (WF == OPURE_W_I4G128 ? 1 : 0);   // compute waves' prologue barriers
+    extern __shared__ __align__(16) uint8_t lds[];
+    __shared__ float sinv[OPURE_MAX_ROWS];
+    float* xsl = reinterpret_cast<float*>(lds + p.off_xsum);          // uint4: [G][16]
+    float* slotb = reinterpret_cast<float*>(lds + p.off_red);         // [NW][64 lanes][4]
+    lds_u32* filled = (lds_u32*)(lds + p.off_ring + NW * p.ring * SLOT);
+    lds_u32* consumed = filled + NW;
+
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    const uint32_t g4 = lane >> 4, r16 = lane & 15u;
+    const uint32_t M = p.M;
+    const uint32_t nblk = p.nblk, npass = nblk / SB, R = p.ring;
+    const uint32_t G = p.in / 128u;
+    const uint32_t stride = gridDim.x * NW;
+    auto first_of = [&](uint32_t c) { return blockIdx.x + gridDim.x * c; };
+    auto steps_of = [&](uint32_t c) {
+        const uint32_t f = first_of(c);
+        return f < p.tiles ? (p.tiles - f + stride - 1u) / stride * npass : 0u;
+    };
+    if (threadIdx.x < 2u * NW) filled[threadIdx.x] = 0u;     // filled[0..7], consumed[0..7]
+    __syncthreads();
+    bool bail = false;
+
+    if (wave >= static_cast<uint32_t>(NW))
+    {
+        // ---- loader wave: compute waves c0 = l, c1 = l + 4 (waves of the low
+        // indices are the ones that have tiles when there are few) ---------------
+        const uint32_t l = wave - NW, c0 = l, c1 = l + static_cast<uint32_t>(PC_NL);
+        const uint32_t S0 = steps_of(c0), S1 = steps_of(c1), Smax = S0 > S1 ? S0 : S1;
+        auto issue = [&](uint32_t c, uint32_t s) {
+            const uint32_t k = s / npass, ps = s - k * npass;
+            const uint32_t tile = first_of(c) + stride * k;
+            uint8_t* base = lds + p.off_ring + (c * R + s % R) * SLOT;
+#pragma unroll
+            for (uint32_t u = 0; u < SB; ++u)
+                __builtin_amdgcn_global_load_lds(
+                    p.w + ((static_cast<uint64_t>(tile) * nblk + ps * SB + u) << 10) + (lane << 4),
+                    (__attribute__((address_space(3))) void*)(base + u * 1024u), 16, 0, 0);
+            if constexpr (WF == OPURE_W_I4G128)
+                __builtin_amdgcn_global_load_lds(
+                    static_cast<const uint32_t*>(p.sc) + (static_cast<uint64_t>(tile) * G + ps * SB) * 16u + lane,
+                    (__attribute__((address_space(3))) void*)(base + SB * 1024u), 4, 0, 0);
+        };
+        bool joined = false;
+        auto join = [&] {
+#pragma unroll
+            for (int i = 0; i < NBAR; ++i) __syncthreads();
+            joined = true;
+        };
+        // Steps are signalled R - 1 iterations behind the issue: after issuing
+        // step s, the loads of the last R - 1 iterations may stay in flight
+        // (loads retire in order), so steps <= s - R + 1 have landed.  A slot
+        // is taken back for step s once step s - R is consumed, which only
+        // needs steps signalled up to s - R: no wait can deadlock.
+        constexpr uint32_t L = SB + (WF == OPURE_W_I4G128 ? 1u : 0u);   // loads a wave-step
+        uint32_t n_prev = 0;                                             // waves issued an iteration ago
+        for (uint32_t s = 0; s < Smax; ++s)
+        {
+            // the compute waves take slots only after their prologue: join it
+            // before the first wait on a slot
+            if (s == R && !joined) join();
+            const bool i0 = s < S0, i1 = s < S1;
+            if (i0)
+            {
+                if (s >= R) pc_wait(consumed + c0, s - R + 1u, bail);
+                issue(c0, s);
+            }
+            if (i1)
+            {
+                if (s >= R) pc_wait(consumed + c1, s - R + 1u, bail);
+                issue(c1, s);
+            }
+            const uint32_t n_cur = (i0 ? 1u : 0u) + (i1 ? 1u : 0u);
+            const uint32_t keep = R >= 3u ? n_prev + n_cur : n_cur;      // iterations' loads left in flight
+            if (keep >= 4u) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(4u * L) : "memory");
+            else if (keep == 3u) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3u * L) : "memory");
+            else if (keep == 2u) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2u * L) : "memory");
+            else asm volatile("s_waitcnt vmcnt(%0)" ::"n"(L) : "memory");
+            n_prev = n_cur;
+            const uint32_t lag = R >= 3u ? 2u : 1u;
+            const uint32_t ready = s + 1u >= lag ? s + 1u - lag : 0u;   // steps landed
+            if (lane == 0u)
+            {
+                filled[c0] = ready < S0 ? ready : S0;
+                filled[c1] = ready < S1 ? ready : S1;
+            }
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        if (lane == 0u)
+        {
+            filled[c0] = S0;
+            filled[c1] = S1;
+        }
+        if (!joined) join();
+        if constexpr (EPI == opure_hip::EPI_LOGITS)
+        {
+            __syncthreads();
+            __syncthreads();
+        }
+        return;
+    }
+
+    // ---- compute wave ------------------------------------------------------
+    const uint32_t mc = r16 < M ? r16 : M - 1u;
+    const uint32_t first = first_of(wave);
+    const uint32_t S = steps_of(wave);
+    staged_prologue<WF, AF, NORM, NW>(p, lds, sinv, [] {}, [] {});
+    if constexpr (WF == OPURE_W_I4G128)
+    {
+        for (uint32_t blk = wave; blk < G; blk += NW)
+        {
+            const u4_t* src = reinterpret_cast<const u4_t*>(lds + mc * p.x_stride + (blk * KB + VALS * g4) * EB);
+            f4_t xs = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+            {
+                const u4_t v = src[j];
+                if constexpr (AF == OPURE_A_F16)
+                    xs = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(v[0], v[1], v[2], v[3]),
+                                                                as_half8(0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u),
+                                                                xs, 0, 0, 0);
+                else
+                    xs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf8(v[0], v[1], v[2], v[3]),
+                                                                 as_bf8(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u),
+                                                                 xs, 0, 0, 0);
+            }
+            if (r16 == 0) *reinterpret_cast<f4_t*>(xsl + blk * 16u + 4u * g4) = xs;
+        }
+        __syncthreads();
+    }
+
+    f4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    float best_v[4];
+    int32_t best_i[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) { best_v[j] = -__builtin_huge_valf(); best_i[j] = 0x7FFFFFFF; }
+    float* my = slotb + wave * 256u;
+    for (uint32_t s = 0; s < S; ++s)
+    {
+        const uint32_t k = s / npass, ps = s - k * npass;
+        pc_wait(filled + wave, s + 1u, bail);
+        const uint8_t* base = lds + p.off_ring + (wave * R + s % R) * SLOT;
+        u4_t w[SB];
+        uint32_t sz[SB];
+#pragma unroll
+        for (uint32_t u = 0; u < SB; ++u)
+        {
+            w[u] = *reinterpret_cast<const u4_t*>(base + u * 1024u + (lane << 4));
+            if constexpr (WF == OPURE_W_I4G128) sz[u] = reinterpret_cast<const uint32_t*>(base + SB * 1024u)[u * 16u + r16];
+        }
+        // the slot's words are in registers: hand the slot back
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        if (lane == 0u) consumed[wave] = s + 1u;
+#pragma unroll
+        for (uint32_t u = 0; u < SB; ++u)
+        {
+            const uint32_t blk = ps * SB + u;
+            uint32_t xd[N];
+            const u4_t* src = reinterpret_cast<const u4_t*>(lds + mc * p.x_stride + (blk * KB + VALS * g4) * EB);
+#pragma unroll
+            for (uint32_t i = 0; i < N / 4u; ++i)
+            {
+                const u4_t v = src[i];
+                xd[4 * i] = v[0]; xd[4 * i + 1] = v[1]; xd[4 * i + 2] = v[2]; xd[4 * i + 3] = v[3];
+            }
+            if constexpr (WF == OPURE_W_I8PC)
+            {
+                uint32_t a[8];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) u8x4_to_f16(w[u][j], a[2 * j], a[2 * j + 1]);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(xd[0], xd[1], xd[2], xd[3]), as_half8(a[0], a[1], a[2], a[3]), acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(xd[4], xd[5], xd[6], xd[7]), as_half8(a[4], a[5], a[6], a[7]), acc, 0, 0, 0);
+            }
+            else
+            {
+                const f4_t xs = *reinterpret_cast<const f4_t*>(xsl + blk * 16u + 4u * g4);
+                f4_t bacc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                {
+                    uint32_t a[4];
+                    u4x8_pairs<AF>(w[u][j], a);
+                    if constexpr (AF == OPURE_A_F16)
+                        bacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(xd[4 * j], xd[4 * j + 1], xd[4 * j + 2], xd[4 * j + 3]),
+                                                                      as_half8(a[0], a[1], a[2], a[3]), bacc, 0, 0, 0);
+                    else
+                        bacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf8(xd[4 * j], xd[4 * j + 1], xd[4 * j + 2], xd[4 * j + 3]),
+                                                                       as_bf8(a[0], a[1], a[2], a[3]), bacc, 0, 0, 0);
+                }
+                const float sc = __uint_as_float(sz[u] << 16), z = __uint_as_float(sz[u] & 0xFFFF0000u);
+                const float zo = AF == OPURE_A_BF16 ? __fadd_rn(z, 128.0f) : z;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[i] = __fmaf_rn(sc, __fmaf_rn(-zo, xs[i], bacc[i]), acc[i]);
+            }
+        }
+        if (ps + 1u == npass)
+        {
+            const uint32_t tile = first + stride * k;
+            *reinterpret_cast<f4_t*>(my + lane * 4u) = acc;
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+            {
+                const uint32_t m = g4 + 4u * j;
+                const float v = my[(((m >> 2) << 4) + r16) * 4u + (m & 3u)];
+                epilogue_elem<WF, EPI>(p, tile, m, r16, v, best_v[j], best_i[j]);
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            acc = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+    }
+
+    if constexpr (EPI == opure_hip::EPI_LOGITS)
+    {
+        __syncthreads();
+        float* sv = slotb;
+        int32_t* si = reinterpret_cast<int32_t*>(slotb + NW * 16u);
+        if (r16 == 0)
+        {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) { sv[wave * 16u + g4 + 4u * j] = best_v[j]; si[wave * 16u + g4 + 4u * j] = best_i[j]; }
+        }
+        __syncthreads();
+        if (threadIdx.x < M)
+        {
+            float v = sv[threadIdx.x];
+            int32_t i = si[threadIdx.x];
+#pragma unroll
+            for (int w = 1; w < NW; ++w) best_merge(v, i, sv[w * 16 + threadIdx.x], si[w * 16 + threadIdx.x]);
+            p.lg.am_val[static_cast<uint64_t>(blockIdx.x) * M + threadIdx.x] = v;
+            p.lg.am_idx[static_cast<uint64_t>(blockIdx.x) * M + threadIdx.x] = i;
+        }
+    }
+}
+
+template <int WF, int AF, int EPI, bool NORM>
+int launch_pc(opure_dev* dev, const KParams& kp, uint32_t grid, uint32_t lds)
+{
+    static bool configured = false;
+    if (!configured)
+    {
+        OPURE_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemv_pc<WF, AF, EPI, NORM>),
+                                          hipFuncAttributeMaxDynamicSharedMemorySize, 159 * 1024));
+        configured = true;
+    }
+    hipLaunchKernelGGL((k_gemv_pc<WF, AF, EPI, NORM>), dim3(grid), dim3((PC_NC + PC_NL) * 64), lds, dev->stream, kp);
+    OPURE_LAUNCH_CHECK("k_gemv_pc");
+    return OPURE_OK;
+}
+
 #ifndef OPURE_WPT_DEPTH
 #define OPURE_WPT_DEPTH 3
 #endif
@@ -1261,6 +1565,8 @@ int launch_recipe(opure_dev* dev, const KParams& kp, const Recipe& r, uint32_t g
 {
     if constexpr (STAGED)
     {
+        if constexpr (WF != OPURE_W_F32 && AF != OPURE_A_F32)
+            if (r.wpt == 2) return launch_pc<WF, AF, EPI, NORM>(dev, kp, grid, lds);
         if (r.wpt) return launch_wpt<WF, AF, EPI, 8, NORM>(dev, kp, grid, lds);
         if (r.nw == 8 && r.t == 2) return launch<WF, AF, EPI, 8, 2, 4, NORM, XM_STAGED>(dev, kp, grid, lds);
         if (r.nw == 8) return launch<WF, AF, EPI, 8, 1, 4, NORM, XM_STAGED>(dev, kp, grid, lds);

@@ -289,6 +289,33 @@ def test_gemv_swiglu_matches_oracle(dev, case):
             b.free()
 
 
+@pytest.mark.parametrize("case", [(H.W_I4G128, H.A_BF16, 28672, 4096), (H.W_I8PC, H.A_F16, 24576, 2048)],
+                         ids=["i4bf16-28672x4096", "i8-24576x2048"])
+def test_gemv_loader_waves_equal_wave_per_tile(dev, case):
+    """6 to 8 tiles a CU run the loader-wave kernel where its LDS rings fit
+    beside X: uint4 4096-long rows up to 8 rows (16 rows: the wave-per-tile
+    kernel), int8 2048-long rows with 3 slots a wave at 8 rows and 2 at 16.
+    Same tiles, blocks and order of sums in every case: the rows agree bit for
+    bit, and with the oracle."""
+    wfmt, afmt, out, inn = case
+    say("gemv loader waves", case)
+    rng = np.random.default_rng(out - inn)
+    lin = O.make_linear(rng, out, inn, wfmt)
+    desc, keep = dev_linear(dev, lin)
+    x_bits, x_f = to_act(rng.standard_normal((16, inn)), afmt)
+    y16 = run_gemv(dev, wfmt, desc, x_bits, 16, afmt, H.A_F32, H.EPI_STORE)
+    for M in (1, 8):
+        yM = run_gemv(dev, wfmt, desc, x_bits, M, afmt, H.A_F32, H.EPI_STORE)
+        assert np.array_equal(yM, y16[:M]), M
+    ref = O.gemv(lin, wfmt, x_f[:2])
+    absref = np.abs(x_f[:2]).astype(np.float64) @ np.abs(O.dequant(lin, wfmt)).T
+    slack = 20.0 if (wfmt == H.W_I4G128 and afmt == H.A_BF16) else 1.0
+    assert np.all(np.abs(y16[:2] - ref) <= 1e-5 * slack * absref + 1e-6)
+    for b in keep:
+        if b:
+            b.free()
+
+
 def test_gemv_known_answer_fixtures(dev):
     g = np.load(os.path.join(GOLD, "gemv_f32.npz"))
     lin = {"w": g["W"], "out": 64, "in": 128}
