@@ -65,6 +65,51 @@ int opure_engine_generate_speculative(opure_engine* e, const int32_t* prompt, ui
                                       int32_t* out, uint32_t* accepted_hist, uint32_t hist_cap,
                                       opure_engine_stats* stats);
 
+/* Running totals since opure_engine_create or the last reset.  Replaces the
+ * reference's speculativeAcceptance, which is declared but always -1 because
+ * nothing drafts (src/core/Opure_Metrics.cpp:65-68, set from
+ * Opure_VoxelEngine.cpp:666). */
+typedef struct opure_engine_metrics {
+    uint64_t generate_calls;          /* generate / generate_speculative calls with n_new > 0 */
+    uint64_t verify_steps;            /* speculative verify steps */
+    uint64_t drafts_proposed;         /* K per speculative verify step */
+    uint64_t drafts_accepted;
+    uint64_t tokens_emitted;          /* ids returned by both generators */
+    double   speculative_acceptance;  /* drafts_accepted / drafts_proposed; -1 before any speculative step */
+} opure_engine_metrics;
+
+int opure_engine_get_metrics(const opure_engine* e, opure_engine_metrics* out);
+int opure_engine_reset_metrics(opure_engine* e);
+
+/* ---- page pool: the free list of a paged KV pool's pages (host bookkeeping,
+ *      no device calls).  Sequences own 16-token pages through their
+ *      page-table rows (opure_kv.page_table); a row takes pages as the
+ *      sequence grows and opure_kv_rollback's freed lists give them back.
+ *      Replaces the reference's fixed contiguous cache
+ *      (ModelConfig::KvCacheWords, src/core/Opure_Graph.h:81-84) and its
+ *      EvictOldestKV (src/engine/Opure_VoxelEngine.cpp:721-763).  Not
+ *      thread-safe. */
+typedef struct opure_page_pool opure_page_pool;
+
+int opure_page_pool_create(uint32_t n_pages, opure_page_pool** out);
+int opure_page_pool_destroy(opure_page_pool* p);
+/* *out = pages free now */
+int opure_page_pool_available(const opure_page_pool* p, uint32_t* out);
+/* n pages into ids[n], all or none (OPURE_E_CAPACITY when fewer are free).
+ * A fresh pool hands out 0, 1, 2, ...; released pages are handed out again
+ * first, last released first. */
+int opure_page_pool_alloc(opure_page_pool* p, uint32_t n, int32_t* ids);
+/* Entries < 0 are skipped (the -1 padding of opure_kv_rollback's freed
+ * lists).  An id past the pool, not handed out, or listed twice is
+ * OPURE_E_INVALID and releases nothing. */
+int opure_page_pool_release(opure_page_pool* p, const int32_t* ids, uint32_t n);
+/* Entries [0, ceil(tokens / OPURE_PAGE_SIZE)) of one host page-table row
+ * made valid, a page taken for each entry < 0; all or none (OPURE_E_CAPACITY
+ * when the row or the pool is too short).  *added (may be NULL) = pages
+ * taken.  The caller uploads the row before the step that writes there. */
+int opure_page_pool_grow_seq(opure_page_pool* p, int32_t* row, uint32_t max_pages, uint32_t tokens,
+                             uint32_t* added);
+
 #ifdef __cplusplus
 }
 #endif

@@ -9,10 +9,16 @@
 #include <vector>
 
 #include "opure_engine.h"
+#include "page_pool.h"
 #include "voxel_engine.h"
 
 struct opure_engine {
     opure::engine::VoxelEngine impl;
+};
+
+struct opure_page_pool {
+    explicit opure_page_pool(uint32_t n) : impl(n) {}
+    opure::engine::PagePool impl;
 };
 
 namespace {
@@ -130,6 +136,67 @@ int opure_engine_generate_speculative(opure_engine* e, const int32_t* prompt, ui
             for (uint32_t i = 0; i < hist_cap; ++i)
                 accepted_hist[i] = i < r.acceptedPerStep.size() ? r.acceptedPerStep[i] : 0u;
         fill_stats(stats, r);
+    });
+}
+
+int opure_engine_get_metrics(const opure_engine* e, opure_engine_metrics* out)
+{
+    if (!e || !out) return fail(OPURE_E_INVALID, "opure_engine_get_metrics: null argument");
+    const auto& m = e->impl.Metrics();
+    out->generate_calls = m.generateCalls;
+    out->verify_steps = m.verifySteps;
+    out->drafts_proposed = m.draftsProposed;
+    out->drafts_accepted = m.draftsAccepted;
+    out->tokens_emitted = m.tokensEmitted;
+    out->speculative_acceptance = m.SpeculativeAcceptance();
+    return OPURE_OK;
+}
+
+int opure_engine_reset_metrics(opure_engine* e)
+{
+    if (!e) return fail(OPURE_E_INVALID, "opure_engine_reset_metrics: null engine");
+    e->impl.ResetMetrics();
+    return OPURE_OK;
+}
+
+int opure_page_pool_create(uint32_t n_pages, opure_page_pool** out)
+{
+    if (!out) return fail(OPURE_E_INVALID, "opure_page_pool_create: null argument");
+    *out = nullptr;
+    return guarded([&] { *out = new opure_page_pool(n_pages); });
+}
+
+int opure_page_pool_destroy(opure_page_pool* p)
+{
+    delete p;
+    return OPURE_OK;
+}
+
+int opure_page_pool_available(const opure_page_pool* p, uint32_t* out)
+{
+    if (!p || !out) return fail(OPURE_E_INVALID, "opure_page_pool_available: null argument");
+    *out = p->impl.Available();
+    return OPURE_OK;
+}
+
+int opure_page_pool_alloc(opure_page_pool* p, uint32_t n, int32_t* ids)
+{
+    if (!p) return fail(OPURE_E_INVALID, "opure_page_pool_alloc: null pool");
+    return guarded([&] { p->impl.Alloc(n, ids); });
+}
+
+int opure_page_pool_release(opure_page_pool* p, const int32_t* ids, uint32_t n)
+{
+    if (!p) return fail(OPURE_E_INVALID, "opure_page_pool_release: null pool");
+    return guarded([&] { p->impl.Release(ids, n); });
+}
+
+int opure_page_pool_grow_seq(opure_page_pool* p, int32_t* row, uint32_t max_pages, uint32_t tokens, uint32_t* added)
+{
+    if (!p) return fail(OPURE_E_INVALID, "opure_page_pool_grow_seq: null pool");
+    return guarded([&] {
+        const uint32_t n = p->impl.GrowSeq(row, max_pages, tokens, OPURE_PAGE_SIZE);
+        if (added) *added = n;
     });
 }
 

@@ -386,6 +386,8 @@ GenerateResult VoxelEngine::Generate(const std::vector<uint32_t>& prompt, uint32
     }
     r.msGenerate = ms_since(t1);
     finish(r, nNew, opts_.stopToken);
+    ++metrics_.generateCalls;
+    metrics_.tokensEmitted += r.generated.size();
     return r;
 }
 
@@ -413,6 +415,9 @@ GenerateResult VoxelEngine::GenerateSpeculative(const std::vector<uint32_t>& pro
         const uint32_t n = SpecIteration(pendingLen, nxt, ctx, dctx, pending, toks);
         r.acceptedPerStep.push_back(n);
         ++r.verifySteps;
+        ++metrics_.verifySteps;
+        metrics_.draftsProposed += K;
+        metrics_.draftsAccepted += n;
         r.draftSteps += pendingLen + K - 1u;
         r.generated.push_back(nxt);
         for (uint32_t i = 0; i < n; ++i) r.generated.push_back(static_cast<uint32_t>(toks[i]));
@@ -435,6 +440,8 @@ GenerateResult VoxelEngine::GenerateSpeculative(const std::vector<uint32_t>& pro
     }
     r.msGenerate = ms_since(t1);
     finish(r, nNew, opts_.stopToken);
+    ++metrics_.generateCalls;
+    metrics_.tokensEmitted += r.generated.size();
     return r;
 }
 

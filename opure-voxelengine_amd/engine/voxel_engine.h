@@ -60,6 +60,25 @@ struct GenerateResult {
     double   msPerToken = 0.0;
 };
 
+// Running totals over an engine's lifetime (or since ResetMetrics): the
+// source of the serving metric speculativeAcceptance, which the reference
+// declares but pins at -1 because nothing drafts (src/core/Opure_Metrics.cpp:
+// 65-68; MetricsSnapshot in src/core/Opure_Metrics.h).
+struct EngineMetrics {
+    uint64_t generateCalls = 0;    // Generate / GenerateSpeculative calls with n_new > 0 that finished
+    uint64_t verifySteps = 0;      // speculative verify steps
+    uint64_t draftsProposed = 0;   // K per speculative verify step
+    uint64_t draftsAccepted = 0;
+    uint64_t tokensEmitted = 0;    // ids returned by both generators
+
+    // accepted / proposed drafts; -1 before any speculative step (the
+    // reference's value for "no speculative decoder has run")
+    [[nodiscard]] double SpeculativeAcceptance() const
+    {
+        return draftsProposed ? static_cast<double>(draftsAccepted) / static_cast<double>(draftsProposed) : -1.0;
+    }
+};
+
 class VoxelEngine {
 public:
     VoxelEngine();
@@ -85,6 +104,9 @@ public:
     // Appends `token` at `position` of the target cache; returns the argmax.
     uint32_t DecodeStep(uint32_t token, uint32_t position);
 
+    [[nodiscard]] const EngineMetrics& Metrics() const { return metrics_; }
+    void ResetMetrics() { metrics_ = EngineMetrics{}; }
+
 private:
     struct ModelState;
     struct Step;
@@ -104,6 +126,7 @@ private:
     std::unique_ptr<Step> decode_;                    // one row of the target
     opure_graph* iterGraph_[2] = {nullptr, nullptr};  // pending length 1 or 2
     opure_graph* decodeGraph_ = nullptr;
+    EngineMetrics metrics_{};
 };
 
 }  // namespace opure::engine

@@ -23,6 +23,12 @@ class Stats(C.Structure):
                 ("accepted_total", C.c_uint32), ("ms_prefill", C.c_double), ("ms_generate", C.c_double)]
 
 
+class Metrics(C.Structure):
+    _fields_ = [("generate_calls", C.c_uint64), ("verify_steps", C.c_uint64), ("drafts_proposed", C.c_uint64),
+                ("drafts_accepted", C.c_uint64), ("tokens_emitted", C.c_uint64),
+                ("speculative_acceptance", C.c_double)]
+
+
 def lib():
     global _lib
     if _lib is None:
@@ -36,8 +42,18 @@ def lib():
         L.opure_engine_destroy.argtypes = [vp]
         L.opure_engine_generate.argtypes = [vp, vp, u32, u32, vp, C.POINTER(Stats)]
         L.opure_engine_generate_speculative.argtypes = [vp, vp, u32, u32, vp, vp, u32, C.POINTER(Stats)]
+        L.opure_engine_get_metrics.argtypes = [vp, C.POINTER(Metrics)]
+        L.opure_engine_reset_metrics.argtypes = [vp]
+        L.opure_page_pool_create.argtypes = [u32, C.POINTER(vp)]
+        L.opure_page_pool_destroy.argtypes = [vp]
+        L.opure_page_pool_available.argtypes = [vp, C.POINTER(u32)]
+        L.opure_page_pool_alloc.argtypes = [vp, u32, vp]
+        L.opure_page_pool_release.argtypes = [vp, vp, u32]
+        L.opure_page_pool_grow_seq.argtypes = [vp, vp, u32, u32, C.POINTER(u32)]
         for f in ("opure_engine_create", "opure_engine_destroy", "opure_engine_generate",
-                  "opure_engine_generate_speculative"):
+                  "opure_engine_generate_speculative", "opure_engine_get_metrics", "opure_engine_reset_metrics",
+                  "opure_page_pool_create", "opure_page_pool_destroy", "opure_page_pool_available",
+                  "opure_page_pool_alloc", "opure_page_pool_release", "opure_page_pool_grow_seq"):
             getattr(L, f).restype = i
         _lib = L
     return _lib
@@ -89,3 +105,52 @@ class Engine:
             self.close()
         except Exception:
             pass
+
+    def metrics(self) -> Metrics:
+        m = Metrics()
+        check(lib().opure_engine_get_metrics(self.h, C.byref(m)))
+        return m
+
+    def reset_metrics(self) -> None:
+        check(lib().opure_engine_reset_metrics(self.h))
+
+
+class PagePool:
+    """opure_page_pool: the free list of a paged KV pool's pages (host only)."""
+
+    def __init__(self, n_pages: int):
+        h = C.c_void_p()
+        check(lib().opure_page_pool_create(n_pages, C.byref(h)))
+        self.h = h.value
+
+    def close(self) -> None:
+        if self.h:
+            lib().opure_page_pool_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def available(self) -> int:
+        n = C.c_uint32()
+        check(lib().opure_page_pool_available(self.h, C.byref(n)))
+        return n.value
+
+    def alloc(self, n: int) -> np.ndarray:
+        ids = np.full(max(n, 1), -1, dtype=np.int32)
+        check(lib().opure_page_pool_alloc(self.h, n, ids.ctypes.data))
+        return ids[:n]
+
+    def release(self, ids) -> None:
+        a = np.ascontiguousarray(ids, dtype=np.int32).ravel()
+        check(lib().opure_page_pool_release(self.h, a.ctypes.data if a.size else None, a.size))
+
+    def grow_seq(self, row: np.ndarray, tokens: int) -> int:
+        """Fills the -1 entries of row[:ceil(tokens/16)] in place; returns the pages taken."""
+        assert row.dtype == np.int32 and row.flags.c_contiguous
+        added = C.c_uint32()
+        check(lib().opure_page_pool_grow_seq(self.h, row.ctypes.data, row.size, tokens, C.byref(added)))
+        return added.value

@@ -48,6 +48,11 @@ def test_speculative_equals_greedy_c1(models):
     assert np.array_equal(spec, greedy)
     assert sst.emitted == N_NEW and gst.emitted == N_NEW
     assert int(hist.sum()) == sst.accepted_total
+    m = eng.metrics()
+    assert (m.generate_calls, m.tokens_emitted) == (2, 2 * N_NEW)
+    assert (m.verify_steps, m.drafts_accepted) == (sst.verify_steps, sst.accepted_total)
+    assert m.drafts_proposed == K * sst.verify_steps
+    assert m.speculative_acceptance == sst.accepted_total / (K * sst.verify_steps)
     eng.close()
 
 
@@ -55,10 +60,15 @@ def test_identical_draft_accepts_everything(models):
     dev, tgt, _, prompt, max_pos = models
     eng = E.Engine(dev, tgt.desc, tgt.desc, max_positions=max_pos, draft_tokens=K)
     greedy, _ = eng.generate(prompt, N_NEW)
+    assert eng.metrics().speculative_acceptance == -1.0     # no speculative step yet
     spec, hist, st = eng.generate_speculative(prompt, N_NEW)
     assert np.array_equal(spec, greedy)
     assert (hist == K).all(), hist.tolist()
     assert st.verify_steps == -(-N_NEW // (K + 1))
+    assert eng.metrics().speculative_acceptance == 1.0
+    eng.reset_metrics()
+    m = eng.metrics()
+    assert (m.generate_calls, m.verify_steps, m.speculative_acceptance) == (0, 0, -1.0)
     eng.close()
 
 
