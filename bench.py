@@ -478,7 +478,8 @@ def bench_c1(args):
                    "accepted_per_verify_step": hist.tolist(), "verify_steps": int(st.verify_steps),
                    "draft_steps": int(st.draft_steps), "greedy_ms": round(gms, 4),
                    "greedy_tokens_per_s": round(n_new / (gms * 1e-3), 1),
-                   "target_weight_bytes": int(wbytes)},
+                   "target_weight_bytes": int(wbytes),
+                   "speculative_acceptance": round(eng.metrics().speculative_acceptance, 4)},
     }
     if args.cpu_baseline == "auto":
         sys.path.insert(0, os.path.join(ROOT, "oracle"))
