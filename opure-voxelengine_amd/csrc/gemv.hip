@@ -215,6 +215,12 @@ Plan make_plan(const opure_dev* dev, uint32_t wfmt, uint32_t xfmt, uint32_t out,
             }
         }
     }
+    // at most four tiles a workgroup (the 1B gate/up: 1024 tiles on 256 CUs,
+    // so 4 of the 8 waves would own a tile): two waves a tile, each streaming
+    // half of its blocks, so every wave loads
+    if (wpt && pl.r.wpt == 1u && wfmt != OPURE_W_F32 && xfmt != OPURE_A_F32 && pl.nblk % 2u == 0 &&
+        pl.tiles <= 4u * n_cu_pc)
+        pl.r.wpt = 4;
     // persistent workgroups, one per CU
     const uint32_t n_cu = dev->n_cu > 0 ? static_cast<uint32_t>(dev->n_cu) : 256u;
     pl.grid = std::min(pl.groups, n_cu);

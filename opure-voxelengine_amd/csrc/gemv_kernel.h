@@ -998,10 +998,15 @@ __global__ __launch_bounds__(NW * 64) void k_gemv(KParams p)
 // tile's end the wave transposes its accumulator through its own 1 KB of LDS
 // and runs the element epilogue on 4 elements a lane: lane (g4, r16) takes
 // rows g4 + 4 j, so every DPP row still holds one row m.
-template <int WF, int AF, int EPI, int U, bool NORM, int D>
+// SPLIT = 2 (exactly four tiles a workgroup, at most one a wave): waves w and
+// w + 4 take the first and the second half of tile w's blocks, and after the
+// stream the second half's sum is added to the first's through LDS (lo + hi),
+// so all 8 waves load.
+template <int WF, int AF, int EPI, int U, bool NORM, int D, int SPLIT = 1>
 __global__ __launch_bounds__(512) void k_gemv_wpt(KParams p)
 {
     constexpr int NW = 8;
+    constexpr uint32_t TW = NW / SPLIT;                 // waves that own tiles
     constexpr uint32_t KB = Fmt<WF>::KB, N = Fmt<WF>::N;
     constexpr uint32_t EB = AF == OPURE_A_F32 ? 4u : 2u;
     constexpr uint32_t VALS = KB / 4u;
@@ -1015,9 +1020,10 @@ __global__ __launch_bounds__(512) void k_gemv_wpt(KParams p)
     const uint32_t M = p.M;
     const uint32_t mc = r16 < M ? r16 : M - 1u;
     const uint32_t nblk = p.nblk;
-    const uint32_t npass = (nblk + U - 1u) / U;
+    const uint32_t part = wave / TW, kblk = nblk / SPLIT, kb0 = part * kblk;   // this wave's blocks [kb0, kb0 + kblk)
+    const uint32_t npass = (kblk + U - 1u) / U;
     const uint32_t G = p.in / 128u;
-    const uint32_t first = blockIdx.x + gridDim.x * wave, stride = gridDim.x * NW;
+    const uint32_t first = blockIdx.x + gridDim.x * (wave % TW), stride = gridDim.x * TW;
     const uint32_t ntile = first < p.tiles ? (p.tiles - first + stride - 1u) / stride : 0u;
     const uint32_t S = ntile * npass;
 
@@ -1031,7 +1037,7 @@ __global__ __launch_bounds__(512) void k_gemv_wpt(KParams p)
 #pragma unroll
         for (int u = 0; u < U; ++u)
         {
-            const uint32_t blk = min(ps * U + u, nblk - 1u);
+            const uint32_t blk = kb0 + min(ps * U + u, kblk - 1u);
             b.w[u] = __builtin_nontemporal_load(
                 reinterpret_cast<const u4_t*>(p.w + ((static_cast<uint64_t>(tile) * nblk + blk) << 10) + (lane << 4)));
             if constexpr (WF == OPURE_W_I4G128)
@@ -1079,13 +1085,32 @@ __global__ __launch_bounds__(512) void k_gemv_wpt(KParams p)
 #pragma unroll
     for (int j = 0; j < 4; ++j) { best_v[j] = -__builtin_huge_valf(); best_i[j] = 0x7FFFFFFF; }
     float* my = slot + wave * 256u;
+    // a tile is done: transpose its sums through this wave's LDS slot, run
+    // the element epilogue, start the next tile from zero
+    auto finish = [&](uint32_t tile) {
+        *reinterpret_cast<f4_t*>(my + lane * 4u) = acc;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+        {
+            const uint32_t m = g4 + 4u * j;
+            const float v = my[(((m >> 2) << 4) + r16) * 4u + (m & 3u)];
+            epilogue_elem<WF, EPI>(p, tile, m, r16, v, best_v[j], best_i[j]);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        acc = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    };
     auto run = [&](const PL& b, uint32_t s) {
         const uint32_t k = s / npass, ps = s - k * npass;
 #pragma unroll
         for (int u = 0; u < U; ++u)
         {
-            const uint32_t blk = ps * U + u;
-            if (blk >= nblk) continue;
+            if (ps * U + u >= kblk) continue;
+            const uint32_t blk = kb0 + ps * U + u;
             uint32_t xd[N];
             const u4_t* src = reinterpret_cast<const u4_t*>(lds + mc * p.x_stride + (blk * KB + VALS * g4) * EB);
 #pragma unroll
@@ -1131,26 +1156,7 @@ __global__ __launch_bounds__(512) void k_gemv_wpt(KParams p)
                 for (int i = 0; i < 4; ++i) acc[i] = __fmaf_rn(sc, __fmaf_rn(-zo, xs[i], bacc[i]), acc[i]);
             }
         }
-        if (ps + 1u == npass)
-        {
-            // this wave's tile is done: transpose through its own LDS slot
-            const uint32_t tile = first + stride * k;
-            *reinterpret_cast<f4_t*>(my + lane * 4u) = acc;
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-            {
-                const uint32_t m = g4 + 4u * j;
-                const float v = my[(((m >> 2) << 4) + r16) * 4u + (m & 3u)];
-                epilogue_elem<WF, EPI>(p, tile, m, r16, v, best_v[j], best_i[j]);
-            }
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-            acc = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
-        }
+        if (SPLIT == 1 && ps + 1u == npass) finish(first + stride * k);
     };
 
     // a ring of D buffers: the D - 1 steps after the one computing are in
@@ -1179,6 +1185,20 @@ __global__ __launch_bounds__(512) void k_gemv_wpt(KParams p)
     {
         if (s + D + d >= S) break;
         run(buf[d], s + D + d);
+    }
+    if constexpr (SPLIT == 2)
+    {
+        // the host launches this only with at most one tile a wave (S <= npass);
+        // the barrier is outside every branch
+        if (part == 1u && S > 0u) *reinterpret_cast<f4_t*>(my + lane * 4u) = acc;
+        __syncthreads();
+        if (part == 0u && S > 0u)
+        {
+            const f4_t hi = *reinterpret_cast<const f4_t*>(slot + (wave + TW) * 256u + lane * 4u);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[i] = __fadd_rn(acc[i], hi[i]);
+            finish(first);
+        }
     }
 
     if constexpr (EPI == opure_hip::EPI_LOGITS)
@@ -1512,18 +1532,18 @@ int launch_pc(opure_dev* dev, const KParams& kp, uint32_t grid, uint32_t lds)
 #ifndef OPURE_WPT_DEPTH
 #define OPURE_WPT_DEPTH 3
 #endif
-template <int WF, int AF, int EPI, int U, bool NORM>
+template <int WF, int AF, int EPI, int U, bool NORM, int SPLIT = 1>
 int launch_wpt(opure_dev* dev, const KParams& kp, uint32_t grid, uint32_t lds)
 {
     constexpr int D = OPURE_WPT_DEPTH;
     static bool configured = false;
     if (!configured)
     {
-        OPURE_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemv_wpt<WF, AF, EPI, U, NORM, D>),
+        OPURE_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemv_wpt<WF, AF, EPI, U, NORM, D, SPLIT>),
                                           hipFuncAttributeMaxDynamicSharedMemorySize, 159 * 1024));
         configured = true;
     }
-    hipLaunchKernelGGL((k_gemv_wpt<WF, AF, EPI, U, NORM, D>), dim3(grid), dim3(512), lds, dev->stream, kp);
+    hipLaunchKernelGGL((k_gemv_wpt<WF, AF, EPI, U, NORM, D, SPLIT>), dim3(grid), dim3(512), lds, dev->stream, kp);
     OPURE_LAUNCH_CHECK("k_gemv_wpt");
     return OPURE_OK;
 }
@@ -1566,7 +1586,10 @@ int launch_recipe(opure_dev* dev, const KParams& kp, const Recipe& r, uint32_t g
     if constexpr (STAGED)
     {
         if constexpr (WF != OPURE_W_F32 && AF != OPURE_A_F32)
+        {
             if (r.wpt == 2) return launch_pc<WF, AF, EPI, NORM>(dev, kp, grid, lds);
+            if (r.wpt == 4) return launch_wpt<WF, AF, EPI, 8, NORM, 2>(dev, kp, grid, lds);
+        }
         if (r.wpt) return launch_wpt<WF, AF, EPI, 8, NORM>(dev, kp, grid, lds);
         if (r.nw == 8 && r.t == 2) return launch<WF, AF, EPI, 8, 2, 4, NORM, XM_STAGED>(dev, kp, grid, lds);
         if (r.nw == 8) return launch<WF, AF, EPI, 8, 1, 4, NORM, XM_STAGED>(dev, kp, grid, lds);

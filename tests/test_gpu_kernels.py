@@ -316,6 +316,31 @@ def test_gemv_loader_waves_equal_wave_per_tile(dev, case):
             b.free()
 
 
+@pytest.mark.parametrize("case", [(H.W_I8PC, H.A_F16, 16384, 2048), (H.W_I4G128, H.A_BF16, 16384, 4096)],
+                         ids=["i8-16384x2048", "i4bf16-16384x4096"])
+def test_gemv_two_waves_a_tile(dev, case):
+    """1024 tiles (four a CU): two waves share each tile, half of its blocks
+    each, and add the halves at the end.  The rows agree bit for bit at any
+    row count, and with the oracle."""
+    wfmt, afmt, out, inn = case
+    say("gemv two waves a tile", case)
+    rng = np.random.default_rng(out + 3 * inn)
+    lin = O.make_linear(rng, out, inn, wfmt)
+    desc, keep = dev_linear(dev, lin)
+    x_bits, x_f = to_act(rng.standard_normal((16, inn)), afmt)
+    y16 = run_gemv(dev, wfmt, desc, x_bits, 16, afmt, H.A_F32, H.EPI_STORE)
+    for M in (1, 6, 8):
+        yM = run_gemv(dev, wfmt, desc, x_bits, M, afmt, H.A_F32, H.EPI_STORE)
+        assert np.array_equal(yM, y16[:M]), M
+    ref = O.gemv(lin, wfmt, x_f[:3])
+    absref = np.abs(x_f[:3]).astype(np.float64) @ np.abs(O.dequant(lin, wfmt)).T
+    slack = 20.0 if (wfmt == H.W_I4G128 and afmt == H.A_BF16) else 1.0
+    assert np.all(np.abs(y16[:3] - ref) <= 1e-5 * slack * absref + 1e-6)
+    for b in keep:
+        if b:
+            b.free()
+
+
 def test_gemv_known_answer_fixtures(dev):
     g = np.load(os.path.join(GOLD, "gemv_f32.npz"))
     lin = {"w": g["W"], "out": 64, "in": 128}
