@@ -1572,8 +1572,9 @@ int launch(opure_dev* dev, const KParams& kp, uint32_t grid, uint32_t lds)
 struct Recipe { uint32_t nw, t, u, wpt = 0; };
 constexpr Recipe R_WPT{8, 1, 8, 1};   // at least four tiles per wave: waves own whole tiles (staged X)
 constexpr Recipe R_WIDE{8, 2, 4};     // many tiles: 2 tiles share each X fragment
+constexpr Recipe R_MID{8, 1, 4};      // about one tile per CU, rows of 8192 or more: 8 waves (paired X)
 constexpr Recipe R_NARROW{16, 1, 2};  // up to about one tile per CU: 16 waves split K (more loads
-                                      // in flight per CU than 8; measured faster at 256 tiles too)
+                                      // in flight per CU than 8)
 
 // Blocks go to waves by index (wave w takes w, w+NW, ...) whatever T and U
 // are, so the sums depend on NW alone.
