@@ -168,7 +168,9 @@ Plan make_plan(const opure_dev* dev, uint32_t wfmt, uint32_t xfmt, uint32_t out,
     // 1 KB slot per wave fit in LDS
     const uint32_t wpt_xs = wfmt == OPURE_W_I4G128 ? (in / 128u) * 64u : 0u;
     const bool wpt = pl.tiles >= 1024u && xbytes + wpt_xs + R_WPT.nw * 1024u <= 159u * 1024u;
-    pl.r = wpt ? R_WPT : (pl.tiles >= 320u ? R_WIDE : (pl.tiles > 192u && in >= 8192u ? R_MID : R_NARROW));
+    pl.r = wpt ? R_WPT
+               : (pl.tiles >= 1024u ? R_WIDE
+                                    : (pl.tiles >= 320u ? R_WIDE16 : (pl.tiles > 192u && in >= 8192u ? R_MID : R_NARROW)));
     pl.groups = (pl.tiles + pl.r.t - 1u) / pl.r.t;
     // the K-split kernels: one reduction buffer per group parity; the
     // wave-per-tile kernel: a 1 KB transposition slot per wave

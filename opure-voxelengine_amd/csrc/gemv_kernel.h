@@ -1572,6 +1572,7 @@ int launch(opure_dev* dev, const KParams& kp, uint32_t grid, uint32_t lds)
 struct Recipe { uint32_t nw, t, u, wpt = 0; };
 constexpr Recipe R_WPT{8, 1, 8, 1};   // at least four tiles per wave: waves own whole tiles (staged X)
 constexpr Recipe R_WIDE{8, 2, 4};     // many tiles: 2 tiles share each X fragment
+constexpr Recipe R_WIDE16{16, 2, 2};  // 320 to 1023 tiles: 2 tiles a group on 16 waves
 constexpr Recipe R_MID{8, 1, 4};      // about one tile per CU, rows of 8192 or more: 8 waves (paired X)
 constexpr Recipe R_NARROW{16, 1, 2};  // up to about one tile per CU: 16 waves split K (more loads
                                       // in flight per CU than 8)
@@ -1592,6 +1593,7 @@ int launch_recipe(opure_dev* dev, const KParams& kp, const Recipe& r, uint32_t g
             if (r.wpt == 4) return launch_wpt<WF, AF, EPI, 8, NORM, 2>(dev, kp, grid, lds);
         }
         if (r.wpt) return launch_wpt<WF, AF, EPI, 8, NORM>(dev, kp, grid, lds);
+        if (r.nw == 16 && r.t == 2) return launch<WF, AF, EPI, 16, 2, 2, NORM, XM_STAGED>(dev, kp, grid, lds);
         if (r.nw == 8 && r.t == 2) return launch<WF, AF, EPI, 8, 2, 4, NORM, XM_STAGED>(dev, kp, grid, lds);
         if (r.nw == 8) return launch<WF, AF, EPI, 8, 1, 4, NORM, XM_STAGED>(dev, kp, grid, lds);
         return launch<WF, AF, EPI, 16, 1, 2, NORM, XM_STAGED>(dev, kp, grid, lds);
@@ -1600,6 +1602,7 @@ int launch_recipe(opure_dev* dev, const KParams& kp, const Recipe& r, uint32_t g
     {
         // same blocks per wave, so the same sums, paired or not
         const bool paired = kp.M <= 8u;
+        if (r.nw == 16 && r.t == 2) return launch<WF, AF, EPI, 16, 2, 1, NORM, XM_DIRECT>(dev, kp, grid, lds);
         if (r.nw == 8 && r.t == 2)
             return paired ? launch<WF, AF, EPI, 8, 2, 2, NORM, XM_PAIRED>(dev, kp, grid, lds)
                           : launch<WF, AF, EPI, 8, 2, 2, NORM, XM_DIRECT>(dev, kp, grid, lds);
