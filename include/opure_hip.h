@@ -327,6 +327,28 @@ int opure_verify_reserve(opure_dev* dev, const opure_model* model, uint32_t batc
                          uint32_t max_ctx);
 int opure_verify_step(opure_dev* dev, const opure_verify_args* a);
 
+/* ---- one layer of the verify step on a caller's residual: rmsnorm -> fused
+ *      QKV GEMV with RoPE and paged K/V append -> paged attention -> o_proj +
+ *      residual -> rmsnorm -> gate/up GEMV with SwiGLU -> down + residual, the
+ *      same kernels as one iteration of opure_verify_step's layer loop.
+ *      x (fp32 [batch*rows][hidden]) is updated in place; the rows' K/V are
+ *      appended to layer `layer` of the cache.  The RMSNorm's sums of squares
+ *      are recomputed from x (a step carries them from the previous layer), so
+ *      the normalised rows can differ from a step's in the last bit.  Replaces
+ *      the body of RecordForward's layer loop (Opure_VoxelEngine.cpp:296-492)
+ *      and the per-layer runs of RunLayersTraced (Opure_VoxelEngine.h:226-227). */
+typedef struct opure_verify_layer_args {
+    const opure_model* model;
+    const opure_kv*    kv;
+    uint32_t           layer;
+    uint32_t           batch, rows;  /* batch * rows <= OPURE_MAX_BATCH_ROWS, rows <= OPURE_MAX_ROWS */
+    const int32_t*     seq_len;      /* device [batch]: row j of sequence b sits at seq_len[b] + j */
+    uint32_t           max_ctx;      /* host upper bound on seq_len[b] + rows */
+    float*             x;            /* device [batch*rows][hidden] fp32 residual, in and out */
+} opure_verify_layer_args;
+
+int opure_verify_layer(opure_dev* dev, const opure_verify_layer_args* a);
+
 /* ---- stage timing of eager verify steps.  With profiling on, every stage of
  *      opure_verify_step is bracketed by HIP events on the device's stream
  *      (skipped while a graph is being captured).  opure_profile_read waits

@@ -21,9 +21,12 @@
 //  (k_attn_mfma): S^T = K Q^T and O^T = V^T P^T with v_mfma_f32_16x16x32, K
 //  tokens assigned to MFMA rows so that the score tile a lane holds is already
 //  its P^T operand, and V read as V^T tiles straight from the channel-major V
-//  planes of the pool.  P^T enters as a hi + lo pair of 16-bit operands
-//  (about 16 significant bits, where one bf16 operand would give 8).  fp32
-//  caches and other head sizes use VALU kernels.
+//  planes of the pool.  P^T enters as a sum of 16-bit operands: fp16 hi + lo
+//  (22 significant bits), bf16 hi + mid + lo (the fp32 probability to within
+//  2^-25 relative, where one bf16 operand would give 8 bits).  A bf16 model
+//  rounds the attention output to 8 bits next, and any difference from the
+//  exactly summed softmax moves some of those roundings.  fp32 caches and other
+//  head sizes use VALU kernels.
 // ============================================================================
 #include "internal.h"
 
@@ -332,12 +335,20 @@ __device__ __forceinline__ uint32_t pack_pair(float a, float b)
 // are shared out over the waves, each merging in wave order, and the chunk's
 // partial is written for the combine kernel.
 // exp(x) for x <= 0 as 2^(x log2 e) on the transcendental unit (v_exp_f32,
-// about 1 ulp): the probabilities are rounded to a 16-bit pair next, so the
-// softmax needs no more, and the ~15-instruction exp of the oracle was the
-// kernel's largest VALU cost
+// about 1 ulp).  x log2 e is carried as t + dt: t = fl(x L), dt = the fma
+// residual of that product plus x (log2 e - L), so 2^(t + dt) = 2^t (1 + dt ln 2)
+// to within dt^2 -- without dt the rounding of t alone (up to 2^-24 |t|, 14x the
+// ulp of the result at x = -10) would dominate the error of every probability.
+// The ~15-instruction exp of the oracle was the kernel's largest VALU cost.
 __device__ __forceinline__ float exp_hw(float x)
 {
-    return __builtin_amdgcn_exp2f(__fmul_rn(x, 1.44269504088896341f));
+    constexpr float L = 1.44269502162933349609375f;          // log2 e rounded to fp32
+    constexpr float L_LO = 1.92596299e-8f;                       // log2 e - L
+    constexpr float LN2 = 0.693147182464599609375f;
+    const float t = __fmul_rn(x, L);
+    const float dt = __fmaf_rn(x, L_LO, __fmaf_rn(x, L, -t));
+    const float e = __builtin_amdgcn_exp2f(t);
+    return __fmaf_rn(e, __fmul_rn(dt, LN2), e);
 }
 
 template <int HD, int NT, int NWV>
@@ -448,8 +459,10 @@ __global__ __launch_bounds__(NWV * 64) void k_attn_mfma(AttnParams p)
     }
 
     // ---- softmax statistics of each query row over this wave's tokens -----
+    // P^T = hi + lo (fp16) or hi + mid + lo (bf16), every part in the 16-bit format
+    constexpr bool P3 = AF == OPURE_A_BF16;
     float mrow[NT], lrow[NT];
-    u4v pop[KK][NT], plo[KK][NT];   // P^T = hi + lo, both in the 16-bit format: ~16 significant bits
+    u4v pop[KK][NT], plo[KK][NT], plo2[KK][NT];
 #pragma unroll
     for (int n = 0; n < NT; ++n)
     {
@@ -487,6 +500,20 @@ __global__ __launch_bounds__(NWV * 64) void k_attn_mfma(AttnParams p)
             }
             plo[kk][n] = u4v{pack_pair<AF>(lo[0], lo[1]), pack_pair<AF>(lo[2], lo[3]), pack_pair<AF>(lo[4], lo[5]),
                              pack_pair<AF>(lo[6], lo[7])};
+            if constexpr (P3)
+            {
+                // the remainders are exact in fp32: e - hi and (e - hi) - mid
+                float lo2[8];
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                {
+                    const uint32_t pr = plo[kk][n][i];
+                    lo2[2 * i] = __fsub_rn(lo[2 * i], unpack_lo<AF>(pr));
+                    lo2[2 * i + 1] = __fsub_rn(lo[2 * i + 1], unpack_hi<AF>(pr));
+                }
+                plo2[kk][n] = u4v{pack_pair<AF>(lo2[0], lo2[1]), pack_pair<AF>(lo2[2], lo2[3]),
+                                  pack_pair<AF>(lo2[4], lo2[5]), pack_pair<AF>(lo2[6], lo2[7])};
+            }
         }
         sum = add_xor32(add_xor16(sum));
         mrow[n] = mx;
@@ -504,6 +531,7 @@ __global__ __launch_bounds__(NWV * 64) void k_attn_mfma(AttnParams p)
 #pragma unroll
             for (uint32_t kk = 0; kk < KK; ++kk)
             {
+                if constexpr (P3) o[dt][n] = mfma32<AF>(vop[kk][dt], plo2[kk][n], o[dt][n]);
                 o[dt][n] = mfma32<AF>(vop[kk][dt], plo[kk][n], o[dt][n]);
                 o[dt][n] = mfma32<AF>(vop[kk][dt], pop[kk][n], o[dt][n]);
             }

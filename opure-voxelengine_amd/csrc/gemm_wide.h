@@ -191,9 +191,9 @@ __global__ __launch_bounds__(256) void k_gemm_wide(WParams wp)
                                 bacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, af[q]),
                                                                                __builtin_bit_cast(bf16x8_t, bx), bacc, 0, 0, 0);
                         }
-                        // acc += s * (bacc - (z + off) * xs), off = 128 for bf16 (MAGIC)
+                        // acc += s * (bacc - (z + off) * xs), off = U4_BF16_OFFSET for bf16
                         const float xs = xsum[m * wp.ckb + bb];
-                        const float xoff = AF == OPURE_A_BF16 ? __fmul_rn(xs, 128.0f) : 0.0f;
+                        const float xoff = AF == OPURE_A_BF16 ? __fmul_rn(xs, U4_BF16_OFFSET) : 0.0f;
 #pragma unroll
                         for (int i = 0; i < 4; ++i)
                         {

@@ -104,14 +104,20 @@ __device__ __forceinline__ void u8x4_to_f16(uint32_t u, uint32_t& lo, uint32_t& 
 // A tiled uint4 word holds elements e0..e7 at nibbles 0,4,1,5,2,6,3,7, so
 // the low nibbles of its bytes are (e0,e4,e1,e5) and the high nibbles
 // (e2,e6,e3,e7); byte permutes against MAGIC then give MAGIC|q pairs in k
-// order.  fp16 MAGIC 0x64 (1024 + q, minus 1024 exactly); bf16 0x43 (128 + q,
-// the 128 is taken out with the zero point).
+// order.  fp16: MAGIC 0x64 over the nibble (1024 + q), minus 1024 exactly.
+// bf16 has no packed subtract, so the offset stays in the operand and is taken
+// out with the zero point (U4_BF16_OFFSET * group sum of X); to keep that
+// cancellation small the nibble goes to the top of the 7-bit mantissa under
+// the exponent of 16: high byte 0x41, low byte 0x80 | q << 3, value 16 + q
+// (the smallest offset a 4-bit field below an implicit leading one allows;
+// 0x43|q = 128 + q cost about 3 more bits of every group sum).
+constexpr float U4_BF16_OFFSET = 16.0f;
 template <int AF>
 __device__ __forceinline__ void u4x8_pairs(uint32_t d, uint32_t (&o)[4])
 {
-    constexpr uint32_t MAGIC = AF == OPURE_A_F16 ? 0x64646464u : 0x43434343u;
-    const uint32_t lo = d & 0x0F0F0F0Fu;
-    const uint32_t hi = (d >> 4) & 0x0F0F0F0Fu;
+    constexpr uint32_t MAGIC = AF == OPURE_A_F16 ? 0x64646464u : 0x41414141u;
+    const uint32_t lo = AF == OPURE_A_F16 ? d & 0x0F0F0F0Fu : ((d << 3) & 0x78787878u) | 0x80808080u;
+    const uint32_t hi = AF == OPURE_A_F16 ? (d >> 4) & 0x0F0F0F0Fu : ((d >> 1) & 0x78787878u) | 0x80808080u;
     o[0] = __builtin_amdgcn_perm(MAGIC, lo, 0x04020400u);   // e0 e1
     o[1] = __builtin_amdgcn_perm(MAGIC, hi, 0x04020400u);   // e2 e3
     o[2] = __builtin_amdgcn_perm(MAGIC, lo, 0x04030401u);   // e4 e5
@@ -842,7 +848,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemv(KParams p)
                 // one 128-k group per block.  The group sums of X rows 4*g4 + i
                 // come from the matrix core too (B = ones), then per tile a
                 // fresh accumulator of (MAGIC + q) * x and
-                //   acc += s * (bacc - (z + off) * xs),  off = 128 for bf16 (MAGIC)
+                //   acc += s * (bacc - (z + off) * xs),  off = U4_BF16_OFFSET for bf16
                 f4_t xs = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
@@ -876,7 +882,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemv(KParams p)
                     }
                     const uint32_t sz = b.s[t][u];
                     const float sc = __uint_as_float(sz << 16), z = __uint_as_float(sz & 0xFFFF0000u);
-                    const float zo = AF == OPURE_A_BF16 ? __fadd_rn(z, 128.0f) : z;
+                    const float zo = AF == OPURE_A_BF16 ? __fadd_rn(z, U4_BF16_OFFSET) : z;
 #pragma unroll
                     for (int i = 0; i < 4; ++i) acc[t][i] = __fmaf_rn(sc, __fmaf_rn(-zo, xs[i], bacc[i]), acc[t][i]);
                 }
@@ -1151,7 +1157,7 @@ __global__ __launch_bounds__(512) void k_gemv_wpt(KParams p)
                 }
                 const uint32_t sz = b.s[u];
                 const float sc = __uint_as_float(sz << 16), z = __uint_as_float(sz & 0xFFFF0000u);
-                const float zo = AF == OPURE_A_BF16 ? __fadd_rn(z, 128.0f) : z;
+                const float zo = AF == OPURE_A_BF16 ? __fadd_rn(z, U4_BF16_OFFSET) : z;
 #pragma unroll
                 for (int i = 0; i < 4; ++i) acc[i] = __fmaf_rn(sc, __fmaf_rn(-zo, xs[i], bacc[i]), acc[i]);
             }
@@ -1465,7 +1471,7 @@ __global__ __launch_bounds__((PC_NC + PC_NL) * 64) void k_gemv_pc(KParams p)
                                                                        as_bf8(a[0], a[1], a[2], a[3]), bacc, 0, 0, 0);
                 }
                 const float sc = __uint_as_float(sz[u] << 16), z = __uint_as_float(sz[u] & 0xFFFF0000u);
-                const float zo = AF == OPURE_A_BF16 ? __fadd_rn(z, 128.0f) : z;
+                const float zo = AF == OPURE_A_BF16 ? __fadd_rn(z, U4_BF16_OFFSET) : z;
 #pragma unroll
                 for (int i = 0; i < 4; ++i) acc[i] = __fmaf_rn(sc, __fmaf_rn(-zo, xs[i], bacc[i]), acc[i]);
             }

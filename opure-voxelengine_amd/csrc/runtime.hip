@@ -381,7 +381,8 @@ __global__ void k_quant_i8pc(const float* w, uint32_t out, uint32_t in, int8_t* 
     float m = 0.0f;
     for (uint32_t i = lane; i < in; i += 64) m = fmaxf(m, fabsf(r[i]));
     for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
-    const uint16_t s16 = f32_to_f16(fmaxf(m, 1e-8f) / 127.0f);
+    uint16_t s16 = f32_to_f16(fmaxf(m, 1e-8f) / 127.0f);
+    if (s16 == 0u) s16 = 1u;     // below the fp16 range (an all-zero row): the smallest positive scale
     const float s = f16_to_f32(s16);
     if (lane == 0) scale[row] = s16;
     for (uint32_t i = lane; i < in; i += 64)

@@ -103,6 +103,22 @@ __global__ __launch_bounds__(256) void k_embed(const int32_t* tokens, opure_line
     }
 }
 
+// Per-16-column-tile sums of squares of a given fp32 residual [M][h] (the
+// value every residual producer leaves for the next fused RMSNorm), summed in
+// column order: one thread per (row, tile).
+__global__ __launch_bounds__(256) void k_tile_sumsq(const float* x, uint32_t M, uint32_t h, float* ss)
+{
+    const uint32_t tiles = h / 16u;
+    const uint64_t i = static_cast<uint64_t>(blockIdx.x) * 256u + threadIdx.x;
+    if (i >= static_cast<uint64_t>(M) * tiles) return;
+    const uint32_t r = static_cast<uint32_t>(i / tiles), c16 = static_cast<uint32_t>(i - static_cast<uint64_t>(r) * tiles);
+    const float* xr = x + static_cast<uint64_t>(r) * h + 16u * c16;
+    float sq = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) sq = __fmaf_rn(xr[e], xr[e], sq);
+    ss[static_cast<uint64_t>(c16) * M + r] = sq;
+}
+
 }  // namespace
 
 namespace opure_hip {
@@ -188,6 +204,102 @@ static int check_model(const opure_model* m, const opure_kv* kv, uint32_t B, uin
     return OPURE_OK;
 }
 
+// One layer of the verify step on the residual x (fp32 [B*R][hidden]) whose
+// per-tile sums of squares are in ss: rmsnorm + qkv GEMV + RoPE + paged K/V
+// append, attention, o_proj + residual, rmsnorm + gate/up + SwiGLU, down +
+// residual.  `c` carries the step-wide GEMV fields (formats, rows, scratch).
+// The body of RecordForward's layer loop (Opure_VoxelEngine.cpp:296-492).
+static int layer_launch(opure_dev* dev, const opure_model* m, const opure_kv* kv, uint32_t L, uint32_t B, uint32_t R,
+                        const int32_t* seq_len, uint32_t max_ctx, const VerifyPlan& P, float* x, float* ss, GemvCall& c)
+{
+    char* ws = static_cast<char*>(dev->ws);
+    void* q = ws + P.q;
+    void* att = ws + P.att;
+    void* hbuf = ws + P.h;
+    const uint32_t qdim = m->n_heads * m->head_dim, kvdim = m->n_kv_heads * m->head_dim;
+    int rc;
+    const opure_layer_weights& W = m->layers[L];
+    c.W = W.qkv;
+    c.x = x;
+    c.gain = W.attn_norm;
+    c.ss_in = ss;
+    c.ss_out = nullptr;
+    c.y = q;
+    c.yfmt = m->afmt;
+    c.epi = EPI_QKV;
+    c.qkv.qdim = qdim;
+    c.qkv.kvdim = kvdim;
+    c.qkv.head_dim = m->head_dim;
+    c.qkv.n_kv_heads = m->n_kv_heads;
+    c.qkv.rope_cos = m->rope_cos;
+    c.qkv.rope_sin = m->rope_sin;
+    c.qkv.rope_max_pos = m->rope_max_pos;
+    c.qkv.seq_len = seq_len;
+    c.qkv.rows_per_seq = R;
+    c.qkv.kv_pool = kv->pool;
+    c.qkv.page_table = kv->page_table;
+    c.qkv.max_pages = kv->max_pages_per_seq;
+    c.qkv.n_pages = kv->n_pages;
+    c.qkv.layer = L;
+    if ((rc = gemv_validate(c)) || (rc = prof_begin(dev, OPURE_STAGE_QKV)) || (rc = gemv_launch(dev, c)) ||
+        (rc = prof_end(dev)))
+        return rc;
+
+    if ((rc = prof_begin(dev, OPURE_STAGE_ATTN)) ||
+        (rc = attn_launch(dev, m, kv, L, B, R, seq_len, max_ctx, q, att, reinterpret_cast<float*>(ws + P.attn))) ||
+        (rc = prof_end(dev)))
+        return rc;
+
+    c.W = W.o;
+    c.x = att;
+    c.gain = nullptr;
+    c.ss_out = ss;
+    c.y = x;
+    c.yfmt = OPURE_A_F32;
+    c.epi = EPI_RESIDUAL;
+    if ((rc = gemv_validate(c)) || (rc = prof_begin(dev, OPURE_STAGE_O)) || (rc = gemv_launch(dev, c)) ||
+        (rc = prof_end(dev)))
+        return rc;
+
+    c.W = W.gate_up;
+    c.x = x;
+    c.gain = W.mlp_norm;
+    c.ss_out = nullptr;
+    c.y = hbuf;
+    c.yfmt = m->afmt;
+    c.epi = EPI_SWIGLU;
+    if ((rc = gemv_validate(c)) || (rc = prof_begin(dev, OPURE_STAGE_GATE_UP)) || (rc = gemv_launch(dev, c)) ||
+        (rc = prof_end(dev)))
+        return rc;
+
+    c.W = W.down;
+    c.x = hbuf;
+    c.gain = nullptr;
+    c.ss_out = ss;
+    c.y = x;
+    c.yfmt = OPURE_A_F32;
+    c.epi = EPI_RESIDUAL;
+    if ((rc = gemv_validate(c)) || (rc = prof_begin(dev, OPURE_STAGE_DOWN)) || (rc = gemv_launch(dev, c)) ||
+        (rc = prof_end(dev)))
+        return rc;
+    return OPURE_OK;
+}
+
+// The GEMV fields shared by every launch of a step over B*R rows.
+static GemvCall step_gemv(const opure_model* m, uint32_t MR, const VerifyPlan& P, char* ws, float* ss)
+{
+    GemvCall c;
+    c.wfmt = m->wfmt;
+    c.xfmt = m->afmt;
+    c.M = MR;
+    c.eps = m->rms_eps;
+    c.ss_tiles = m->hidden / 16u;
+    c.ss_in = ss;
+    c.xn_scratch = ws + P.xn;
+    c.part_scratch = ws + P.part;
+    return c;
+}
+
 }  // namespace opure_hip
 
 using namespace opure_hip;
@@ -225,6 +337,27 @@ int opure_debug_verify_offsets(const opure_model* model, uint32_t batch, uint32_
     return OPURE_OK;
 }
 
+int opure_verify_layer(opure_dev* dev, const opure_verify_layer_args* a)
+{
+    OPURE_REQUIRE(dev && a && a->model && a->kv && a->seq_len && a->x, OPURE_E_INVALID,
+                  "opure_verify_layer: null argument");
+    const opure_model* m = a->model;
+    const uint32_t B = a->batch, R = a->rows, MR = B * R;
+    int rc = check_model(m, a->kv, B, R, a->max_ctx);
+    if (rc) return rc;
+    OPURE_REQUIRE(a->layer < m->n_layers, OPURE_E_INVALID, "opure_verify_layer: layer %u of %u", a->layer, m->n_layers);
+    const VerifyPlan P = make_plan(dev, m, B, R, a->max_ctx);
+    if ((rc = ensure_workspace(dev, P.total))) return rc;
+    char* ws = static_cast<char*>(dev->ws);
+    float* ss = reinterpret_cast<float*>(ws + P.ss);
+    const uint64_t n = static_cast<uint64_t>(MR) * (m->hidden / 16u);
+    hipLaunchKernelGGL(k_tile_sumsq, dim3(static_cast<uint32_t>((n + 255u) / 256u)), dim3(256), 0, dev->stream, a->x, MR,
+                       m->hidden, ss);
+    OPURE_LAUNCH_CHECK("k_tile_sumsq");
+    GemvCall c = step_gemv(m, MR, P, ws, ss);
+    return layer_launch(dev, m, a->kv, a->layer, B, R, a->seq_len, a->max_ctx, P, a->x, ss, c);
+}
+
 int opure_verify_step(opure_dev* dev, const opure_verify_args* a)
 {
     OPURE_REQUIRE(dev && a && a->model && a->kv && a->tokens && a->seq_len && a->logits, OPURE_E_INVALID,
@@ -254,10 +387,6 @@ int opure_verify_step(opure_dev* dev, const opure_verify_args* a)
     char* ws = static_cast<char*>(dev->ws);
     float* x = reinterpret_cast<float*>(ws + P.x);
     float* ss = reinterpret_cast<float*>(ws + P.ss);
-    void* q = ws + P.q;
-    void* att = ws + P.att;
-    void* hbuf = ws + P.h;
-    const uint32_t qdim = m->n_heads * m->head_dim, kvdim = m->n_kv_heads * m->head_dim;
 
     if ((rc = prof_begin(dev, OPURE_STAGE_EMBED))) return rc;
     hipLaunchKernelGGL(k_embed, dim3(MR), dim3(256), 0, dev->stream, a->tokens, m->embed, m->wfmt, m->hidden, m->vocab,
@@ -268,82 +397,9 @@ int opure_verify_step(opure_dev* dev, const opure_verify_args* a)
     // Each residual producer (embed, o, down) leaves per-tile sums of squares in
     // `ss`; the next consumer (qkv, gate/up, LM head) applies the RMSNorm while
     // loading x.  Stream order keeps the single buffer consistent.
-    GemvCall c;
-    c.wfmt = m->wfmt;
-    c.xfmt = m->afmt;
-    c.M = MR;
-    c.eps = m->rms_eps;
-    c.ss_tiles = m->hidden / 16u;
-    c.xn_scratch = ws + P.xn;
-    c.part_scratch = ws + P.part;
+    GemvCall c = step_gemv(m, MR, P, ws, ss);
     for (uint32_t L = 0; L < m->n_layers; ++L)
-    {
-        const opure_layer_weights& W = m->layers[L];
-        c.W = W.qkv;
-        c.x = x;
-        c.gain = W.attn_norm;
-        c.ss_in = ss;
-        c.ss_out = nullptr;
-        c.y = q;
-        c.yfmt = m->afmt;
-        c.epi = EPI_QKV;
-        c.qkv.qdim = qdim;
-        c.qkv.kvdim = kvdim;
-        c.qkv.head_dim = m->head_dim;
-        c.qkv.n_kv_heads = m->n_kv_heads;
-        c.qkv.rope_cos = m->rope_cos;
-        c.qkv.rope_sin = m->rope_sin;
-        c.qkv.rope_max_pos = m->rope_max_pos;
-        c.qkv.seq_len = a->seq_len;
-        c.qkv.rows_per_seq = R;
-        c.qkv.kv_pool = kv->pool;
-        c.qkv.page_table = kv->page_table;
-        c.qkv.max_pages = kv->max_pages_per_seq;
-        c.qkv.n_pages = kv->n_pages;
-        c.qkv.layer = L;
-        if ((rc = gemv_validate(c)) || (rc = prof_begin(dev, OPURE_STAGE_QKV)) || (rc = gemv_launch(dev, c)) ||
-            (rc = prof_end(dev)))
-            return rc;
-
-        if ((rc = prof_begin(dev, OPURE_STAGE_ATTN)) ||
-            (rc = attn_launch(dev, m, kv, L, B, R, a->seq_len, a->max_ctx, q, att,
-                              reinterpret_cast<float*>(ws + P.attn))) ||
-            (rc = prof_end(dev)))
-            return rc;
-
-        c.W = W.o;
-        c.x = att;
-        c.gain = nullptr;
-        c.ss_out = ss;
-        c.y = x;
-        c.yfmt = OPURE_A_F32;
-        c.epi = EPI_RESIDUAL;
-        if ((rc = gemv_validate(c)) || (rc = prof_begin(dev, OPURE_STAGE_O)) || (rc = gemv_launch(dev, c)) ||
-            (rc = prof_end(dev)))
-            return rc;
-
-        c.W = W.gate_up;
-        c.x = x;
-        c.gain = W.mlp_norm;
-        c.ss_out = nullptr;
-        c.y = hbuf;
-        c.yfmt = m->afmt;
-        c.epi = EPI_SWIGLU;
-        if ((rc = gemv_validate(c)) || (rc = prof_begin(dev, OPURE_STAGE_GATE_UP)) || (rc = gemv_launch(dev, c)) ||
-            (rc = prof_end(dev)))
-            return rc;
-
-        c.W = W.down;
-        c.x = hbuf;
-        c.gain = nullptr;
-        c.ss_out = ss;
-        c.y = x;
-        c.yfmt = OPURE_A_F32;
-        c.epi = EPI_RESIDUAL;
-        if ((rc = gemv_validate(c)) || (rc = prof_begin(dev, OPURE_STAGE_DOWN)) || (rc = gemv_launch(dev, c)) ||
-            (rc = prof_end(dev)))
-            return rc;
-    }
+        if ((rc = layer_launch(dev, m, kv, L, B, R, a->seq_len, a->max_ctx, P, x, ss, c))) return rc;
 
     c.W = m->lm_head;
     c.x = x;

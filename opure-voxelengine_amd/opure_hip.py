@@ -101,6 +101,11 @@ class VerifyArgs(C.Structure):
                 ("poison", C.c_uint32), ("poison_bits", C.c_uint32)]
 
 
+class VerifyLayerArgs(C.Structure):
+    _fields_ = [("model", C.POINTER(Model)), ("kv", C.POINTER(KV)), ("layer", C.c_uint32), ("batch", C.c_uint32),
+                ("rows", C.c_uint32), ("seq_len", C.c_void_p), ("max_ctx", C.c_uint32), ("x", C.c_void_p)]
+
+
 _lib = None
 
 
@@ -141,6 +146,7 @@ def _declare(L):
         "opure_kv_rollback": ([vp, C.POINTER(RollbackArgs)], i),
         "opure_verify_reserve": ([vp, C.POINTER(Model), u32, u32, u32], i),
         "opure_verify_step": ([vp, C.POINTER(VerifyArgs)], i),
+        "opure_verify_layer": ([vp, C.POINTER(VerifyLayerArgs)], i),
         "opure_debug_workspace": ([vp, C.POINTER(vp), C.POINTER(u64)], i),
         "opure_debug_verify_offsets": ([C.POINTER(Model), u32, u32, u32, C.POINTER(u64)], i),
         "opure_tiled_bytes": ([u32, u32, u32, C.POINTER(u64), C.POINTER(u64)], i),

@@ -26,7 +26,11 @@
 //                         KV append Opure_RoPE.usf:105-114 (rotated K, raw V)
 //    orc_verify_forward   per-token order of Opure_CpuReference.cpp:225-345,
 //                         run layer-major over R rows (equivalent: row j at
-//                         layer L reads only K/V of rows <= j at layer L)
+//                         layer L reads only K/V of rows <= j at layer L);
+//                         composed of orc_verify_embed / _layers / _head so a
+//                         test can feed any residual into any layer, as the
+//                         reference harness traces layers
+//                         (Opure_TestHarness.cpp:956-987)
 //    orc_argmax_rows      Opure_ArgMax.usf contract, ties -> lowest index
 //    orc_accept_*         absent from the reference; Leviathan et al. 2023 /
 //                         Chen et al. 2023 with the fixed-point conventions
@@ -429,29 +433,34 @@ void orc_attention_paged(const orc_model* m, const orc_kv* kv, uint32_t layer,
     }
 }
 
-static int verify_impl(const orc_model* m, orc_kv* kv, uint32_t B, uint32_t R,
-                       const int32_t* tokens, const int32_t* seq_len, float* logits, float* trace);
+// ---------------------------------------------------------------------------
+//  The verify forward, in three parts that compose to orc_verify_forward:
+//  the embedding gather, layers [first, first+count) applied to a residual in
+//  place, and the final RMSNorm + LM head.  A test can run the parts one at a
+//  time (the reference's per-layer tracing, Opure_TestHarness.cpp:956-987) and
+//  feed any residual into any layer.
+// ---------------------------------------------------------------------------
+namespace {
 
-int orc_verify_forward(const orc_model* m, orc_kv* kv, uint32_t B, uint32_t R,
-                       const int32_t* tokens, const int32_t* seq_len, float* logits)
+// One element of one intermediate moved by one unit in the last place of the
+// activation format, after that intermediate's rounding (a test hook: it shows
+// how far a single rounding decision travels through the layers).
+struct Perturbation { int32_t layer = -1; uint32_t stage = 0; uint64_t index = 0; };
+Perturbation g_perturb;
+
+void perturb_at(float* a, uint64_t n, uint32_t L, uint32_t stage, uint32_t afmt)
 {
-    return verify_impl(m, kv, B, R, tokens, seq_len, logits, nullptr);
+    if (g_perturb.layer < 0 || static_cast<uint32_t>(g_perturb.layer) != L || g_perturb.stage != stage ||
+        g_perturb.index >= n)
+        return;
+    float& v = a[g_perturb.index];
+    if (afmt == ORC_A_F32) { v = bits_f(f_bits(v) + 1u); return; }
+    if (afmt == ORC_A_F16) { v = orc_f16_to_f32(static_cast<uint16_t>(orc_f32_to_f16(v) + 1u)); return; }
+    v = orc_bf16_to_f32(static_cast<uint16_t>(orc_f32_to_bf16(v) + 1u));
 }
 
-int orc_verify_forward_traced(const orc_model* m, orc_kv* kv, uint32_t B, uint32_t R,
-                              const int32_t* tokens, const int32_t* seq_len, float* logits,
-                              float* trace)
+int check_step(const orc_model* m, const orc_kv* kv, uint32_t B, uint32_t R, const int32_t* seq_len)
 {
-    return verify_impl(m, kv, B, R, tokens, seq_len, logits, trace);
-}
-
-static int verify_impl(const orc_model* m, orc_kv* kv, uint32_t B, uint32_t R,
-                       const int32_t* tokens, const int32_t* seq_len, float* logits, float* trace)
-{
-    if (!m || !kv || !tokens || !seq_len || !logits || B == 0 || R == 0) return -1;
-    const uint32_t h = m->hidden, hd = m->head_dim, nh = m->n_heads, nkv = m->n_kv_heads;
-    const uint32_t qdim = nh * hd, kvdim = nkv * hd, ff = m->ffn;
-    const uint32_t MR = B * R;
     for (uint32_t b = 0; b < B; ++b)
     {
         if (seq_len[b] < 0) return -1;
@@ -463,19 +472,106 @@ static int verify_impl(const orc_model* m, orc_kv* kv, uint32_t B, uint32_t R,
             const int32_t pg = kv->page_table[static_cast<uint64_t>(b) * kv->max_pages_per_seq + p];
             if (pg < 0 || static_cast<uint32_t>(pg) >= kv->n_pages) return -2;
         }
+    }
+    return 0;
+}
+
+// Layer L of Opure_CpuReference.cpp:225-345 for B*R rows: x is updated in
+// place and the rows' K/V are appended to the cache.  `trace` (layer 0 only)
+// receives the intermediates listed at orc_verify_forward_traced.
+void run_layer(const orc_model* m, orc_kv* kv, uint32_t B, uint32_t R, const int32_t* seq_len, uint32_t L,
+               float* x, float* trace)
+{
+    const uint32_t h = m->hidden, hd = m->head_dim, nh = m->n_heads, nkv = m->n_kv_heads;
+    const uint32_t qdim = nh * hd, kvdim = nkv * hd, ff = m->ffn;
+    const uint32_t MR = B * R;
+    const uint64_t xs = static_cast<uint64_t>(MR) * h;
+    std::vector<float> xn(xs);
+    std::vector<float> qkv(static_cast<uint64_t>(MR) * (qdim + 2 * kvdim));
+    std::vector<float> q(static_cast<uint64_t>(MR) * qdim), att(q.size()), proj(xs);
+    std::vector<float> gu(static_cast<uint64_t>(MR) * 2 * ff), hh(static_cast<uint64_t>(MR) * ff);
+    const orc_layer& P = m->layers[L];
+
+    orc_rmsnorm_rows(x, P.attn_norm, xn.data(), MR, h, m->rms_eps, m->afmt);
+    perturb_at(xn.data(), xs, L, ORC_STAGE_XN_ATTN, m->afmt);
+    orc_gemv(&P.qkv, m->wfmt, xn.data(), qkv.data(), MR);
+    const uint32_t qkvw = qdim + 2 * kvdim;
+    for (uint32_t b = 0; b < B; ++b)
+    {
         for (uint32_t j = 0; j < R; ++j)
         {
-            const int32_t t = tokens[b * R + j];
-            if (t < 0 || static_cast<uint32_t>(t) >= m->vocab) return -4;
+            const uint32_t r = b * R + j;
+            const uint32_t pos = static_cast<uint32_t>(seq_len[b]) + j;
+            float* row = qkv.data() + static_cast<uint64_t>(r) * qkvw;
+            orc_rope_rows(row, nh, hd, m->rope_cos, m->rope_sin, pos);
+            orc_rope_rows(row + qdim, nkv, hd, m->rope_cos, m->rope_sin, pos);
+            orc_round_act(row, qkvw, m->afmt);
+            std::memcpy(q.data() + static_cast<uint64_t>(r) * qdim, row, qdim * 4);
+            const int32_t pg = kv->page_table[static_cast<uint64_t>(b) * kv->max_pages_per_seq + pos / kv->page_size];
+            for (uint32_t kh = 0; kh < nkv; ++kh)
+            {
+                for (uint32_t d = 0; d < hd; ++d)
+                {
+                    store_act(kv->pool, kv_elem(m, kv, L, pg, 0, kh, pos % kv->page_size, d), row[qdim + kh * hd + d],
+                              m->afmt);
+                    store_act(kv->pool, kv_elem(m, kv, L, pg, 1, kh, pos % kv->page_size, d),
+                              row[qdim + kvdim + kh * hd + d], m->afmt);
+                }
+            }
         }
     }
+    perturb_at(q.data(), q.size(), L, ORC_STAGE_Q, m->afmt);
+    for (uint32_t b = 0; b < B; ++b)
+        orc_attention_paged(m, kv, L, b, static_cast<uint32_t>(seq_len[b]), R,
+                            q.data() + static_cast<uint64_t>(b) * R * qdim,
+                            att.data() + static_cast<uint64_t>(b) * R * qdim);
+    orc_round_act(att.data(), att.size(), m->afmt);
+    perturb_at(att.data(), att.size(), L, ORC_STAGE_ATT, m->afmt);
+    orc_gemv(&P.o, m->wfmt, att.data(), proj.data(), MR);
+    for (uint64_t i = 0; i < xs; ++i) x[i] = x[i] + proj[i];
+    if (trace)
+    {
+        float* t = trace;
+        std::memcpy(t, q.data(), q.size() * 4); t += q.size();
+        std::memcpy(t, att.data(), att.size() * 4); t += att.size();
+        std::memcpy(t, x, xs * 4);
+    }
 
-    std::vector<float> x(static_cast<uint64_t>(MR) * h), xn(x.size());
-    std::vector<float> qkv(static_cast<uint64_t>(MR) * (qdim + 2 * kvdim));
-    std::vector<float> q(static_cast<uint64_t>(MR) * qdim), att(q.size()), proj(x.size());
-    std::vector<float> gu(static_cast<uint64_t>(MR) * 2 * ff), hh(static_cast<uint64_t>(MR) * ff);
+    orc_rmsnorm_rows(x, P.mlp_norm, xn.data(), MR, h, m->rms_eps, m->afmt);
+    perturb_at(xn.data(), xs, L, ORC_STAGE_XN_MLP, m->afmt);
+    orc_gemv(&P.gate_up, m->wfmt, xn.data(), gu.data(), MR);
+    for (uint32_t r = 0; r < MR; ++r)
+        orc_swiglu(gu.data() + static_cast<uint64_t>(r) * 2 * ff,
+                   gu.data() + static_cast<uint64_t>(r) * 2 * ff + ff,
+                   hh.data() + static_cast<uint64_t>(r) * ff, ff);
+    orc_round_act(hh.data(), hh.size(), m->afmt);
+    perturb_at(hh.data(), hh.size(), L, ORC_STAGE_H, m->afmt);
+    orc_gemv(&P.down, m->wfmt, hh.data(), proj.data(), MR);
+    for (uint64_t i = 0; i < xs; ++i) x[i] = x[i] + proj[i];
+    if (trace)
+    {
+        float* t = trace + 2 * q.size() + xs;
+        std::memcpy(t, hh.data(), hh.size() * 4); t += hh.size();
+        std::memcpy(t, x, xs * 4);
+    }
+}
 
-    // embedding (Opure_CpuReference.cpp:225; dequantised row for quantised tables)
+}  // namespace
+
+void orc_set_perturbation(int32_t layer, uint32_t stage, uint64_t index)
+{
+    g_perturb.layer = layer;
+    g_perturb.stage = stage;
+    g_perturb.index = index;
+}
+
+// embedding (Opure_CpuReference.cpp:225; dequantised row for quantised tables)
+int orc_verify_embed(const orc_model* m, uint32_t MR, const int32_t* tokens, float* x)
+{
+    if (!m || !tokens || !x) return -1;
+    const uint32_t h = m->hidden;
+    for (uint32_t r = 0; r < MR; ++r)
+        if (tokens[r] < 0 || static_cast<uint32_t>(tokens[r]) >= m->vocab) return -4;
     for (uint32_t r = 0; r < MR; ++r)
     {
         const uint32_t t = static_cast<uint32_t>(tokens[r]);
@@ -497,74 +593,59 @@ static int verify_impl(const orc_model* m, orc_kv* kv, uint32_t B, uint32_t R,
             x[static_cast<uint64_t>(r) * h + i] = v;
         }
     }
+    return 0;
+}
 
-    for (uint32_t L = 0; L < m->n_layers; ++L)
-    {
-        const orc_layer& P = m->layers[L];
-        orc_rmsnorm_rows(x.data(), P.attn_norm, xn.data(), MR, h, m->rms_eps, m->afmt);
-        orc_gemv(&P.qkv, m->wfmt, xn.data(), qkv.data(), MR);
-        const uint32_t qkvw = qdim + 2 * kvdim;
-        for (uint32_t b = 0; b < B; ++b)
-        {
-            for (uint32_t j = 0; j < R; ++j)
-            {
-                const uint32_t r = b * R + j;
-                const uint32_t pos = static_cast<uint32_t>(seq_len[b]) + j;
-                float* row = qkv.data() + static_cast<uint64_t>(r) * qkvw;
-                orc_rope_rows(row, nh, hd, m->rope_cos, m->rope_sin, pos);
-                orc_rope_rows(row + qdim, nkv, hd, m->rope_cos, m->rope_sin, pos);
-                orc_round_act(row, qkvw, m->afmt);
-                std::memcpy(q.data() + static_cast<uint64_t>(r) * qdim, row, qdim * 4);
-                const int32_t pg = kv->page_table[static_cast<uint64_t>(b) * kv->max_pages_per_seq + pos / kv->page_size];
-                for (uint32_t kh = 0; kh < nkv; ++kh)
-                {
-                    for (uint32_t d = 0; d < hd; ++d)
-                    {
-                        store_act(kv->pool, kv_elem(m, kv, L, pg, 0, kh, pos % kv->page_size, d), row[qdim + kh * hd + d],
-                                  m->afmt);
-                        store_act(kv->pool, kv_elem(m, kv, L, pg, 1, kh, pos % kv->page_size, d),
-                                  row[qdim + kvdim + kh * hd + d], m->afmt);
-                    }
-                }
-            }
-        }
-        for (uint32_t b = 0; b < B; ++b)
-            orc_attention_paged(m, kv, L, b, static_cast<uint32_t>(seq_len[b]), R,
-                                q.data() + static_cast<uint64_t>(b) * R * qdim,
-                                att.data() + static_cast<uint64_t>(b) * R * qdim);
-        orc_round_act(att.data(), att.size(), m->afmt);
-        orc_gemv(&P.o, m->wfmt, att.data(), proj.data(), MR);
-        for (uint64_t i = 0; i < x.size(); ++i) x[i] = x[i] + proj[i];
-        if (trace && L == 0)
-        {
-            float* t = trace;
-            std::memcpy(t, q.data(), q.size() * 4); t += q.size();
-            std::memcpy(t, att.data(), att.size() * 4); t += att.size();
-            std::memcpy(t, x.data(), x.size() * 4);
-        }
+int orc_verify_layers(const orc_model* m, orc_kv* kv, uint32_t B, uint32_t R, const int32_t* seq_len, float* x,
+                      uint32_t first, uint32_t count)
+{
+    if (!m || !kv || !seq_len || !x || B == 0 || R == 0 || first + count > m->n_layers) return -1;
+    const int rc = check_step(m, kv, B, R, seq_len);
+    if (rc) return rc;
+    for (uint32_t L = first; L < first + count; ++L) run_layer(m, kv, B, R, seq_len, L, x, nullptr);
+    return 0;
+}
 
-        orc_rmsnorm_rows(x.data(), P.mlp_norm, xn.data(), MR, h, m->rms_eps, m->afmt);
-        orc_gemv(&P.gate_up, m->wfmt, xn.data(), gu.data(), MR);
-        for (uint32_t r = 0; r < MR; ++r)
-            orc_swiglu(gu.data() + static_cast<uint64_t>(r) * 2 * ff,
-                       gu.data() + static_cast<uint64_t>(r) * 2 * ff + ff,
-                       hh.data() + static_cast<uint64_t>(r) * ff, ff);
-        orc_round_act(hh.data(), hh.size(), m->afmt);
-        orc_gemv(&P.down, m->wfmt, hh.data(), proj.data(), MR);
-        for (uint64_t i = 0; i < x.size(); ++i) x[i] = x[i] + proj[i];
-        if (trace && L == 0)
-        {
-            float* t = trace + 2 * q.size() + x.size();
-            std::memcpy(t, hh.data(), hh.size() * 4); t += hh.size();
-            std::memcpy(t, x.data(), x.size() * 4);
-        }
-    }
-
-    orc_rmsnorm_rows(x.data(), m->final_norm, xn.data(), MR, h, m->rms_eps, m->afmt);
-    if (trace)
-        std::memcpy(trace + 2 * q.size() + 2 * x.size() + hh.size(), xn.data(), xn.size() * 4);
+// final RMSNorm (Opure_VoxelEngine.cpp:523-527) and the LM head (:528-532)
+int orc_verify_head(const orc_model* m, uint32_t MR, const float* x, float* logits)
+{
+    if (!m || !x || !logits) return -1;
+    std::vector<float> xn(static_cast<uint64_t>(MR) * m->hidden);
+    orc_rmsnorm_rows(x, m->final_norm, xn.data(), MR, m->hidden, m->rms_eps, m->afmt);
     orc_gemv(&m->lm_head, m->wfmt, xn.data(), logits, MR);
     return 0;
+}
+
+static int verify_impl(const orc_model* m, orc_kv* kv, uint32_t B, uint32_t R,
+                       const int32_t* tokens, const int32_t* seq_len, float* logits, float* trace)
+{
+    if (!m || !kv || !tokens || !seq_len || !logits || B == 0 || R == 0) return -1;
+    int rc = check_step(m, kv, B, R, seq_len);
+    if (rc) return rc;
+    const uint32_t MR = B * R, h = m->hidden;
+    std::vector<float> x(static_cast<uint64_t>(MR) * h);
+    if ((rc = orc_verify_embed(m, MR, tokens, x.data()))) return rc;
+    for (uint32_t L = 0; L < m->n_layers; ++L) run_layer(m, kv, B, R, seq_len, L, x.data(), L == 0 ? trace : nullptr);
+    if (trace)
+    {
+        const uint64_t qs = static_cast<uint64_t>(MR) * m->n_heads * m->head_dim, xs = static_cast<uint64_t>(MR) * h;
+        orc_rmsnorm_rows(x.data(), m->final_norm, trace + 2 * qs + 2 * xs + static_cast<uint64_t>(MR) * m->ffn, MR, h,
+                         m->rms_eps, m->afmt);
+    }
+    return orc_verify_head(m, MR, x.data(), logits);
+}
+
+int orc_verify_forward(const orc_model* m, orc_kv* kv, uint32_t B, uint32_t R,
+                       const int32_t* tokens, const int32_t* seq_len, float* logits)
+{
+    return verify_impl(m, kv, B, R, tokens, seq_len, logits, nullptr);
+}
+
+int orc_verify_forward_traced(const orc_model* m, orc_kv* kv, uint32_t B, uint32_t R,
+                              const int32_t* tokens, const int32_t* seq_len, float* logits,
+                              float* trace)
+{
+    return verify_impl(m, kv, B, R, tokens, seq_len, logits, trace);
 }
 
 // ---------------------------------------------------------------------------

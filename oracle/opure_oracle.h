@@ -116,6 +116,23 @@ void orc_attention_paged(const orc_model* m, const orc_kv* kv, uint32_t layer,
 int orc_verify_forward(const orc_model* m, orc_kv* kv, uint32_t B, uint32_t R,
                        const int32_t* tokens, const int32_t* seq_len, float* logits);
 
+/* The forward in parts: orc_verify_forward = orc_verify_embed, then
+ * orc_verify_layers(0, n_layers), then orc_verify_head, bit for bit.
+ * x: fp32 residual [B*R][hidden].  orc_verify_layers applies layers
+ * [first, first+count) to x in place and appends the rows' K/V to the cache
+ * (the checks and return codes of orc_verify_forward). */
+int orc_verify_embed(const orc_model* m, uint32_t MR, const int32_t* tokens, float* x);
+int orc_verify_layers(const orc_model* m, orc_kv* kv, uint32_t B, uint32_t R, const int32_t* seq_len, float* x,
+                      uint32_t first, uint32_t count);
+int orc_verify_head(const orc_model* m, uint32_t MR, const float* x, float* logits);
+
+/* Test hook: after the rounding of intermediate `stage` in layer `layer`,
+ * element `index` moves by one unit in the last place of the activation
+ * format (layer < 0 turns it off).  It measures how far one rounding decision
+ * travels through the rest of the forward. */
+enum { ORC_STAGE_XN_ATTN = 0, ORC_STAGE_Q = 1, ORC_STAGE_ATT = 2, ORC_STAGE_XN_MLP = 3, ORC_STAGE_H = 4 };
+void orc_set_perturbation(int32_t layer, uint32_t stage, uint64_t index);
+
 /* As orc_verify_forward, also recording layer 0's intermediates (the
  * reference's ForwardTraced idea, Opure_CpuReference.h:48-54):
  * trace = [q (MR*nh*hd, after RoPE, rounded) | att (MR*nh*hd) | x after the

@@ -92,6 +92,11 @@ def _declare(L):
     L.orc_verify_forward.restype = C.c_int
     L.orc_verify_forward_traced.argtypes = [C.POINTER(OrcModel), C.POINTER(OrcKV), u32, u32, vp, vp, vp, vp]
     L.orc_verify_forward_traced.restype = C.c_int
+    L.orc_verify_embed.argtypes = [C.POINTER(OrcModel), u32, vp, vp]; L.orc_verify_embed.restype = C.c_int
+    L.orc_verify_layers.argtypes = [C.POINTER(OrcModel), C.POINTER(OrcKV), u32, u32, vp, vp, u32, u32]
+    L.orc_verify_layers.restype = C.c_int
+    L.orc_verify_head.argtypes = [C.POINTER(OrcModel), u32, vp, vp]; L.orc_verify_head.restype = C.c_int
+    L.orc_set_perturbation.argtypes = [C.c_int32, u32, u64]; L.orc_set_perturbation.restype = None
     L.orc_argmax_rows.argtypes = [vp, u32, u32, vp, vp]; L.orc_argmax_rows.restype = None
     L.orc_accept_greedy.argtypes = [vp, vp, u32, u32, u32, vp, vp]; L.orc_accept_greedy.restype = None
     L.orc_accept_rejection.argtypes = [vp, vp, vp, u32, u32, u32, f32, u64, vp, vp, vp, vp]
@@ -175,6 +180,9 @@ def quant_i8pc(w: np.ndarray):
     w = np.asarray(w, dtype=np.float32)
     amax = np.abs(w).max(axis=1)
     s16 = (np.maximum(amax, 1e-8) / 127.0).astype(np.float16)
+    # a row too small for an fp16 scale (an all-zero row) gets the smallest
+    # positive one, so its codes are 0 rather than 0/0
+    s16[s16 == 0] = np.uint16(1).view(np.float16)
     s = s16.astype(np.float32)
     q = np.clip(np.rint(w / s[:, None]), -127, 127).astype(np.int8)
     return {"w": np.ascontiguousarray(q), "scale": s16.view(np.uint16).copy(), "zero": None,
@@ -345,6 +353,47 @@ def verify_forward(model: HostModel, kv: HostKV, tokens: np.ndarray, seq_len: np
     if rc != 0:
         raise ValueError(f"orc_verify_forward failed: {rc}")
     return logits
+
+
+STAGE_XN_ATTN, STAGE_Q, STAGE_ATT, STAGE_XN_MLP, STAGE_H = 0, 1, 2, 3, 4
+
+
+def verify_embed(model: HostModel, tokens: np.ndarray) -> np.ndarray:
+    """fp32 residual [B*R][hidden] of the embedding rows of `tokens`."""
+    t = np.ascontiguousarray(tokens, dtype=np.int32).reshape(-1)
+    x = np.zeros((t.size, model.cfg["hidden"]), dtype=np.float32)
+    rc = lib().orc_verify_embed(C.byref(model.desc), t.size, _p(t), _p(x))
+    if rc != 0:
+        raise ValueError(f"orc_verify_embed failed: {rc}")
+    return x
+
+
+def verify_layers(model: HostModel, kv: HostKV, x: np.ndarray, seq_len, R: int, first: int, count: int) -> np.ndarray:
+    """Applies layers [first, first+count) to a copy of residual x ([B*R][hidden]),
+    appending the rows' K/V to the cache; returns the new residual."""
+    seq_len = np.ascontiguousarray(seq_len, dtype=np.int32)
+    x = np.array(x, dtype=np.float32, order="C", copy=True)
+    kv._mk()
+    rc = lib().orc_verify_layers(C.byref(model.desc), C.byref(kv.desc), seq_len.size, R, _p(seq_len), _p(x), first,
+                                 count)
+    if rc != 0:
+        raise ValueError(f"orc_verify_layers failed: {rc}")
+    return x
+
+
+def verify_head(model: HostModel, x: np.ndarray) -> np.ndarray:
+    """Final RMSNorm + LM head of residual rows x: logits [rows][vocab]."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.zeros((x.shape[0], model.cfg["vocab"]), dtype=np.float32)
+    rc = lib().orc_verify_head(C.byref(model.desc), x.shape[0], _p(x), _p(out))
+    if rc != 0:
+        raise ValueError(f"orc_verify_head failed: {rc}")
+    return out
+
+
+def set_perturbation(layer: int = -1, stage: int = 0, index: int = 0) -> None:
+    """One element of one rounded intermediate moved by one ulp (layer < 0: off)."""
+    lib().orc_set_perturbation(int(layer), int(stage), int(index))
 
 
 def verify_forward_traced(model: HostModel, kv: HostKV, tokens: np.ndarray, seq_len: np.ndarray):

@@ -48,6 +48,7 @@ def test_error_paths_without_device():
     assert L.opure_dev_create(0, None) == H.E_INVALID
     assert L.opure_gemv_batched_f32(None, None) == H.E_INVALID
     assert L.opure_verify_step(None, None) == H.E_INVALID
+    assert L.opure_verify_layer(None, None) == H.E_INVALID
     assert L.opure_kv_rollback(None, None) == H.E_INVALID
     assert L.opure_graph_destroy(None) == H.OK
 
@@ -57,6 +58,7 @@ STRUCTS = {
     "opure_kv": H.KV, "opure_gemv_args": H.GemvArgs, "opure_attn_args": H.AttnArgs,
     "opure_accept_args": H.AcceptArgs, "opure_sample_args": H.SampleArgs,
     "opure_rollback_args": H.RollbackArgs, "opure_verify_args": H.VerifyArgs,
+    "opure_verify_layer_args": H.VerifyLayerArgs,
 }
 
 

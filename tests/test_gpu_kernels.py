@@ -171,6 +171,7 @@ GEMV_CASES = [
     (H.W_I4G128, H.A_F16, 1024, 4096),
     (H.W_I4G128, H.A_BF16, 6144, 4096),
     (H.W_I4G128, H.A_BF16, 4096, 14336),
+    (H.W_I8PC, H.A_F16, 128256, 2048),       # the 1B LM head over a batch of 32 x 7 rows
 ]
 
 
@@ -188,7 +189,7 @@ def test_gemv_store_residual_matches_oracle(dev, case):
     x_bits, x_f = to_act(rng.standard_normal((16, inn)), afmt)
     ref = O.gemv(lin, wfmt, x_f)
     absref = np.abs(x_f).astype(np.float64) @ np.abs(O.dequant(lin, wfmt)).T
-    slack = 20.0 if (wfmt == H.W_I4G128 and afmt == H.A_BF16) else 1.0
+    slack = 4.0 if (wfmt == H.W_I4G128 and afmt == H.A_BF16) else 1.0
     y16 = run_gemv(dev, wfmt, desc, x_bits, 16, afmt, H.A_F32, H.EPI_STORE)
     err = np.abs(y16 - ref)
     assert np.all(err <= 1e-5 * slack * absref + 1e-6), (err.max(), (err / (absref + 1e-9)).max())
@@ -215,6 +216,7 @@ WIDE_CASES = [
     (H.W_I4G128, H.A_BF16, 6144, 4096),
     (H.W_I4G128, H.A_F16, 1024, 4096),
     (H.W_I4G128, H.A_BF16, 4096, 14336),
+    (H.W_I8PC, H.A_F16, 128256, 2048),       # the 1B LM head over a batch of 32 x 7 rows
 ]
 
 
@@ -234,7 +236,7 @@ def test_gemv_wide_matches_reference(dev, case):
     wd = O.dequant(lin, wfmt).astype(np.float64)
     ref = x_f.astype(np.float64) @ wd.T
     absref = np.abs(x_f).astype(np.float64) @ np.abs(wd).T
-    slack = 20.0 if (wfmt == H.W_I4G128 and afmt == H.A_BF16) else 1.0
+    slack = 4.0 if (wfmt == H.W_I4G128 and afmt == H.A_BF16) else 1.0
     y = run_gemv(dev, wfmt, desc, x_bits, M, afmt, H.A_F32, H.EPI_STORE)
     err = np.abs(y - ref)
     assert np.all(err <= 1e-5 * slack * absref + 1e-6), (err.max(), (err / (absref + 1e-9)).max())
@@ -309,7 +311,7 @@ def test_gemv_loader_waves_equal_wave_per_tile(dev, case):
         assert np.array_equal(yM, y16[:M]), M
     ref = O.gemv(lin, wfmt, x_f[:2])
     absref = np.abs(x_f[:2]).astype(np.float64) @ np.abs(O.dequant(lin, wfmt)).T
-    slack = 20.0 if (wfmt == H.W_I4G128 and afmt == H.A_BF16) else 1.0
+    slack = 4.0 if (wfmt == H.W_I4G128 and afmt == H.A_BF16) else 1.0
     assert np.all(np.abs(y16[:2] - ref) <= 1e-5 * slack * absref + 1e-6)
     for b in keep:
         if b:
@@ -334,7 +336,7 @@ def test_gemv_two_waves_a_tile(dev, case):
         assert np.array_equal(yM, y16[:M]), M
     ref = O.gemv(lin, wfmt, x_f[:3])
     absref = np.abs(x_f[:3]).astype(np.float64) @ np.abs(O.dequant(lin, wfmt)).T
-    slack = 20.0 if (wfmt == H.W_I4G128 and afmt == H.A_BF16) else 1.0
+    slack = 4.0 if (wfmt == H.W_I4G128 and afmt == H.A_BF16) else 1.0
     assert np.all(np.abs(y16[:3] - ref) <= 1e-5 * slack * absref + 1e-6)
     for b in keep:
         if b:
@@ -424,40 +426,58 @@ def test_attention_known_answers(dev, hd):
     assert rms <= 1e-5 * np.abs(g["ref"]).max()
 
 
-@pytest.mark.parametrize("afmt", [H.A_F32, H.A_F16, H.A_BF16], ids=["f32", "f16", "bf16"])
-def test_attention_paged_matches_oracle(dev, afmt):
-    say("attention afmt", afmt)
-    rng = np.random.default_rng(31 + afmt)
-    nh, nkv, hd, R, B, ps = 8, 2, 64, 5, 2, 16
-    ctx = [131, 37]
-    n_pages = 24
+ATTN_CASES = [
+    # afmt, head_dim, rows, contexts (several 128/256-token chunks at head_dim 64/128)
+    (H.A_F32, 64, 5, [131, 37]),
+    (H.A_F16, 64, 5, [131, 37]),
+    (H.A_BF16, 64, 5, [131, 37]),
+    (H.A_F16, 128, 8, [1100, 531]),
+    (H.A_BF16, 128, 8, [1100, 531]),
+]
+
+
+@pytest.mark.parametrize("case", ATTN_CASES,
+                         ids=[f"{['f32', 'f16', 'bf16'][c[0]]}-hd{c[1]}-r{c[2]}" for c in ATTN_CASES])
+def test_attention_paged_matches_oracle(dev, case):
+    afmt, hd, R, ctx = case
+    say("attention", case)
+    rng = np.random.default_rng(31 + afmt + hd)
+    nh, nkv, B, ps = 8, 2, 2, 16
+    mp = [(c + R + ps - 1) // ps for c in ctx]
+    n_pages = sum(mp) + 4
     mcfg = dict(n_layers=2, hidden=64, n_heads=nh, n_kv_heads=nkv, head_dim=hd, ffn=64, vocab=64,
                 wfmt=O.W_F32, afmt=afmt)
-    hm = O.HostModel(**mcfg, attn_scale=0.125, max_pos=512, seed=1)
-    kv = O.HostKV(hm, n_pages=n_pages, batch=B, max_pages_per_seq=12)
+    hm = O.HostModel(**mcfg, attn_scale=hd ** -0.5, max_pos=max(ctx) + 64, seed=1)
+    kv = O.HostKV(hm, n_pages=n_pages, batch=B, max_pages_per_seq=max(mp))
     kv.fill_random(rng, 1.0)
     perm = rng.permutation(n_pages)
-    kv.page_table[0, :10] = perm[:10]
-    kv.page_table[1, :4] = perm[10:14]
-    q_bits, q_f = to_act(rng.standard_normal((B * R, nh * hd)), afmt)
+    kv.page_table[0, :mp[0]] = perm[:mp[0]]
+    kv.page_table[1, :mp[1]] = perm[mp[0]:mp[0] + mp[1]]
+    q_bits, q_f = to_act(rng.standard_normal((B * R, nh * hd)) * 1.5, afmt)
     want = np.zeros_like(q_f)
     kv._mk()
-    for b in range(B):
-        qb = np.ascontiguousarray(q_f[b * R:(b + 1) * R])
-        ob = np.zeros_like(qb)
-        O.lib().orc_attention_paged(C.byref(hm.desc), C.byref(kv.desc), 1, b, ctx[b], R, qb.ctypes.data,
-                                    ob.ctypes.data)
-        want[b * R:(b + 1) * R] = ob
-    m = attn_model(nh, nkv, hd, afmt, 0.125, n_layers=2)
+    O.set_threads(16)
+    try:
+        for b in range(B):
+            qb = np.ascontiguousarray(q_f[b * R:(b + 1) * R])
+            ob = np.zeros_like(qb)
+            O.lib().orc_attention_paged(C.byref(hm.desc), C.byref(kv.desc), 1, b, ctx[b], R, qb.ctypes.data,
+                                        ob.ctypes.data)
+            want[b * R:(b + 1) * R] = ob
+    finally:
+        O.set_threads(1)
+    m = attn_model(nh, nkv, hd, afmt, hd ** -0.5, n_layers=2)
     got = run_attn(dev, m, kv.pool, kv.page_table, ctx, R, q_bits, layer=1)
     got_f = from_act(got, afmt)
     if afmt == H.A_F32:
         np.testing.assert_allclose(got_f, want, rtol=2e-5, atol=2e-5)
     else:
+        # within one storage ulp of the oracle's rounded output
         want_r = to_act(want, afmt)[1]
-        ulp = 2e-3 if afmt == H.A_F16 else 1.6e-2
-        np.testing.assert_allclose(got_f, want_r, rtol=ulp, atol=ulp * 0.1)
-    # row j of a 5-row call equals a 1-row call at position ctx+j, bit for bit
+        ulp = 2.0 ** -10 if afmt == H.A_F16 else 2.0 ** -7
+        assert (np.abs(got_f - want_r) <= ulp * np.abs(want_r) + 1e-6).all()
+        say("storage roundings that differ from the oracle:", int((got_f != want_r).sum()), "of", got_f.size)
+    # row j of an R-row call equals a 1-row call at position ctx+j, bit for bit
     for j in range(R):
         one = run_attn(dev, m, kv.pool, kv.page_table[:1], [ctx[0] + j], 1, q_bits[j:j + 1], layer=1)
         assert np.array_equal(one[0], got[j])
@@ -576,3 +596,33 @@ def test_rollback_bit_exact(dev):
     assert np.array_equal(dev.download(fr, np.int32, (3, 8)), want_freed)
     assert np.array_equal(dkv.get_page_table(), kv.page_table)
     assert np.array_equal(dkv.get_pool(), kv.pool)
+
+
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("wfmt", [H.W_I8PC, H.W_I4G128], ids=["i8pc", "i4g128"])
+def test_device_quantisers_match_oracle(dev, wfmt):
+    """The device quantisers that build every synthetic model (opure_quantize_*)
+    produce the oracle quantisers' bits (oracle.quant_i8pc / quant_i4g128):
+    same int8 / packed uint4 codes, same fp16 / bf16 scales and zero points."""
+    rng = np.random.default_rng(17 + wfmt)
+    out, inn = 96, 4096
+    w = (rng.standard_normal((out, inn)) * 0.02).astype(np.float32)
+    w[3] = 0.0                                      # an all-zero row (scale from the 1e-8 floor)
+    w[5, :128] = 0.01                               # a constant group
+    w[7] *= 40.0                                    # a wide row
+    wb = dev.upload(w)
+    want = O.quant_i8pc(w) if wfmt == H.W_I8PC else O.quant_i4g128(w)
+    if wfmt == H.W_I8PC:
+        q, s = dev.alloc(out * inn), dev.alloc(out * 2)
+        H.check(H.lib().opure_quantize_i8pc(dev.h, int(wb), out, inn, int(q), int(s)))
+        dev.sync()
+        assert np.array_equal(dev.download(q, np.int8, (out, inn)), want["w"])
+        assert np.array_equal(dev.download(s, np.uint16, (out,)), want["scale"])
+    else:
+        G = inn // 128
+        q, s, z = dev.alloc(out * inn // 2), dev.alloc(out * G * 2), dev.alloc(out * G * 2)
+        H.check(H.lib().opure_quantize_i4g128(dev.h, int(wb), out, inn, int(q), int(s), int(z)))
+        dev.sync()
+        assert np.array_equal(dev.download(q, np.uint8, (out, inn // 2)), want["w"])
+        assert np.array_equal(dev.download(s, np.uint16, (out, G)), want["scale"])
+        assert np.array_equal(dev.download(z, np.uint16, (out, G)), want["zero"])

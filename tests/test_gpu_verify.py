@@ -3,8 +3,8 @@
 - logits within max_abs 1e-4 (fp32 path) or 2e-2 (fp16/bf16 paths);
 - the K/V rows the step appends agree with the oracle's;
 - the in-step acceptance equals the oracle's acceptance applied to the same
-  GPU logits, bit for bit, and equals the oracle's own decision wherever the
-  oracle's top-1/top-2 gap exceeds the logit tolerance;
+  GPU logits, bit for bit, and equals the oracle's own decision (the token
+  seeds give every row a top-1/top-2 gap above twice the logit bar);
 - a K+1-row step equals K+1 single-row steps bit for bit (so greedy
   speculative decoding reproduces greedy decoding exactly on the GPU);
 - a captured hipGraph replays to the eager result;
@@ -25,6 +25,10 @@ pytestmark = pytest.mark.gpu
 FMTS = [(O.W_F32, O.A_F32, 1e-4), (O.W_I8PC, O.A_F16, 2e-2), (O.W_I4G128, O.A_F16, 2e-2),
         (O.W_I4G128, O.A_BF16, 2e-2)]
 FMT_IDS = ["f32", "i8-f16", "i4-f16", "i4-bf16"]
+# token seeds whose oracle logits have every row's top-1/top-2 gap above twice
+# the logit bar, so the GPU's greedy decisions must equal the oracle's
+# (found by searching seeds on the oracle alone)
+TOKEN_SEED = {"f32": 3, "i8-f16": 3, "i4-f16": 11, "i4-bf16": 11}
 
 
 @pytest.fixture(scope="module")
@@ -72,7 +76,7 @@ def test_verify_step_matches_oracle(dev, fmt):
     B, R = 2, 5
     kv = random_cache(m, B, 320, 48, seed=7)
     seq_len = np.array([251, 96], np.int32)
-    rng = np.random.default_rng(3)
+    rng = np.random.default_rng(TOKEN_SEED[FMT_IDS[FMTS.index(fmt)]])
     tokens = rng.integers(0, m.cfg["vocab"], size=(B, R)).astype(np.int32)
     dm, dkv = device_model(dev, m), device_kv(dev, m, kv)
     run = VerifyRunner(dev, dm, dkv, B, R, max_ctx=320)
@@ -100,10 +104,10 @@ def test_verify_step_matches_oracle(dev, fmt):
     out, acc = run.get_accept()
     w_out, w_acc = O.accept_greedy(got, tokens[:, 1:])
     assert np.array_equal(out, w_out) and np.array_equal(acc, w_acc)
-    # and == the oracle's own decision wherever its top-1/top-2 gap exceeds the tolerance
+    # and == the oracle's own decision (every row's gap clears twice the bar)
     o_out, o_acc = O.accept_greedy(want, tokens[:, 1:])
-    if np.all(top2_gap(want) > tol):
-        assert np.array_equal(out, o_out) and np.array_equal(acc, o_acc)
+    assert top2_gap(want).min() > 2 * tol
+    assert np.array_equal(out, o_out) and np.array_equal(acc, o_acc)
     say("accepted", acc, "oracle", o_acc)
     assert acc[0] == R - 1
 
@@ -181,19 +185,6 @@ def test_verify_with_rollback_matches_oracle(dev):
     assert diff[keep].max() <= 2e-2
 
 
-def logit_tolerance(want, afmt):
-    """max_abs bar on logits: 1e-4 for fp32 activations, 2e-2 for fp16; for bf16
-    activations the larger of 2e-2 and one bf16 ulp of the largest logit, since a
-    bf16 model rounds its activations to 8 significant bits at every stage and
-    the two sides' rounding decisions diverge through that chain."""
-    if afmt == O.A_F32:
-        return 1e-4
-    if afmt == O.A_F16:
-        return 2e-2
-    top = float(np.abs(want).max())
-    return max(2e-2, 2.0 ** (np.floor(np.log2(top)) - 7))
-
-
 def _full_width(wfmt, afmt, shape, n_layers, vocab, seed, attn_scale):
     h, nh, nkv, hd, ff = shape
     return O.HostModel(n_layers=n_layers, hidden=h, n_heads=nh, n_kv_heads=nkv, head_dim=hd, ffn=ff, vocab=vocab,
@@ -202,19 +193,22 @@ def _full_width(wfmt, afmt, shape, n_layers, vocab, seed, attn_scale):
 
 
 # attn_scale 1.0 is the reference's literal (unscaled) attention; 1/sqrt(hd) the
-# Llama-3 value used for the Llama-shaped configurations
+# Llama-3 value used for the Llama-shaped configurations.  The 8B-shape bf16
+# case runs one layer: the depth at which the 2e-2 logit bar holds end to end
+# for a bf16 model (tests/test_gpu_c4_depth.py holds all 32 layers to it one
+# layer at a time).  Token seeds give every row a top-2 gap above twice the bar.
 @pytest.mark.parametrize("cfg", [
-    ("c3-1b-int8-2layers-unscaled", O.W_I8PC, O.A_F16, (2048, 32, 8, 64, 8192), 128256, 2048, 6, 1.0),
-    ("c3-1b-int8-2layers", O.W_I8PC, O.A_F16, (2048, 32, 8, 64, 8192), 128256, 2048, 6, 0.125),
-    ("c4-8b-int4-2layers", O.W_I4G128, O.A_BF16, (4096, 32, 8, 128, 14336), 16384, 8192, 8, 128 ** -0.5),
+    ("c3-1b-int8-2layers-unscaled", O.W_I8PC, O.A_F16, (2048, 32, 8, 64, 8192), 128256, 2048, 6, 1.0, 2, 7),
+    ("c3-1b-int8-2layers", O.W_I8PC, O.A_F16, (2048, 32, 8, 64, 8192), 128256, 2048, 6, 0.125, 2, 1),
+    ("c4-8b-int4-1layer", O.W_I4G128, O.A_BF16, (4096, 32, 8, 128, 14336), 16384, 8192, 8, 128 ** -0.5, 1, 2),
 ], ids=lambda c: c[0] if isinstance(c, tuple) else str(c))
-def test_full_width_two_layers(dev, cfg):
-    name, wfmt, afmt, shape, vocab, ctx, R, scale = cfg
+def test_full_width(dev, cfg):
+    name, wfmt, afmt, shape, vocab, ctx, R, scale, n_layers, token_seed = cfg
     say("full width", name)
-    m = _full_width(wfmt, afmt, shape, 2, vocab, seed=101, attn_scale=scale)
+    m = _full_width(wfmt, afmt, shape, n_layers, vocab, seed=101, attn_scale=scale)
     kv = random_cache(m, 1, ctx + R, (ctx + R + 15) // 16, seed=5)
     seq_len = np.array([ctx], np.int32)
-    tokens = np.random.default_rng(1).integers(0, vocab, size=(1, R)).astype(np.int32)
+    tokens = np.random.default_rng(token_seed).integers(0, vocab, size=(1, R)).astype(np.int32)
     dm, dkv = device_model(dev, m), device_kv(dev, m, kv)
     run = VerifyRunner(dev, dm, dkv, 1, R, ctx + R)
     O.set_threads(16)
@@ -223,10 +217,6 @@ def test_full_width_two_layers(dev, cfg):
         kv_o.pool[...] = kv.pool
         kv_o.page_table[...] = kv.page_table
         tokens = self_drafts(m, kv_o, kv.pool, tokens, seq_len)   # the oracle's greedy continuation
-    finally:
-        O.set_threads(1)
-    O.set_threads(16)
-    try:
         want = O.verify_forward(m, kv_o, tokens, seq_len)
     finally:
         O.set_threads(1)
@@ -235,16 +225,16 @@ def test_full_width_two_layers(dev, cfg):
     got = run.get_logits()
     err = np.abs(got - want).max()
     gap = top2_gap(want).min()
-    tol = logit_tolerance(want, afmt)
-    say(name, "max_abs", err, "tolerance", tol, "min top2 gap", gap)
+    tol = 2e-2
+    say(name, "max_abs", err, "min top2 gap", gap)
     assert err <= tol
+    assert gap > 2 * tol
     out, acc = run.get_accept()
     w_out, w_acc = O.accept_greedy(got, tokens[:, 1:])
     assert np.array_equal(out, w_out) and np.array_equal(acc, w_acc)
-    if gap > tol:
-        o_out, o_acc = O.accept_greedy(want, tokens[:, 1:])
-        assert np.array_equal(out, o_out) and np.array_equal(acc, o_acc)
-        assert acc[0] == R - 1
+    o_out, o_acc = O.accept_greedy(want, tokens[:, 1:])
+    assert np.array_equal(out, o_out) and np.array_equal(acc, o_acc)
+    assert acc[0] == R - 1
 
 
 def test_c1_shape_speculative_equals_greedy(dev):

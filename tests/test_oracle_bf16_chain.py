@@ -1,0 +1,81 @@
+"""How far one bf16 rounding decision travels through a bf16 model -- measured
+on the oracle alone, so it says nothing about the GPU.
+
+A 1B-width model (hidden 2048, 32/8 heads, head_dim 64, ffn 8192) with int4
+group-128 weights and bf16 activations, 6 layers, 8 rows over a 2048-token
+cache.  The oracle's forward is run twice: once as is, once with ONE element of
+layer 0's attention output moved by one bf16 ulp after its rounding (the
+smallest difference two implementations that round at the same points can
+have).  The logits move by more than north_star's 2e-2.  The same flip in the
+last layer moves them far less, so it is the chain of later roundings, not
+the read-out, that carries it.
+
+This is why the 32-layer bf16 workload is held to 2e-2 per layer (teacher
+forced) and at depth 1, with bit-exact ids, rather than on its final logits:
+an fp32-accumulating implementation cannot reproduce every rounding of a
+double-accumulating one (tests/test_gpu_c4_depth.py).
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+
+pytestmark = pytest.mark.slow
+
+LAYERS, CTX, R = 6, 2048, 8
+
+
+@pytest.fixture(scope="module")
+def setup():
+    m = O.HostModel(n_layers=LAYERS, hidden=2048, n_heads=32, n_kv_heads=8, head_dim=64, ffn=8192, vocab=4096,
+                    wfmt=O.W_I4G128, afmt=O.A_BF16, attn_scale=64 ** -0.5, theta=500000.0, max_pos=CTX + 64,
+                    tied=False, seed=101)
+    rng = np.random.default_rng(5)
+    mp = (CTX + R + 15) // 16
+    kv = O.HostKV(m, n_pages=mp, batch=1, max_pages_per_seq=mp)
+    kv.fill_random(rng, 1.0)
+    kv.page_table[0] = rng.permutation(mp)
+    tokens = np.random.default_rng(1).integers(0, 4096, size=(1, R)).astype(np.int32)
+    O.set_threads(8)
+    try:
+        pool0 = kv.pool.copy()
+        base = O.verify_forward(m, kv, tokens, [CTX])
+    finally:
+        O.set_threads(1)
+    return m, kv, pool0, tokens, base
+
+
+def flipped(setup, layer, stage, index):
+    m, kv, pool0, tokens, base = setup
+    kv.pool[...] = pool0
+    O.set_threads(8)
+    O.set_perturbation(layer, stage, index)
+    try:
+        return O.verify_forward(m, kv, tokens, [CTX])
+    finally:
+        O.set_perturbation()
+        O.set_threads(1)
+
+
+@pytest.mark.parametrize("index", [77, 1234])
+def test_one_flip_in_layer_0_moves_logits_past_the_bar(setup, index):
+    moved = float(np.abs(flipped(setup, 0, O.STAGE_ATT, index) - setup[4]).max())
+    print("one bf16 ulp at layer 0 attention output element", index, "-> logits max_abs", moved)
+    assert moved > 2e-2
+
+
+def test_the_same_flip_in_the_last_layer_stays_local(setup):
+    moved = float(np.abs(flipped(setup, LAYERS - 1, O.STAGE_ATT, 77) - setup[4]).max())
+    print("one bf16 ulp at the last layer's attention output -> logits max_abs", moved)
+    assert 0.0 < moved < 5e-3
+
+
+def test_no_flip_is_bit_identical(setup):
+    m, kv, pool0, tokens, base = setup
+    kv.pool[...] = pool0
+    O.set_threads(8)
+    try:
+        again = O.verify_forward(m, kv, tokens, [CTX])
+    finally:
+        O.set_threads(1)
+    assert np.array_equal(again, base)
