@@ -249,6 +249,19 @@ typedef struct opure_accept_args {
 int opure_accept_greedy(opure_dev* dev, const opure_accept_args* a);
 int opure_accept_rejection(opure_dev* dev, const opure_accept_args* a);
 
+/* The same rejection sampling as opure_accept_rejection, for callers that
+ * cannot allocate device memory (code under hipGraph capture, serving loops,
+ * harnesses that forbid hipMalloc); it has no counterpart in the reference.
+ * Its scratch is a device array of OPURE_NOALLOC_SCRATCH_BYTES built into the
+ * library (one per GPU, held until the process ends); the call never
+ * allocates or frees.  A shape needs batch * (2k + 1) * 16, batch *
+ * ceil(vocab / 4096) * 16 and batch * vocab * 4 bytes of it (each rounded up
+ * to 256); one that does not fit returns OPURE_E_CAPACITY (at vocab 128256,
+ * up to 65 sequences fit).  Every call on one GPU shares that GPU's array, so calls
+ * that overlap on one GPU (streams of two opure_dev handles) race. */
+#define OPURE_NOALLOC_SCRATCH_BYTES (32ull << 20)
+int opure_accept_rejection_noalloc(opure_dev* dev, const opure_accept_args* a);
+
 /* sample one id per row from softmax(logits/temperature) (Philox stream
  * `stream`, counter (pos[r], seq[r])): drafting at temperature. */
 typedef struct opure_sample_args {

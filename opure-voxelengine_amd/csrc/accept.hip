@@ -979,6 +979,32 @@ int rollback_validate(const opure_rollback_args* a)
 
 }  // namespace opure_hip
 
+// Device scratch of opure_accept_rejection_noalloc: one copy per GPU, held for
+// the life of the process.  Host code never passes this name to a kernel (on
+// the host it is only a stand-in for the symbol); it uses the device address
+// that hipGetSymbolAddress returns, looked up once per device.
+static __device__ __align__(256) uint8_t scratch[OPURE_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr uint64_t NOALLOC_SCRATCH_BYTES = OPURE_NOALLOC_SCRATCH_BYTES;
+
+int noalloc_scratch(opure_dev* dev, void** out)
+{
+    if (!dev->noalloc_scratch)
+    {
+        OPURE_HIP_TRY(hipSetDevice(dev->ordinal));
+        void* ptr = nullptr;
+        OPURE_HIP_TRY(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+        OPURE_REQUIRE(ptr, OPURE_E_HIP, "opure_accept_rejection_noalloc: no device address for the scratch array");
+        dev->noalloc_scratch = ptr;
+    }
+    *out = dev->noalloc_scratch;
+    return OPURE_OK;
+}
+
+}  // namespace
+
 using namespace opure_hip;
 
 extern "C" {
@@ -1001,6 +1027,23 @@ int opure_accept_rejection(opure_dev* dev, const opure_accept_args* a)
     rc = ensure_workspace(dev, accept_ws_bytes(a->batch, a->k, a->vocab, OPURE_ACCEPT_REJECTION));
     if (rc) return rc;
     return accept_rejection_launch(dev, a, dev->ws, nullptr, nullptr);
+}
+
+int opure_accept_rejection_noalloc(opure_dev* dev, const opure_accept_args* a)
+{
+    OPURE_REQUIRE(dev, OPURE_E_INVALID, "opure_accept_rejection_noalloc: null device");
+    int rc = accept_validate(a, true);
+    if (rc) return rc;
+    const uint64_t need = accept_ws_bytes(a->batch, a->k, a->vocab, OPURE_ACCEPT_REJECTION);
+    OPURE_REQUIRE(need <= NOALLOC_SCRATCH_BYTES, OPURE_E_CAPACITY,
+                  "opure_accept_rejection_noalloc: batch %u x vocab %u needs %llu bytes of scratch, beyond the "
+                  "%llu-byte device array",
+                  a->batch, a->vocab, static_cast<unsigned long long>(need),
+                  static_cast<unsigned long long>(NOALLOC_SCRATCH_BYTES));
+    void* ws = nullptr;
+    if ((rc = noalloc_scratch(dev, &ws))) return rc;
+    // every scratch word the kernels read was written earlier in the same call
+    return accept_rejection_launch(dev, a, ws, nullptr, nullptr);
 }
 
 int opure_sample_rows(opure_dev* dev, const opure_sample_args* a)

@@ -26,6 +26,8 @@ struct opure_dev {
     // statistics, activations of a verify step).
     void*       ws = nullptr;
     uint64_t    ws_bytes = 0;
+    // device address of opure_accept_rejection_noalloc's scratch array (looked up once)
+    void*       noalloc_scratch = nullptr;
     // stage timing of eager verify steps: event pairs and the stage of each pair
     bool                   prof_on = false;
     std::vector<hipEvent_t> prof_ev;

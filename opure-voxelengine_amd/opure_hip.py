@@ -141,6 +141,7 @@ def _declare(L):
         "opure_attn_decode_paged": ([vp, C.POINTER(AttnArgs)], i),
         "opure_accept_greedy": ([vp, C.POINTER(AcceptArgs)], i),
         "opure_accept_rejection": ([vp, C.POINTER(AcceptArgs)], i),
+        "opure_accept_rejection_noalloc": ([vp, C.POINTER(AcceptArgs)], i),
         "opure_sample_rows": ([vp, C.POINTER(SampleArgs)], i),
         "opure_philox_uniform": ([vp, u64, vp, vp, u32, u32, vp], i),
         "opure_kv_rollback": ([vp, C.POINTER(RollbackArgs)], i),
