@@ -14,6 +14,14 @@
  *   - One stream per device.  Calls on one device are not thread-safe; the
  *     caller serialises them (the reference's server does, Opure_Server.cpp:21-25).
  *   - Kernel entry points enqueue work and return; opure_stream_sync waits.
+ *     Conditions only a kernel can see are reported at the next
+ *     opure_stream_sync or opure_buf_download of that device, which then
+ *     return a code instead of OPURE_OK (the outputs of the work before it
+ *     are invalid): a token id outside the vocabulary (OPURE_E_INVALID; its
+ *     row reads NaN), a row position seq_len + j at or past max_ctx or with no
+ *     page in the page table (OPURE_E_CAPACITY; its K/V are not written and
+ *     its attention is clamped), a bounded wait between waves that gave up
+ *     (OPURE_E_DEVICE).
  *     Uploads and downloads are synchronous, like UploadToBuffer /
  *     ReadbackFromBuffer (Opure_Dx12.h:230-244).
  *
@@ -51,6 +59,7 @@ extern "C" {
 #define OPURE_E_OOM          -4   /* device allocation failed */
 #define OPURE_E_UNSUPPORTED  -5   /* weight/activation combination not built */
 #define OPURE_E_CAPACITY     -6   /* rows > OPURE_MAX_ROWS, ctx past capacity, pages missing */
+#define OPURE_E_DEVICE       -7   /* a kernel reported that its outputs are invalid (see below) */
 
 #define OPURE_MAX_ROWS       16   /* rows of one sequence's verify step (K+1); GEMV rows scored by the K+1-row kernel */
 #define OPURE_MAX_BATCH_ROWS 256  /* rows of one verify step or GEMV (batch * (K+1)); above OPURE_MAX_ROWS the
@@ -295,7 +304,7 @@ typedef struct opure_rollback_args {
     const int32_t*     accepted;
     int32_t*           new_seq_len;
     int32_t*           freed;        /* [batch][freed_stride] or NULL */
-    uint32_t           freed_stride;
+    uint32_t           freed_stride; /* >= ceil(k / OPURE_PAGE_SIZE), the most pages one rollback releases */
     int32_t*           n_freed;      /* [batch] or NULL */
     uint32_t           poison;
     uint32_t           poison_bits;  /* element bits in the model's afmt */
@@ -389,6 +398,11 @@ int opure_profile_read(opure_dev* dev, uint32_t counts[OPURE_STAGE_COUNT], doubl
  *      [hidden/16][rows], feeding the fused RMSNorm), q (afmt), att (afmt),
  *      h (afmt). */
 int opure_debug_workspace(opure_dev* dev, void** ptr, uint64_t* bytes);
+/* Sleeps a bounded wait between the waves of a workgroup takes before it gives
+ * up (default 4M).  A test hook: 0 makes any wait that is not already met give
+ * up at once, so the failure report can be checked while every wave still
+ * runs to its end. */
+int opure_debug_set_wait_limit(opure_dev* dev, uint32_t sleeps);
 int opure_debug_verify_offsets(const opure_model* model, uint32_t batch, uint32_t rows, uint32_t max_ctx,
                                uint64_t offsets[5]);
 

@@ -973,7 +973,12 @@ int rollback_validate(const opure_rollback_args* a)
     OPURE_REQUIRE(a && a->model && a->kv && a->kv->pool && a->kv->page_table && a->seq_len && a->accepted &&
                       a->new_seq_len, OPURE_E_INVALID, "rollback: null argument");
     OPURE_REQUIRE(a->batch >= 1 && a->kv->page_size == OPURE_PAGE_SIZE, OPURE_E_INVALID, "rollback: bad shape");
-    OPURE_REQUIRE(!a->freed || a->freed_stride >= 1, OPURE_E_INVALID, "rollback: freed_stride must be >= 1");
+    // the K positions past seq_len hold at most ceil(K / page) page starts: the
+    // most pages one rollback can release into a sequence's freed row
+    const uint32_t most = a->k == 0u ? 1u : (a->k + OPURE_PAGE_SIZE - 1u) / OPURE_PAGE_SIZE;
+    OPURE_REQUIRE(!a->freed || a->freed_stride >= most, OPURE_E_INVALID,
+                  "rollback: freed_stride %u < %u, the most pages a rollback of %u drafts can release",
+                  a->freed_stride, most, a->k);
     return OPURE_OK;
 }
 

@@ -47,6 +47,7 @@ struct AttnParams {
     uint32_t n_heads, n_kv, hd, rows, n_pages, max_pages, layer, nch, chunk, afmt;
     float scale;
     uint32_t qoff;       // matrix-core path: first query row of this launch
+    uint32_t* err;       // opure_dev::err: a row past max_ctx sets ERR_POSITION
 };
 
 // zero the elements n.. of a 16-byte piece of consecutive tokens (stale slots
@@ -607,7 +608,13 @@ __global__ __launch_bounds__(64) void k_attn_combine(AttnParams p)
     const uint32_t group = p.n_heads / p.n_kv, kh = head / group, qi = j * group + (head - kh * group);
     const uint32_t Gq = group * R, hd = p.hd, lane = threadIdx.x;
     uint32_t last = (static_cast<uint32_t>(p.seq_len[b]) + j) / p.chunk;
-    if (last >= p.nch) last = p.nch - 1u;          // length beyond the launch bound: clamp, never overrun
+    if (last >= p.nch)
+    {
+        // a position beyond the launch's max_ctx: clamped (never read past the
+        // partials) and reported, since the row's output is then wrong
+        last = p.nch - 1u;
+        if (lane == 0u && p.err) p.err[ERR_POSITION] = 1u;
+    }
     const uint64_t base = (static_cast<uint64_t>(b) * p.n_kv + kh) * p.nch;
     auto acc_at = [&](uint32_t c, int i) {
         const uint32_t d = min(lane + 64u * i, hd - 1u);
@@ -779,6 +786,7 @@ int attn_launch(opure_dev* dev, const opure_model* m, const opure_kv* kv, uint32
     p.nch = (max_ctx + p.chunk - 1u) / p.chunk;
     p.afmt = m->afmt;
     p.scale = m->attn_scale;
+    p.err = dev->err;
     const uint64_t q_elems = static_cast<uint64_t>(batch) * p.n_kv * p.nch * Gq;
     p.part_acc = part;
     p.part_ml = part + align_up(q_elems * p.hd * 4u, 256) / 4u;

@@ -165,9 +165,12 @@ Plan make_plan(const opure_dev* dev, uint32_t wfmt, uint32_t xfmt, uint32_t out,
     const uint32_t stride = in * EB + 16u;
     const uint32_t xbytes = static_cast<uint32_t>(opure_hip::align_up(static_cast<uint64_t>(M) * stride, 16));
     // 1024 tiles and more: waves own whole tiles, if X, the group sums and a
-    // 1 KB slot per wave fit in LDS
+    // 1 KB slot per wave fit in LDS -- judged at OPURE_MAX_ROWS rows, so that the
+    // recipe (and with it every row's summation order) is the same for any M
     const uint32_t wpt_xs = wfmt == OPURE_W_I4G128 ? (in / 128u) * 64u : 0u;
-    const bool wpt = pl.tiles >= 1024u && xbytes + wpt_xs + R_WPT.nw * 1024u <= 159u * 1024u;
+    const uint32_t xbytes_max =
+        static_cast<uint32_t>(opure_hip::align_up(static_cast<uint64_t>(OPURE_MAX_ROWS) * stride, 16));
+    const bool wpt = pl.tiles >= 1024u && xbytes_max + wpt_xs + R_WPT.nw * 1024u <= 159u * 1024u;
     pl.r = wpt ? R_WPT
                : (pl.tiles >= 1024u ? R_WIDE
                                     : (pl.tiles >= 320u ? R_WIDE16 : (pl.tiles > 192u && in >= 8192u ? R_MID : R_NARROW)));
@@ -364,6 +367,8 @@ static int gemv_launch_wide(opure_dev* dev, const GemvCall& c)
     kp.y = c.y;
     kp.yfmt = c.yfmt;
     kp.ss_out = c.ss_out;
+    kp.err = dev->err;
+    kp.wait_limit = dev->wait_limit;
     kp.x_stride = w.x_stride;
     kp.off_xsum = w.off_xsum;
     kp.qkv = c.qkv;
@@ -414,6 +419,8 @@ int gemv_launch(opure_dev* dev, const GemvCall& c)
     kp.ss_in = c.ss_in;
     kp.ss_tiles = c.ss_tiles;
     kp.ss_out = c.ss_out;
+    kp.err = dev->err;
+    kp.wait_limit = dev->wait_limit;
     kp.x_stride = pl.x_stride;
     kp.off_xsum = pl.off_xsum;
     kp.off_red = pl.off_red;

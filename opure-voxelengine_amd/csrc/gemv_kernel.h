@@ -68,6 +68,8 @@ struct KParams {
     uint32_t off_xsum;         // STAGED uint4: LDS offset of the group sums [M][in/128]
     uint32_t off_red;          // LDS offset of the wave reduction [NW][T][64] f4
     uint32_t off_ring, ring;   // loader-wave kernel: LDS offset of the slot rings, slots per compute wave
+    uint32_t* err;             // opure_dev::err (ERR_WAIT: a bounded wait gave up)
+    uint32_t wait_limit;       // loader-wave kernel: sleeps before a wait gives up
     opure_hip::QkvEpilogue qkv;
     opure_hip::LogitsEpilogue lg;
 };
@@ -454,7 +456,11 @@ __device__ __forceinline__ void epilogue(const KParams& p, uint32_t tile, uint32
         const opure_hip::QkvEpilogue& e = p.qkv;
         const uint32_t b = m / e.rows_per_seq, j = m - b * e.rows_per_seq;
         const uint32_t pos = static_cast<uint32_t>(e.seq_len[b]) + j;
-        if (pos >= e.rope_max_pos || pos / OPURE_PAGE_SIZE >= e.max_pages) return;   // past the tables: drop
+        if (pos >= e.rope_max_pos || pos / OPURE_PAGE_SIZE >= e.max_pages)   // past the tables: dropped, reported
+        {
+            if (e.err) e.err[ERR_POSITION] = 1u;
+            return;
+        }
         const uint32_t o0 = 16u * tile + 4u * g4;   // even; o0..o0+3 lie in one head
         const uint32_t hd = e.head_dim, half = hd >> 1;
         if (o0 < e.qdim + e.kvdim)
@@ -482,7 +488,11 @@ __device__ __forceinline__ void epilogue(const KParams& p, uint32_t tile, uint32
         const uint32_t ok = o0 - e.qdim - kvsel * e.kvdim;
         const uint32_t kh = ok / hd, d0 = ok - kh * hd;
         const int32_t page = e.page_table[static_cast<uint64_t>(b) * e.max_pages + pos / OPURE_PAGE_SIZE];
-        if (page < 0 || static_cast<uint32_t>(page) >= e.n_pages) return;
+        if (page < 0 || static_cast<uint32_t>(page) >= e.n_pages)   // no page for the row: dropped, reported
+        {
+            if (e.err) e.err[ERR_POSITION] = 1u;
+            return;
+        }
 #pragma unroll
         for (int i = 0; i < 4; ++i)
             store_act_rt(e.kv_pool,
@@ -571,7 +581,11 @@ __device__ __forceinline__ void epilogue_elem(const KParams& p, uint32_t tile, u
         if (!live) return;
         const uint32_t b = m / e.rows_per_seq, j = m - b * e.rows_per_seq;
         const uint32_t pos = static_cast<uint32_t>(e.seq_len[b]) + j;
-        if (pos >= e.rope_max_pos || pos / OPURE_PAGE_SIZE >= e.max_pages) return;   // past the tables: drop
+        if (pos >= e.rope_max_pos || pos / OPURE_PAGE_SIZE >= e.max_pages)   // past the tables: dropped, reported
+        {
+            if (e.err) e.err[ERR_POSITION] = 1u;
+            return;
+        }
         const uint32_t hd = e.head_dim, half = hd >> 1;
         const bool rot = o < e.qdim + e.kvdim;
         if (rot)
@@ -593,7 +607,11 @@ __device__ __forceinline__ void epilogue_elem(const KParams& p, uint32_t tile, u
         const uint32_t ok = o - e.qdim - kvsel * e.kvdim;
         const uint32_t kh = ok / hd, dk = ok - kh * hd;
         const int32_t page = e.page_table[static_cast<uint64_t>(b) * e.max_pages + pos / OPURE_PAGE_SIZE];
-        if (page < 0 || static_cast<uint32_t>(page) >= e.n_pages) return;
+        if (page < 0 || static_cast<uint32_t>(page) >= e.n_pages)   // no page for the row: dropped, reported
+        {
+            if (e.err) e.err[ERR_POSITION] = 1u;
+            return;
+        }
         store_act_rt(e.kv_pool,
                      kv_elem(e.layer, e.n_pages, static_cast<uint32_t>(page), kvsel, e.n_kv_heads, kh, hd,
                              pos % OPURE_PAGE_SIZE, dk),
@@ -1245,10 +1263,11 @@ __global__ __launch_bounds__(512) void k_gemv_wpt(KParams p)
 // vmcnt) and of its steps consumed (written once the compute wave holds the
 // slot's words in registers).  Every wait is a bounded sleep loop; a wave
 // that gives up stops waiting (its results are then wrong) but still reaches
-// every barrier, so the grid always drains.
+// every barrier, so the grid always drains, and reports it (ERR_WAIT), so the
+// host's next sync returns an error instead of the wrong results.  The number
+// of sleeps before giving up is KParams::wait_limit (opure_dev::wait_limit).
 constexpr int PC_NC = 8, PC_NL = 4;                   // compute and loader waves
 constexpr uint32_t PC_SB = 4;                          // blocks a slot
-constexpr uint32_t PC_SPIN = 1u << 22;                 // sleeps before a wait gives up
 
 template <int WF>
 constexpr uint32_t pc_slot_bytes() { return PC_SB * 1024u + (WF == OPURE_W_I4G128 ? 256u : 0u); }
@@ -1258,13 +1277,13 @@ constexpr uint32_t pc_slot_bytes() { return PC_SB * 1024u + (WF == OPURE_W_I4G12
 typedef __attribute__((address_space(3))) volatile uint32_t lds_u32;
 
 // wait until *f >= want (a count another wave raises); false if given up
-__device__ __forceinline__ bool pc_wait(const lds_u32* f, uint32_t want, bool& bail)
+__device__ __forceinline__ bool pc_wait(const lds_u32* f, uint32_t want, uint32_t limit, bool& bail)
 {
     if (bail) return false;
     // every lane reads the same count: take lane 0's, so the loop is scalar
     for (uint32_t n = 0; static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(*f))) < want; ++n)
     {
-        if (n >= PC_SPIN)
+        if (n >= limit)
         {
             bail = true;
             return false;
@@ -1345,12 +1364,12 @@ __global__ __launch_bounds__((PC_NC + PC_NL) * 64) void k_gemv_pc(KParams p)
             const bool i0 = s < S0, i1 = s < S1;
             if (i0)
             {
-                if (s >= R) pc_wait(consumed + c0, s - R + 1u, bail);
+                if (s >= R) pc_wait(consumed + c0, s - R + 1u, p.wait_limit, bail);
                 issue(c0, s);
             }
             if (i1)
             {
-                if (s >= R) pc_wait(consumed + c1, s - R + 1u, bail);
+                if (s >= R) pc_wait(consumed + c1, s - R + 1u, p.wait_limit, bail);
                 issue(c1, s);
             }
             const uint32_t n_cur = (i0 ? 1u : 0u) + (i1 ? 1u : 0u);
@@ -1373,6 +1392,7 @@ __global__ __launch_bounds__((PC_NC + PC_NL) * 64) void k_gemv_pc(KParams p)
         {
             filled[c0] = S0;
             filled[c1] = S1;
+            if (bail && p.err) p.err[ERR_WAIT] = 1u;
         }
         if (!joined) join();
         if constexpr (EPI == opure_hip::EPI_LOGITS)
@@ -1421,7 +1441,7 @@ __global__ __launch_bounds__((PC_NC + PC_NL) * 64) void k_gemv_pc(KParams p)
     for (uint32_t s = 0; s < S; ++s)
     {
         const uint32_t k = s / npass, ps = s - k * npass;
-        pc_wait(filled + wave, s + 1u, bail);
+        pc_wait(filled + wave, s + 1u, p.wait_limit, bail);
         const uint8_t* base = lds + p.off_ring + (wave * R + s % R) * SLOT;
         u4_t w[SB];
         uint32_t sz[SB];
@@ -1496,6 +1516,7 @@ __global__ __launch_bounds__((PC_NC + PC_NL) * 64) void k_gemv_pc(KParams p)
             acc = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
         }
     }
+    if (bail && lane == 0u && p.err) p.err[ERR_WAIT] = 1u;
 
     if constexpr (EPI == opure_hip::EPI_LOGITS)
     {

@@ -28,6 +28,18 @@ struct opure_dev {
     uint64_t    ws_bytes = 0;
     // device address of opure_accept_rejection_noalloc's scratch array (looked up once)
     void*       noalloc_scratch = nullptr;
+    // Conditions a kernel found that make its outputs invalid, one word each
+    // (ERR_* below), in pinned host memory: a kernel sets a word with an
+    // ordinary store, the host reads and clears it after the stream is idle
+    // (opure_stream_sync, opure_buf_download), so nothing is added to a step
+    // or a captured graph.
+    uint32_t*   err = nullptr;
+    // sleeps before a bounded inter-wave wait gives up (opure_debug_set_wait_limit)
+    uint32_t    wait_limit = 1u << 22;
+    // captured graphs still alive: a workspace they point into is kept, not
+    // freed, when a larger call replaces it
+    uint32_t    live_graphs = 0;
+    std::vector<void*> retired_ws;
     // stage timing of eager verify steps: event pairs and the stage of each pair
     bool                   prof_on = false;
     std::vector<hipEvent_t> prof_ev;
@@ -38,6 +50,15 @@ struct opure_dev {
 struct opure_graph {
     hipGraph_t     graph = nullptr;
     hipGraphExec_t exec = nullptr;
+    opure_dev*     dev = nullptr;
+};
+
+// words of opure_dev::err
+enum : uint32_t {
+    ERR_WAIT = 0,       // a bounded wait between waves gave up (loader-wave GEMV)
+    ERR_TOKEN = 1,      // a token id outside the vocabulary (its embedding row is NaN)
+    ERR_POSITION = 2,   // a row's position past max_ctx or the page table
+    ERR_WORDS = 4
 };
 
 namespace opure_hip {
@@ -46,6 +67,8 @@ int set_error(int code, const char* fmt, ...);
 int hip_fail(hipError_t e, const char* what);
 const char* afmt_name(uint32_t afmt);
 int  ensure_workspace(opure_dev* dev, uint64_t bytes);
+// the error words a kernel reported since the last check, as an OPURE_E_* code (cleared)
+int  check_device_errors(opure_dev* dev);
 // bracket one stage's launches with events (no-op unless profiling, or while capturing)
 int  prof_begin(opure_dev* dev, uint32_t stage);
 int  prof_end(opure_dev* dev);
@@ -88,6 +111,7 @@ struct QkvEpilogue {
     void* kv_pool = nullptr;
     const int32_t* page_table = nullptr;
     uint32_t max_pages = 0, n_pages = 0, layer = 0;
+    uint32_t* err = nullptr;     // opure_dev::err: a row past the tables sets ERR_POSITION
 };
 
 struct LogitsEpilogue {

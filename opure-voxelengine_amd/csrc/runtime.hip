@@ -54,12 +54,34 @@ int ensure_workspace(opure_dev* dev, uint64_t bytes)
                       "opure_verify_reserve before capturing", (unsigned long long)dev->ws_bytes,
                       (unsigned long long)bytes);
         OPURE_HIP_TRY(hipStreamSynchronize(dev->stream));
-        if (dev->ws) OPURE_HIP_TRY(hipFree(dev->ws));
+        // a captured graph may still point into the old workspace: keep it until
+        // the last graph is destroyed
+        if (dev->ws && dev->live_graphs) dev->retired_ws.push_back(dev->ws);
+        else if (dev->ws) OPURE_HIP_TRY(hipFree(dev->ws));
         dev->ws = nullptr;
         dev->ws_bytes = 0;
         OPURE_HIP_TRY(hipMalloc(&dev->ws, bytes));
         dev->ws_bytes = bytes;
     }
+    return OPURE_OK;
+}
+
+int check_device_errors(opure_dev* dev)
+{
+    if (!dev->err) return OPURE_OK;
+    uint32_t w[ERR_WORDS];
+    for (uint32_t i = 0; i < ERR_WORDS; ++i) { w[i] = dev->err[i]; dev->err[i] = 0u; }
+    if (w[ERR_WAIT])
+        return set_error(OPURE_E_DEVICE, "a bounded wait between waves gave up in a GEMV (after %u sleeps): that "
+                         "launch's outputs are invalid%s%s", dev->wait_limit,
+                         w[ERR_TOKEN] ? "; a token id was outside the vocabulary" : "",
+                         w[ERR_POSITION] ? "; a position reached past max_ctx or the page table" : "");
+    if (w[ERR_TOKEN])
+        return set_error(OPURE_E_INVALID, "a token id outside the vocabulary reached the embedding: its row's outputs "
+                         "are NaN%s", w[ERR_POSITION] ? "; a position reached past max_ctx or the page table" : "");
+    if (w[ERR_POSITION])
+        return set_error(OPURE_E_CAPACITY, "a row's position (seq_len + row) reached past max_ctx or the page table: "
+                         "its attention and K/V append are invalid");
     return OPURE_OK;
 }
 
@@ -119,11 +141,18 @@ int opure_dev_create(int ordinal, opure_dev** out)
     hipError_t e = hipStreamCreateWithFlags(&d->stream, hipStreamNonBlocking);
     if (e == hipSuccess) e = hipEventCreate(&d->ev_begin);
     if (e == hipSuccess) e = hipEventCreate(&d->ev_end);
+    if (e == hipSuccess) e = hipHostMalloc(reinterpret_cast<void**>(&d->err), ERR_WORDS * sizeof(uint32_t),
+                                           hipHostMallocCoherent);
     if (e != hipSuccess)
     {
+        if (d->err) hipHostFree(d->err);
+        if (d->ev_end) hipEventDestroy(d->ev_end);
+        if (d->ev_begin) hipEventDestroy(d->ev_begin);
+        if (d->stream) hipStreamDestroy(d->stream);
         delete d;
         return hip_fail(e, "opure_dev_create");
     }
+    for (uint32_t i = 0; i < ERR_WORDS; ++i) d->err[i] = 0u;
     *out = d;
     return OPURE_OK;
 }
@@ -134,6 +163,8 @@ int opure_dev_destroy(opure_dev* dev)
     hipSetDevice(dev->ordinal);
     hipStreamSynchronize(dev->stream);
     if (dev->ws) hipFree(dev->ws);
+    for (void* p : dev->retired_ws) hipFree(p);
+    if (dev->err) hipHostFree(dev->err);
     for (hipEvent_t e : dev->prof_ev) hipEventDestroy(e);
     if (dev->ev_begin) hipEventDestroy(dev->ev_begin);
     if (dev->ev_end) hipEventDestroy(dev->ev_end);
@@ -195,7 +226,7 @@ int opure_buf_download(opure_dev* dev, void* dst, const void* dptr, uint64_t off
     OPURE_HIP_TRY(hipMemcpyAsync(dst, static_cast<const char*>(dptr) + offset, bytes, hipMemcpyDeviceToHost,
                                  dev->stream));
     OPURE_HIP_TRY(hipStreamSynchronize(dev->stream));
-    return OPURE_OK;
+    return check_device_errors(dev);
 }
 
 int opure_buf_fill_u32(opure_dev* dev, void* dptr, uint32_t value, uint64_t count)
@@ -229,7 +260,7 @@ int opure_stream_sync(opure_dev* dev)
 {
     OPURE_REQUIRE(dev, OPURE_E_INVALID, "opure_stream_sync: null device");
     OPURE_HIP_TRY(hipStreamSynchronize(dev->stream));
-    return OPURE_OK;
+    return check_device_errors(dev);
 }
 
 int opure_graph_begin(opure_dev* dev)
@@ -254,6 +285,8 @@ int opure_graph_end(opure_dev* dev, opure_graph** out)
         delete g;
         return hip_fail(e, "opure_graph_end");
     }
+    g->dev = dev;
+    ++dev->live_graphs;
     *out = g;
     return OPURE_OK;
 }
@@ -270,10 +303,25 @@ int opure_graph_destroy(opure_graph* g)
     if (!g) return OPURE_OK;
     if (g->exec) hipGraphExecDestroy(g->exec);
     if (g->graph) hipGraphDestroy(g->graph);
+    opure_dev* dev = g->dev;
     delete g;
+    if (dev && dev->live_graphs && --dev->live_graphs == 0)
+    {
+        // no graph can point into a retired workspace any more
+        hipStreamSynchronize(dev->stream);
+        for (void* p : dev->retired_ws) hipFree(p);
+        dev->retired_ws.clear();
+    }
     return OPURE_OK;
 }
 
+
+int opure_debug_set_wait_limit(opure_dev* dev, uint32_t sleeps)
+{
+    OPURE_REQUIRE(dev, OPURE_E_INVALID, "opure_debug_set_wait_limit: null device");
+    dev->wait_limit = sleeps;
+    return OPURE_OK;
+}
 
 int opure_profile_enable(opure_dev* dev, int on)
 {

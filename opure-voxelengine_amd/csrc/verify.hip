@@ -37,13 +37,15 @@ namespace {
 // 16-column tile: its columns are one 16-byte piece (int8), half a piece
 // (uint4) or four pieces (fp32) of the tiled layout, loaded at once.
 __global__ __launch_bounds__(256) void k_embed(const int32_t* tokens, opure_linear E, uint32_t wfmt, uint32_t h,
-                                               uint32_t vocab, uint32_t M, uint32_t KB, float* x, float* ss)
+                                               uint32_t vocab, uint32_t M, uint32_t KB, float* x, float* ss,
+                                               uint32_t* err)
 {
     typedef uint32_t u4v __attribute__((ext_vector_type(4)));
     const uint32_t r = blockIdx.x;
     const int32_t t = tokens[r];
     float* xr = x + static_cast<uint64_t>(r) * h;
     const bool bad = t < 0 || static_cast<uint32_t>(t) >= vocab;
+    if (bad && threadIdx.x == 0 && err) err[ERR_TOKEN] = 1u;   // reported at the host's next sync
     const uint32_t nblk = h / KB;
     const uint32_t row = bad ? 0u : static_cast<uint32_t>(t), tile = row >> 4, rr = row & 15u;
     const uint8_t* w = static_cast<const uint8_t*>(E.w);
@@ -241,6 +243,7 @@ static int layer_launch(opure_dev* dev, const opure_model* m, const opure_kv* kv
     c.qkv.max_pages = kv->max_pages_per_seq;
     c.qkv.n_pages = kv->n_pages;
     c.qkv.layer = L;
+    c.qkv.err = dev->err;
     if ((rc = gemv_validate(c)) || (rc = prof_begin(dev, OPURE_STAGE_QKV)) || (rc = gemv_launch(dev, c)) ||
         (rc = prof_end(dev)))
         return rc;
@@ -390,7 +393,7 @@ int opure_verify_step(opure_dev* dev, const opure_verify_args* a)
 
     if ((rc = prof_begin(dev, OPURE_STAGE_EMBED))) return rc;
     hipLaunchKernelGGL(k_embed, dim3(MR), dim3(256), 0, dev->stream, a->tokens, m->embed, m->wfmt, m->hidden, m->vocab,
-                       MR, tiled_block_k(m->wfmt), x, ss);
+                       MR, tiled_block_k(m->wfmt), x, ss, dev->err);
     OPURE_LAUNCH_CHECK("k_embed");
     if ((rc = prof_end(dev))) return rc;
 

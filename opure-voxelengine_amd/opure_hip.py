@@ -15,7 +15,7 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "lib", "libopure_hip.so")
 
-OK, E_INVALID, E_NODEVICE, E_HIP, E_OOM, E_UNSUPPORTED, E_CAPACITY = 0, -1, -2, -3, -4, -5, -6
+OK, E_INVALID, E_NODEVICE, E_HIP, E_OOM, E_UNSUPPORTED, E_CAPACITY, E_DEVICE = 0, -1, -2, -3, -4, -5, -6, -7
 MAX_ROWS, PAGE_SIZE = 16, 16
 W_F32, W_I8PC, W_I4G128 = 0, 1, 2
 A_F32, A_F16, A_BF16 = 0, 1, 2
@@ -149,6 +149,7 @@ def _declare(L):
         "opure_verify_step": ([vp, C.POINTER(VerifyArgs)], i),
         "opure_verify_layer": ([vp, C.POINTER(VerifyLayerArgs)], i),
         "opure_debug_workspace": ([vp, C.POINTER(vp), C.POINTER(u64)], i),
+        "opure_debug_set_wait_limit": ([vp, u32], i),
         "opure_debug_verify_offsets": ([C.POINTER(Model), u32, u32, u32, C.POINTER(u64)], i),
         "opure_tiled_bytes": ([u32, u32, u32, C.POINTER(u64), C.POINTER(u64)], i),
         "opure_tile_linear": ([vp, u32, u32, C.POINTER(Linear), vp, vp, C.POINTER(Linear)], i),

@@ -171,7 +171,8 @@ GEMV_CASES = [
     (H.W_I4G128, H.A_F16, 1024, 4096),
     (H.W_I4G128, H.A_BF16, 6144, 4096),
     (H.W_I4G128, H.A_BF16, 4096, 14336),
-    (H.W_I8PC, H.A_F16, 128256, 2048),       # the 1B LM head over a batch of 32 x 7 rows
+    (H.W_I8PC, H.A_F16, 128256, 2048),       # the 1B LM head
+    (H.W_I8PC, H.A_F16, 16384, 8192),        # 1024 tiles whose X fits in LDS below 16 rows only
 ]
 
 
