@@ -153,33 +153,11 @@ def time_graph(dev, step, tokens, ctx, warmup, steps, eager=False):
                 out_tokens=out[0].tolist())
 
 
-def stage_bytes(cfg, stage, M, ctx):
-    """Algorithmic HBM bytes of one launch of a verify-step stage for M rows
-    over a ctx-token cache: the weights once, activations in and out once."""
-    h, nh, nkv, hd, ff, V = (cfg[k] for k in ("hidden", "n_heads", "n_kv_heads", "head_dim", "ffn", "vocab"))
-    w = cfg["wfmt"]
-    eb = 4 if cfg["afmt"] == H.A_F32 else 2
-    qkv_out = (nh + 2 * nkv) * hd
-    if stage == "embed":
-        return M * synth.linear_bytes(w, 1, h) + M * h * 4
-    if stage == "qkv":      # fp32 residual + gain in, q out, K/V rows appended
-        return synth.linear_bytes(w, qkv_out, h) + M * h * 4 + h * 4 + M * qkv_out * eb
-    if stage == "attention":
-        return 2 * nkv * hd * eb * (ctx + M) + 2 * M * nh * hd * eb
-    if stage == "o_proj":   # attention output in, residual read and written
-        return synth.linear_bytes(w, h, nh * hd) + M * nh * hd * eb + 2 * M * h * 4
-    if stage == "gate_up":  # residual + gain in, SwiGLU output out
-        return synth.linear_bytes(w, 2 * ff, h) + M * h * 4 + h * 4 + M * ff * eb
-    if stage == "down":
-        return synth.linear_bytes(w, h, ff) + M * ff * eb + 2 * M * h * 4
-    if stage == "lm_head":  # fp32 logits out
-        return synth.linear_bytes(w, V, h) + M * h * 4 + h * 4 + M * V * 4
-    return 0
-
-
 def time_stages(dev, step, tokens, ctx, steps):
-    """Per-stage timing of eager verify steps: each stage's launches are
-    bracketed by HIP events on the library's stream (opure_profile_*)."""
+    """Per-stage timing of eager verify steps (opure_profile_*): every kernel of
+    a stage is launched with start/stop events stamped by its own dispatch, so
+    a stage's time is its kernels' execution time -- what a profiler's kernel
+    trace reports -- without the gaps between launches."""
     step.dev.write(step.tokens, tokens)
     step.dev.write(step.seq_len, np.array([ctx], np.int32))
     a = step.args(H.ACCEPT_GREEDY)
@@ -197,7 +175,7 @@ def time_stages(dev, step, tokens, ctx, steps):
         if n == 0:
             continue
         avg_us = ms * 1e3 / n
-        by = stage_bytes(cfg, st, step.B * step.R, ctx)
+        by = synth.stage_bytes(cfg, st, step.B * step.R, ctx)
         out[st] = dict(launches_per_step=n / steps, avg_us=avg_us, us_per_step=ms * 1e3 / steps,
                        bytes_per_launch=by, gbs=by / (avg_us * 1e-6) / 1e9 if by else None)
     return out
@@ -623,14 +601,19 @@ def kernel_of(config, stage):
 
 
 def traffic_of(config, stage):
-    """Measured HBM bytes per launch of a stage's kernel (profiles/traffic.json:
-    FETCH_SIZE + WRITE_SIZE from rocprofv3 --pmc runs, each scaled by the copy
-    calibration), or None when not measured."""
+    """HBM bytes per launch of a stage's kernel measured by the hardware counters
+    (profiles/traffic.json: FETCH_SIZE + WRITE_SIZE of rocprofv3 --pmc runs of
+    this benchmark, each scaled by the copy calibration) with the run they came
+    from, or None when not measured.  Counters cannot be read inside this
+    process, so the figure comes from that separate profiled run."""
     path = os.path.join(ROOT, "profiles", "traffic.json")
     if not os.path.exists(path):
         return None
-    t = json.load(open(path)).get(config, {}).get(stage)
-    return int(t["bytes"]) if t else None
+    doc = json.load(open(path))
+    t = doc.get(config, {}).get(stage)
+    if not t:
+        return None
+    return {"bytes": int(t["bytes"]), "source": t.get("source", doc.get("source"))}
 
 
 def main():
@@ -712,12 +695,20 @@ def main():
                    "wall_ms_per_step": round(res["wall_ms_per_step"], 4)},
     }
     if kern:
+        tr = traffic_of(args.config, kern["stage"])
         line["roofline"] = {"bound": "hbm", "achieved": round(kern["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                             "frac": round(kern["gbs"] / HBM_PEAK_GBS, 4),
-                            "traffic": traffic_of(args.config, kern["stage"]),
+                            "traffic": tr["bytes"] if tr else None,
                             "kernel": f"{kernel_of(args.config, kern['stage'])} ({kern['stage']} stage of the verify step)",
-                            "bytes_per_launch": kern["bytes_per_launch"], "avg_us": round(kern["avg_us"], 2)}
-        line["stages_us_per_step"] = {st: round(d["us_per_step"], 1) for st, d in stages.items()}
+                            "bytes_per_launch": kern["bytes_per_launch"], "avg_us": round(kern["avg_us"], 2),
+                            "timing": "kernel execution time from start/stop events stamped by each dispatch "
+                                      "(hipExtLaunchKernelGGL) over 10 eager steps, averaged per launch",
+                            "traffic_source": tr["source"] if tr else None}
+        line["stages"] = {st: {"launches_per_step": round(d["launches_per_step"], 2), "us": round(d["avg_us"], 2),
+                               "us_per_step": round(d["us_per_step"], 1),
+                               "GBps": round(d["gbs"], 1) if d["gbs"] else None,
+                               "frac": round(d["gbs"] / HBM_PEAK_GBS, 4) if d["gbs"] else None}
+                          for st, d in stages.items()}
     if cpu:
         line["cpu_baseline"] = rounded(cpu)
         line["parity"] = parity

@@ -130,9 +130,10 @@ int opure_rope_table(double theta, uint32_t head_dim, uint32_t max_pos, uint32_t
  *   (t * (in_bytes/64) + b) * 1024, and lane l = 16*g + r of a wave reads its
  *   16 bytes [16g, 16g+16) of row r's block at offset 16*l -- one contiguous
  *   1 KB load per wave, already in MFMA operand order.
- *   int8 is stored offset-binary (q ^ 0x80); uint4 nibbles are reordered
- *   inside each 32-bit word so that byte masks and permutes yield element
- *   pairs in k order; scales follow the tiles: int8 fp16[tile][16], uint4
+ *   int8 is stored offset-binary (q ^ 0x80); uint4 elements e0..e7 of a
+ *   32-bit word sit at nibbles 0,4,1,5,2,6,3,7 and the word is rotated left by
+ *   3 bits, so that byte masks (one of them after a 4-bit rotation) and byte
+ *   permutes yield element pairs in k order; scales follow the tiles: int8 fp16[tile][16], uint4
  *   uint32 (bf16 scale | bf16 zero << 16)[tile][in/128][16]; zero is unused.
  * TILED_SWIGLU additionally interleaves the rows of a [gate; up] linear
  * (out = 2F): tile t holds gate rows 8t..8t+7 and up rows 8t..8t+7 alternately,

@@ -885,7 +885,7 @@ int greedy_from_partials(opure_dev* dev, const float* am_val, const int32_t* am_
     g.accepted = accepted;
     g.rollback = rb ? 1u : 0u;
     if (rb) g.rb = rollback_params(rb);
-    hipLaunchKernelGGL(k_accept_greedy, dim3(batch), dim3(GNT), 0, dev->stream, g);
+    OPURE_LAUNCH(dev, k_accept_greedy, dim3(batch), dim3(GNT), 0, g);
     OPURE_LAUNCH_CHECK("k_accept_greedy");
     return OPURE_OK;
 }
@@ -901,7 +901,7 @@ int argmax_partials_launch(opure_dev* dev, const float* logits, uint32_t rows, u
     ap.parts = argmax_parts(V);
     ap.am_val = am_val;
     ap.am_idx = am_idx;
-    hipLaunchKernelGGL(k_argmax_partial, dim3(ap.parts, rows), dim3(NT), 0, dev->stream, ap);
+    OPURE_LAUNCH(dev, k_argmax_partial, dim3(ap.parts, rows), dim3(NT), 0, ap);
     OPURE_LAUNCH_CHECK("k_argmax_partial");
     return OPURE_OK;
 }
@@ -946,16 +946,16 @@ int accept_rejection_launch(opure_dev* dev, const opure_accept_args* a, void* ws
     const bool aligned = ((reinterpret_cast<uintptr_t>(a->target_logits) | reinterpret_cast<uintptr_t>(a->draft_logits)) & 15u) == 0;
     const bool reg = V % 4u == 0 && V <= 4u * RNT * RVEC && aligned, div = r.tau != 1.0f;
     const dim3 rows(2u * K + 1u, B), slices(r.slices, B);
-    if (reg && div) hipLaunchKernelGGL((k_rej_rowstat<true, true>), rows, dim3(RNT), 0, dev->stream, r);
-    if (reg && !div) hipLaunchKernelGGL((k_rej_rowstat<true, false>), rows, dim3(RNT), 0, dev->stream, r);
-    if (!reg && div) hipLaunchKernelGGL((k_rej_rowstat<false, true>), rows, dim3(RNT), 0, dev->stream, r);
-    if (!reg && !div) hipLaunchKernelGGL((k_rej_rowstat<false, false>), rows, dim3(RNT), 0, dev->stream, r);
+    if (reg && div) OPURE_LAUNCH(dev, (k_rej_rowstat<true, true>), rows, dim3(RNT), 0, r);
+    if (reg && !div) OPURE_LAUNCH(dev, (k_rej_rowstat<true, false>), rows, dim3(RNT), 0, r);
+    if (!reg && div) OPURE_LAUNCH(dev, (k_rej_rowstat<false, true>), rows, dim3(RNT), 0, r);
+    if (!reg && !div) OPURE_LAUNCH(dev, (k_rej_rowstat<false, false>), rows, dim3(RNT), 0, r);
     OPURE_LAUNCH_CHECK("k_rej_rowstat");
-    if (div) hipLaunchKernelGGL(k_rej_slice<true>, slices, dim3(NT), 0, dev->stream, r);
-    else hipLaunchKernelGGL(k_rej_slice<false>, slices, dim3(NT), 0, dev->stream, r);
+    if (div) OPURE_LAUNCH(dev, k_rej_slice<true>, slices, dim3(NT), 0, r);
+    else OPURE_LAUNCH(dev, k_rej_slice<false>, slices, dim3(NT), 0, r);
     OPURE_LAUNCH_CHECK("k_rej_slice");
-    if (div) hipLaunchKernelGGL(k_rej_draw<true>, slices, dim3(NT), 0, dev->stream, r);
-    else hipLaunchKernelGGL(k_rej_draw<false>, slices, dim3(NT), 0, dev->stream, r);
+    if (div) OPURE_LAUNCH(dev, k_rej_draw<true>, slices, dim3(NT), 0, r);
+    else OPURE_LAUNCH(dev, k_rej_draw<false>, slices, dim3(NT), 0, r);
     OPURE_LAUNCH_CHECK("k_rej_draw");
     return OPURE_OK;
 }
@@ -963,7 +963,7 @@ int accept_rejection_launch(opure_dev* dev, const opure_accept_args* a, void* ws
 int rollback_launch(opure_dev* dev, const opure_rollback_args* a)
 {
     const RollbackParams r = rollback_params(a);
-    hipLaunchKernelGGL(k_rollback, dim3(a->batch), dim3(NT), 0, dev->stream, r);
+    OPURE_LAUNCH(dev, k_rollback, dim3(a->batch), dim3(NT), 0, r);
     OPURE_LAUNCH_CHECK("k_rollback");
     return OPURE_OK;
 }
@@ -1057,7 +1057,7 @@ int opure_sample_rows(opure_dev* dev, const opure_sample_args* a)
                   "opure_sample_rows: bad argument");
     OPURE_REQUIRE(a->temperature > 0.0f, OPURE_E_INVALID, "opure_sample_rows: temperature must be > 0");
     SampleParams s{a->logits, a->vocab, a->temperature, a->seed, a->pos, a->seq, a->stream, a->out};
-    hipLaunchKernelGGL(k_sample, dim3(a->rows), dim3(NT), 0, dev->stream, s);
+    OPURE_LAUNCH(dev, k_sample, dim3(a->rows), dim3(NT), 0, s);
     OPURE_LAUNCH_CHECK("k_sample");
     return OPURE_OK;
 }
@@ -1067,7 +1067,7 @@ int opure_philox_uniform(opure_dev* dev, uint64_t seed, const uint32_t* pos, con
 {
     OPURE_REQUIRE(dev && pos && seq && out, OPURE_E_INVALID, "opure_philox_uniform: null argument");
     if (!n) return OPURE_OK;
-    hipLaunchKernelGGL(k_philox, dim3((n + 255u) / 256u), dim3(256), 0, dev->stream, seed, pos, seq, stream, n, out);
+    OPURE_LAUNCH(dev, k_philox, dim3((n + 255u) / 256u), dim3(256), 0, seed, pos, seq, stream, n, out);
     OPURE_LAUNCH_CHECK("k_philox");
     return OPURE_OK;
 }

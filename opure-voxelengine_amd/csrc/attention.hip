@@ -680,7 +680,7 @@ int launch_mfma(opure_dev* dev, dim3 grid, const AttnParams& p)
                                           hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
         configured = true;
     }
-    hipLaunchKernelGGL((k_attn_mfma<HD, AF, NT, KK, NWV>), grid, dim3(NWV * 64), lds, dev->stream, p);
+    OPURE_LAUNCH(dev, (k_attn_mfma<HD, AF, NT, KK, NWV>), grid, dim3(NWV * 64), lds, p);
     OPURE_LAUNCH_CHECK("k_attn_mfma");
     return OPURE_OK;
 }
@@ -695,7 +695,7 @@ int launch_fast(opure_dev* dev, dim3 grid, uint32_t lds, const AttnParams& p)
                                           hipFuncAttributeMaxDynamicSharedMemorySize, 64 * 1024));
         configured = true;
     }
-    hipLaunchKernelGGL((k_attn_chunk<HD, AF>), grid, dim3(256), lds, dev->stream, p);
+    OPURE_LAUNCH(dev, (k_attn_chunk<HD, AF>), grid, dim3(256), lds, p);
     OPURE_LAUNCH_CHECK("k_attn_chunk");
     return OPURE_OK;
 }
@@ -836,16 +836,16 @@ int attn_launch(opure_dev* dev, const opure_model* m, const opure_kv* kv, uint32
                                               hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
             configured = true;
         }
-        hipLaunchKernelGGL(k_attn_chunk_generic, grid, dim3(256), lds, dev->stream, p);
+        OPURE_LAUNCH(dev, k_attn_chunk_generic, grid, dim3(256), lds, p);
         OPURE_LAUNCH_CHECK("k_attn_chunk_generic");
     }
     const dim3 cgrid(p.n_heads, batch * rows);
     switch ((p.hd + 63u) / 64u)
     {
-    case 1: hipLaunchKernelGGL(k_attn_combine<1>, cgrid, dim3(64), 0, dev->stream, p); break;
-    case 2: hipLaunchKernelGGL(k_attn_combine<2>, cgrid, dim3(64), 0, dev->stream, p); break;
-    case 3: hipLaunchKernelGGL(k_attn_combine<3>, cgrid, dim3(64), 0, dev->stream, p); break;
-    default: hipLaunchKernelGGL(k_attn_combine<4>, cgrid, dim3(64), 0, dev->stream, p); break;
+    case 1: OPURE_LAUNCH(dev, k_attn_combine<1>, cgrid, dim3(64), 0, p); break;
+    case 2: OPURE_LAUNCH(dev, k_attn_combine<2>, cgrid, dim3(64), 0, p); break;
+    case 3: OPURE_LAUNCH(dev, k_attn_combine<3>, cgrid, dim3(64), 0, p); break;
+    default: OPURE_LAUNCH(dev, k_attn_combine<4>, cgrid, dim3(64), 0, p); break;
     }
     OPURE_LAUNCH_CHECK("k_attn_combine");
     return OPURE_OK;

@@ -191,16 +191,14 @@ __global__ __launch_bounds__(256) void k_gemm_wide(WParams wp)
                                 bacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, af[q]),
                                                                                __builtin_bit_cast(bf16x8_t, bx), bacc, 0, 0, 0);
                         }
-                        // acc += s * (bacc - (z + off) * xs), off = U4_BF16_OFFSET for bf16
+                        // acc += (s / MUL) * (bacc - (OFF + MUL z) * xs)   (see U4)
                         const float xs = xsum[m * wp.ckb + bb];
-                        const float xoff = AF == OPURE_A_BF16 ? __fmul_rn(xs, U4_BF16_OFFSET) : 0.0f;
 #pragma unroll
                         for (int i = 0; i < 4; ++i)
                         {
-                            const uint32_t szi = sz[i];
-                            const float sc = __uint_as_float(szi << 16), z = __uint_as_float(szi & 0xFFFF0000u);
-                            const float yv = __fmaf_rn(-z, xs, __fsub_rn(bacc[i], xoff));
-                            acc[t][j][i] = __fmaf_rn(sc, yv, acc[t][j][i]);
+                            float sc, zo;
+                            u4_group<AF>(sz[i], sc, zo);
+                            acc[t][j][i] = __fmaf_rn(sc, __fmaf_rn(-zo, xs, bacc[i]), acc[t][j][i]);
                         }
                     }
                 }
@@ -260,12 +258,12 @@ int launch_wide_epi(opure_dev* dev, const WParams& wp, uint32_t lds)
         configured = true;
     }
     const uint32_t groups = (wp.p.tiles + WIDE_TO - 1u) / WIDE_TO;
-    hipLaunchKernelGGL((k_gemm_wide<WF, AF, EPI>), dim3(groups, wp.splits), dim3(256), lds, dev->stream, wp);
+    OPURE_LAUNCH(dev, (k_gemm_wide<WF, AF, EPI>), dim3(groups, wp.splits), dim3(256), lds, wp);
     OPURE_LAUNCH_CHECK("k_gemm_wide");
     if (wp.splits > 1u)
     {
         const uint32_t n = wp.p.tiles * wp.mt;
-        hipLaunchKernelGGL((k_wide_reduce<WF, EPI>), dim3((n + 3u) / 4u), dim3(256), 0, dev->stream, wp);
+        OPURE_LAUNCH(dev, (k_wide_reduce<WF, EPI>), dim3((n + 3u) / 4u), dim3(256), 0, wp);
         OPURE_LAUNCH_CHECK("k_wide_reduce");
     }
     return OPURE_OK;

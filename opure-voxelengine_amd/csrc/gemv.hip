@@ -58,7 +58,8 @@ __global__ __launch_bounds__(256) void k_tile_w(const uint8_t* src, uint8_t* dst
     }
     else if (wfmt == OPURE_W_I4G128)
     {
-        // element 2i = high nibble of byte i -> element e at nibble {0,4,1,5,2,6,3,7}[e]
+        // element 2i = high nibble of byte i -> element e at nibble {0,4,1,5,2,6,3,7}[e],
+        // then the word rotated left by 3 bits (nibbles at bits 3..6 of a byte)
         constexpr uint32_t pos[8] = {0, 4, 1, 5, 2, 6, 3, 7};
 #pragma unroll
         for (int j = 0; j < 4; ++j)
@@ -72,7 +73,7 @@ __global__ __launch_bounds__(256) void k_tile_w(const uint8_t* src, uint8_t* dst
                 const uint32_t q = (e & 1u) ? (byte & 0x0Fu) : (byte >> 4);
                 o |= q << (4u * pos[e]);
             }
-            v[j] = o;
+            v[j] = (o << 3) | (o >> 29);
         }
     }
     *reinterpret_cast<u4_t*>(dst + (tb << 10) + (static_cast<uint64_t>(lane) << 4)) = v;
@@ -137,11 +138,11 @@ int rmsnorm_rows_launch(opure_dev* dev, const opure_gemv::KParams& kp, uint32_t 
 {
     const dim3 grid((kp.in / 8u + 255u) / 256u, M);
     if (afmt == OPURE_A_F32)
-        hipLaunchKernelGGL(k_rmsnorm_rows<OPURE_A_F32>, grid, dim3(256), 0, dev->stream, kp, xn);
+        OPURE_LAUNCH(dev, k_rmsnorm_rows<OPURE_A_F32>, grid, dim3(256), 0, kp, xn);
     else if (afmt == OPURE_A_F16)
-        hipLaunchKernelGGL(k_rmsnorm_rows<OPURE_A_F16>, grid, dim3(256), 0, dev->stream, kp, xn);
+        OPURE_LAUNCH(dev, k_rmsnorm_rows<OPURE_A_F16>, grid, dim3(256), 0, kp, xn);
     else
-        hipLaunchKernelGGL(k_rmsnorm_rows<OPURE_A_BF16>, grid, dim3(256), 0, dev->stream, kp, xn);
+        OPURE_LAUNCH(dev, k_rmsnorm_rows<OPURE_A_BF16>, grid, dim3(256), 0, kp, xn);
     OPURE_LAUNCH_CHECK("k_rmsnorm_rows");
     return OPURE_OK;
 }
@@ -509,14 +510,14 @@ int opure_tile_linear(opure_dev* dev, uint32_t wfmt, uint32_t layout, const opur
                   OPURE_E_INVALID, "opure_tile_linear: 16-byte aligned weights");
     const uint32_t nblk = src->in / kb_of(wfmt);
     const uint64_t pieces = static_cast<uint64_t>(src->out / 16u) * nblk * 64u;
-    hipLaunchKernelGGL(k_tile_w, dim3(static_cast<uint32_t>((pieces + 255u) / 256u)), dim3(256), 0, dev->stream,
+    OPURE_LAUNCH(dev, k_tile_w, dim3(static_cast<uint32_t>((pieces + 255u) / 256u)), dim3(256), 0,
                        static_cast<const uint8_t*>(src->w), static_cast<uint8_t*>(w_dst), wfmt, layout, src->out, nblk,
                        row_bytes(wfmt, src->in), pieces);
     OPURE_LAUNCH_CHECK("k_tile_w");
     if (wfmt != OPURE_W_F32)
     {
         const uint64_t n = wfmt == OPURE_W_I8PC ? src->out : static_cast<uint64_t>(src->out) * (src->in / 128u);
-        hipLaunchKernelGGL(k_tile_s, dim3(static_cast<uint32_t>((n + 255u) / 256u)), dim3(256), 0, dev->stream,
+        OPURE_LAUNCH(dev, k_tile_s, dim3(static_cast<uint32_t>((n + 255u) / 256u)), dim3(256), 0,
                            static_cast<const uint16_t*>(src->scale), static_cast<const uint16_t*>(src->zero), scale_dst,
                            wfmt, layout, src->out, src->in / 128u, n);
         OPURE_LAUNCH_CHECK("k_tile_s");

@@ -103,23 +103,31 @@ __device__ __forceinline__ void u8x4_to_f16(uint32_t u, uint32_t& lo, uint32_t& 
     hi = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, b) + bias);
 }
 
-// A tiled uint4 word holds elements e0..e7 at nibbles 0,4,1,5,2,6,3,7, so
-// the low nibbles of its bytes are (e0,e4,e1,e5) and the high nibbles
-// (e2,e6,e3,e7); byte permutes against MAGIC then give MAGIC|q pairs in k
-// order.  fp16: MAGIC 0x64 over the nibble (1024 + q), minus 1024 exactly.
-// bf16 has no packed subtract, so the offset stays in the operand and is taken
-// out with the zero point (U4_BF16_OFFSET * group sum of X); to keep that
-// cancellation small the nibble goes to the top of the 7-bit mantissa under
-// the exponent of 16: high byte 0x41, low byte 0x80 | q << 3, value 16 + q
-// (the smallest offset a 4-bit field below an implicit leading one allows;
-// 0x43|q = 128 + q cost about 3 more bits of every group sum).
-constexpr float U4_BF16_OFFSET = 16.0f;
+// A tiled uint4 word holds elements e0..e7 at nibbles 0,4,1,5,2,6,3,7 and is
+// stored rotated left by 3 bits (opure_tile_linear), so the low nibble of every
+// byte sits at bits 3..6 of that byte, and after a rotation right by 4 the high
+// nibble does: lo bytes are (e0,e4,e1,e5) << 3, hi bytes (e2,e6,e3,e7) << 3.
+// Byte permutes against MAGIC then give operand pairs in k order:
+//   fp16 0x64|q<<3 = 1024 + 8q, minus 1024 exactly: 8q;
+//   bf16 0x41|q<<3 = 8 + q/2 (bf16 has no packed subtract, so the 8 stays and
+//        is taken out with the zero point through the group sum of X; 8 on a
+//        step of 1/2 is the smallest offset a 4-bit field under the implicit
+//        leading one allows -- 128 + q, with the field at the bottom of the
+//        mantissa, cost about 3 more bits of every group sum).
+// So operand = U4<AF>::MUL * q + U4<AF>::OFF exactly, and a group's
+//   s * sum (q - z) x = (s / MUL) * (acc - (OFF + MUL z) * sum x)
+// with both factors exact (MUL a power of two).
+template <int AF> struct U4 {
+    static constexpr uint32_t MAGIC = AF == OPURE_A_F16 ? 0x64646464u : 0x41414141u;
+    static constexpr float MUL = AF == OPURE_A_F16 ? 8.0f : 0.5f;
+    static constexpr float OFF = AF == OPURE_A_F16 ? 0.0f : 8.0f;
+};
 template <int AF>
 __device__ __forceinline__ void u4x8_pairs(uint32_t d, uint32_t (&o)[4])
 {
-    constexpr uint32_t MAGIC = AF == OPURE_A_F16 ? 0x64646464u : 0x41414141u;
-    const uint32_t lo = AF == OPURE_A_F16 ? d & 0x0F0F0F0Fu : ((d << 3) & 0x78787878u) | 0x80808080u;
-    const uint32_t hi = AF == OPURE_A_F16 ? (d >> 4) & 0x0F0F0F0Fu : ((d >> 1) & 0x78787878u) | 0x80808080u;
+    constexpr uint32_t MAGIC = U4<AF>::MAGIC;
+    const uint32_t lo = d & 0x78787878u;
+    const uint32_t hi = __builtin_amdgcn_alignbit(d, d, 4) & 0x78787878u;
     o[0] = __builtin_amdgcn_perm(MAGIC, lo, 0x04020400u);   // e0 e1
     o[1] = __builtin_amdgcn_perm(MAGIC, hi, 0x04020400u);   // e2 e3
     o[2] = __builtin_amdgcn_perm(MAGIC, lo, 0x04030401u);   // e4 e5
@@ -130,6 +138,15 @@ __device__ __forceinline__ void u4x8_pairs(uint32_t d, uint32_t (&o)[4])
 #pragma unroll
         for (int j = 0; j < 4; ++j) o[j] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, o[j]) + bias);
     }
+}
+
+// a uint4 group's (scale, zero) word -> the factor and the offset the group
+// accumulator is corrected with (see U4)
+template <int AF>
+__device__ __forceinline__ void u4_group(uint32_t sz, float& sc, float& zo)
+{
+    sc = __fmul_rn(__uint_as_float(sz << 16), 1.0f / U4<AF>::MUL);
+    zo = __fmaf_rn(__uint_as_float(sz & 0xFFFF0000u), U4<AF>::MUL, U4<AF>::OFF);
 }
 
 // sum of 8 rounded activations (4 pairs): packed dot products with (1, 1)
@@ -866,7 +883,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemv(KParams p)
                 // one 128-k group per block.  The group sums of X rows 4*g4 + i
                 // come from the matrix core too (B = ones), then per tile a
                 // fresh accumulator of (MAGIC + q) * x and
-                //   acc += s * (bacc - (z + off) * xs),  off = U4_BF16_OFFSET for bf16
+                //   acc += (s / MUL) * (bacc - (OFF + MUL z) * xs)   (see U4)
                 f4_t xs = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
@@ -898,9 +915,8 @@ __global__ __launch_bounds__(NW * 64) void k_gemv(KParams p)
                                 as_bf8(xd[4 * j], xd[4 * j + 1], xd[4 * j + 2], xd[4 * j + 3]),
                                 as_bf8(a[0], a[1], a[2], a[3]), bacc, 0, 0, 0);
                     }
-                    const uint32_t sz = b.s[t][u];
-                    const float sc = __uint_as_float(sz << 16), z = __uint_as_float(sz & 0xFFFF0000u);
-                    const float zo = AF == OPURE_A_BF16 ? __fadd_rn(z, U4_BF16_OFFSET) : z;
+                    float sc, zo;
+                    u4_group<AF>(b.s[t][u], sc, zo);
 #pragma unroll
                     for (int i = 0; i < 4; ++i) acc[t][i] = __fmaf_rn(sc, __fmaf_rn(-zo, xs[i], bacc[i]), acc[t][i]);
                 }
@@ -1173,9 +1189,8 @@ __global__ __launch_bounds__(512) void k_gemv_wpt(KParams p)
                         bacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf8(xd[4 * j], xd[4 * j + 1], xd[4 * j + 2], xd[4 * j + 3]),
                                                                        as_bf8(a[0], a[1], a[2], a[3]), bacc, 0, 0, 0);
                 }
-                const uint32_t sz = b.s[u];
-                const float sc = __uint_as_float(sz << 16), z = __uint_as_float(sz & 0xFFFF0000u);
-                const float zo = AF == OPURE_A_BF16 ? __fadd_rn(z, U4_BF16_OFFSET) : z;
+                float sc, zo;
+                u4_group<AF>(b.s[u], sc, zo);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) acc[i] = __fmaf_rn(sc, __fmaf_rn(-zo, xs[i], bacc[i]), acc[i]);
             }
@@ -1490,8 +1505,8 @@ __global__ __launch_bounds__((PC_NC + PC_NL) * 64) void k_gemv_pc(KParams p)
                         bacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf8(xd[4 * j], xd[4 * j + 1], xd[4 * j + 2], xd[4 * j + 3]),
                                                                        as_bf8(a[0], a[1], a[2], a[3]), bacc, 0, 0, 0);
                 }
-                const float sc = __uint_as_float(sz[u] << 16), z = __uint_as_float(sz[u] & 0xFFFF0000u);
-                const float zo = AF == OPURE_A_BF16 ? __fadd_rn(z, U4_BF16_OFFSET) : z;
+                float sc, zo;
+                u4_group<AF>(sz[u], sc, zo);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) acc[i] = __fmaf_rn(sc, __fmaf_rn(-zo, xs[i], bacc[i]), acc[i]);
             }
@@ -1551,7 +1566,7 @@ int launch_pc(opure_dev* dev, const KParams& kp, uint32_t grid, uint32_t lds)
                                           hipFuncAttributeMaxDynamicSharedMemorySize, 159 * 1024));
         configured = true;
     }
-    hipLaunchKernelGGL((k_gemv_pc<WF, AF, EPI, NORM>), dim3(grid), dim3((PC_NC + PC_NL) * 64), lds, dev->stream, kp);
+    OPURE_LAUNCH(dev, (k_gemv_pc<WF, AF, EPI, NORM>), dim3(grid), dim3((PC_NC + PC_NL) * 64), lds, kp);
     OPURE_LAUNCH_CHECK("k_gemv_pc");
     return OPURE_OK;
 }
@@ -1570,7 +1585,7 @@ int launch_wpt(opure_dev* dev, const KParams& kp, uint32_t grid, uint32_t lds)
                                           hipFuncAttributeMaxDynamicSharedMemorySize, 159 * 1024));
         configured = true;
     }
-    hipLaunchKernelGGL((k_gemv_wpt<WF, AF, EPI, U, NORM, D, SPLIT>), dim3(grid), dim3(512), lds, dev->stream, kp);
+    OPURE_LAUNCH(dev, (k_gemv_wpt<WF, AF, EPI, U, NORM, D, SPLIT>), dim3(grid), dim3(512), lds, kp);
     OPURE_LAUNCH_CHECK("k_gemv_wpt");
     return OPURE_OK;
 }
@@ -1586,7 +1601,7 @@ int launch(opure_dev* dev, const KParams& kp, uint32_t grid, uint32_t lds)
                                           hipFuncAttributeMaxDynamicSharedMemorySize, 159 * 1024));
         configured = true;
     }
-    hipLaunchKernelGGL((k_gemv<WF, AF, EPI, NW, T, U, NORM, XM>), dim3(grid), dim3(NW * 64), lds, dev->stream, kp);
+    OPURE_LAUNCH(dev, (k_gemv<WF, AF, EPI, NW, T, U, NORM, XM>), dim3(grid), dim3(NW * 64), lds, kp);
     OPURE_LAUNCH_CHECK("k_gemv");
     return OPURE_OK;
 }

@@ -4,6 +4,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
 #include <stdint.h>
 
 #include <string>
@@ -40,11 +41,15 @@ struct opure_dev {
     // freed, when a larger call replaces it
     uint32_t    live_graphs = 0;
     std::vector<void*> retired_ws;
-    // stage timing of eager verify steps: event pairs and the stage of each pair
+    // stage timing of eager verify steps: every kernel launched inside an open
+    // stage gets a start/stop event pair of its own (kernel time, not launch gaps)
     bool                   prof_on = false;
-    std::vector<hipEvent_t> prof_ev;
-    std::vector<uint32_t>  prof_stage;
-    uint32_t               prof_used = 0;    // events recorded since the last read
+    bool                   prof_open = false;       // between prof_begin and prof_end
+    uint32_t               prof_cur = 0;            // the open stage
+    uint32_t               prof_count[OPURE_STAGE_COUNT] = {};   // stage instances since the last read
+    std::vector<hipEvent_t> prof_ev;                // pairs
+    std::vector<uint32_t>  prof_stage;              // stage of each pair
+    uint32_t               prof_used = 0;           // pairs recorded since the last read
 };
 
 struct opure_graph {
@@ -69,9 +74,12 @@ const char* afmt_name(uint32_t afmt);
 int  ensure_workspace(opure_dev* dev, uint64_t bytes);
 // the error words a kernel reported since the last check, as an OPURE_E_* code (cleared)
 int  check_device_errors(opure_dev* dev);
-// bracket one stage's launches with events (no-op unless profiling, or while capturing)
+// open / close a stage of an eager verify step (no-op unless profiling, or while capturing)
 int  prof_begin(opure_dev* dev, uint32_t stage);
 int  prof_end(opure_dev* dev);
+// a start/stop event pair for the next kernel of the open stage; false when
+// nothing is being timed
+bool prof_kernel_events(opure_dev* dev, hipEvent_t* start, hipEvent_t* stop);
 inline uint64_t align_up(uint64_t v, uint64_t a) { return (v + a - 1) / a * a; }
 inline uint32_t act_bytes(uint32_t afmt) { return afmt == OPURE_A_F32 ? 4u : 2u; }
 
@@ -84,6 +92,20 @@ inline uint32_t act_bytes(uint32_t afmt) { return afmt == OPURE_A_F32 ? 4u : 2u;
 #define OPURE_REQUIRE(cond, code, ...)                                       \
     do {                                                                     \
         if (!(cond)) return ::opure_hip::set_error((code), __VA_ARGS__);     \
+    } while (0)
+
+// Every kernel launch of the library, on the device's stream.  While a stage of
+// an eager verify step is profiled (opure_profile_enable), the extended launch
+// stamps start/stop events from the dispatch itself: the kernel's own
+// execution time, as a profiler's kernel trace reports it, without the gaps
+// between launches.
+#define OPURE_LAUNCH(dev, kernel, grid, block, lds, ...)                                              \
+    do {                                                                                              \
+        hipEvent_t _ks = nullptr, _ke = nullptr;                                                      \
+        if (::opure_hip::prof_kernel_events((dev), &_ks, &_ke))                                       \
+            hipExtLaunchKernelGGL(kernel, grid, block, lds, (dev)->stream, _ks, _ke, 0, __VA_ARGS__);  \
+        else                                                                                          \
+            hipLaunchKernelGGL(kernel, grid, block, lds, (dev)->stream, __VA_ARGS__);                 \
     } while (0)
 
 #define OPURE_LAUNCH_CHECK(what)                                             \

@@ -94,25 +94,34 @@ namespace opure_hip {
 
 int prof_begin(opure_dev* dev, uint32_t stage)
 {
-    if (!dev->prof_on || dev->capturing) return OPURE_OK;
-    while (dev->prof_ev.size() < dev->prof_used + 2u)
-    {
-        hipEvent_t e;
-        OPURE_HIP_TRY(hipEventCreate(&e));
-        dev->prof_ev.push_back(e);
-    }
-    if (dev->prof_stage.size() < dev->prof_ev.size() / 2u) dev->prof_stage.resize(dev->prof_ev.size() / 2u);
-    dev->prof_stage[dev->prof_used / 2u] = stage;
-    OPURE_HIP_TRY(hipEventRecord(dev->prof_ev[dev->prof_used], dev->stream));
+    if (!dev->prof_on || dev->capturing || stage >= OPURE_STAGE_COUNT) return OPURE_OK;
+    dev->prof_open = true;
+    dev->prof_cur = stage;
+    ++dev->prof_count[stage];
     return OPURE_OK;
 }
 
 int prof_end(opure_dev* dev)
 {
-    if (!dev->prof_on || dev->capturing) return OPURE_OK;
-    OPURE_HIP_TRY(hipEventRecord(dev->prof_ev[dev->prof_used + 1u], dev->stream));
-    dev->prof_used += 2u;
+    dev->prof_open = false;
     return OPURE_OK;
+}
+
+bool prof_kernel_events(opure_dev* dev, hipEvent_t* start, hipEvent_t* stop)
+{
+    if (!dev->prof_on || !dev->prof_open || dev->capturing) return false;
+    while (dev->prof_ev.size() < 2u * (dev->prof_used + 1u))
+    {
+        hipEvent_t e;
+        if (hipEventCreate(&e) != hipSuccess) return false;
+        dev->prof_ev.push_back(e);
+    }
+    if (dev->prof_stage.size() < dev->prof_used + 1u) dev->prof_stage.resize(dev->prof_used + 1u);
+    dev->prof_stage[dev->prof_used] = dev->prof_cur;
+    *start = dev->prof_ev[2u * dev->prof_used];
+    *stop = dev->prof_ev[2u * dev->prof_used + 1u];
+    ++dev->prof_used;
+    return true;
 }
 
 }  // namespace opure_hip
@@ -327,7 +336,9 @@ int opure_profile_enable(opure_dev* dev, int on)
 {
     OPURE_REQUIRE(dev, OPURE_E_INVALID, "opure_profile_enable: null device");
     dev->prof_on = on != 0;
+    dev->prof_open = false;
     dev->prof_used = 0;
+    for (uint32_t& c : dev->prof_count) c = 0u;
     return OPURE_OK;
 }
 
@@ -336,13 +347,16 @@ int opure_profile_read(opure_dev* dev, uint32_t counts[OPURE_STAGE_COUNT], doubl
     OPURE_REQUIRE(dev && counts && ms, OPURE_E_INVALID, "opure_profile_read: null argument");
     for (uint32_t i = 0; i < OPURE_STAGE_COUNT; ++i) { counts[i] = 0; ms[i] = 0.0; }
     OPURE_HIP_TRY(hipStreamSynchronize(dev->stream));
-    for (uint32_t k = 0; k + 1u < dev->prof_used; k += 2u)
+    for (uint32_t k = 0; k < dev->prof_used; ++k)
     {
         float t = 0.0f;
-        OPURE_HIP_TRY(hipEventElapsedTime(&t, dev->prof_ev[k], dev->prof_ev[k + 1u]));
-        const uint32_t st = dev->prof_stage[k / 2u];
-        counts[st] += 1u;
-        ms[st] += t;
+        OPURE_HIP_TRY(hipEventElapsedTime(&t, dev->prof_ev[2u * k], dev->prof_ev[2u * k + 1u]));
+        ms[dev->prof_stage[k]] += t;
+    }
+    for (uint32_t i = 0; i < OPURE_STAGE_COUNT; ++i)
+    {
+        counts[i] = dev->prof_count[i];
+        dev->prof_count[i] = 0u;
     }
     dev->prof_used = 0;
     return OPURE_OK;

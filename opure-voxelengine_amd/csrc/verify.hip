@@ -81,7 +81,8 @@ __global__ __launch_bounds__(256) void k_embed(const int32_t* tokens, opure_line
             // word sits at nibble {0,4,1,5,2,6,3,7}[e]
             const uint32_t g = kk / 32u, half = (kk % 32u) / 16u;
             const uint32_t* wd = reinterpret_cast<const uint32_t*>(w + blk + ((16u * g + rr) << 4)) + 2u * half;
-            const uint32_t w0 = wd[0], w1 = wd[1];
+            // the tiled words are stored rotated left by 3 bits: undo it
+            const uint32_t w0 = __builtin_amdgcn_alignbit(wd[0], wd[0], 3), w1 = __builtin_amdgcn_alignbit(wd[1], wd[1], 3);
             const uint32_t sz = static_cast<const uint32_t*>(E.scale)[(static_cast<uint64_t>(tile) * nblk + b) * 16u + rr];
             const float s = __uint_as_float(sz << 16), z = __uint_as_float(sz & 0xFFFF0000u);
 #pragma unroll
@@ -354,7 +355,7 @@ int opure_verify_layer(opure_dev* dev, const opure_verify_layer_args* a)
     char* ws = static_cast<char*>(dev->ws);
     float* ss = reinterpret_cast<float*>(ws + P.ss);
     const uint64_t n = static_cast<uint64_t>(MR) * (m->hidden / 16u);
-    hipLaunchKernelGGL(k_tile_sumsq, dim3(static_cast<uint32_t>((n + 255u) / 256u)), dim3(256), 0, dev->stream, a->x, MR,
+    OPURE_LAUNCH(dev, k_tile_sumsq, dim3(static_cast<uint32_t>((n + 255u) / 256u)), dim3(256), 0, a->x, MR,
                        m->hidden, ss);
     OPURE_LAUNCH_CHECK("k_tile_sumsq");
     GemvCall c = step_gemv(m, MR, P, ws, ss);
@@ -392,7 +393,7 @@ int opure_verify_step(opure_dev* dev, const opure_verify_args* a)
     float* ss = reinterpret_cast<float*>(ws + P.ss);
 
     if ((rc = prof_begin(dev, OPURE_STAGE_EMBED))) return rc;
-    hipLaunchKernelGGL(k_embed, dim3(MR), dim3(256), 0, dev->stream, a->tokens, m->embed, m->wfmt, m->hidden, m->vocab,
+    OPURE_LAUNCH(dev, k_embed, dim3(MR), dim3(256), 0, a->tokens, m->embed, m->wfmt, m->hidden, m->vocab,
                        MR, tiled_block_k(m->wfmt), x, ss, dev->err);
     OPURE_LAUNCH_CHECK("k_embed");
     if ((rc = prof_end(dev))) return rc;

@@ -166,3 +166,27 @@ class SynthModel:
                                   "mlp_norm": self.dev.download(d["mlp_norm"], np.float32, (h,)),
                                   **{k: self._dl_linear(d[k]) for k in ("qkv", "o", "gate_up", "down")}})
         return out
+
+
+def stage_bytes(cfg, stage, M, ctx):
+    """Algorithmic HBM bytes of one launch of a verify-step stage for M rows
+    over a ctx-token cache: the weights once, activations in and out once."""
+    h, nh, nkv, hd, ff, V = (cfg[k] for k in ("hidden", "n_heads", "n_kv_heads", "head_dim", "ffn", "vocab"))
+    w = cfg["wfmt"]
+    eb = 4 if cfg["afmt"] == H.A_F32 else 2
+    qkv_out = (nh + 2 * nkv) * hd
+    if stage == "embed":
+        return M * linear_bytes(w, 1, h) + M * h * 4
+    if stage == "qkv":      # fp32 residual + gain in, q out, K/V rows appended
+        return linear_bytes(w, qkv_out, h) + M * h * 4 + h * 4 + M * qkv_out * eb
+    if stage == "attention":
+        return 2 * nkv * hd * eb * (ctx + M) + 2 * M * nh * hd * eb
+    if stage == "o_proj":   # attention output in, residual read and written
+        return linear_bytes(w, h, nh * hd) + M * nh * hd * eb + 2 * M * h * 4
+    if stage == "gate_up":  # residual + gain in, SwiGLU output out
+        return linear_bytes(w, 2 * ff, h) + M * h * 4 + h * 4 + M * ff * eb
+    if stage == "down":
+        return linear_bytes(w, h, ff) + M * ff * eb + 2 * M * h * 4
+    if stage == "lm_head":  # fp32 logits out
+        return linear_bytes(w, V, h) + M * h * 4 + h * 4 + M * V * 4
+    return 0

@@ -74,6 +74,7 @@ def np_tiled(wfmt, lin, layout):
             byte = (d >> np.uint32(8 * (e // 2))) & np.uint32(0xFF)
             q = (byte & np.uint32(0xF)) if e % 2 else (byte >> np.uint32(4))
             o |= q << np.uint32(4 * pos)
+        o = (o << np.uint32(3)) | (o >> np.uint32(29))          # stored rotated left by 3 bits
         wb = o.view(np.uint8).reshape(out, -1)
     nblk = wb.shape[1] // 64
     tiled = wb.reshape(tiles, 16, nblk, 4, 16).transpose(0, 2, 3, 1, 4).reshape(-1)
