@@ -15,7 +15,10 @@
  *
  *  The engine borrows the device and the models (their weights and the host
  *  array of layer descriptors must outlive it) and owns its KV pools, page
- *  tables, step buffers and captured graphs.
+ *  tables, step buffers and captured graphs.  Each model's KV pool is a set of
+ *  16-token pages handed out by a free list as the sequence grows and given
+ *  back by the rollback; prompts of quantised models are prefilled 256 rows a
+ *  launch.
  * ========================================================================== */
 #ifndef OPURE_ENGINE_H
 #define OPURE_ENGINE_H
@@ -65,9 +68,28 @@ int opure_engine_generate_speculative(opure_engine* e, const int32_t* prompt, ui
                                       int32_t* out, uint32_t* accepted_hist, uint32_t hist_cap,
                                       opure_engine_stats* stats);
 
+/* One verify step of the target on explicit rows: tokens[0] is the last
+ * accepted token, tokens[1..n) the drafts, at positions seq_len .. seq_len +
+ * n - 1 (n <= OPURE_MAX_ROWS); greedy acceptance.  *accepted = drafts kept;
+ * out[0 .. *accepted] = those drafts then the target's own next token.  The
+ * rows' K/V stay in the cache until opure_engine_rollback_kv.  The engine's
+ * VerifyStep (SURVEY's build plan; the reference has none). */
+int opure_engine_verify_step(opure_engine* e, const int32_t* tokens, uint32_t n, uint32_t seq_len, int32_t* out,
+                             uint32_t* accepted);
+/* After a verify step of k drafts at seq_len that kept `accepted`: the cache
+ * keeps seq_len + accepted + 1 positions, the rest are rolled back and the
+ * pages wholly past them return to the pool.  *new_len = the kept length.
+ * Replaces EvictOldestKV (src/engine/Opure_VoxelEngine.cpp:721-763). */
+int opure_engine_rollback_kv(opure_engine* e, uint32_t seq_len, uint32_t accepted, uint32_t k, uint32_t* new_len);
+/* Page accounting of the target's (draft != 0: the draft's) KV pool: pages in
+ * the pool, pages free, and the sequence's page-table row (-1 = no page) into
+ * row[0 .. min(row_cap, *row_len)). */
+int opure_engine_pages(const opure_engine* e, int draft, uint32_t* total, uint32_t* available, int32_t* row,
+                       uint32_t row_cap, uint32_t* row_len);
+
 /* Running totals since opure_engine_create or the last reset.  Replaces the
  * reference's speculativeAcceptance, which is declared but always -1 because
- * nothing drafts (src/core/Opure_Metrics.cpp:65-68, set from
+ * nothing drafts (src/engine/Opure_Metrics.cpp:65-68, set from
  * Opure_VoxelEngine.cpp:666). */
 typedef struct opure_engine_metrics {
     uint64_t generate_calls;          /* generate / generate_speculative calls with n_new > 0 */
@@ -86,7 +108,7 @@ int opure_engine_reset_metrics(opure_engine* e);
  *      page-table rows (opure_kv.page_table); a row takes pages as the
  *      sequence grows and opure_kv_rollback's freed lists give them back.
  *      Replaces the reference's fixed contiguous cache
- *      (ModelConfig::KvCacheWords, src/core/Opure_Graph.h:81-84) and its
+ *      (ModelConfig::KvCacheWords, src/engine/Opure_Graph.h:81-84) and its
  *      EvictOldestKV (src/engine/Opure_VoxelEngine.cpp:721-763).  Not
  *      thread-safe. */
 typedef struct opure_page_pool opure_page_pool;

@@ -326,7 +326,8 @@ typedef struct opure_verify_args {
     const int32_t*     tokens;       /* device [batch][rows]: last token, then K drafts */
     const int32_t*     seq_len;      /* device [batch] */
     uint32_t           max_ctx;      /* host upper bound on seq_len[b] + rows */
-    float*             logits;       /* device [batch][rows][vocab] */
+    float*             logits;       /* device [batch][rows][vocab]; NULL (with OPURE_ACCEPT_NONE): a prefill,
+                                      * which writes the rows' K/V and stops before the LM head */
     uint32_t           accept_mode;  /* OPURE_ACCEPT_* */
     const float*       draft_logits; /* rejection: [batch][rows-1][vocab] */
     float              temperature;

@@ -364,8 +364,11 @@ int opure_verify_layer(opure_dev* dev, const opure_verify_layer_args* a)
 
 int opure_verify_step(opure_dev* dev, const opure_verify_args* a)
 {
-    OPURE_REQUIRE(dev && a && a->model && a->kv && a->tokens && a->seq_len && a->logits, OPURE_E_INVALID,
+    OPURE_REQUIRE(dev && a && a->model && a->kv && a->tokens && a->seq_len, OPURE_E_INVALID,
                   "opure_verify_step: null argument");
+    // no logits: a prefill, which stops after the last layer
+    OPURE_REQUIRE(a->logits || (a->accept_mode == OPURE_ACCEPT_NONE && !a->rollback), OPURE_E_INVALID,
+                  "opure_verify_step: acceptance needs logits");
     const opure_model* m = a->model;
     const opure_kv* kv = a->kv;
     const uint32_t B = a->batch, R = a->rows, MR = B * R;
@@ -404,6 +407,7 @@ int opure_verify_step(opure_dev* dev, const opure_verify_args* a)
     GemvCall c = step_gemv(m, MR, P, ws, ss);
     for (uint32_t L = 0; L < m->n_layers; ++L)
         if ((rc = layer_launch(dev, m, kv, L, B, R, a->seq_len, a->max_ctx, P, x, ss, c))) return rc;
+    if (!a->logits) return OPURE_OK;
 
     c.W = m->lm_head;
     c.x = x;

@@ -139,6 +139,37 @@ int opure_engine_generate_speculative(opure_engine* e, const int32_t* prompt, ui
     });
 }
 
+int opure_engine_verify_step(opure_engine* e, const int32_t* tokens, uint32_t n, uint32_t seq_len, int32_t* out,
+                             uint32_t* accepted)
+{
+    if (!e || !tokens || !n || !out || !accepted) return fail(OPURE_E_INVALID, "opure_engine_verify_step: bad argument");
+    return guarded([&] {
+        const auto r = e->impl.VerifyStep(to_tokens(tokens, n), seq_len);
+        *accepted = r.accepted;
+        for (uint32_t i = 0; i < n; ++i) out[i] = i < r.emitted.size() ? static_cast<int32_t>(r.emitted[i]) : -1;
+    });
+}
+
+int opure_engine_rollback_kv(opure_engine* e, uint32_t seq_len, uint32_t accepted, uint32_t k, uint32_t* new_len)
+{
+    if (!e || !new_len) return fail(OPURE_E_INVALID, "opure_engine_rollback_kv: null argument");
+    return guarded([&] { *new_len = e->impl.RollbackKV(seq_len, accepted, k); });
+}
+
+int opure_engine_pages(const opure_engine* e, int draft, uint32_t* total, uint32_t* available, int32_t* row,
+                       uint32_t row_cap, uint32_t* row_len)
+{
+    if (!e || !total || !available || !row_len || (!row && row_cap))
+        return fail(OPURE_E_INVALID, "opure_engine_pages: bad argument");
+    return guarded([&] {
+        const auto u = e->impl.Pages(draft != 0);
+        *total = u.total;
+        *available = u.available;
+        *row_len = static_cast<uint32_t>(u.row.size());
+        for (uint32_t i = 0; i < row_cap && i < u.row.size(); ++i) row[i] = u.row[i];
+    });
+}
+
 int opure_engine_get_metrics(const opure_engine* e, opure_engine_metrics* out)
 {
     if (!e || !out) return fail(OPURE_E_INVALID, "opure_engine_get_metrics: null argument");

@@ -2,7 +2,7 @@
 //  page_pool.h -- the free list of a paged KV pool's pages.
 //
 //  The reference sizes one contiguous cache per layer up front
-//  (ModelConfig::KvCacheWords, src/core/Opure_Graph.h:81-84) and its only way
+//  (ModelConfig::KvCacheWords, src/engine/Opure_Graph.h:81-84) and its only way
 //  to give positions back is EvictOldestKV (src/engine/Opure_VoxelEngine.cpp:
 //  721-763), a memmove that never reaches the KV buffer.  Here sequences own
 //  16-token pages of a shared pool through their page-table rows: a sequence

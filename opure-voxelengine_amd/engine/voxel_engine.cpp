@@ -39,12 +39,20 @@ void* alloc(opure_dev* dev, uint64_t bytes, const char* what)
 
 }  // namespace
 
-// Device state of one model: its paged KV pool (identity page table, one
-// sequence) and a 16-row prefill step.
+// Device state of one model: its paged KV pool with the free list of its
+// pages, the sequence's page-table row (host mirror and device copy), the
+// same row 16 times for the 256-row prefill, and the prefill steps.
 struct VoxelEngine::ModelState {
+    explicit ModelState(uint32_t nPages) : pool(nPages) {}
     opure_model desc{};
-    opure_kv kv{};
-    std::unique_ptr<Step> prefill;
+    opure_kv kv{};                  // one sequence: kv.page_table = the row
+    opure_kv kv16{};                // the same pool, page_table = the row x 16 (wide prefill)
+    PagePool pool;
+    std::vector<int32_t> row;       // host mirror of kv.page_table
+    bool rowsDirty16 = true;        // kv16's rows lag the row
+    bool wide = false;              // quantised weights and 16-bit activations: 256-row prefill
+    std::unique_ptr<Step> prefill;      // 16 rows
+    std::unique_ptr<Step> prefillWide;  // 16 parts x 16 rows
 };
 
 // One fixed-shape verify step of a model: the argument block and the buffers
@@ -55,10 +63,15 @@ struct VoxelEngine::Step {
     int32_t* tokens = nullptr;
     int32_t* seqLen = nullptr;
     float* logits = nullptr;
-    int32_t* out = nullptr;        // out_tokens[rows], then accepted
+    int32_t* out = nullptr;        // out_tokens[batch*rows], accepted[batch], then (rollback) n_freed, freed[2]
     int32_t* newSeqLen = nullptr;
     opure_verify_args args{};
 };
+
+namespace {
+constexpr uint32_t kFreedStride = 2;   // pages one rollback of <= 15 drafts can release: ceil(15 / 16) = 1
+constexpr uint32_t kWideParts = 16;    // 16 parts x 16 rows = 256 prefill rows a launch
+}  // namespace
 
 VoxelEngine::VoxelEngine() = default;
 
@@ -94,18 +107,23 @@ void VoxelEngine::Shutdown()
     for (auto& s : draftSteps_) free_step(s, false);
     draftSteps_.clear();
     free_step(verify_, false);
+    free_step(verifyRows_, true);
     free_step(decode_, true);
     for (auto* m : {target_.get(), draft_.get()})
     {
         if (!m) continue;
         free_step(m->prefill, true);
+        free_step(m->prefillWide, true);
         opure_buf_free(dev_, m->kv.pool);
         opure_buf_free(dev_, m->kv.page_table);
+        opure_buf_free(dev_, m->kv16.page_table);
     }
     target_.reset();
     draft_.reset();
     if (io_) opure_buf_free(dev_, io_);
     io_ = nullptr;
+    if (rbIo_) opure_buf_free(dev_, rbIo_);
+    rbIo_ = nullptr;
     dev_ = nullptr;
     ready_ = false;
 }
@@ -128,8 +146,9 @@ void VoxelEngine::Initialize(opure_dev* dev, const opure_model& target, const op
     auto make_model = [&](const opure_model& d) {
         if (d.rope_max_pos < P)
             throw Error(OPURE_E_INVALID, "VoxelEngine::Initialize: model RoPE table shorter than maxPositions");
-        auto m = std::make_unique<ModelState>();
+        auto m = std::make_unique<ModelState>(n_pages);
         m->desc = d;
+        m->wide = d.wfmt != OPURE_W_F32 && d.afmt != OPURE_A_F32;
         const uint64_t pool = static_cast<uint64_t>(d.n_layers) * n_pages * 2u * d.n_kv_heads * OPURE_PAGE_SIZE *
                               d.head_dim * act_bytes(d.afmt);
         m->kv.pool = alloc(dev, pool, "kv pool");
@@ -137,34 +156,37 @@ void VoxelEngine::Initialize(opure_dev* dev, const opure_model& target, const op
         m->kv.page_size = OPURE_PAGE_SIZE;
         m->kv.max_pages_per_seq = n_pages;
         m->kv.page_table = static_cast<int32_t*>(alloc(dev, n_pages * 4ull, "page table"));
-        std::vector<int32_t> pt(n_pages);
-        for (uint32_t i = 0; i < n_pages; ++i) pt[i] = static_cast<int32_t>(i);
-        Check(opure_buf_upload(dev, m->kv.page_table, 0, pt.data(), n_pages * 4ull), "page table upload");
+        m->row.assign(n_pages, -1);
+        Check(opure_buf_upload(dev, m->kv.page_table, 0, m->row.data(), n_pages * 4ull), "page table upload");
+        m->kv16 = m->kv;
+        m->kv16.page_table = static_cast<int32_t*>(alloc(dev, kWideParts * n_pages * 4ull, "page table x16"));
         return m;
     };
     target_ = make_model(target);
     if (draft) draft_ = make_model(*draft);
 
-    // a step of `rows` rows of model m; tokens/seq_len given, or own buffers
-    auto make_step = [&](ModelState* m, uint32_t rows, int32_t* tokens, int32_t* seqLen, bool accept, bool rollback) {
+    // a step of `batch` x `rows` rows of model m; tokens/seq_len given, or own buffers
+    auto make_step = [&](ModelState* m, uint32_t rows, int32_t* tokens, int32_t* seqLen, bool accept, bool rollback,
+                         uint32_t batch = 1, bool logits = true) {
         auto s = std::make_unique<Step>();
         s->m = m;
         s->rows = rows;
+        const uint64_t n = static_cast<uint64_t>(batch) * rows;
         if (!tokens)
         {
-            int32_t* io = static_cast<int32_t*>(alloc(dev, (rows + 1ull) * 4, "step inputs"));
+            int32_t* io = static_cast<int32_t*>(alloc(dev, (n + batch) * 4, "step inputs"));
             tokens = io;
-            seqLen = io + rows;
+            seqLen = io + n;
         }
         s->tokens = tokens;
         s->seqLen = seqLen;
-        s->logits = static_cast<float*>(alloc(dev, static_cast<uint64_t>(rows) * m->desc.vocab * 4, "logits"));
-        s->out = static_cast<int32_t*>(alloc(dev, (rows + 1ull) * 4, "out tokens"));
+        s->logits = logits ? static_cast<float*>(alloc(dev, n * m->desc.vocab * 4, "logits")) : nullptr;
+        s->out = static_cast<int32_t*>(alloc(dev, (n + batch + 1ull + kFreedStride) * 4, "out tokens"));
         if (rollback) s->newSeqLen = static_cast<int32_t*>(alloc(dev, 4, "new seq len"));
         opure_verify_args& a = s->args;
         a.model = &m->desc;
-        a.kv = &m->kv;
-        a.batch = 1;
+        a.kv = batch > 1 ? &m->kv16 : &m->kv;
+        a.batch = batch;
         a.rows = rows;
         a.tokens = s->tokens;
         a.seq_len = s->seqLen;
@@ -172,9 +194,15 @@ void VoxelEngine::Initialize(opure_dev* dev, const opure_model& target, const op
         a.logits = s->logits;
         a.accept_mode = accept ? OPURE_ACCEPT_GREEDY : OPURE_ACCEPT_NONE;
         a.out_tokens = s->out;
-        a.accepted = s->out + rows;
+        a.accepted = s->out + n;
         a.rollback = rollback ? 1u : 0u;
         a.new_seq_len = s->newSeqLen;
+        if (rollback)
+        {
+            a.n_freed = s->out + n + batch;
+            a.freed = s->out + n + batch + 1;
+            a.freed_stride = kFreedStride;
+        }
         return s;
     };
 
@@ -189,10 +217,17 @@ void VoxelEngine::Initialize(opure_dev* dev, const opure_model& target, const op
     for (ModelState* m : {target_.get(), draft_.get()})
     {
         if (!m) continue;
-        m->prefill = make_step(m, OPURE_MAX_ROWS, nullptr, nullptr, false, false);
+        m->prefill = make_step(m, OPURE_MAX_ROWS, nullptr, nullptr, false, false, 1, false);
         Check(opure_verify_reserve(dev, &m->desc, 1, OPURE_MAX_ROWS, P), "verify reserve");
+        if (m->wide)
+        {
+            m->prefillWide = make_step(m, OPURE_MAX_ROWS, nullptr, nullptr, false, false, kWideParts, false);
+            Check(opure_verify_reserve(dev, &m->desc, kWideParts, OPURE_MAX_ROWS, P), "verify reserve (prefill)");
+        }
     }
     decode_ = make_step(target_.get(), 1, nullptr, nullptr, true, false);
+    verifyRows_ = make_step(target_.get(), OPURE_MAX_ROWS, nullptr, nullptr, true, false);
+    rbIo_ = static_cast<int32_t*>(alloc(dev, (4ull + kFreedStride) * 4, "rollback io"));
     if (draft_)
     {
         verify_ = make_step(target_.get(), K + 1, vtok, vseq, true, true);
@@ -207,6 +242,45 @@ void VoxelEngine::RunStep(Step& s)
     Check(opure_verify_step(dev_, &s.args), "opure_verify_step");
 }
 
+void VoxelEngine::EnsurePages(ModelState& m, uint32_t tokens)
+{
+    if (m.pool.GrowSeq(m.row.data(), m.kv.max_pages_per_seq, tokens, OPURE_PAGE_SIZE) == 0) return;
+    Check(opure_buf_upload(dev_, m.kv.page_table, 0, m.row.data(), m.row.size() * 4ull), "page table upload");
+    m.rowsDirty16 = true;
+}
+
+void VoxelEngine::ReleasePages(ModelState& m, const int32_t* ids, uint32_t n)
+{
+    if (n == 0) return;
+    m.pool.Release(ids, n);
+    // the rollback already unlinked them on the device
+    for (uint32_t i = 0; i < n; ++i)
+        for (int32_t& e : m.row)
+            if (e == ids[i])
+            {
+                e = -1;
+                break;
+            }
+}
+
+namespace {
+
+// every page of a sequence's row back to its pool (a new generation starts at 0)
+void reset_row(opure_dev* dev, PagePool& pool, std::vector<int32_t>& row, int32_t* devRow)
+{
+    std::vector<int32_t> held;
+    for (int32_t& e : row)
+        if (e >= 0)
+        {
+            held.push_back(e);
+            e = -1;
+        }
+    pool.Release(held.data(), static_cast<uint32_t>(held.size()));
+    Check(opure_buf_upload(dev, devRow, 0, row.data(), row.size() * 4ull), "page table upload");
+}
+
+}  // namespace
+
 uint32_t VoxelEngine::Prefill(bool draft, const std::vector<uint32_t>& tokens, uint32_t start, bool wantNext)
 {
     ModelState* m = draft ? draft_.get() : target_.get();
@@ -214,10 +288,40 @@ uint32_t VoxelEngine::Prefill(bool draft, const std::vector<uint32_t>& tokens, u
     if (tokens.empty()) throw Error(OPURE_E_INVALID, "VoxelEngine::Prefill: no tokens");
     if (start + tokens.size() > opts_.maxPositions)
         throw Error(OPURE_E_CAPACITY, "VoxelEngine::Prefill: prompt exceeds maxPositions");
-    Step& s = *m->prefill;
+    EnsurePages(*m, start + static_cast<uint32_t>(tokens.size()));
     const size_t body = wantNext ? tokens.size() - 1 : tokens.size();
+    size_t c = 0;
+    if (m->wide)
+    {
+        // 16 parts of 16 rows a launch, every part at its own offset of the
+        // prompt and all on the prompt's page-table row
+        Step& w = *m->prefillWide;
+        const uint32_t maxPages = m->kv.max_pages_per_seq;
+        while (body - c >= 2u * OPURE_MAX_ROWS)
+        {
+            const uint32_t parts = static_cast<uint32_t>(std::min<size_t>(kWideParts, (body - c) / OPURE_MAX_ROWS));
+            if (m->rowsDirty16)
+            {
+                std::vector<int32_t> rows(static_cast<size_t>(kWideParts) * maxPages);
+                for (uint32_t b = 0; b < kWideParts; ++b)
+                    std::copy(m->row.begin(), m->row.end(), rows.begin() + static_cast<std::ptrdiff_t>(b) * maxPages);
+                Check(opure_buf_upload(dev_, m->kv16.page_table, 0, rows.data(), rows.size() * 4ull), "page table upload");
+                m->rowsDirty16 = false;
+            }
+            std::vector<int32_t> io(kWideParts * OPURE_MAX_ROWS + kWideParts, 0);
+            for (uint32_t i = 0; i < parts * OPURE_MAX_ROWS; ++i) io[i] = static_cast<int32_t>(tokens[c + i]);
+            for (uint32_t b = 0; b < parts; ++b)
+                io[kWideParts * OPURE_MAX_ROWS + b] = static_cast<int32_t>(start + c + b * OPURE_MAX_ROWS);
+            Check(opure_buf_upload(dev_, w.tokens, 0, io.data(), io.size() * 4ull), "prefill upload");
+            w.args.batch = parts;         // no logits: the step stops before the LM head
+            RunStep(w);
+            c += parts * OPURE_MAX_ROWS;
+        }
+        w.args.batch = kWideParts;
+    }
+    Step& s = *m->prefill;
     std::vector<int32_t> io(OPURE_MAX_ROWS + 1);
-    for (size_t c = 0; c < body; c += OPURE_MAX_ROWS)
+    for (; c < body; c += OPURE_MAX_ROWS)
     {
         const uint32_t r = static_cast<uint32_t>(std::min<size_t>(OPURE_MAX_ROWS, body - c));
         for (uint32_t i = 0; i < r; ++i) io[i] = static_cast<int32_t>(tokens[c + i]);
@@ -240,6 +344,7 @@ uint32_t VoxelEngine::DecodeStep(uint32_t token, uint32_t position)
 {
     if (!ready_) throw Error(OPURE_E_INVALID, "VoxelEngine::DecodeStep: not initialised");
     if (position + 1u > opts_.maxPositions) throw Error(OPURE_E_CAPACITY, "VoxelEngine::DecodeStep: cache full");
+    EnsurePages(*target_, position + 1u);
     Step& s = *decode_;
     const int32_t io[2] = {static_cast<int32_t>(token), static_cast<int32_t>(position)};
     Check(opure_buf_upload(dev_, s.tokens, 0, io, sizeof(io)), "decode upload");
@@ -290,6 +395,8 @@ uint32_t VoxelEngine::SpecIteration(uint32_t pendingLen, uint32_t nxt, uint32_t 
     for (uint32_t i = 0; i < pendingLen; ++i) dtok[i] = static_cast<int32_t>(pending[i]);
     *vseq = static_cast<int32_t>(ctx);
     vtok[0] = static_cast<int32_t>(nxt);
+    EnsurePages(*target_, ctx + K + 1u);        // the verify rows' positions
+    EnsurePages(*draft_, dctx + nsteps);        // the draft steps' positions
     Check(opure_buf_upload(dev_, io_, 0, io.data(), io.size() * 4), "speculative upload");
 
     int32_t* dio = static_cast<int32_t*>(io_);
@@ -331,11 +438,15 @@ uint32_t VoxelEngine::SpecIteration(uint32_t pendingLen, uint32_t nxt, uint32_t 
     {
         record();
     }
-    outTokens.assign(K + 2u, 0);
-    Check(opure_buf_download(dev_, outTokens.data(), verify_->out, 0, (K + 2ull) * 4), "speculative download");
-    const int32_t n = outTokens[K + 1u];
-    outTokens.resize(K + 1u);
+    // out_tokens[K+1], accepted, n_freed, freed[kFreedStride]
+    outTokens.assign(K + 3u + kFreedStride, 0);
+    Check(opure_buf_download(dev_, outTokens.data(), verify_->out, 0, outTokens.size() * 4ull), "speculative download");
+    const int32_t n = outTokens[K + 1u], nFreed = outTokens[K + 2u];
     if (n < 0 || static_cast<uint32_t>(n) > K) throw Error(OPURE_E_INVALID, "speculative: bad accepted count");
+    if (nFreed < 0 || static_cast<uint32_t>(nFreed) > kFreedStride)
+        throw Error(OPURE_E_INVALID, "speculative: bad released page count");
+    ReleasePages(*target_, outTokens.data() + K + 3u, static_cast<uint32_t>(nFreed));
+    outTokens.resize(K + 1u);
     return static_cast<uint32_t>(n);
 }
 
@@ -372,6 +483,8 @@ GenerateResult VoxelEngine::Generate(const std::vector<uint32_t>& prompt, uint32
     GenerateResult r;
     r.promptTokens = prompt;
     if (nNew == 0) return r;
+    reset_row(dev_, target_->pool, target_->row, target_->kv.page_table);
+    target_->rowsDirty16 = true;
     auto t0 = std::chrono::steady_clock::now();
     uint32_t nxt = Prefill(false, prompt, 0, true);
     r.msPrefill = ms_since(t0);
@@ -400,6 +513,11 @@ GenerateResult VoxelEngine::GenerateSpeculative(const std::vector<uint32_t>& pro
     GenerateResult r;
     r.promptTokens = prompt;
     if (nNew == 0) return r;
+    for (ModelState* m : {target_.get(), draft_.get()})
+    {
+        reset_row(dev_, m->pool, m->row, m->kv.page_table);
+        m->rowsDirty16 = true;
+    }
     auto t0 = std::chrono::steady_clock::now();
     uint32_t nxt = Prefill(false, prompt, 0, true);
     Prefill(true, prompt, 0, false);
@@ -443,6 +561,82 @@ GenerateResult VoxelEngine::GenerateSpeculative(const std::vector<uint32_t>& pro
     ++metrics_.generateCalls;
     metrics_.tokensEmitted += r.generated.size();
     return r;
+}
+
+VerifyResult VoxelEngine::VerifyStep(const std::vector<uint32_t>& tokens, uint32_t seqLen)
+{
+    if (!ready_) throw Error(OPURE_E_INVALID, "VoxelEngine::VerifyStep: not initialised");
+    const uint32_t R = static_cast<uint32_t>(tokens.size());
+    if (R < 1 || R > OPURE_MAX_ROWS)
+        throw Error(OPURE_E_CAPACITY, "VoxelEngine::VerifyStep: 1.." + std::to_string(OPURE_MAX_ROWS) + " rows");
+    if (seqLen + R > opts_.maxPositions) throw Error(OPURE_E_CAPACITY, "VoxelEngine::VerifyStep: exceeds maxPositions");
+    EnsurePages(*target_, seqLen + R);
+    Step& s = *verifyRows_;
+    std::vector<int32_t> io(OPURE_MAX_ROWS + 1, 0);
+    for (uint32_t i = 0; i < R; ++i) io[i] = static_cast<int32_t>(tokens[i]);
+    io[OPURE_MAX_ROWS] = static_cast<int32_t>(seqLen);
+    Check(opure_buf_upload(dev_, s.tokens, 0, io.data(), io.size() * 4ull), "verify upload");
+    s.args.rows = R;
+    try
+    {
+        RunStep(s);
+    }
+    catch (...)
+    {
+        s.args.rows = OPURE_MAX_ROWS;
+        throw;
+    }
+    s.args.rows = OPURE_MAX_ROWS;
+    // out_tokens[0..R), accepted at out + OPURE_MAX_ROWS (the step's shape at creation)
+    std::vector<int32_t> out(OPURE_MAX_ROWS + 1);
+    Check(opure_buf_download(dev_, out.data(), s.out, 0, out.size() * 4ull), "verify download");
+    const int32_t n = out[OPURE_MAX_ROWS];
+    if (n < 0 || static_cast<uint32_t>(n) >= R) throw Error(OPURE_E_INVALID, "VerifyStep: bad accepted count");
+    VerifyResult r;
+    r.accepted = static_cast<uint32_t>(n);
+    for (int32_t i = 0; i <= n; ++i) r.emitted.push_back(static_cast<uint32_t>(out[static_cast<size_t>(i)]));
+    ++metrics_.verifySteps;
+    metrics_.draftsProposed += R - 1u;
+    metrics_.draftsAccepted += r.accepted;
+    return r;
+}
+
+uint32_t VoxelEngine::RollbackKV(uint32_t seqLen, uint32_t accepted, uint32_t k)
+{
+    if (!ready_) throw Error(OPURE_E_INVALID, "VoxelEngine::RollbackKV: not initialised");
+    if (accepted > k || k + 1u > OPURE_MAX_ROWS || seqLen + k + 1u > opts_.maxPositions)
+        throw Error(OPURE_E_INVALID, "VoxelEngine::RollbackKV: accepted > k, or k past the step's rows");
+    int32_t io[4 + kFreedStride] = {static_cast<int32_t>(seqLen), static_cast<int32_t>(accepted), 0, 0};
+    for (uint32_t i = 0; i < kFreedStride; ++i) io[4 + i] = -1;
+    Check(opure_buf_upload(dev_, rbIo_, 0, io, sizeof(io)), "rollback upload");
+    opure_rollback_args rb{};
+    rb.model = &target_->desc;
+    rb.kv = &target_->kv;
+    rb.batch = 1;
+    rb.k = k;
+    rb.seq_len = rbIo_;
+    rb.accepted = rbIo_ + 1;
+    rb.new_seq_len = rbIo_ + 2;
+    rb.n_freed = rbIo_ + 3;
+    rb.freed = rbIo_ + 4;
+    rb.freed_stride = kFreedStride;
+    Check(opure_kv_rollback(dev_, &rb), "opure_kv_rollback");
+    Check(opure_buf_download(dev_, io, rbIo_, 0, sizeof(io)), "rollback download");
+    if (io[3] < 0 || io[3] > static_cast<int32_t>(kFreedStride))
+        throw Error(OPURE_E_INVALID, "RollbackKV: bad released page count");
+    ReleasePages(*target_, io + 4, static_cast<uint32_t>(io[3]));
+    return static_cast<uint32_t>(io[2]);
+}
+
+PageUsage VoxelEngine::Pages(bool draft) const
+{
+    const ModelState* m = draft ? draft_.get() : target_.get();
+    if (!ready_ || !m) throw Error(OPURE_E_INVALID, "VoxelEngine::Pages: no such model");
+    PageUsage u;
+    u.total = m->pool.Capacity();
+    u.available = m->pool.Available();
+    u.row = m->row;
+    return u;
 }
 
 }  // namespace opure::engine

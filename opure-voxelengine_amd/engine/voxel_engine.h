@@ -14,7 +14,16 @@
 //  steps feed each other's argmax on the device (out_tokens -> next tokens
 //  by a device copy) and the verify step reads the drafts from the same
 //  buffer, so the host writes one small input block and reads back
-//  accepted + out_tokens once per iteration.
+//  accepted + out_tokens (+ the pages the rollback released) once per
+//  iteration.
+//
+//  Each model's KV cache is a pool of 16-token pages handed out by a PagePool:
+//  a sequence's page-table row takes pages as it grows (before a step writes
+//  there) and the rollback's freed pages go back to the pool.  Prompts are
+//  prefilled 256 rows a launch where the weights are quantised and the
+//  activations 16-bit: one verify step over 16 "sequences" of 16 rows that
+//  share the prompt's page-table row (row j of part b sits at start + 16 b + j
+//  and sees every position before it), so every GEMV runs as a thin GEMM.
 // ============================================================================
 #pragma once
 
@@ -25,6 +34,7 @@
 #include <vector>
 
 #include "opure_hip.h"
+#include "page_pool.h"
 
 namespace opure::engine {
 
@@ -48,6 +58,20 @@ struct EngineOptions {
     int32_t  stopToken = -1;        // < 0: none
 };
 
+// One verify step on explicit rows (VerifyStep): the drafts kept and the
+// target's own token after them.
+struct VerifyResult {
+    uint32_t accepted = 0;              // longest prefix of the drafts the target agrees with
+    std::vector<uint32_t> emitted;      // the accepted drafts, then the correction (or bonus) token
+};
+
+// Page accounting of a model's KV pool (Pages).
+struct PageUsage {
+    uint32_t total = 0;                 // pages in the pool
+    uint32_t available = 0;             // pages free
+    std::vector<int32_t> row;           // the sequence's page-table row (-1 = no page)
+};
+
 struct GenerateResult {
     std::vector<uint32_t> promptTokens;
     std::vector<uint32_t> generated;
@@ -62,8 +86,8 @@ struct GenerateResult {
 
 // Running totals over an engine's lifetime (or since ResetMetrics): the
 // source of the serving metric speculativeAcceptance, which the reference
-// declares but pins at -1 because nothing drafts (src/core/Opure_Metrics.cpp:
-// 65-68; MetricsSnapshot in src/core/Opure_Metrics.h).
+// declares but pins at -1 because nothing drafts (src/engine/Opure_Metrics.cpp:
+// 65-68; MetricsSnapshot in src/engine/Opure_Metrics.h).
 struct EngineMetrics {
     uint64_t generateCalls = 0;    // Generate / GenerateSpeculative calls with n_new > 0 that finished
     uint64_t verifySteps = 0;      // speculative verify steps
@@ -104,6 +128,20 @@ public:
     // Appends `token` at `position` of the target cache; returns the argmax.
     uint32_t DecodeStep(uint32_t token, uint32_t position);
 
+    // The verify step as its own call (SURVEY's VerifyStep): tokens = the last
+    // accepted token then K drafts (K + 1 <= 16 rows) at positions seqLen ..
+    // seqLen + K of the target; greedy acceptance.  The rows' K/V stay in the
+    // cache until RollbackKV.
+    [[nodiscard]] VerifyResult VerifyStep(const std::vector<uint32_t>& tokens, uint32_t seqLen);
+    // After a verify step of k drafts at seqLen that kept `accepted`: the cache
+    // keeps seqLen + accepted + 1 positions, the rows past them are rolled
+    // back and the pages wholly past them go back to the pool.  Returns the
+    // new length.  Replaces EvictOldestKV (Opure_VoxelEngine.cpp:721-763).
+    uint32_t RollbackKV(uint32_t seqLen, uint32_t accepted, uint32_t k);
+
+    // The target's (draft's: `draft` true) page accounting.
+    [[nodiscard]] PageUsage Pages(bool draft) const;
+
     [[nodiscard]] const EngineMetrics& Metrics() const { return metrics_; }
     void ResetMetrics() { metrics_ = EngineMetrics{}; }
 
@@ -112,6 +150,10 @@ private:
     struct Step;
 
     void RunStep(Step& s);
+    // pages for positions [0, tokens) of model m's sequence, uploaded if any were taken
+    void EnsurePages(ModelState& m, uint32_t tokens);
+    // pages the rollback released (ids from the device): back to the pool, out of the row
+    void ReleasePages(ModelState& m, const int32_t* ids, uint32_t n);
     uint32_t SpecIteration(uint32_t pendingLen, uint32_t nxt, uint32_t ctx, uint32_t dctx, const uint32_t* pending,
                            std::vector<int32_t>& outTokens);
 
@@ -122,8 +164,10 @@ private:
     // one speculative iteration's inputs (one upload) and outputs (one download)
     void* io_ = nullptr;            // int32 [dseq K+1 | dtok K+1 | vseq | vtok K+1]
     std::vector<std::unique_ptr<Step>> draftSteps_;   // K+1 single-row draft slots
-    std::unique_ptr<Step> verify_;                    // K+1 rows of the target
+    std::unique_ptr<Step> verify_;                    // K+1 rows of the target (speculative loop)
+    std::unique_ptr<Step> verifyRows_;                // up to 16 rows of the target (VerifyStep)
     std::unique_ptr<Step> decode_;                    // one row of the target
+    int32_t* rbIo_ = nullptr;       // RollbackKV: int32 [seq_len | accepted | new_len | n_freed | freed 2]
     opure_graph* iterGraph_[2] = {nullptr, nullptr};  // pending length 1 or 2
     opure_graph* decodeGraph_ = nullptr;
     EngineMetrics metrics_{};

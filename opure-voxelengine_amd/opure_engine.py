@@ -50,10 +50,14 @@ def lib():
         L.opure_page_pool_alloc.argtypes = [vp, u32, vp]
         L.opure_page_pool_release.argtypes = [vp, vp, u32]
         L.opure_page_pool_grow_seq.argtypes = [vp, vp, u32, u32, C.POINTER(u32)]
+        L.opure_engine_verify_step.argtypes = [vp, vp, u32, u32, vp, C.POINTER(u32)]
+        L.opure_engine_rollback_kv.argtypes = [vp, u32, u32, u32, C.POINTER(u32)]
+        L.opure_engine_pages.argtypes = [vp, i, C.POINTER(u32), C.POINTER(u32), vp, u32, C.POINTER(u32)]
         for f in ("opure_engine_create", "opure_engine_destroy", "opure_engine_generate",
                   "opure_engine_generate_speculative", "opure_engine_get_metrics", "opure_engine_reset_metrics",
                   "opure_page_pool_create", "opure_page_pool_destroy", "opure_page_pool_available",
-                  "opure_page_pool_alloc", "opure_page_pool_release", "opure_page_pool_grow_seq"):
+                  "opure_page_pool_alloc", "opure_page_pool_release", "opure_page_pool_grow_seq",
+                  "opure_engine_verify_step", "opure_engine_rollback_kv", "opure_engine_pages"):
             getattr(L, f).restype = i
         _lib = L
     return _lib
@@ -85,6 +89,28 @@ class Engine:
         st = Stats()
         check(lib().opure_engine_generate(self.h, p.ctypes.data, p.size, n_new, out.ctypes.data, C.byref(st)))
         return out, st
+
+    def verify_step(self, tokens, seq_len: int):
+        """(accepted, emitted ids): one verify step of the target on these rows."""
+        t = np.ascontiguousarray(tokens, dtype=np.int32)
+        out = np.zeros(t.size, dtype=np.int32)
+        acc = C.c_uint32()
+        check(lib().opure_engine_verify_step(self.h, t.ctypes.data, t.size, seq_len, out.ctypes.data, C.byref(acc)))
+        return int(acc.value), out[:acc.value + 1].tolist()
+
+    def rollback_kv(self, seq_len: int, accepted: int, k: int) -> int:
+        n = C.c_uint32()
+        check(lib().opure_engine_rollback_kv(self.h, seq_len, accepted, k, C.byref(n)))
+        return int(n.value)
+
+    def pages(self, draft: bool = False):
+        """(pages in the pool, pages free, the sequence's page-table row)."""
+        tot, av, n = C.c_uint32(), C.c_uint32(), C.c_uint32()
+        check(lib().opure_engine_pages(self.h, 1 if draft else 0, C.byref(tot), C.byref(av), None, 0, C.byref(n)))
+        row = np.zeros(n.value, dtype=np.int32)
+        check(lib().opure_engine_pages(self.h, 1 if draft else 0, C.byref(tot), C.byref(av), row.ctypes.data, n.value,
+                                       C.byref(n)))
+        return int(tot.value), int(av.value), row
 
     def generate_speculative(self, prompt, n_new: int):
         p = np.ascontiguousarray(prompt, dtype=np.int32)

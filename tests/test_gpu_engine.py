@@ -30,7 +30,7 @@ N_NEW, K, PROMPT = 64, 4, 32
 def models():
     dev = H.Dev(0)
     cfg = synth.CONFIGS["c1"]
-    max_pos = PROMPT + N_NEW + 2 * K + 16
+    max_pos = 256                         # cache and RoPE capacity: prompt + 112 new + K + 1, rounded up
     say("building c1 target (30 layers) and draft (2 layers) on the device")
     tgt = synth.SynthModel(dev, cfg, seed=1234, max_pos=max_pos)
     drf = synth.SynthModel(dev, dict(cfg, n_layers=2), seed=4321, max_pos=max_pos)
@@ -129,9 +129,20 @@ def test_partial_acceptance_matches_oracle_c1(models):
     d = H.Model()
     C.memmove(C.byref(d), C.byref(tgt.desc), C.sizeof(H.Model))
     d.n_layers = 29
-    n_new = 24
+    n_new = 112
     eng = E.Engine(dev, tgt.desc, d, max_positions=max_pos, draft_tokens=K)
-    spec, hist, _ = eng.generate_speculative(prompt, n_new)
+    spec, hist, st = eng.generate_speculative(prompt, n_new)
+    # every page of the target's pool is held by the sequence or free, once:
+    # the sequence holds exactly the pages of its kept positions, the rollbacks
+    # of ~30 steps having returned the rest
+    total, avail, row = eng.pages()
+    held = row[row >= 0]
+    kept = len(prompt) + st.verify_steps + st.accepted_total
+    assert len(set(held.tolist())) == len(held) == -(-kept // 16)
+    assert avail == total - len(held)
+    dt, da, drow = eng.pages(draft=True)
+    dheld = drow[drow >= 0]
+    assert len(set(dheld.tolist())) == len(dheld) and da == dt - len(dheld)
     eng.close()
     w = tgt.download()
     want, want_hist = oracle_speculative(tgt.cfg, w, dict(tgt.cfg, n_layers=29), dict(w, layers=w["layers"][:29]),
@@ -139,4 +150,60 @@ def test_partial_acceptance_matches_oracle_c1(models):
     say("29-layer draft accepted per step", hist.tolist(), "oracle", want_hist)
     assert spec.tolist() == want
     assert hist.tolist() == want_hist
+    assert len(want_hist) >= 30
     assert 0 < sum(want_hist) < K * len(want_hist)
+
+
+def test_verify_step_and_rollback_kv_c1(models):
+    """The engine's VerifyStep and RollbackKV on their own: rows scored against
+    the target's greedy continuation (a K+1-row step equals K+1 decode steps),
+    a rejected draft, and the rollback giving the page past the kept length
+    back to the pool."""
+    dev, tgt, _, prompt, max_pos = models
+    eng = E.Engine(dev, tgt.desc, None, max_positions=max_pos, draft_tokens=K)
+    p, ctx = prompt[:30], 30
+    g, _ = eng.generate(p, K + 2)                 # g[0] after the prompt, g[1..] its continuation
+    g = g.tolist()
+    bad = [g[0], (g[1] + 1) % 49152] + g[2:K + 1]
+    acc, emitted = eng.verify_step(bad, ctx)
+    assert (acc, emitted) == (0, [g[1]])
+    assert eng.rollback_kv(ctx, acc, K) == ctx + 1
+    total, avail, row = eng.pages()
+    held = row[row >= 0]
+    assert len(held) == 2 and avail == total - 2          # positions 0..30: pages 0 and 1; page 2 went back
+    acc, emitted = eng.verify_step(g[:K + 1], ctx)
+    assert (acc, emitted) == (K, g[1:K + 2])
+    assert eng.rollback_kv(ctx, acc, K) == ctx + K + 1
+    total, avail, row = eng.pages()
+    assert (row >= 0).sum() == 3 and avail == total - 3
+    m = eng.metrics()
+    assert (m.verify_steps, m.drafts_proposed, m.drafts_accepted) == (2, 2 * K, K)
+    eng.close()
+
+
+def test_prefill_256_rows_engine():
+    """A quantised model's 300-token prompt is prefilled 256 rows a launch
+    (16 parts x 16 rows on one page-table row), then 32, then 11 in a 16-row
+    step: the greedy continuation equals the oracle's (every decision's top-2
+    gap is well above the logit bar)."""
+    from test_gpu_verify import small_model
+    from gpu_util import device_model
+    m = small_model(O.W_I8PC, O.A_F16, max_pos=512)
+    prompt = list(np.random.default_rng(0).integers(0, m.cfg["vocab"], 300))
+    dev = H.Dev(0)
+    try:
+        dm = device_model(dev, m)
+        eng = E.Engine(dev, dm.desc, None, max_positions=400, draft_tokens=K)
+        got, _ = eng.generate(prompt, 4)
+        eng.close()
+    finally:
+        dev.close()
+    kv = O.HostKV(m, n_pages=32, batch=1, max_pages_per_seq=32)
+    kv.page_table[0] = np.arange(32)
+
+    def step(_key, toks, ctx):
+        return O.verify_forward(m, kv, toks, np.array([ctx], np.int32))
+
+    want, gaps = spec_loop.greedy(step, prompt, 4)
+    assert min(gaps) > 4e-2
+    assert got.tolist() == want

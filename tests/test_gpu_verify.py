@@ -366,3 +366,44 @@ def test_batched_verify_greedy_matches_oracle(dev):
     w_out, w_acc = O.accept_greedy(got, tokens[:, 1:])
     assert np.array_equal(out, w_out) and np.array_equal(acc, w_acc)
     assert acc[2] == R - 1
+
+
+def test_prefill_256_rows_on_one_page_table_row(dev):
+    """A 300-token prompt written by one verify step of 16 parts x 16 rows
+    that share the prompt's page-table row (part b at start + 16 b: its rows see
+    every earlier part's K/V, appended by the same launch before attention), a
+    second of 2 parts, then a 12-row step: the last 12 rows' logits agree with
+    the oracle's one pass over all 300 rows (the wide parts run every GEMV as a
+    thin GEMM)."""
+    m = small_model(O.W_I8PC, O.A_F16, max_pos=512)
+    V, P = m.cfg["vocab"], 300
+    mp = (P + 15) // 16
+    kv = O.HostKV(m, n_pages=mp + 8, batch=1, max_pages_per_seq=mp)
+    rng = np.random.default_rng(41)
+    kv.page_table[0] = rng.permutation(mp + 8)[:mp]
+    prompt = rng.integers(0, V, size=P).astype(np.int32)
+    want = O.verify_forward(m, kv, prompt[None, :], np.array([0], np.int32))[0, -12:]
+    dm = device_model(dev, m)
+    wide = H.DeviceKV(dev, m.cfg, mp + 8, 16, mp)
+    wide.set_page_table(np.repeat(kv.page_table, 16, axis=0))
+    toks = dev.alloc(256 * 4)
+    sl = dev.alloc(16 * 4)
+    for start, parts in ((0, 16), (256, 2)):
+        dev.write(toks, prompt[start:start + 16 * parts])
+        dev.write(sl, np.arange(parts, dtype=np.int32) * 16 + start)
+        a = H.VerifyArgs()
+        a.model = C.pointer(dm.desc)
+        a.kv = C.pointer(wide.desc)
+        a.batch, a.rows, a.max_ctx = parts, 16, mp * 16
+        a.tokens, a.seq_len, a.logits = int(toks), int(sl), None
+        H.check(H.lib().opure_verify_step(dev.h, C.byref(a)))
+    dev.sync()
+    one = H.DeviceKV.__new__(H.DeviceKV)
+    one.__dict__.update(wide.__dict__)
+    one.desc = H.KV(int(wide.pool), mp + 8, 16, int(wide.page_table), mp)   # row 0 of the same table
+    one.batch = 1
+    run = VerifyRunner(dev, dm, one, 1, 12, mp * 16)
+    run.step(prompt[None, 288:], [288])
+    err = np.abs(run.get_logits()[0] - want).max()
+    say("prefill 256 rows: last 12 rows max_abs", err)
+    assert err <= 2e-2
