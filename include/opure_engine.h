@@ -103,6 +103,116 @@ typedef struct opure_engine_metrics {
 int opure_engine_get_metrics(const opure_engine* e, opure_engine_metrics* out);
 int opure_engine_reset_metrics(opure_engine* e);
 
+/* ---- model directories: config.json + model.safetensors (or the shards of
+ *      model.safetensors.index.json) in the Llama layout.  Replaces the
+ *      reference's Graph::LoadConfigOnly / UploadWeights and
+ *      ModelSpec::Resolve (src/engine/Opure_Graph.cpp:267-300, :430-530;
+ *      src/engine/Opure_ModelSpec.cpp:120-320) and its safetensors reader
+ *      (src/core/Opure_Streamer.h), whose packed-int4 sizes and per-tensor
+ *      scale uploads are wrong (ElementBytes(I4) = 1, Opure_Streamer.cpp:
+ *      104-117; every scale uploaded from one loop variable's address,
+ *      Opure_Graph.cpp:521-527).
+ *
+ *      Stored forms (X = e.g. model.layers.0.self_attn.q_proj):
+ *        float      X.weight F32 / F16 / BF16 [out][in]
+ *        int8 pc    X.weight I8 [out][in], X.weight_scale F16 [out] (or [out][1])
+ *        int4 g128  X.weight U8 [out][in/2] or U4 [out][in], element 2i in the
+ *                   high nibble; X.weight_scale BF16 [out][in/128];
+ *                   X.weight_zero BF16 [out][in/128] (absent: 0);
+ *                   w = scale * (q - zero).  I4 [out][in]: signed, zero 8.
+ *        the reference's form: I8 / U4 / I4 with a "scale" number in the
+ *                   header entry, w = q * scale (per tensor)
+ *      q/k/v and gate/up are fused on load; a float linear of a model that
+ *      computes in int8 / int4 is quantised on the device at load time.
+ *      config.json: vocab_size, hidden_size, intermediate_size,
+ *      num_hidden_layers, num_attention_heads, num_key_value_heads, head_dim,
+ *      max_position_embeddings, rms_norm_eps, rope_theta, tie_word_embeddings
+ *      (default true, as the reference), quantization_config.activation_dtype
+ *      ("float16" | "bfloat16" | "float32").  hidden_act other than silu,
+ *      bias terms, rope_scaling and head_dim other than 64 / 128 are
+ *      OPURE_E_UNSUPPORTED. */
+enum {
+    OPURE_ROLE_EMBED = 0, OPURE_ROLE_LM_HEAD = 1, OPURE_ROLE_QKV = 2, OPURE_ROLE_O = 3, OPURE_ROLE_GATE_UP = 4,
+    OPURE_ROLE_DOWN = 5, OPURE_ROLE_ATTN_NORM = 6, OPURE_ROLE_MLP_NORM = 7, OPURE_ROLE_FINAL_NORM = 8
+};
+
+typedef struct opure_load_options {
+    uint32_t max_positions;   /* RoPE table rows; 0: config.json's max_position_embeddings */
+    int32_t  wfmt;            /* OPURE_W_* to compute in; -1: as stored (the first q_proj's form) */
+    int32_t  afmt;            /* OPURE_A_*; -1: quantization_config.activation_dtype, else F32 / F16 / BF16
+                               * for float / int8 / int4 weights */
+    float    attn_scale;      /* 0: 1/sqrt(head_dim); 1.0: the reference's unscaled scores */
+} opure_load_options;
+
+typedef struct opure_model_info {
+    uint32_t n_layers, hidden, n_heads, n_kv_heads, head_dim, ffn, vocab, max_position_embeddings;
+    float    rms_eps, attn_scale;
+    double   rope_theta;
+    uint32_t tied;
+    uint32_t stored_wfmt;     /* form of the first q_proj on disk */
+    uint32_t wfmt, afmt;      /* what the loaded model computes in */
+    uint32_t rope_max_pos;
+    uint32_t n_tensors;
+    uint64_t file_bytes;
+} opure_model_info;
+
+/* Host half of loading (no device calls): config.json parsed, weights mapped,
+ * every tensor found and shape-checked.  opts may be NULL (all defaults). */
+typedef struct opure_model_files opure_model_files;
+int opure_model_files_open(const char* model_dir, const opure_load_options* opts, opure_model_files** out);
+int opure_model_files_info(const opure_model_files* f, opure_model_info* out);
+/* One role (layer ignored for EMBED, LM_HEAD, FINAL_NORM) in the row-major
+ * interchange form of opure_hip.h, as stored (float linears widened to fp32;
+ * norms: out = hidden, in = 1, fp32).  The buffers belong to f and stay
+ * valid until the next read or close. */
+typedef struct opure_host_linear {
+    uint32_t wfmt, out, in;
+    const void* w;
+    const void* scale;
+    const void* zero;
+    uint64_t w_bytes, scale_bytes, zero_bytes;
+} opure_host_linear;
+int opure_model_files_read(opure_model_files* f, uint32_t role, uint32_t layer, opure_host_linear* out);
+int opure_model_files_close(opure_model_files* f);
+
+/* A model directory on the device, tiled, with its RoPE table: *desc is
+ * valid (and its weights resident) until opure_model_unload. */
+typedef struct opure_loaded_model opure_loaded_model;
+int opure_model_load(opure_dev* dev, const char* model_dir, const opure_load_options* opts, opure_loaded_model** out);
+int opure_loaded_model_desc(const opure_loaded_model* m, const opure_model** desc, uint64_t* device_bytes);
+int opure_model_unload(opure_loaded_model* m);
+
+/* Initialize(modelDir, ...) of the reference (Opure_VoxelEngine.h:127-140):
+ * loads the target (and the draft, when draft_dir is not NULL) from their
+ * directories and creates an engine that owns them; opure_engine_destroy
+ * frees the models too. */
+int opure_engine_initialize(opure_dev* dev, const char* target_dir, const char* draft_dir,
+                            const opure_load_options* load, const opure_engine_options* opts, opure_engine** out);
+
+/* ---- safetensors files, read-only (host, no device calls) */
+typedef struct opure_safetensors opure_safetensors;
+enum { OPURE_DT_F32 = 0, OPURE_DT_F16 = 1, OPURE_DT_BF16 = 2, OPURE_DT_U8 = 3, OPURE_DT_I8 = 4, OPURE_DT_U4 = 5,
+       OPURE_DT_I4 = 6 };
+typedef struct opure_tensor_info {
+    const char* name;         /* valid while the file is open */
+    uint32_t dtype;           /* OPURE_DT_* */
+    uint32_t ndim;            /* <= 8 */
+    int64_t  shape[8];
+    uint64_t offset;          /* bytes from the start of the file */
+    uint64_t bytes;           /* stored bytes (packed 4-bit: two elements a byte) */
+    const void* data;         /* in the read-only mapping */
+    uint32_t has_scale;       /* the entry carries the reference's "scale" key */
+    double   scale;
+} opure_tensor_info;
+/* Maps the file and checks every entry's byte span against its shape and
+ * dtype; OPURE_E_INVALID names the first bad entry. */
+int opure_safetensors_open(const char* path, opure_safetensors** out);
+int opure_safetensors_count(const opure_safetensors* f, uint32_t* n);
+int opure_safetensors_tensor(const opure_safetensors* f, uint32_t i, opure_tensor_info* out);
+/* OPURE_E_INVALID when absent */
+int opure_safetensors_find(const opure_safetensors* f, const char* name, opure_tensor_info* out);
+int opure_safetensors_close(opure_safetensors* f);
+
 /* ---- page pool: the free list of a paged KV pool's pages (host bookkeeping,
  *      no device calls).  Sequences own 16-token pages through their
  *      page-table rows (opure_kv.page_table); a row takes pages as the

@@ -4,16 +4,36 @@
 // ============================================================================
 #include <cstring>
 #include <exception>
+#include <memory>
 #include <new>
 #include <string>
 #include <vector>
 
+#include "model_loader.h"
 #include "opure_engine.h"
 #include "page_pool.h"
 #include "voxel_engine.h"
+#include "weight_streamer.h"
 
 struct opure_engine {
+    // models loaded by opure_engine_initialize; declared first so the engine
+    // (which borrows them) is destroyed before them
+    std::unique_ptr<opure::engine::LoadedModel> target, draft;
     opure::engine::VoxelEngine impl;
+};
+
+struct opure_model_files {
+    opure_model_files(const std::string& dir, const opure::engine::LoadOptions& o) : impl(dir, o) {}
+    opure::engine::ModelFiles impl;
+    opure::engine::HostLinear last;   // the buffers of the last read
+};
+
+struct opure_loaded_model {
+    std::unique_ptr<opure::engine::LoadedModel> impl;
+};
+
+struct opure_safetensors {
+    opure::engine::WeightStreamer impl;
 };
 
 struct opure_page_pool {
@@ -65,6 +85,44 @@ void fill_stats(opure_engine_stats* st, const opure::engine::GenerateResult& r)
     st->ms_generate = r.msGenerate;
 }
 
+opure::engine::LoadOptions load_options(const opure_load_options* o)
+{
+    opure::engine::LoadOptions r;
+    if (o)
+    {
+        r.maxPositions = o->max_positions;
+        r.wfmt = o->wfmt;
+        r.afmt = o->afmt;
+        r.attnScale = o->attn_scale;
+    }
+    return r;
+}
+
+opure::engine::EngineOptions engine_options(const opure_engine_options* opts)
+{
+    opure::engine::EngineOptions o;
+    o.maxPositions = opts->max_positions;
+    o.draftTokens = opts->draft_tokens;
+    o.useGraphs = opts->use_graphs != 0;
+    o.stopToken = opts->stop_token;
+    return o;
+}
+
+void tensor_info(const opure::engine::WeightStreamer& f, const opure::engine::Tensor& t, opure_tensor_info* out)
+{
+    std::memset(out, 0, sizeof(*out));
+    if (t.shape.size() > 8) throw opure::engine::Error(OPURE_E_UNSUPPORTED, "safetensors: '" + t.name + "' has more than 8 dimensions");
+    out->name = t.name.c_str();
+    out->dtype = static_cast<uint32_t>(t.dtype);
+    out->ndim = static_cast<uint32_t>(t.shape.size());
+    for (size_t i = 0; i < t.shape.size(); ++i) out->shape[i] = t.shape[i];
+    out->offset = t.byteBegin;
+    out->bytes = t.ByteCount();
+    out->data = f.Data(t);
+    out->has_scale = t.hasHeaderScale ? 1u : 0u;
+    out->scale = t.headerScale;
+}
+
 std::vector<uint32_t> to_tokens(const int32_t* p, uint32_t n)
 {
     std::vector<uint32_t> v(n);
@@ -89,13 +147,29 @@ int opure_engine_create(opure_dev* dev, const opure_model* target, const opure_m
     *out = nullptr;
     opure_engine* e = new (std::nothrow) opure_engine();
     if (!e) return fail(OPURE_E_OOM, "opure_engine_create: host allocation failed");
+    const int rc = guarded([&] { e->impl.Initialize(dev, *target, draft, engine_options(opts)); });
+    if (rc != OPURE_OK)
+    {
+        delete e;
+        return rc;
+    }
+    *out = e;
+    return OPURE_OK;
+}
+
+int opure_engine_initialize(opure_dev* dev, const char* target_dir, const char* draft_dir,
+                            const opure_load_options* load, const opure_engine_options* opts, opure_engine** out)
+{
+    if (!out || !dev || !target_dir || !opts) return fail(OPURE_E_INVALID, "opure_engine_initialize: null argument");
+    *out = nullptr;
+    opure_engine* e = new (std::nothrow) opure_engine();
+    if (!e) return fail(OPURE_E_OOM, "opure_engine_initialize: host allocation failed");
     const int rc = guarded([&] {
-        opure::engine::EngineOptions o;
-        o.maxPositions = opts->max_positions;
-        o.draftTokens = opts->draft_tokens;
-        o.useGraphs = opts->use_graphs != 0;
-        o.stopToken = opts->stop_token;
-        e->impl.Initialize(dev, *target, draft, o);
+        const auto lo = load_options(load);
+        e->target = std::make_unique<opure::engine::LoadedModel>(dev, opure::engine::ModelFiles(target_dir, lo));
+        if (draft_dir)
+            e->draft = std::make_unique<opure::engine::LoadedModel>(dev, opure::engine::ModelFiles(draft_dir, lo));
+        e->impl.Initialize(dev, e->target->Desc(), e->draft ? &e->draft->Desc() : nullptr, engine_options(opts));
     });
     if (rc != OPURE_OK)
     {
@@ -103,6 +177,127 @@ int opure_engine_create(opure_dev* dev, const opure_model* target, const opure_m
         return rc;
     }
     *out = e;
+    return OPURE_OK;
+}
+
+int opure_model_files_open(const char* model_dir, const opure_load_options* opts, opure_model_files** out)
+{
+    if (!model_dir || !out) return fail(OPURE_E_INVALID, "opure_model_files_open: null argument");
+    *out = nullptr;
+    return guarded([&] { *out = new opure_model_files(model_dir, load_options(opts)); });
+}
+
+int opure_model_files_info(const opure_model_files* f, opure_model_info* out)
+{
+    if (!f || !out) return fail(OPURE_E_INVALID, "opure_model_files_info: null argument");
+    const auto& m = f->impl;
+    const auto& c = m.Config();
+    std::memset(out, 0, sizeof(*out));
+    out->n_layers = c.nLayers;
+    out->hidden = c.hidden;
+    out->n_heads = c.nHeads;
+    out->n_kv_heads = c.nKvHeads;
+    out->head_dim = c.headDim;
+    out->ffn = c.ffn;
+    out->vocab = c.vocab;
+    out->max_position_embeddings = c.maxPositionEmbeddings;
+    out->rms_eps = c.rmsEps;
+    out->attn_scale = m.AttnScale();
+    out->rope_theta = c.ropeTheta;
+    out->tied = c.tied ? 1u : 0u;
+    out->stored_wfmt = m.StoredWfmt();
+    out->wfmt = m.Wfmt();
+    out->afmt = m.Afmt();
+    out->rope_max_pos = m.MaxPositions();
+    out->n_tensors = m.TensorCount();
+    out->file_bytes = m.FileBytes();
+    return OPURE_OK;
+}
+
+int opure_model_files_read(opure_model_files* f, uint32_t role, uint32_t layer, opure_host_linear* out)
+{
+    if (!f || !out) return fail(OPURE_E_INVALID, "opure_model_files_read: null argument");
+    if (role > OPURE_ROLE_FINAL_NORM) return fail(OPURE_E_INVALID, "opure_model_files_read: role " + std::to_string(role));
+    return guarded([&] {
+        f->last = f->impl.Read(static_cast<opure::engine::Role>(role), layer);
+        const auto& h = f->last;
+        out->wfmt = h.wfmt;
+        out->out = h.out;
+        out->in = h.in;
+        out->w = h.w.data();
+        out->scale = h.scale.empty() ? nullptr : h.scale.data();
+        out->zero = h.zero.empty() ? nullptr : h.zero.data();
+        out->w_bytes = h.w.size();
+        out->scale_bytes = h.scale.size();
+        out->zero_bytes = h.zero.size();
+    });
+}
+
+int opure_model_files_close(opure_model_files* f)
+{
+    delete f;
+    return OPURE_OK;
+}
+
+int opure_model_load(opure_dev* dev, const char* model_dir, const opure_load_options* opts, opure_loaded_model** out)
+{
+    if (!dev || !model_dir || !out) return fail(OPURE_E_INVALID, "opure_model_load: null argument");
+    *out = nullptr;
+    return guarded([&] {
+        auto m = std::make_unique<opure_loaded_model>();
+        m->impl = std::make_unique<opure::engine::LoadedModel>(dev, opure::engine::ModelFiles(model_dir, load_options(opts)));
+        *out = m.release();
+    });
+}
+
+int opure_loaded_model_desc(const opure_loaded_model* m, const opure_model** desc, uint64_t* device_bytes)
+{
+    if (!m || !desc) return fail(OPURE_E_INVALID, "opure_loaded_model_desc: null argument");
+    *desc = &m->impl->Desc();
+    if (device_bytes) *device_bytes = m->impl->DeviceBytes();
+    return OPURE_OK;
+}
+
+int opure_model_unload(opure_loaded_model* m)
+{
+    delete m;
+    return OPURE_OK;
+}
+
+int opure_safetensors_open(const char* path, opure_safetensors** out)
+{
+    if (!path || !out) return fail(OPURE_E_INVALID, "opure_safetensors_open: null argument");
+    *out = nullptr;
+    return guarded([&] {
+        auto f = std::make_unique<opure_safetensors>();
+        f->impl.Open(path);
+        *out = f.release();
+    });
+}
+
+int opure_safetensors_count(const opure_safetensors* f, uint32_t* n)
+{
+    if (!f || !n) return fail(OPURE_E_INVALID, "opure_safetensors_count: null argument");
+    *n = static_cast<uint32_t>(f->impl.Tensors().size());
+    return OPURE_OK;
+}
+
+int opure_safetensors_tensor(const opure_safetensors* f, uint32_t i, opure_tensor_info* out)
+{
+    if (!f || !out) return fail(OPURE_E_INVALID, "opure_safetensors_tensor: null argument");
+    if (i >= f->impl.Tensors().size()) return fail(OPURE_E_INVALID, "opure_safetensors_tensor: index past the end");
+    return guarded([&] { tensor_info(f->impl, f->impl.Tensors()[i], out); });
+}
+
+int opure_safetensors_find(const opure_safetensors* f, const char* name, opure_tensor_info* out)
+{
+    if (!f || !name || !out) return fail(OPURE_E_INVALID, "opure_safetensors_find: null argument");
+    return guarded([&] { tensor_info(f->impl, f->impl.Find(name), out); });
+}
+
+int opure_safetensors_close(opure_safetensors* f)
+{
+    delete f;
     return OPURE_OK;
 }
 

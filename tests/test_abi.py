@@ -93,26 +93,29 @@ def test_struct_layouts_match_header(tmp_path):
 def engine_symbols():
     text = open(os.path.join(ROOT, "include", "opure_engine.h")).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(opure_engine_[a-z0-9_]+)\s*\(", text)))
+    return sorted(set(re.findall(r"^\s*(?:int|const char\s*\*)\s+(opure_[a-z0-9_]+)\s*\(", text, flags=re.M)))
 
 
 def test_engine_library_exports_every_declared_symbol():
     import opure_engine as E
     L = E.lib()
     names = engine_symbols()
-    assert len(names) >= 5
+    assert len(names) >= 25 and "opure_model_load" in names and "opure_page_pool_grow_seq" in names
     assert not [n for n in names if not hasattr(L, n)]
 
 
 def test_engine_struct_layouts_match_header(tmp_path):
     import subprocess
     import opure_engine as E
-    structs = {"opure_engine_options": E.Options, "opure_engine_stats": E.Stats}
+    structs = {"opure_engine_options": E.Options, "opure_engine_stats": E.Stats, "opure_engine_metrics": E.Metrics,
+               "opure_load_options": E.LoadOptions, "opure_model_info": E.ModelInfo,
+               "opure_host_linear": E.HostLinearC, "opure_tensor_info": E.TensorInfo}
+    cname_of = {"in_": "in"}
     lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "opure_engine.h"', "int main(void){"]
     for cname, cls in structs.items():
         lines.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')
         for fname, _ in cls._fields_:
-            lines.append(f'printf("{cname} {fname} %zu\\n", offsetof({cname}, {fname}));')
+            lines.append(f'printf("{cname} {fname} %zu\\n", offsetof({cname}, {cname_of.get(fname, fname)}));')
     lines.append("return 0;}")
     src = tmp_path / "probe.c"
     src.write_text("\n".join(lines))
@@ -137,3 +140,10 @@ def test_engine_error_paths_without_device():
     assert L.opure_engine_generate(None, None, 0, 0, None, None) == H.E_INVALID
     assert L.opure_engine_generate_speculative(None, None, 0, 0, None, None, 0, None) == H.E_INVALID
     assert L.opure_engine_destroy(None) == H.OK
+    assert L.opure_model_files_open(None, None, C.byref(h)) == H.E_INVALID
+    assert L.opure_model_load(None, b"/nonexistent", None, C.byref(h)) == H.E_INVALID
+    assert L.opure_engine_initialize(None, None, None, None, None, C.byref(h)) == H.E_INVALID
+    assert L.opure_safetensors_open(b"/nonexistent/model.safetensors", C.byref(h)) == H.E_INVALID
+    assert b"cannot open" in L.opure_engine_last_error()
+    assert L.opure_model_files_open(b"/nonexistent", None, C.byref(h)) == H.E_INVALID
+    assert b"config.json" in L.opure_engine_last_error()
