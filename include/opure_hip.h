@@ -300,7 +300,7 @@ int opure_philox_uniform(opure_dev* dev, uint64_t seed, const uint32_t* pos, con
 typedef struct opure_rollback_args {
     const opure_model* model;
     const opure_kv*    kv;           /* kv->page_table is updated in place */
-    uint32_t           batch, k;
+    uint32_t           batch, k;     /* k + 1 <= OPURE_MAX_ROWS (the rows of the verify step rolled back) */
     const int32_t*     seq_len;
     const int32_t*     accepted;
     int32_t*           new_seq_len;

@@ -207,21 +207,44 @@ struct RollbackParams {
     uint32_t poison, poison_bits;
 };
 
+// What a sequence's rollback reads before it can decide anything: its
+// context length and the page-table entries of positions ctx .. ctx + K (at
+// most two pages, K + 1 <= 16).  Loaded together, early, by one thread.
+struct RollbackPre {
+    uint32_t ctx;
+    int32_t pte[2];           // entries ctx/16 and ctx/16 + 1 (-1 past the table)
+};
+
+__device__ __forceinline__ RollbackPre rollback_pre(const RollbackParams& p, uint32_t b)
+{
+    RollbackPre r;
+    r.ctx = static_cast<uint32_t>(p.seq_len[b]);
+    const int32_t* pt = p.page_table + static_cast<uint64_t>(b) * p.max_pages;
+    const uint32_t q0 = r.ctx / OPURE_PAGE_SIZE;
+    r.pte[0] = q0 < p.max_pages ? pt[q0] : -1;
+    r.pte[1] = q0 + 1u < p.max_pages ? pt[q0 + 1u] : -1;
+    return r;
+}
+
 // Rollback of sequence b, run by one workgroup: poison the rolled-back slots,
-// then release the pages wholly past the new length.
-__device__ void rollback_seq(const RollbackParams& p, uint32_t b, uint32_t acc)
+// then release the pages wholly past the new length.  `pre` (from
+// rollback_pre, shared by the workgroup) holds everything read before the
+// writes, so the rollback costs no further round trip to memory.
+__device__ void rollback_seq(const RollbackParams& p, uint32_t b, uint32_t acc, const RollbackPre& pre)
 {
     int32_t* pt = p.page_table + static_cast<uint64_t>(b) * p.max_pages;
-    const uint32_t ctx = static_cast<uint32_t>(p.seq_len[b]);
+    const uint32_t ctx = pre.ctx, q0 = ctx / OPURE_PAGE_SIZE;
     if (acc > p.K) acc = p.K;
     const uint32_t old_end = ctx + p.K + 1u, nl = ctx + acc + 1u;
+    // positions nl .. old_end - 1 lie in pages q0 and q0 + 1
+    auto entry = [&](uint32_t q) { return pre.pte[q - q0]; };
     if (p.poison)
     {
         const uint32_t per_pos = p.n_layers * 2u * p.n_kv * p.hd;
         for (uint32_t pos = nl; pos < old_end; ++pos)
         {
             if (pos / OPURE_PAGE_SIZE >= p.max_pages) break;
-            const int32_t page = pt[pos / OPURE_PAGE_SIZE];
+            const int32_t page = entry(pos / OPURE_PAGE_SIZE);
             if (page < 0 || static_cast<uint32_t>(page) >= p.n_pages) continue;
             for (uint32_t e = threadIdx.x; e < per_pos; e += blockDim.x)
             {
@@ -246,8 +269,8 @@ __device__ void rollback_seq(const RollbackParams& p, uint32_t b, uint32_t acc)
             const uint32_t last_used = (old_end - 1u) / OPURE_PAGE_SIZE;
             for (uint32_t q = first_free; q <= last_used && q < p.max_pages; ++q)
             {
-                if (pt[q] < 0) continue;
-                if (static_cast<uint32_t>(nf) < p.freed_stride) p.freed[static_cast<uint64_t>(b) * p.freed_stride + nf] = pt[q];
+                if (entry(q) < 0) continue;
+                if (static_cast<uint32_t>(nf) < p.freed_stride) p.freed[static_cast<uint64_t>(b) * p.freed_stride + nf] = entry(q);
                 pt[q] = -1;
                 ++nf;
             }
@@ -258,7 +281,15 @@ __device__ void rollback_seq(const RollbackParams& p, uint32_t b, uint32_t acc)
 
 __global__ __launch_bounds__(256) void k_rollback(RollbackParams p)
 {
-    rollback_seq(p, blockIdx.x, static_cast<uint32_t>(p.accepted[blockIdx.x]));
+    __shared__ RollbackPre pre;
+    __shared__ uint32_t acc;
+    if (threadIdx.x == 0)
+    {
+        pre = rollback_pre(p, blockIdx.x);
+        acc = static_cast<uint32_t>(p.accepted[blockIdx.x]);
+    }
+    __syncthreads();
+    rollback_seq(p, blockIdx.x, acc, pre);
 }
 
 struct GreedyParams {
@@ -286,9 +317,14 @@ __global__ __launch_bounds__(GNT) void k_accept_greedy(GreedyParams p)
     __shared__ float sv[NWV][RB];
     __shared__ int32_t si[NWV][RB];
     __shared__ int32_t am[64];
+    __shared__ int32_t sdraft[OPURE_MAX_ROWS];
+    __shared__ RollbackPre pre;
     __shared__ uint32_t s_n;
     const uint32_t b = blockIdx.x, R = p.K + 1u;
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    // the drafts and the rollback's reads, in flight with the partials below
+    if (threadIdx.x < p.K) sdraft[threadIdx.x] = p.drafts[static_cast<uint64_t>(b) * p.drafts_stride + threadIdx.x];
+    if (p.rollback && threadIdx.x == 64u) pre = rollback_pre(p.rb, b);
     for (uint32_t r0 = 0; r0 < R; r0 += RB)
     {
         const uint32_t nr = min(RB, R - r0);
@@ -350,14 +386,14 @@ __global__ __launch_bounds__(GNT) void k_accept_greedy(GreedyParams p)
     if (threadIdx.x == 0)
     {
         uint32_t n = 0;
-        while (n < p.K && am[n] == p.drafts[static_cast<uint64_t>(b) * p.drafts_stride + n]) ++n;
-        for (uint32_t j = 0; j < R; ++j)
-            p.out_tokens[b * R + j] = j < n ? p.drafts[static_cast<uint64_t>(b) * p.drafts_stride + j] : (j == n ? am[n] : -1);
-        p.accepted[b] = static_cast<int32_t>(n);
+        while (n < p.K && am[n] == sdraft[n]) ++n;
         s_n = n;
     }
     __syncthreads();
-    if (p.rollback) rollback_seq(p.rb, b, s_n);
+    const uint32_t n = s_n;
+    if (threadIdx.x < R) p.out_tokens[b * R + threadIdx.x] = threadIdx.x < n ? sdraft[threadIdx.x] : (threadIdx.x == n ? am[n] : -1);
+    if (threadIdx.x == 0) p.accepted[b] = static_cast<int32_t>(n);
+    if (p.rollback) rollback_seq(p.rb, b, n, pre);
 }
 
 // ---------------------------------------------------------------------------
@@ -973,6 +1009,10 @@ int rollback_validate(const opure_rollback_args* a)
     OPURE_REQUIRE(a && a->model && a->kv && a->kv->pool && a->kv->page_table && a->seq_len && a->accepted &&
                       a->new_seq_len, OPURE_E_INVALID, "rollback: null argument");
     OPURE_REQUIRE(a->batch >= 1 && a->kv->page_size == OPURE_PAGE_SIZE, OPURE_E_INVALID, "rollback: bad shape");
+    // a rollback follows a verify step of k + 1 <= OPURE_MAX_ROWS rows, so its
+    // positions lie in two pages at most
+    OPURE_REQUIRE(a->k + 1u <= OPURE_MAX_ROWS, OPURE_E_CAPACITY, "rollback: k = %u drafts, more than a verify step holds",
+                  a->k);
     // the K positions past seq_len hold at most ceil(K / page) page starts: the
     // most pages one rollback can release into a sequence's freed row
     const uint32_t most = a->k == 0u ? 1u : (a->k + OPURE_PAGE_SIZE - 1u) / OPURE_PAGE_SIZE;

@@ -368,36 +368,55 @@ __global__ __launch_bounds__(NWV * 64) void k_attn_mfma(AttnParams p)
     const uint32_t kh = blockIdx.x, c = blockIdx.y, b = blockIdx.z;
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u, g = lane >> 4, r = lane & 15u;
     const uint32_t group = p.n_heads / p.n_kv, R = p.rows, Gq = group * R;
-    const uint32_t ctx = static_cast<uint32_t>(p.seq_len[b]);
-    const uint32_t total = ctx + R;
     const uint32_t t0 = c * NWV * TPW;
-    if (t0 >= total) return;                          // whole workgroup: no row reaches this chunk
     const uint32_t tw = t0 + TPW * wave;
     const int32_t* pt = p.page_table + static_cast<uint64_t>(b) * p.max_pages;
     const uint8_t* pool = static_cast<const uint8_t*>(p.pool);
     const uint32_t nan2 = AF == OPURE_A_F16 ? 0x7E007E00u : 0x7FC07FC0u;
-    const bool active = tw < total;
 
-    // page of a token, -1 if missing (read as NaN) or past the table
-    auto page_of = [&](uint32_t tok) -> int32_t {
-        if (tok / OPURE_PAGE_SIZE >= p.max_pages) return -1;
-        const int32_t pg = pt[tok / OPURE_PAGE_SIZE];
-        return (pg >= 0 && static_cast<uint32_t>(pg) < p.n_pages) ? pg : -1;
+    // ---- the sequence length, the page-table entries of this wave's tokens
+    //      and Q^T in one round trip: none of them depends on another, and the
+    //      entries are loaded unconditionally (index clamped to the table) and
+    //      checked only when used, so no load waits behind another -----------
+    const int32_t seq = p.seq_len[b];
+    int32_t pgk[KK][2], pgv[KK];
+    auto raw_entry = [&](uint32_t tok) { return pt[min(tok / OPURE_PAGE_SIZE, p.max_pages - 1u)]; };
+#pragma unroll
+    for (uint32_t kk = 0; kk < KK; ++kk)
+    {
+        const uint32_t tb = tw + 32u * kk;
+#pragma unroll
+        for (uint32_t T = 0; T < 2; ++T) pgk[kk][T] = raw_entry(tb + 8u * (r >> 2) + (r & 3u) + 4u * T);
+        pgv[kk] = raw_entry(tb + 8u * g);
+    }
+    // the entry of `tok` as page_of gives it, from its raw load
+    auto checked = [&](uint32_t tok, int32_t pg) -> int32_t {
+        return tok / OPURE_PAGE_SIZE < p.max_pages && pg >= 0 && static_cast<uint32_t>(pg) < p.n_pages ? pg : -1;
     };
-
-    // ---- every load first: Q^T, K (both score tiles of each k-step), V^T ----
     u4v qop[NT][KS];
-    uint32_t lim[NT];
+    uint32_t qj[NT];
 #pragma unroll
     for (int n = 0; n < NT; ++n)
     {
         const uint32_t qi = min(p.qoff + 16u * n + r, Gq - 1u);
         const uint32_t j = qi / group, head = kh * group + (qi - j * group);
-        lim[n] = ctx + j;
+        qj[n] = j;
         const uint8_t* qrow = static_cast<const uint8_t*>(p.q) + ((static_cast<uint64_t>(b * R + j) * p.n_heads + head) * HD) * EB;
 #pragma unroll
         for (uint32_t s = 0; s < KS; ++s) qop[n][s] = *reinterpret_cast<const u4v*>(qrow + (32u * s + 8u * g) * EB);
     }
+    // keeps the loads above issued before the exit below (the compiler would
+    // otherwise test the length first and make them wait for it)
+    asm volatile("" ::: "memory");
+    const uint32_t ctx = static_cast<uint32_t>(seq);
+    const uint32_t total = ctx + R;
+    if (t0 >= total) return;                          // whole workgroup: no row reaches this chunk
+    const bool active = tw < total;
+    uint32_t lim[NT];
+#pragma unroll
+    for (int n = 0; n < NT; ++n) lim[n] = ctx + qj[n];
+
+    // ---- then K (both score tiles of each k-step) and V^T --------------------
     u4v kop[KK][2][KS], vop[KK][DT];
 #pragma unroll
     for (uint32_t kk = 0; kk < KK; ++kk)
@@ -407,7 +426,7 @@ __global__ __launch_bounds__(NWV * 64) void k_attn_mfma(AttnParams p)
         for (uint32_t T = 0; T < 2; ++T)
         {
             const uint32_t tok = tb + 8u * (r >> 2) + (r & 3u) + 4u * T;
-            const int32_t pg = active && tok < total ? page_of(tok) : -1;
+            const int32_t pg = active && tok < total ? checked(tok, pgk[kk][T]) : -1;
             const uint32_t f = active && tok < total ? nan2 : 0u;
 #pragma unroll
             for (uint32_t s = 0; s < KS; ++s)
@@ -417,7 +436,7 @@ __global__ __launch_bounds__(NWV * 64) void k_attn_mfma(AttnParams p)
                                         : u4v{f, f, f, f};
         }
         const uint32_t tok = tb + 8u * g;             // 8 tokens of one page
-        const int32_t pg = active && tok < total ? page_of(tok) : -1;
+        const int32_t pg = active && tok < total ? checked(tok, pgv[kk]) : -1;
         const uint32_t f = active && tok < total ? nan2 : 0u;
 #pragma unroll
         for (uint32_t dt = 0; dt < DT; ++dt)
@@ -607,7 +626,24 @@ __global__ __launch_bounds__(64) void k_attn_combine(AttnParams p)
     const uint32_t R = p.rows, b = rr / R, j = rr - b * R;
     const uint32_t group = p.n_heads / p.n_kv, kh = head / group, qi = j * group + (head - kh * group);
     const uint32_t Gq = group * R, hd = p.hd, lane = threadIdx.x;
-    uint32_t last = (static_cast<uint32_t>(p.seq_len[b]) + j) / p.chunk;
+    const int32_t seq = p.seq_len[b];
+    const uint64_t base = (static_cast<uint64_t>(b) * p.n_kv + kh) * p.nch;
+    // chunks are clamped to the launch's last, not the row's: these loads do
+    // not wait for the sequence length, and chunks past the row's last are
+    // loaded but never used
+    auto acc_at = [&](uint32_t c, int i) {
+        const uint32_t d = min(lane + 64u * i, hd - 1u);
+        return p.part_acc[((base + min(c, p.nch - 1u)) * Gq + qi) * hd + d];
+    };
+    // statistics of chunks lane, lane + 64, ... and the first CB chunks' outputs
+    const uint32_t c0 = min(lane, p.nch - 1u);
+    const float m0 = p.part_ml[((base + c0) * Gq + qi) * 2u], l0 = p.part_ml[((base + c0) * Gq + qi) * 2u + 1u];
+    float v[CB][DPL];
+#pragma unroll
+    for (uint32_t c = 0; c < CB; ++c)
+#pragma unroll
+        for (int i = 0; i < DPL; ++i) v[c][i] = acc_at(c, i);
+    uint32_t last = (static_cast<uint32_t>(seq) + j) / p.chunk;
     if (last >= p.nch)
     {
         // a position beyond the launch's max_ctx: clamped (never read past the
@@ -615,19 +651,6 @@ __global__ __launch_bounds__(64) void k_attn_combine(AttnParams p)
         last = p.nch - 1u;
         if (lane == 0u && p.err) p.err[ERR_POSITION] = 1u;
     }
-    const uint64_t base = (static_cast<uint64_t>(b) * p.n_kv + kh) * p.nch;
-    auto acc_at = [&](uint32_t c, int i) {
-        const uint32_t d = min(lane + 64u * i, hd - 1u);
-        return p.part_acc[((base + min(c, last)) * Gq + qi) * hd + d];
-    };
-    // statistics of chunks lane, lane + 64, ... and the first CB chunks' outputs
-    const uint32_t c0 = min(lane, last);
-    const float m0 = p.part_ml[((base + c0) * Gq + qi) * 2u], l0 = p.part_ml[((base + c0) * Gq + qi) * 2u + 1u];
-    float v[CB][DPL];
-#pragma unroll
-    for (uint32_t c = 0; c < CB; ++c)
-#pragma unroll
-        for (int i = 0; i < DPL; ++i) v[c][i] = acc_at(c, i);
     float mx = -__builtin_huge_valf();
     if (lane <= last) mx = fmaxf(mx, m0);
     for (uint32_t c = lane + 64u; c <= last; c += 64u) mx = fmaxf(mx, p.part_ml[((base + c) * Gq + qi) * 2u]);

@@ -703,8 +703,8 @@ __device__ __forceinline__ void staged_prologue(const KParams& p, uint8_t* lds, 
             stage_issue<AF, NORM, NTH, KR>(p, r, j0, i0);
             stage_store<WF, AF, NORM, NTH, KR>(p, r, j0, i0, lds, sinv);
         }
-    late();
     __syncthreads();
+    late();
 }
 
 template <int WF, int AF, int T, int U, bool STAGED>
@@ -1073,7 +1073,7 @@ __global__ __launch_bounds__(512) void k_gemv_wpt(KParams p)
     };
     auto load = [&](PL& b, uint32_t s) {
         const uint32_t k = s / npass, ps = s - k * npass;
-        const uint32_t tile = first + stride * k;
+        const uint32_t tile = min(first + stride * k, p.tiles - 1u);   // a wave with no tile loads the last one
 #pragma unroll
         for (int u = 0; u < U; ++u)
         {
@@ -1085,14 +1085,17 @@ __global__ __launch_bounds__(512) void k_gemv_wpt(KParams p)
         }
     };
 
+    // One step's loads are in flight across the staging, the others are
+    // issued after it (issuing them all first keeps the waves in the issue
+    // queue until most of the stream has landed).  Every prologue load is
+    // issued on every path (a wave with fewer steps loads its last again, one
+    // with none the last tile): the compiler counts outstanding loads along
+    // the path with the fewest, so behind a branch the waits for the staging
+    // would also wait for the weights.
     PL buf[D];
-    staged_prologue<WF, AF, NORM, NW>(p, lds, sinv, [&] {
-        if (S > 0u) load(buf[0], 0);
-        if (S > 1u) load(buf[1], 1);
-    }, [&] {
+    staged_prologue<WF, AF, NORM, NW>(p, lds, sinv, [&] { load(buf[0], 0); }, [&] {
 #pragma unroll
-        for (int d = 2; d < D; ++d)
-            if (S > static_cast<uint32_t>(d)) load(buf[d], d);   // the staging registers are free now
+        for (int d = 1; d < D; ++d) load(buf[d], min(static_cast<uint32_t>(d), S ? S - 1u : 0u));
     });
     if constexpr (WF == OPURE_W_I4G128)
     {
