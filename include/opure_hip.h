@@ -405,6 +405,12 @@ int opure_debug_workspace(opure_dev* dev, void** ptr, uint64_t* bytes);
  * up at once, so the failure report can be checked while every wave still
  * runs to its end. */
 int opure_debug_set_wait_limit(opure_dev* dev, uint32_t sleeps);
+/* GEMV engine of opure_gemv_batched_i8pc at M <= 8 rows with fp16 X and a
+ * STORE / RESIDUAL / SWIGLU epilogue: the matrix-core kernels (default) or the
+ * vector-ALU kernel (v_dot2_f32_f16, one output row per lane), kept for the
+ * engine comparison.  The verify step always uses the matrix cores. */
+enum { OPURE_GEMV_MFMA = 0, OPURE_GEMV_VALU = 1 };
+int opure_debug_set_gemv_engine(opure_dev* dev, uint32_t engine);
 int opure_debug_verify_offsets(const opure_model* model, uint32_t batch, uint32_t rows, uint32_t max_ctx,
                                uint64_t offsets[5]);
 

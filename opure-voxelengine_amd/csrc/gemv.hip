@@ -17,6 +17,7 @@ int launch_i8(opure_dev*, uint32_t, uint32_t, bool, const KParams&, const Recipe
 int launch_i4_f16(opure_dev*, uint32_t, uint32_t, bool, const KParams&, const Recipe&, uint32_t, uint32_t);
 int launch_i4_bf16(opure_dev*, uint32_t, uint32_t, bool, const KParams&, const Recipe&, uint32_t, uint32_t);
 int launch_wide_i8(opure_dev*, uint32_t, const WParams&, uint32_t);
+int launch_valu_i8(opure_dev*, uint32_t, const KParams&);
 int launch_wide_i4_f16(opure_dev*, uint32_t, const WParams&, uint32_t);
 int launch_wide_i4_bf16(opure_dev*, uint32_t, const WParams&, uint32_t);
 
@@ -429,6 +430,11 @@ int gemv_launch(opure_dev* dev, const GemvCall& c)
     kp.ring = pl.ring;
     kp.qkv = c.qkv;
     kp.lg = c.logits;
+    // the vector-ALU engine, where it is chosen and built (int8 weights, fp16 X,
+    // at most 8 rows, a plain epilogue)
+    if (dev->gemv_engine == OPURE_GEMV_VALU && c.wfmt == OPURE_W_I8PC && c.xfmt == OPURE_A_F16 && c.M <= VALU_MAXM &&
+        !norm && (c.epi == EPI_STORE || c.epi == EPI_RESIDUAL || c.epi == EPI_SWIGLU))
+        return launch_valu_i8(dev, c.epi, kp);
     uint32_t nm = norm ? 1u : 0u;
     if (norm && !pl.staged)
     {

@@ -1559,6 +1559,84 @@ __global__ __launch_bounds__((PC_NC + PC_NL) * 64) void k_gemv_pc(KParams p)
     }
 }
 
+// Vector-ALU GEMV, the other side of the engine choice (opure_debug_set_gemv_engine):
+// int8 weights, fp16 X, M <= 8 rows, no fused rmsnorm.  One workgroup of 16
+// waves per tile, K split over the waves as in k_gemv (wave w takes blocks w,
+// w + 16, ...).  Lane (g4, r16) holds 16 int8 of row r16 in each block, widens
+// them once to fp16 pairs and takes v_dot2_f32_f16 against the same 16 values
+// of every X row, so each X fragment feeds one output row per lane where the
+// matrix core feeds 16.  The 4 lanes of a row add by butterfly, the waves in
+// wave order through LDS; then the element epilogue.  Sums are ordered
+// differently from the matrix-core path (results agree to rounding).
+constexpr uint32_t VALU_NW = 16, VALU_MAXM = 8;
+
+template <int EPI>
+__global__ __launch_bounds__(VALU_NW * 64) void k_gemv_valu(KParams p)
+{
+    __shared__ float red[VALU_NW][VALU_MAXM][16];
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    const uint32_t g4 = lane >> 4, r16 = lane & 15u;
+    const uint32_t tile = blockIdx.x, nblk = p.nblk, M = p.M;
+    float acc[VALU_MAXM];
+#pragma unroll
+    for (uint32_t m = 0; m < VALU_MAXM; ++m) acc[m] = 0.0f;
+    const u4_t* wp = reinterpret_cast<const u4_t*>(p.w + (static_cast<uint64_t>(tile) * nblk << 10) + (lane << 4));
+    const half2_t* xp = reinterpret_cast<const half2_t*>(p.x) + 8u * g4;      // k = 64 blk + 16 g4 .. + 16
+    u4_t wn = __builtin_nontemporal_load(wp + 64u * min(wave, nblk - 1u));
+    for (uint32_t blk = wave; blk < nblk; blk += VALU_NW)
+    {
+        const u4_t w = wn;
+        if (blk + VALU_NW < nblk) wn = __builtin_nontemporal_load(wp + 64u * (blk + VALU_NW));
+        half2_t wh[8];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+        {
+            uint32_t lo, hi;
+            u8x4_to_f16(w[j], lo, hi);
+            wh[2 * j] = __builtin_bit_cast(half2_t, lo);
+            wh[2 * j + 1] = __builtin_bit_cast(half2_t, hi);
+        }
+#pragma unroll
+        for (uint32_t m = 0; m < VALU_MAXM; ++m)
+        {
+            if (m >= M) break;                               // uniform
+            const half2_t* xr = xp + (static_cast<uint64_t>(m) * p.in + 64u * blk) / 2u;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) acc[m] = __builtin_amdgcn_fdot2(wh[j], xr[j], acc[m], false);
+        }
+    }
+#pragma unroll
+    for (uint32_t m = 0; m < VALU_MAXM; ++m)
+    {
+        acc[m] = __fadd_rn(acc[m], __shfl_xor(acc[m], 16));
+        acc[m] = __fadd_rn(acc[m], __shfl_xor(acc[m], 32));
+    }
+    if (g4 == 0)
+    {
+#pragma unroll
+        for (uint32_t m = 0; m < VALU_MAXM; ++m) red[wave][m][r16] = acc[m];
+    }
+    __syncthreads();
+    if (threadIdx.x < 16u * M)
+    {
+        const uint32_t m = threadIdx.x >> 4, c = threadIdx.x & 15u;
+        float v = red[0][m][c];
+#pragma unroll
+        for (uint32_t w = 1; w < VALU_NW; ++w) v = __fadd_rn(v, red[w][m][c]);
+        float bv = 0.0f;
+        int32_t bi = 0;
+        epilogue_elem<OPURE_W_I8PC, EPI>(p, tile, m, c, v, bv, bi);
+    }
+}
+
+template <int EPI>
+int launch_valu(opure_dev* dev, const KParams& kp)
+{
+    OPURE_LAUNCH(dev, k_gemv_valu<EPI>, dim3(kp.tiles), dim3(VALU_NW * 64), 0, kp);
+    OPURE_LAUNCH_CHECK("k_gemv_valu");
+    return OPURE_OK;
+}
+
 template <int WF, int AF, int EPI, bool NORM>
 int launch_pc(opure_dev* dev, const KParams& kp, uint32_t grid, uint32_t lds)
 {

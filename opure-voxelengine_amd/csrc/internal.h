@@ -37,6 +37,8 @@ struct opure_dev {
     uint32_t*   err = nullptr;
     // sleeps before a bounded inter-wave wait gives up (opure_debug_set_wait_limit)
     uint32_t    wait_limit = 1u << 22;
+    // GEMV engine of opure_gemv_batched_i8pc for M <= 8 (opure_debug_set_gemv_engine)
+    uint32_t    gemv_engine = OPURE_GEMV_MFMA;
     // captured graphs still alive: a workspace they point into is kept, not
     // freed, when a larger call replaces it
     uint32_t    live_graphs = 0;

@@ -332,6 +332,15 @@ int opure_debug_set_wait_limit(opure_dev* dev, uint32_t sleeps)
     return OPURE_OK;
 }
 
+int opure_debug_set_gemv_engine(opure_dev* dev, uint32_t engine)
+{
+    OPURE_REQUIRE(dev, OPURE_E_INVALID, "opure_debug_set_gemv_engine: null device");
+    OPURE_REQUIRE(engine == OPURE_GEMV_MFMA || engine == OPURE_GEMV_VALU, OPURE_E_INVALID,
+                  "opure_debug_set_gemv_engine: engine %u", engine);
+    dev->gemv_engine = engine;
+    return OPURE_OK;
+}
+
 int opure_profile_enable(opure_dev* dev, int on)
 {
     OPURE_REQUIRE(dev, OPURE_E_INVALID, "opure_profile_enable: null device");

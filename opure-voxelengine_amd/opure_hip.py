@@ -23,6 +23,7 @@ ROPE_GPU, ROPE_CPUREF = 0, 1
 EPI_STORE, EPI_RESIDUAL, EPI_SWIGLU = 0, 1, 2
 STAGES = ("embed", "qkv", "attention", "o_proj", "gate_up", "down", "lm_head", "accept")
 ACCEPT_NONE, ACCEPT_GREEDY, ACCEPT_REJECTION = 0, 1, 2
+GEMV_MFMA, GEMV_VALU = 0, 1
 
 
 class OpureError(RuntimeError):
@@ -150,6 +151,7 @@ def _declare(L):
         "opure_verify_layer": ([vp, C.POINTER(VerifyLayerArgs)], i),
         "opure_debug_workspace": ([vp, C.POINTER(vp), C.POINTER(u64)], i),
         "opure_debug_set_wait_limit": ([vp, u32], i),
+        "opure_debug_set_gemv_engine": ([vp, u32], i),
         "opure_debug_verify_offsets": ([C.POINTER(Model), u32, u32, u32, C.POINTER(u64)], i),
         "opure_tiled_bytes": ([u32, u32, u32, C.POINTER(u64), C.POINTER(u64)], i),
         "opure_tile_linear": ([vp, u32, u32, C.POINTER(Linear), vp, vp, C.POINTER(Linear)], i),

@@ -293,6 +293,48 @@ def test_gemv_swiglu_matches_oracle(dev, case):
             b.free()
 
 
+VALU_CASES = [(3072, 2048), (2048, 8192), (16384, 2048), (128256, 2048)]
+
+
+@pytest.mark.parametrize("case", VALU_CASES, ids=[f"{o}x{i}" for o, i in VALU_CASES])
+def test_gemv_valu_engine_matches_oracle(dev, case):
+    """The vector-ALU engine (int8 weights, fp16 X, M <= 8) against the
+    oracle, to the matrix-core path's bound, for every epilogue it takes."""
+    out, inn = case
+    say("gemv valu", case)
+    rng = np.random.default_rng(out * 3 + inn)
+    lin = O.make_linear(rng, out, inn, H.W_I8PC)
+    desc, keep = dev_linear(dev, lin)
+    x_bits, x_f = to_act(rng.standard_normal((16, inn)), H.A_F16)
+    ref = O.gemv(lin, H.W_I8PC, x_f)
+    absref = np.abs(x_f).astype(np.float64) @ np.abs(O.dequant(lin, H.W_I8PC)).T
+    H.check(H.lib().opure_debug_set_gemv_engine(dev.h, H.GEMV_VALU))
+    try:
+        for M in (1, 6, 8):
+            y = run_gemv(dev, H.W_I8PC, desc, x_bits, M, H.A_F16, H.A_F32, H.EPI_STORE)
+            err = np.abs(y - ref[:M])
+            assert np.all(err <= 1e-5 * absref[:M] + 1e-6), (M, err.max())
+        y0 = rng.standard_normal((8, out)).astype(np.float32)
+        yv = run_gemv(dev, H.W_I8PC, desc, x_bits, 6, H.A_F16, H.A_F32, H.EPI_STORE)
+        yr = run_gemv(dev, H.W_I8PC, desc, x_bits, 6, H.A_F16, H.A_F32, H.EPI_RESIDUAL, y_init=y0)
+        assert np.array_equal(yr, (y0[:6] + yv).astype(np.float32))
+        if out <= 16384:
+            F = out // 2
+            g, u = ref[:6, :F].copy(), ref[:6, F:].copy()
+            h = np.zeros_like(g)
+            O.lib().orc_swiglu(g.ctypes.data, u.ctypes.data, h.ctypes.data, g.size)
+            ys = from_act(run_gemv(dev, H.W_I8PC, desc, x_bits, 6, H.A_F16, H.A_F16, H.EPI_SWIGLU), H.A_F16)
+            np.testing.assert_allclose(ys, h, rtol=2e-3, atol=1e-4 * max(1.0, np.abs(h).max()))
+        # rows past 8 fall back to the matrix cores
+        y16 = run_gemv(dev, H.W_I8PC, desc, x_bits, 16, H.A_F16, H.A_F32, H.EPI_STORE)
+        assert np.all(np.abs(y16 - ref) <= 1e-5 * absref + 1e-6)
+    finally:
+        H.check(H.lib().opure_debug_set_gemv_engine(dev.h, H.GEMV_MFMA))
+    for b in keep:
+        if b:
+            b.free()
+
+
 @pytest.mark.parametrize("case", [(H.W_I4G128, H.A_BF16, 28672, 4096), (H.W_I8PC, H.A_F16, 24576, 2048)],
                          ids=["i4bf16-28672x4096", "i8-24576x2048"])
 def test_gemv_loader_waves_equal_wave_per_tile(dev, case):
