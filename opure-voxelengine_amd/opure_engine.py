@@ -9,7 +9,9 @@ import numpy as np
 
 import opure_hip as H
 
-ENGINE_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", "libopure_engine.so")
+# OPURE_ENGINE_LIB: another build of the engine sources (e.g. with sanitizers)
+ENGINE_PATH = os.environ.get("OPURE_ENGINE_LIB") or os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib",
+                                                                 "libopure_engine.so")
 _lib = None
 
 

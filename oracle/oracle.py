@@ -16,7 +16,8 @@ import subprocess
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "liboracle.so")
+# OPURE_ORACLE_LIB: another build of the same sources (the sanitizer test's)
+LIB_PATH = os.environ.get("OPURE_ORACLE_LIB") or os.path.join(HERE, "liboracle.so")
 
 W_F32, W_I8PC, W_I4G128 = 0, 1, 2
 A_F32, A_F16, A_BF16 = 0, 1, 2
