@@ -632,7 +632,7 @@ def main():
     if args.copy_calibration:
         return copy_calibration()
     if args.gpus != 1:
-        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
+        print(f"bench.py: this benchmark measures one GPU only (asked for --gpus {args.gpus}); "
               "multi-GPU sharding is a design note, not a measured path", file=sys.stderr)
         sys.exit(2)
     if args.config == "c2":

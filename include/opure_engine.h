@@ -73,7 +73,7 @@ int opure_engine_generate_speculative(opure_engine* e, const int32_t* prompt, ui
  * n - 1 (n <= OPURE_MAX_ROWS); greedy acceptance.  *accepted = drafts kept;
  * out[0 .. *accepted] = those drafts then the target's own next token.  The
  * rows' K/V stay in the cache until opure_engine_rollback_kv.  The engine's
- * VerifyStep (SURVEY's build plan; the reference has none). */
+ * VerifyStep (the reference has none). */
 int opure_engine_verify_step(opure_engine* e, const int32_t* tokens, uint32_t n, uint32_t seq_len, int32_t* out,
                              uint32_t* accepted);
 /* After a verify step of k drafts at seq_len that kept `accepted`: the cache
@@ -129,8 +129,9 @@ int opure_engine_reset_metrics(opure_engine* e);
  *      max_position_embeddings, rms_norm_eps, rope_theta, tie_word_embeddings
  *      (default true, as the reference), quantization_config.activation_dtype
  *      ("float16" | "bfloat16" | "float32").  hidden_act other than silu,
- *      bias terms, rope_scaling and head_dim other than 64 / 128 are
- *      OPURE_E_UNSUPPORTED. */
+ *      bias terms, rope_scaling and a head_dim that is not a multiple of 16 in
+ *      16..256 are OPURE_E_UNSUPPORTED (the reference takes 64 and 128 only,
+ *      Opure_Graph.cpp:167-174). */
 enum {
     OPURE_ROLE_EMBED = 0, OPURE_ROLE_LM_HEAD = 1, OPURE_ROLE_QKV = 2, OPURE_ROLE_O = 3, OPURE_ROLE_GATE_UP = 4,
     OPURE_ROLE_DOWN = 5, OPURE_ROLE_ATTN_NORM = 6, OPURE_ROLE_MLP_NORM = 7, OPURE_ROLE_FINAL_NORM = 8

@@ -205,8 +205,11 @@ ModelConfig ModelConfig::Parse(const std::string& text)
     if (c.nHeads % c.nKvHeads)
         fail(OPURE_E_INVALID, "num_attention_heads " + std::to_string(c.nHeads) + " is not a multiple of num_key_value_heads " +
                                   std::to_string(c.nKvHeads));
-    if (c.headDim != 64 && c.headDim != 128)
-        fail(OPURE_E_UNSUPPORTED, "head_dim " + std::to_string(c.headDim) + " (the attention kernels take 64 and 128)");
+    // the reference accepts 64 and 128 only (Opure_Graph.cpp:167-174); the
+    // attention here takes any multiple of 16 up to 256 (64 and 128 on the
+    // matrix cores, the others on the vector path)
+    if (c.headDim < 16 || c.headDim > 256 || c.headDim % 16)
+        fail(OPURE_E_UNSUPPORTED, "head_dim " + std::to_string(c.headDim) + " (attention takes multiples of 16 up to 256)");
     return c;
 }
 

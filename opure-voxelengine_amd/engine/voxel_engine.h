@@ -128,7 +128,7 @@ public:
     // Appends `token` at `position` of the target cache; returns the argmax.
     uint32_t DecodeStep(uint32_t token, uint32_t position);
 
-    // The verify step as its own call (SURVEY's VerifyStep): tokens = the last
+    // The verify step as its own call: tokens = the last
     // accepted token then K drafts (K + 1 <= 16 rows) at positions seqLen ..
     // seqLen + K of the target; greedy acceptance.  The rows' K/V stay in the
     // cache until RollbackKV.

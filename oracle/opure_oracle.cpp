@@ -1,7 +1,7 @@
 // ============================================================================
 //  opure_oracle.cpp -- CPU oracle for the Opure verify path.
 //
-//  TEST INFRASTRUCTURE ONLY: the checker the HIP path is compared against.
+//  TEST INFRASTRUCTURE ONLY: the CPU restatement the HIP path is compared against.
 //  Nothing in the product links or loads this file's library.
 //
 //  Restates src/engine/Opure_CpuReference.cpp (scalar C++, double

@@ -1,7 +1,7 @@
 /*
  * opure_oracle.h -- CPU oracle for the Opure speculative-decoding verify path.
  *
- * TEST INFRASTRUCTURE ONLY.  This library is the checker that the HIP path is
+ * TEST INFRASTRUCTURE ONLY.  This library is the reference restatement the HIP path is
  * compared against.  Only tests/, __graft_entry__.smoke() and bench.py's
  * cpu_baseline leg may load it.  Nothing in the product links it.
  *

@@ -7,7 +7,7 @@ What a bf16 model allows, and what is asserted:
 
 - Every layer, teacher-forced: opure_verify_layer applies layer L to the
   ORACLE's residual entering layer L; its output, read out through the
-  oracle's final RMSNorm and LM head, is within north_star's 2e-2 of the
+  oracle's final RMSNorm and LM head, is within the 2e-2 logit bar of the
   oracle's own layer output read out the same way.  Measured on this
   workload: 0.0146 at layer 0 (whose residual is the 0.02-scale embedding, so
   the RMSNorm magnifies every rounding difference of the layer), at most

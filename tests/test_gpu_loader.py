@@ -88,6 +88,27 @@ def test_loaded_model_verify_step(dev, tmp_path, fmt, tied):
     lm.lm.close()
 
 
+def test_head_dim_96_through_the_vector_attention(dev, tmp_path):
+    """A head size the reference refuses (96): loaded, and verified against
+    the oracle through the attention's vector path."""
+    m = small_model(O.W_I8PC, O.A_F16, hidden=384, heads=(4, 2), hd=96, attn_scale=96 ** -0.5)
+    d = W.write_model_dir(str(tmp_path / "m"), m)
+    lm = Loaded(dev, d)
+    assert lm.desc.head_dim == 96
+    B, R = 2, 5
+    kv = random_cache(m, B, 320, 48, seed=7)
+    seq_len = np.array([251, 96], np.int32)
+    tokens = np.random.default_rng(3).integers(0, m.cfg["vocab"], size=(B, R)).astype(np.int32)
+    got, _ = step_logits(dev, lm, m, kv, tokens, seq_len)
+    kv_o = O.HostKV(m, n_pages=kv.n_pages, batch=B, max_pages_per_seq=kv.max_pages)
+    kv_o.pool[...] = kv.pool
+    kv_o.page_table[...] = kv.page_table
+    err = np.abs(got - O.verify_forward(m, kv_o, tokens, seq_len)).max()
+    say("max_abs logits vs oracle (hd 96)", err)
+    assert err <= 2e-2
+    lm.lm.close()
+
+
 @pytest.mark.parametrize("wfmt,afmt", [(O.W_I8PC, O.A_F16), (O.W_I4G128, O.A_BF16)], ids=["to-i8", "to-i4"])
 def test_float_model_quantised_on_load(dev, tmp_path, wfmt, afmt):
     f = small_model(O.W_F32, O.A_F32, tied=False, seed=9)

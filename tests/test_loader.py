@@ -284,12 +284,13 @@ def test_bad_files_name_the_problem(tmp_path):
 @pytest.mark.parametrize("over,code,words", [
     ({"rope_scaling": {"rope_type": "llama3", "factor": 8.0}}, H.E_UNSUPPORTED, "rope_scaling"),
     ({"hidden_act": "gelu"}, H.E_UNSUPPORTED, "gelu"),
-    ({"head_dim": 96}, H.E_UNSUPPORTED, "head_dim"),
+    ({"head_dim": 72}, H.E_UNSUPPORTED, "head_dim"),
+    ({"head_dim": 320}, H.E_UNSUPPORTED, "head_dim"),
     ({"attention_bias": True}, H.E_UNSUPPORTED, "bias"),
     ({"num_key_value_heads": 3}, H.E_INVALID, "num_key_value_heads"),
     ({"rms_norm_eps": None}, H.E_INVALID, "rms_norm_eps"),
     ({"hidden_size": -1}, H.E_INVALID, "hidden_size"),
-], ids=["rope_scaling", "act", "head_dim", "bias", "gqa", "eps", "negative"])
+], ids=["rope_scaling", "act", "head_dim", "head_dim_big", "bias", "gqa", "eps", "negative"])
 def test_config_refusals(tmp_path, over, code, words):
     m = small(O.W_I8PC, O.A_F16)
     cfg = W.config_of(m, **over)

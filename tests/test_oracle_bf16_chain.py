@@ -6,7 +6,7 @@ group-128 weights and bf16 activations, 6 layers, 8 rows over a 2048-token
 cache.  The oracle's forward is run twice: once as is, once with ONE element of
 layer 0's attention output moved by one bf16 ulp after its rounding (the
 smallest difference two implementations that round at the same points can
-have).  The logits move by more than north_star's 2e-2.  The same flip in the
+have).  The logits move by more than the 2e-2 logit bar.  The same flip in the
 last layer moves them far less, so it is the chain of later roundings, not
 the read-out, that carries it.
 
