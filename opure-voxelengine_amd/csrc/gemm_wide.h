@@ -4,20 +4,33 @@
 //
 //  The same tiled weights and the same MFMA operand mapping as the K+1-row
 //  kernel (gemv_kernel.h): y^T = W X^T in 16 x 16 tiles, A = 16 weight rows
-//  x 32 k, B = 32 k x 16 columns of X.  What changes is the reuse: a weight
-//  block is decoded once into LDS and multiplied against every 16-column
-//  tile of X, so the weights are still read from HBM exactly once.
+//  x 32 k, B = 32 k x 16 columns of X.
 //
-//  Work split.  A workgroup of 4 waves owns 4 consecutive 16-row tiles and
-//  one range of K blocks (a split; shapes with few tiles split K so every CU
-//  gets work).  X is staged into LDS one chunk of K at a time (16-bit
-//  activations; a fused rmsnorm runs as a pre-pass).  Per weight block each
-//  wave loads and decodes the block of "its" tile into an LDS double buffer,
-//  then multiplies all 4 tiles by its column tiles (wave w: w, w+4, w+8,
-//  w+12), accumulating in registers.  With one split the epilogue runs here;
-//  with several, each split writes its raw accumulators and k_wide_reduce
-//  adds the splits in split order and runs the epilogue.  Sums have a fixed
-//  order set by the shape, so results are reproducible.
+//  Work split.  A workgroup owns 8 consecutive 16-row weight tiles (a row
+//  group), up to 8 16-column tiles of X (a column group) and one range of K
+//  blocks (a split; shapes with few row groups split K so the CUs fill).  A
+//  set of 4 waves covers the row group: wave w multiplies tiles 2w, 2w + 1 by
+//  all of the group's column tiles, so it keeps 16 accumulator tiles, loads
+//  each weight byte once and reads each B fragment once per block for two
+//  MFMAs.  Weights go straight from HBM into registers: every wave loads its
+//  own two tiles' 16 bytes a lane per block, in static register slots DW
+//  blocks ahead.  X goes through LDS: per block the set loads its column
+//  group's fragments into registers DX blocks ahead and writes them into a
+//  two-stage ring laid out fragment by fragment, 16 bytes a lane.  One barrier
+//  per block separates a stage's writes from its reads and the reads of two
+//  blocks back from the next writes.  The int8 kernel runs two such sets on
+//  alternate K blocks (KH = 2, two waves a SIMD) and adds them at the end.
+//
+//  The budget per block of a workgroup is L2 -> CU traffic (8 KB of weights
+//  and 16 KB of X at 128 columns), which is why a wave owns whole weight
+//  tiles (no two waves load the same weights) and X loads cover whole
+//  128-byte lines.
+//
+//  With one split the epilogue runs here; with several, each split writes
+//  its raw accumulators and k_wide_reduce adds the splits in split order and
+//  runs the epilogue.  The split count depends on the weight shape only, and
+//  each (row, column) sums its blocks in order, so a row's result does not
+//  depend on how many rows share the call, and runs are reproducible.
 // ============================================================================
 #pragma once
 
@@ -25,208 +38,283 @@
 
 namespace opure_gemv {
 
-constexpr uint32_t WIDE_TO = 4;       // tiles per workgroup (one per wave for loading)
-constexpr uint32_t WIDE_CTW = 4;      // column tiles per wave
+constexpr uint32_t WIDE_WR = 4, WIDE_WC = 1;     // wave grid of a K half: wave rows x wave columns
+constexpr uint32_t WIDE_TA = 2;                  // weight tiles per wave
+constexpr uint32_t WIDE_TB = 8;                  // column tiles per wave
+constexpr uint32_t WIDE_RT = WIDE_WR * WIDE_TA;  // weight tiles per workgroup
+constexpr uint32_t WIDE_CG = WIDE_WC * WIDE_TB;  // column tiles per workgroup at most
 constexpr uint32_t WIDE_MAX_M = 256;  // rows of X
 
+// register slots of the software pipeline: DW weight blocks and DX X blocks
+// in flight; the K loop is unrolled by U = lcm(DW, DX), an even number, so
+// slots and LDS stages are compile-time.  KH = 2 runs two sets of 4 waves on
+// alternate K blocks (two waves a SIMD: one issues MFMAs while the other
+// waits); the uint4 kernel's registers leave room for one.
+template <int WF> struct WideDepth;
+template <> struct WideDepth<OPURE_W_I8PC>   { static constexpr uint32_t DW = 4, DX = 2, U = 4, KH = 2; };
+template <> struct WideDepth<OPURE_W_I4G128> { static constexpr uint32_t DW = 2, DX = 1, U = 2, KH = 1; };
+
 struct WParams {
-    KParams p;        // shape, pointers, epilogue (x_stride: LDS bytes per staged X row)
+    KParams p;        // shape, pointers, epilogue
     uint32_t mt;      // 16-column tiles of X
-    uint32_t ckb;     // weight blocks per staged chunk of X
-    uint32_t splits;  // K splits (gridDim.y)
-    uint32_t bps;     // blocks per split
-    uint32_t off_a;   // LDS: decoded A double buffer [2][TO][AW/4][64] x 16 bytes
-    uint32_t off_s;   // LDS: uint4 scale double buffer [2][TO][16] u32
+    uint32_t nrg;     // row groups (WIDE_RT tiles each)
+    uint32_t ncg;     // column groups
+    uint32_t cgs;     // column tiles per group (<= WIDE_CG)
+    uint32_t splits;  // K splits
+    uint32_t bps;     // blocks per split, a multiple of WideDepth::U
     f4_t* part;       // splits > 1: accumulators [split][tile][mt][64]
 };
 
-// Stage rows 0..16*mt-1 of X, k in [k0, k0 + kn), into LDS rows of x_stride
-// bytes (rows >= M are zero); uint4 also writes each 128-k group's sum to
-// xsum[row * ckb + group].
-template <int WF, int AF>
-__device__ __forceinline__ void stage_wide_x(const WParams& wp, uint8_t* lds, uint32_t k0, uint32_t kn, float* xsum)
+// Workgroup -> (split, row group, column group).  Workgroups are dispatched
+// to the 8 XCDs round robin; the remap gives each XCD a contiguous range of
+// the work list, so the column groups of one row group (the same weights)
+// run on one XCD and share its L2.
+__device__ __forceinline__ void wide_coords(const WParams& wp, uint32_t& split, uint32_t& rg, uint32_t& cg)
 {
-    constexpr uint32_t KU = 8;
-    const KParams& p = wp.p;
-    const uint32_t n8 = kn / 8u, rows = 16u * wp.mt;
-    const uint32_t total = rows * n8;
-    const uint32_t lane = threadIdx.x & 63u;
-    for (uint32_t base = 0; base < total; base += 256u * KU)
-    {
-        u4_t v[KU];
-#pragma unroll
-        for (uint32_t u = 0; u < KU; ++u)
-        {
-            const uint32_t idx = min(base + u * 256u + threadIdx.x, total - 1u);
-            const uint32_t m = idx / n8, j = idx - m * n8;
-            const uint32_t mc = min(m, p.M - 1u);
-            v[u] = *reinterpret_cast<const u4_t*>(p.x + (static_cast<uint64_t>(mc) * p.in + k0 + 8u * j) * 2u);
-        }
-#pragma unroll
-        for (uint32_t u = 0; u < KU; ++u)
-        {
-            const uint32_t idx = base + u * 256u + threadIdx.x;
-            if (idx >= total) continue;
-            const uint32_t m = idx / n8, j = idx - m * n8;
-            const u4_t val = m < p.M ? v[u] : u4_t{0u, 0u, 0u, 0u};
-            *reinterpret_cast<u4_t*>(lds + static_cast<uint64_t>(m) * p.x_stride + 16u * j) = val;
-            if constexpr (WF == OPURE_W_I4G128)
-            {
-                // the 16 units of a group sit in 16 aligned lanes (n8 and 256 are multiples of 16)
-                const float s = row16_sum(unit_sum<AF>(val[0], val[1], val[2], val[3]));
-                if ((lane & 15u) == 0) xsum[m * wp.ckb + j / 16u] = s;
-            }
-        }
-    }
+    const uint32_t G = gridDim.x, i = blockIdx.x;
+    const uint32_t xcd = i & 7u, j = i >> 3, q = G >> 3, r = G & 7u;
+    const uint32_t L = xcd < r ? xcd * (q + 1u) + j : r * (q + 1u) + (xcd - r) * q + j;
+    cg = L % wp.ncg;
+    const uint32_t rest = L / wp.ncg;
+    rg = rest % wp.nrg;
+    split = rest / wp.nrg;
 }
 
 template <int WF, int AF, int EPI>
-__global__ __launch_bounds__(256) void k_gemm_wide(WParams wp)
+__global__ __launch_bounds__(256 * WideDepth<WF>::KH) void k_gemm_wide(WParams wp)
 {
     static_assert(WF == OPURE_W_I8PC || WF == OPURE_W_I4G128, "the wide GEMV reads quantised weights");
     constexpr uint32_t KB = Fmt<WF>::KB;
-    constexpr uint32_t NMF = KB / 32u;          // MFMAs per block per tile pair
-    constexpr uint32_t AQ = NMF;                // 16-byte A fragments per lane per block
-    constexpr uint32_t TO = WIDE_TO, CTW = WIDE_CTW;
-    extern __shared__ __align__(16) uint8_t lds[];
+    constexpr uint32_t NMF = KB / 32u;             // MFMAs (16-byte B fragments) per block per tile pair
+    constexpr uint32_t CH = KB / 8u;               // 16-byte X chunks per row per block
+    constexpr uint32_t XR = WIDE_CG * 16u * CH / 256u;  // X chunks a thread stages per block
+    constexpr uint32_t STAGE = WIDE_CG * NMF * 64u;     // u4_t per LDS stage
+    constexpr uint32_t DW = WideDepth<WF>::DW, DX = WideDepth<WF>::DX, U = WideDepth<WF>::U;
+    constexpr uint32_t KH = WideDepth<WF>::KH;
+    constexpr uint32_t TA = WIDE_TA, TB = WIDE_TB;
+    static_assert(WIDE_WR * WIDE_WC == 4 && TA % 2 == 0, "a K half is 4 waves");
+    static_assert(KH == 1 || 2u * STAGE * 2u >= 2u * 4u * (TA / 2u) * TB * 64u, "the halves' exchange reuses the X stages");
+    __shared__ u4_t xl[KH * 2 * STAGE];
     const KParams& p = wp.p;
-    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u, g4 = lane >> 4, r16 = lane & 15u;
-    const uint32_t mt = wp.mt, nblk = p.nblk, G = p.in / 128u;
-    const uint32_t tile0 = blockIdx.x * TO;
-    const uint32_t ltile = min(tile0 + wave, p.tiles - 1u);
-    const uint32_t b_begin = blockIdx.y * wp.bps, b_end = min(nblk, b_begin + wp.bps);
-    u4_t* abuf = reinterpret_cast<u4_t*>(lds + wp.off_a);
-    uint32_t* sbuf = reinterpret_cast<uint32_t*>(lds + wp.off_s);
-    float* xsum = reinterpret_cast<float*>(lds + p.off_xsum);
+    const uint32_t tid = threadIdx.x & 255u, lane = tid & 63u, g4 = lane >> 4, r16 = lane & 15u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t kh = wave >> 2, w4 = wave & 3u;            // K half, wave within the half
+    const uint32_t wr = w4 / WIDE_WC, wc = w4 % WIDE_WC;
+    const uint32_t nblk = p.nblk, G = p.in / 128u;
+    uint32_t split, rg, cg;
+    wide_coords(wp, split, rg, cg);
+    const uint32_t ct0 = cg * wp.cgs;
+    const uint32_t cn = min(wp.cgs, wp.mt - ct0);            // column tiles of this group
+    const uint32_t tb = cn > wc ? (cn - wc + WIDE_WC - 1u) / WIDE_WC : 0u;  // of this wave: local wc, wc + WC, ...
+    const uint32_t tile0 = rg * WIDE_RT + wr * TA;
+    const uint32_t b_begin = split * wp.bps, b_end = min(nblk, b_begin + wp.bps);
+    u4_t* xh = xl + kh * 2u * STAGE;                          // this half's two stages
 
-    f4_t acc[TO][CTW];
+    // X chunk u of this thread: row rr of local column tile ctl, 16-byte chunk c of the block (a
+    // wave's load covers 8 rows x 128 contiguous bytes).  In LDS, chunk c of row rr sits at row
+    // slot rr ^ c of its fragment: the 8 chunks of a row land in 8 bank groups, and a fragment
+    // read (lane (g4, r16) takes chunk NMF g4 + q of row r16) still reads 16 distinct slots.
+    uint64_t xrow[XR];
+    uint32_t xdst[XR];
+    bool xzero[XR];
 #pragma unroll
-    for (uint32_t t = 0; t < TO; ++t)
-#pragma unroll
-        for (uint32_t j = 0; j < CTW; ++j) acc[t][j] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
-
-    auto wload = [&](uint32_t b, u4_t& w, u4_t& s) {
-        const uint32_t bc = min(b, nblk - 1u);
-        w = __builtin_nontemporal_load(
-            reinterpret_cast<const u4_t*>(p.w + ((static_cast<uint64_t>(ltile) * nblk + bc) << 10) + (lane << 4)));
-        if constexpr (WF == OPURE_W_I4G128)
-            s = *reinterpret_cast<const u4_t*>(static_cast<const uint32_t*>(p.sc) +
-                                               (static_cast<uint64_t>(ltile) * G + bc) * 16u + 4u * g4);
-    };
-    u4_t w0, s0{}, w1, s1{};
-    wload(b_begin, w0, s0);
-    wload(b_begin + 1u, w1, s1);
-    uint32_t par = 0;
-    for (uint32_t c0 = b_begin; c0 < b_end; c0 += wp.ckb)
+    for (uint32_t u = 0; u < XR; ++u)
     {
-        const uint32_t cb = min(wp.ckb, b_end - c0);
-        __syncthreads();                                   // the previous chunk is no longer read
-        stage_wide_x<WF, AF>(wp, lds, c0 * KB, cb * KB, xsum);
-        __syncthreads();
-        for (uint32_t bb = 0; bb < cb; ++bb)
+        const uint32_t e = u * 256u + tid;
+        const uint32_t c = e % CH, rr = (e / CH) & 15u, ctl = e / (16u * CH);
+        const uint32_t m = 16u * (ct0 + ctl) + rr;
+        xzero[u] = ctl >= cn || m >= p.M;
+        xrow[u] = (static_cast<uint64_t>(min(m, p.M - 1u)) * p.in + 8u * c) * 2u;
+        xdst[u] = (ctl * NMF + c % NMF) * 64u + (c / NMF) * 16u + (rr ^ (c & 15u));
+    }
+    auto xload = [&](u4_t (&v)[XR], uint32_t b) {
+        const uint64_t k0 = static_cast<uint64_t>(min(b, nblk - 1u)) * KB * 2u;
+#pragma unroll
+        for (uint32_t u = 0; u < XR; ++u) v[u] = *reinterpret_cast<const u4_t*>(p.x + xrow[u] + k0);
+    };
+    auto xstore = [&](const u4_t (&v)[XR], uint32_t st) {
+#pragma unroll
+        for (uint32_t u = 0; u < XR; ++u) xh[st * STAGE + xdst[u]] = xzero[u] ? u4_t{0u, 0u, 0u, 0u} : v[u];
+    };
+
+    // this wave's weight tiles (clamped for loads; the epilogue skips tiles past the end)
+    const uint8_t* wbase[TA];
+    const uint32_t* sbase[TA];
+#pragma unroll
+    for (uint32_t a = 0; a < TA; ++a)
+    {
+        const uint32_t lt = min(tile0 + a, p.tiles - 1u);
+        wbase[a] = p.w + (static_cast<uint64_t>(lt) * nblk << 10) + (lane << 4);
+        sbase[a] = static_cast<const uint32_t*>(p.sc) + static_cast<uint64_t>(lt) * G * 16u + 4u * g4;
+    }
+    auto wload = [&](u4_t (&w)[TA], u4_t (&s)[TA], uint32_t b) {
+        const uint32_t bc = min(b, nblk - 1u);
+#pragma unroll
+        for (uint32_t a = 0; a < TA; ++a)
         {
-            // this wave's tile: decode the block into A[par]
-            uint32_t a[4 * AQ];
-            if constexpr (WF == OPURE_W_I8PC)
+            w[a] = *reinterpret_cast<const u4_t*>(wbase[a] + (static_cast<uint64_t>(bc) << 10));
+            if constexpr (WF == OPURE_W_I4G128) s[a] = *reinterpret_cast<const u4_t*>(sbase[a] + bc * 16u);
+        }
+    };
+
+    f4_t acc[TA][TB];
+#pragma unroll
+    for (uint32_t a = 0; a < TA; ++a)
+#pragma unroll
+        for (uint32_t j = 0; j < TB; ++j) acc[a][j] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+    // one block: B fragments from LDS stage st, A decoded from the weight registers
+    auto compute = [&](const u4_t (&w)[TA], const u4_t (&s)[TA], uint32_t st) {
+        const u4_t* xb = xh + st * STAGE;
+        f4_t bacc[TA][TB];
+        float xpart[TB];
+        if constexpr (WF == OPURE_W_I4G128)
+        {
+#pragma unroll
+            for (uint32_t a = 0; a < TA; ++a)
+#pragma unroll
+                for (uint32_t j = 0; j < TB; ++j) bacc[a][j] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (uint32_t j = 0; j < TB; ++j) xpart[j] = 0.0f;
+        }
+#pragma unroll
+        for (uint32_t q = 0; q < NMF; ++q)
+        {
+            u4_t bf[TB];
+#pragma unroll
+            for (uint32_t j = 0; j < TB; ++j)
+                bf[j] = xb[(min(wc + WIDE_WC * j, WIDE_CG - 1u) * NMF + q) * 64u + g4 * 16u + (r16 ^ ((NMF * g4 + q) & 15u))];
+            if constexpr (WF == OPURE_W_I4G128)
             {
 #pragma unroll
-                for (int j = 0; j < 4; ++j) u8x4_to_f16(w0[j], a[2 * j], a[2 * j + 1]);
+                for (uint32_t j = 0; j < TB; ++j) xpart[j] += unit_sum<AF>(bf[j][0], bf[j][1], bf[j][2], bf[j][3]);
             }
-            else
-            {
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
+            for (uint32_t a = 0; a < TA; ++a)
+            {
+                u4_t af;
+                if constexpr (WF == OPURE_W_I8PC)
                 {
                     uint32_t o[4];
-                    u4x8_pairs<AF>(w0[j], o);
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) a[4 * j + e] = o[e];
+                    u8x4_to_f16(w[a][2u * q], o[0], o[1]);
+                    u8x4_to_f16(w[a][2u * q + 1u], o[2], o[3]);
+                    af = u4_t{o[0], o[1], o[2], o[3]};
                 }
-            }
-#pragma unroll
-            for (uint32_t q = 0; q < AQ; ++q)
-                abuf[((par * TO + wave) * AQ + q) * 64u + lane] = u4_t{a[4 * q], a[4 * q + 1], a[4 * q + 2], a[4 * q + 3]};
-            if constexpr (WF == OPURE_W_I4G128)
-                if (r16 == 0) *reinterpret_cast<u4_t*>(sbuf + (par * TO + wave) * 16u + 4u * g4) = s0;
-            w0 = w1;
-            s0 = s1;
-            wload(c0 + bb + 2u, w1, s1);
-            __syncthreads();
-            // all TO tiles times this wave's column tiles
-#pragma unroll
-            for (uint32_t t = 0; t < TO; ++t)
-            {
-                u4_t af[AQ];
-#pragma unroll
-                for (uint32_t q = 0; q < AQ; ++q) af[q] = abuf[((par * TO + t) * AQ + q) * 64u + lane];
-                u4_t sz{};
-                if constexpr (WF == OPURE_W_I4G128) sz = *reinterpret_cast<const u4_t*>(sbuf + (par * TO + t) * 16u + 4u * g4);
-#pragma unroll
-                for (uint32_t j = 0; j < CTW; ++j)
+                else
                 {
-                    const uint32_t ct = wave + 4u * j;
-                    if (ct >= mt) continue;
-                    const uint32_t m = 16u * ct + r16;
-                    const uint8_t* xr = lds + static_cast<uint64_t>(m) * p.x_stride + (bb * KB + (KB / 4u) * g4) * 2u;
+                    uint32_t o[4];
+                    u4x8_pairs<AF>(w[a][q], o);
+                    af = u4_t{o[0], o[1], o[2], o[3]};
+                }
+                // every wave runs all TB column slots (a slot past the group reads a
+                // clamped fragment and is never stored): no branches between MFMAs
+#pragma unroll
+                for (uint32_t j = 0; j < TB; ++j)
+                {
                     if constexpr (WF == OPURE_W_I8PC)
-                    {
-                        const half8_t b1 = __builtin_bit_cast(half8_t, *reinterpret_cast<const u4_t*>(xr));
-                        const half8_t b2 = __builtin_bit_cast(half8_t, *reinterpret_cast<const u4_t*>(xr + 16));
-                        acc[t][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, af[0]), b1,
-                                                                           acc[t][j], 0, 0, 0);
-                        acc[t][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, af[1]), b2,
-                                                                           acc[t][j], 0, 0, 0);
-                    }
+                        acc[a][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, af),
+                                                                           __builtin_bit_cast(half8_t, bf[j]), acc[a][j], 0, 0, 0);
+                    else if constexpr (AF == OPURE_A_F16)
+                        bacc[a][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, af),
+                                                                            __builtin_bit_cast(half8_t, bf[j]), bacc[a][j], 0, 0, 0);
                     else
-                    {
-                        f4_t bacc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-                        for (uint32_t q = 0; q < 4; ++q)
-                        {
-                            const u4_t bx = *reinterpret_cast<const u4_t*>(xr + 16u * q);
-                            if constexpr (AF == OPURE_A_F16)
-                                bacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, af[q]),
-                                                                              __builtin_bit_cast(half8_t, bx), bacc, 0, 0, 0);
-                            else
-                                bacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, af[q]),
-                                                                               __builtin_bit_cast(bf16x8_t, bx), bacc, 0, 0, 0);
-                        }
-                        // acc += (s / MUL) * (bacc - (OFF + MUL z) * xs)   (see U4)
-                        const float xs = xsum[m * wp.ckb + bb];
-#pragma unroll
-                        for (int i = 0; i < 4; ++i)
-                        {
-                            float sc, zo;
-                            u4_group<AF>(sz[i], sc, zo);
-                            acc[t][j][i] = __fmaf_rn(sc, __fmaf_rn(-zo, xs, bacc[i]), acc[t][j][i]);
-                        }
-                    }
+                        bacc[a][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, af),
+                                                                             __builtin_bit_cast(bf16x8_t, bf[j]), bacc[a][j], 0, 0, 0);
                 }
             }
-            par ^= 1u;
+        }
+        if constexpr (WF == OPURE_W_I4G128)
+        {
+            // acc += (s / MUL) * (bacc - (OFF + MUL z) * xs), xs = the block's sum of X for this column (see U4)
+#pragma unroll
+            for (uint32_t j = 0; j < TB; ++j)
+            {
+                const float xs = add_xor32(add_xor16(xpart[j]));
+#pragma unroll
+                for (uint32_t a = 0; a < TA; ++a)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                    {
+                        float sc, zo;
+                        u4_group<AF>(s[a][i], sc, zo);
+                        acc[a][j][i] = __fmaf_rn(sc, __fmaf_rn(-zo, xs, bacc[a][j][i]), acc[a][j][i]);
+                    }
+            }
+        }
+    };
+
+    // Half kh takes blocks b_begin + kh, + kh + KH, ...; a step moves both
+    // halves one block on, with one barrier for the whole workgroup.
+    const uint32_t steps = (b_end - b_begin + KH - 1u) / KH;
+    const uint32_t bh = b_begin + kh;
+    u4_t xr[DX][XR];
+    u4_t wv[DW][TA], sv[DW][TA];
+#pragma unroll
+    for (uint32_t d = 0; d < DX; ++d) xload(xr[d], bh + KH * d);
+#pragma unroll
+    for (uint32_t d = 0; d < DW; ++d) wload(wv[d], sv[d], bh + KH * d);
+    for (uint32_t i0 = 0; i0 < steps; i0 += U)
+    {
+#pragma unroll
+        for (uint32_t s = 0; s < U; ++s)
+        {
+            const uint32_t b = bh + KH * (i0 + s);
+            xstore(xr[s % DX], s & 1u);
+            xload(xr[s % DX], b + KH * DX);
+            __syncthreads();
+            if (b < b_end) compute(wv[s % DW], sv[s % DW], s & 1u);
+            wload(wv[s % DW], sv[s % DW], b + KH * DW);
         }
     }
-#pragma unroll
-    for (uint32_t t = 0; t < TO; ++t)
-    {
-        const uint32_t tile = tile0 + t;
-        if (tile >= p.tiles) continue;
-#pragma unroll
-        for (uint32_t j = 0; j < CTW; ++j)
+
+    auto finish = [&](uint32_t a, uint32_t j, const f4_t& tot) {
+        const uint32_t tile = tile0 + a;
+        if (tile >= p.tiles || j >= tb) return;
+        const uint32_t ct = ct0 + wc + WIDE_WC * j;
+        if (wp.splits == 1u)
         {
-            const uint32_t ct = wave + 4u * j;
-            if (ct >= mt) continue;
-            if (wp.splits == 1u)
-            {
-                float bv = 0.0f;
-                int32_t bi = 0;
-                epilogue<WF, EPI>(p, tile, 16u * ct + r16, g4, acc[t][j], bv, bi);
-            }
-            else
-            {
-                wp.part[((static_cast<uint64_t>(blockIdx.y) * p.tiles + tile) * mt + ct) * 64u + lane] = acc[t][j];
-            }
+            float bv = 0.0f;
+            int32_t bi = 0;
+            epilogue<WF, EPI>(p, tile, 16u * ct + r16, g4, tot, bv, bi);
         }
+        else
+        {
+            wp.part[((static_cast<uint64_t>(split) * p.tiles + tile) * wp.mt + ct) * 64u + lane] = tot;
+        }
+    };
+    if constexpr (KH == 1)
+    {
+#pragma unroll
+        for (uint32_t a = 0; a < TA; ++a)
+#pragma unroll
+            for (uint32_t j = 0; j < TB; ++j) finish(a, j, acc[a][j]);
+    }
+    else
+    {
+        // the halves add through LDS (the X stages are free): half 0 finishes
+        // the first TA/2 tiles of its wave, half 1 the others; each sum is
+        // (even blocks) + (odd blocks)
+        constexpr uint32_t HT = TA / 2u;
+        __syncthreads();
+        u4_t* ex = xl + ((1u - kh) * 4u + w4) * (HT * TB * 64u);  // the other half's inbox for this wave
+#pragma unroll
+        for (uint32_t h = 0; h < HT; ++h)
+#pragma unroll
+            for (uint32_t j = 0; j < TB; ++j)
+                ex[(h * TB + j) * 64u + lane] = __builtin_bit_cast(u4_t, kh == 0 ? acc[HT + h][j] : acc[h][j]);
+        __syncthreads();
+        const u4_t* in = xl + (kh * 4u + w4) * (HT * TB * 64u);
+        const uint32_t keep = kh == 0 ? 0u : HT;
+#pragma unroll
+        for (uint32_t h = 0; h < HT; ++h)
+#pragma unroll
+            for (uint32_t j = 0; j < TB; ++j)
+            {
+                const f4_t other = __builtin_bit_cast(f4_t, in[(h * TB + j) * 64u + lane]);
+                const f4_t mine = kh == 0 ? acc[h][j] : acc[HT + h][j];
+                const f4_t even = kh == 0 ? mine : other, odd = kh == 0 ? other : mine;
+                finish(keep + h, j, even + odd);
+            }
     }
 }
 
@@ -250,15 +338,8 @@ __global__ __launch_bounds__(256) void k_wide_reduce(WParams wp)
 template <int WF, int AF, int EPI>
 int launch_wide_epi(opure_dev* dev, const WParams& wp, uint32_t lds)
 {
-    static bool configured = false;
-    if (!configured)
-    {
-        OPURE_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_wide<WF, AF, EPI>),
-                                          hipFuncAttributeMaxDynamicSharedMemorySize, 159 * 1024));
-        configured = true;
-    }
-    const uint32_t groups = (wp.p.tiles + WIDE_TO - 1u) / WIDE_TO;
-    OPURE_LAUNCH(dev, (k_gemm_wide<WF, AF, EPI>), dim3(groups, wp.splits), dim3(256), lds, wp);
+    (void)lds;
+    OPURE_LAUNCH(dev, (k_gemm_wide<WF, AF, EPI>), dim3(wp.nrg * wp.ncg * wp.splits), dim3(256 * WideDepth<WF>::KH), 0, wp);
     OPURE_LAUNCH_CHECK("k_gemm_wide");
     if (wp.splits > 1u)
     {

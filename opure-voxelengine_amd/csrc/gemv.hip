@@ -234,12 +234,12 @@ Plan make_plan(const opure_dev* dev, uint32_t wfmt, uint32_t xfmt, uint32_t out,
     return pl;
 }
 
-// Shape plan of the GEMV over more than OPURE_MAX_ROWS rows: K splits so that
-// every CU gets a workgroup (at least 4 blocks per split), and the largest X
-// chunk whose LDS footprint fits.
+// Shape plan of the GEMV over more than OPURE_MAX_ROWS rows: row groups of 8
+// tiles, column groups of at most 8 column tiles, and K splits for shapes
+// with few row groups.  The splits depend on the weight shape only (not on
+// the row count), so a row's sums do not depend on the batch around it.
 struct WidePlan {
-    uint32_t tiles = 0, nblk = 0, mt = 0, ckb = 0, splits = 1, bps = 0, lds = 0;
-    uint32_t x_stride = 0, off_xsum = 0, off_a = 0, off_s = 0;
+    uint32_t tiles = 0, nblk = 0, mt = 0, nrg = 0, ncg = 0, cgs = 0, splits = 1, bps = 0;
     uint64_t part_bytes = 0;
 };
 
@@ -248,34 +248,21 @@ WidePlan wide_plan(const opure_dev* dev, uint32_t wfmt, uint32_t out, uint32_t i
     using namespace opure_gemv;
     WidePlan w;
     const uint32_t KB = kb_of(wfmt);
+    const uint32_t U = wfmt == OPURE_W_I8PC ? WideDepth<OPURE_W_I8PC>::U : WideDepth<OPURE_W_I4G128>::U;
     w.tiles = out / 16u;
     w.nblk = in / KB;
     w.mt = (M + 15u) / 16u;
-    const uint32_t groups = (w.tiles + WIDE_TO - 1u) / WIDE_TO;
+    w.nrg = (w.tiles + WIDE_RT - 1u) / WIDE_RT;
+    w.ncg = (w.mt + WIDE_CG - 1u) / WIDE_CG;
+    w.cgs = (w.mt + w.ncg - 1u) / w.ncg;
+    // split K while there are fewer row groups than half the CUs (a batch
+    // over 128 rows has two column groups), at most 8 ways and U blocks a split
     const uint32_t n_cu = dev && dev->n_cu > 0 ? static_cast<uint32_t>(dev->n_cu) : 256u;
-    if (groups < n_cu) w.splits = std::min((n_cu + groups - 1u) / groups, std::max(1u, w.nblk / 4u));
+    const uint32_t want = std::max(1u, n_cu / 2u);
+    if (w.nrg < want) w.splits = std::min({(want + w.nrg - 1u) / w.nrg, std::max(1u, w.nblk / U), 8u});
     w.bps = (w.nblk + w.splits - 1u) / w.splits;
+    w.bps = (w.bps + U - 1u) / U * U;
     w.splits = (w.nblk + w.bps - 1u) / w.bps;
-    const uint32_t aq = KB / 32u;
-    const uint32_t abytes = 2u * WIDE_TO * aq * 64u * 16u, sbytes = 2u * WIDE_TO * 16u * 4u;
-    for (uint32_t ckb : {8u, 4u, 2u, 1u})
-    {
-        if (ckb > w.bps && ckb > 1u) continue;
-        const uint32_t stride = ckb * KB * 2u + 16u;
-        const uint32_t xb = static_cast<uint32_t>(opure_hip::align_up(16ull * w.mt * stride, 16));
-        const uint32_t xs = wfmt == OPURE_W_I4G128 ? static_cast<uint32_t>(opure_hip::align_up(16ull * w.mt * ckb * 4u, 16)) : 0u;
-        const uint32_t total = xb + xs + abytes + sbytes;
-        if (total <= 159u * 1024u || ckb == 1u)
-        {
-            w.ckb = ckb;
-            w.x_stride = stride;
-            w.off_xsum = xb;
-            w.off_a = xb + xs;
-            w.off_s = xb + xs + abytes;
-            w.lds = total;
-            break;
-        }
-    }
     w.part_bytes = w.splits > 1u ? static_cast<uint64_t>(w.splits) * w.tiles * w.mt * 64u * 16u : 0u;
     return w;
 }
@@ -371,15 +358,13 @@ static int gemv_launch_wide(opure_dev* dev, const GemvCall& c)
     kp.ss_out = c.ss_out;
     kp.err = dev->err;
     kp.wait_limit = dev->wait_limit;
-    kp.x_stride = w.x_stride;
-    kp.off_xsum = w.off_xsum;
     kp.qkv = c.qkv;
     wp.mt = w.mt;
-    wp.ckb = w.ckb;
+    wp.nrg = w.nrg;
+    wp.ncg = w.ncg;
+    wp.cgs = w.cgs;
     wp.splits = w.splits;
     wp.bps = w.bps;
-    wp.off_a = w.off_a;
-    wp.off_s = w.off_s;
     wp.part = static_cast<f4_t*>(c.part_scratch);
     if (c.gain)
     {
@@ -393,9 +378,9 @@ static int gemv_launch_wide(opure_dev* dev, const GemvCall& c)
         kp.x = static_cast<const uint8_t*>(c.xn_scratch);
         kp.gain = nullptr;
     }
-    if (c.wfmt == OPURE_W_I8PC) return launch_wide_i8(dev, c.epi, wp, w.lds);
-    if (c.xfmt == OPURE_A_F16) return launch_wide_i4_f16(dev, c.epi, wp, w.lds);
-    return launch_wide_i4_bf16(dev, c.epi, wp, w.lds);
+    if (c.wfmt == OPURE_W_I8PC) return launch_wide_i8(dev, c.epi, wp, 0);
+    if (c.xfmt == OPURE_A_F16) return launch_wide_i4_f16(dev, c.epi, wp, 0);
+    return launch_wide_i4_bf16(dev, c.epi, wp, 0);
 }
 
 int gemv_launch(opure_dev* dev, const GemvCall& c)

@@ -393,8 +393,41 @@ constexpr int stage_rows()
     return NTH >= 1024 ? 4 : 8;
 }
 
+typedef float f2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t u2_t __attribute__((ext_vector_type(2)));
+
+// v[0..3] into elements i .. i + 3 of an activation array (i a multiple of 4):
+// one 16- or 8-byte store, the same roundings as store_act_rt
+__device__ __forceinline__ void store4_act_rt(void* base, uint64_t i, const float (&v)[4], uint32_t af)
+{
+    if (af == OPURE_A_F32)
+    {
+        *reinterpret_cast<f4_t*>(static_cast<float*>(base) + i) = f4_t{v[0], v[1], v[2], v[3]};
+        return;
+    }
+    uint32_t h[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) h[k] = af == OPURE_A_F16 ? f32_to_f16(v[k]) : f32_to_bf16(v[k]);
+    *reinterpret_cast<u2_t*>(static_cast<uint16_t*>(base) + i) = u2_t{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+}
+
+// a, b into elements i, i + 1 (i even): one 8- or 4-byte store
+__device__ __forceinline__ void store2_act_rt(void* base, uint64_t i, float a, float b, uint32_t af)
+{
+    if (af == OPURE_A_F32)
+    {
+        *reinterpret_cast<f2_t*>(static_cast<float*>(base) + i) = f2_t{a, b};
+        return;
+    }
+    const uint32_t ha = af == OPURE_A_F16 ? f32_to_f16(a) : f32_to_bf16(a);
+    const uint32_t hb = af == OPURE_A_F16 ? f32_to_f16(b) : f32_to_bf16(b);
+    *reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(base) + i) = ha | (hb << 16);
+}
+
 // EPI_LOGITS keeps the best (value, lowest index) of column m seen so far in
 // (best_v, best_i); the workgroup writes one partial per column at its end.
+// The thin GEMM's epilogue: lane (g4, r16) holds rows 4 g4 .. 4 g4 + 3 of the
+// tile for X row m, stored with one vector store where the layout allows.
 template <int WF, int EPI>
 __device__ __forceinline__ void epilogue(const KParams& p, uint32_t tile, uint32_t m, uint32_t g4, f4_t tot,
                                          float& best_v, int32_t& best_i)
@@ -440,14 +473,15 @@ __device__ __forceinline__ void epilogue(const KParams& p, uint32_t tile, uint32
         float sq = 0.0f;
         if (m < M)
         {
-            float* y = static_cast<float*>(p.y) + static_cast<uint64_t>(m) * p.out + 16u * tile + 4u * g4;
+            f4_t* y = reinterpret_cast<f4_t*>(static_cast<float*>(p.y) + static_cast<uint64_t>(m) * p.out + 16u * tile + 4u * g4);
+            f4_t nv = *y;
 #pragma unroll
             for (int i = 0; i < 4; ++i)
             {
-                const float nv = __fadd_rn(y[i], v[i]);
-                y[i] = nv;
-                sq = __fmaf_rn(nv, nv, sq);
+                nv[i] = __fadd_rn(nv[i], v[i]);
+                sq = __fmaf_rn(nv[i], nv[i], sq);
             }
+            *y = nv;
         }
         sq = add_xor32(add_xor16(sq));
         if (p.ss_out && m < M && g4 == 0) p.ss_out[static_cast<uint64_t>(tile) * M + m] = sq;
@@ -456,17 +490,14 @@ __device__ __forceinline__ void epilogue(const KParams& p, uint32_t tile, uint32
     if (m >= M) return;
     if constexpr (EPI == opure_hip::EPI_STORE)
     {
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-            store_act_rt(p.y, static_cast<uint64_t>(m) * p.out + 16u * tile + 4u * g4 + i, v[i], p.yfmt);
+        store4_act_rt(p.y, static_cast<uint64_t>(m) * p.out + 16u * tile + 4u * g4, v, p.yfmt);
     }
     else if constexpr (EPI == opure_hip::EPI_SWIGLU)
     {
         // tile rows alternate gate / up: (v0, v1) and (v2, v3) are (gate, up) pairs
         const uint32_t F = p.out >> 1;
         const uint32_t f = 8u * tile + 2u * g4;
-        store_act_rt(p.y, static_cast<uint64_t>(m) * F + f, swiglu(v[0], v[1]), p.yfmt);
-        store_act_rt(p.y, static_cast<uint64_t>(m) * F + f + 1u, swiglu(v[2], v[3]), p.yfmt);
+        store2_act_rt(p.y, static_cast<uint64_t>(m) * F + f, swiglu(v[0], v[1]), swiglu(v[2], v[3]), p.yfmt);
     }
     else if constexpr (EPI == opure_hip::EPI_QKV)
     {
@@ -497,8 +528,7 @@ __device__ __forceinline__ void epilogue(const KParams& p, uint32_t tile, uint32
         }
         if (o0 < e.qdim)
         {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) store_act_rt(p.y, static_cast<uint64_t>(m) * e.qdim + o0 + i, v[i], p.yfmt);
+            store4_act_rt(p.y, static_cast<uint64_t>(m) * e.qdim + o0, v, p.yfmt);
             return;
         }
         const uint32_t kvsel = o0 < e.qdim + e.kvdim ? 0u : 1u;
@@ -508,6 +538,15 @@ __device__ __forceinline__ void epilogue(const KParams& p, uint32_t tile, uint32
         if (page < 0 || static_cast<uint32_t>(page) >= e.n_pages)   // no page for the row: dropped, reported
         {
             if (e.err) e.err[ERR_POSITION] = 1u;
+            return;
+        }
+        // K rows are token-major (d0 .. d0 + 3 adjacent), V channel-major
+        if (kvsel == 0u)
+        {
+            store4_act_rt(e.kv_pool,
+                          kv_elem(e.layer, e.n_pages, static_cast<uint32_t>(page), 0u, e.n_kv_heads, kh, hd,
+                                  pos % OPURE_PAGE_SIZE, d0),
+                          v, p.yfmt);
             return;
         }
 #pragma unroll
