@@ -62,7 +62,8 @@ struct WParams {
     uint32_t cgs;     // column tiles per group (<= WIDE_CG)
     uint32_t splits;  // K splits
     uint32_t bps;     // blocks per split, a multiple of WideDepth::U
-    f4_t* part;       // splits > 1: accumulators [split][tile][mt][64]
+    uint32_t part_rows;  // splits > 1: 0 = accumulators [split][tile][mt][64] lanes, 1 = [split][M][out] rows
+    f4_t* part;       // splits > 1: the splits' accumulators
 };
 
 // Workgroup -> (split, row group, column group).  Workgroups are dispatched
@@ -277,6 +278,13 @@ __global__ __launch_bounds__(256 * WideDepth<WF>::KH) void k_gemm_wide(WParams w
             int32_t bi = 0;
             epilogue<WF, EPI>(p, tile, 16u * ct + r16, g4, tot, bv, bi);
         }
+        else if (wp.part_rows)
+        {
+            const uint32_t m = 16u * ct + r16;
+            if (m < p.M)
+                *reinterpret_cast<f4_t*>(reinterpret_cast<float*>(wp.part) +
+                                         (static_cast<uint64_t>(split) * p.M + m) * p.out + 16u * tile + 4u * g4) = tot;
+        }
         else
         {
             wp.part[((static_cast<uint64_t>(split) * p.tiles + tile) * wp.mt + ct) * 64u + lane] = tot;
@@ -335,12 +343,119 @@ __global__ __launch_bounds__(256) void k_wide_reduce(WParams wp)
     epilogue<WF, EPI>(p, tile, 16u * ct + (lane & 15u), lane >> 4, tot, bv, bi);
 }
 
+// The residual GEMV's splits added (row-major accumulators) with the next
+// consumer's rmsnorm fused in: one workgroup per row m.  Per 4 outputs
+// (o = 4u .. 4u + 3: tile u / 4, lane group u % 4) the same operations as the
+// residual epilogue after k_wide_reduce -- splits added in split order, the
+// int8 scale, y += v, the 4-output fma chain of squares and the tile's sum
+// (g0 + g1) + (g2 + g3) -- then inv_rms from the tile sums in inv_rms_wave's
+// order and round(y * inv * gain) as k_rmsnorm_rows, so y, ss_out and the
+// normalised rows equal the separate passes' bit for bit.
+constexpr uint32_t RN_THREADS = 256, RN_SPLITS = 8;   // the plan splits K at most 8 ways
+template <int WF, int AF, int UNITS>
+__global__ __launch_bounds__(RN_THREADS) void k_wide_reduce_norm(WParams wp, const float* gain, void* xn)
+{
+    const KParams& p = wp.p;
+    const uint32_t m = blockIdx.x, tid = threadIdx.x, lane = tid & 63u;
+    const uint32_t units = p.out / 4u;
+    __shared__ float ss_t[RN_THREADS * UNITS / 4u];
+    __shared__ float inv_s;
+    float* y = static_cast<float*>(p.y) + static_cast<uint64_t>(m) * p.out;
+    const float* part = reinterpret_cast<const float*>(wp.part);
+    // every split's accumulators and the residual in one round trip
+    f4_t ps[UNITS][RN_SPLITS], y0[UNITS];
+#pragma unroll
+    for (uint32_t j = 0; j < UNITS; ++j)
+    {
+        const uint32_t uc = min(tid + RN_THREADS * j, units - 1u);
+#pragma unroll
+        for (uint32_t s = 0; s < RN_SPLITS; ++s)
+            ps[j][s] = *reinterpret_cast<const f4_t*>(part + (static_cast<uint64_t>(min(s, wp.splits - 1u)) * p.M + m) * p.out +
+                                                      4u * uc);
+        y0[j] = *reinterpret_cast<const f4_t*>(y + 4u * uc);
+    }
+    f4_t nv[UNITS];
+#pragma unroll
+    for (uint32_t j = 0; j < UNITS; ++j)
+    {
+        const uint32_t u = tid + RN_THREADS * j;
+        const bool live = u < units;
+        const uint32_t uc = live ? u : 0u;
+        f4_t tot = ps[j][0];
+#pragma unroll
+        for (uint32_t s = 1; s < RN_SPLITS; ++s)
+            if (s < wp.splits) tot += ps[j][s];
+        float sq = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+        {
+            float v = tot[i];
+            if constexpr (WF == OPURE_W_I8PC) v = __fmul_rn(v, f16_to_f32(static_cast<const uint16_t*>(p.sc)[4u * uc + i]));
+            nv[j][i] = __fadd_rn(y0[j][i], v);
+            sq = __fmaf_rn(nv[j][i], nv[j][i], sq);
+        }
+        if (live) *reinterpret_cast<f4_t*>(y + 4u * uc) = nv[j];
+        // the tile's 4 lane groups are 4 consecutive threads
+        const float a = __fadd_rn(sq, __shfl_xor(sq, 1));
+        const float t = __fadd_rn(a, __shfl_xor(a, 2));
+        if (live && (u & 3u) == 0u)
+        {
+            ss_t[u >> 2] = t;
+            if (p.ss_out) p.ss_out[static_cast<uint64_t>(u >> 2) * p.M + m] = t;
+        }
+    }
+    __syncthreads();
+    if (tid < 64u)
+    {
+        float ssum = 0.0f;
+        for (uint32_t t = lane; t < p.tiles; t += 64u) ssum += ss_t[t];
+        KParams q = p;
+        q.in = p.out;                 // the rms is over this GEMV's outputs
+        const float inv = inv_rms_finish(q, ssum);
+        if (tid == 0) inv_s = inv;
+    }
+    __syncthreads();
+    const float inv = inv_s;
+    uint8_t* dst = static_cast<uint8_t*>(xn) + static_cast<uint64_t>(m) * p.out * 2u;
+#pragma unroll
+    for (uint32_t j = 0; j < UNITS; ++j)
+    {
+        const uint32_t u = tid + RN_THREADS * j;
+        if (u >= units) continue;
+        const f4_t g = *reinterpret_cast<const f4_t*>(gain + 4u * u);
+        float r[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) r[i] = __fmul_rn(__fmul_rn(nv[j][i], inv), g[i]);
+        *reinterpret_cast<u2_t*>(dst + 8u * u) = u2_t{pack2<AF>(r[0], r[1]), pack2<AF>(r[2], r[3])};
+    }
+}
+
+// outputs up to 2048 (2 units of 4 a thread) or 4096 (4)
+template <int WF, int AF>
+int launch_wide_reduce_norm(opure_dev* dev, const WParams& wp, const float* gain, void* xn)
+{
+    if (wp.p.out <= 8u * RN_THREADS)
+        OPURE_LAUNCH(dev, (k_wide_reduce_norm<WF, AF, 2>), dim3(wp.p.M), dim3(RN_THREADS), 0, wp, gain, xn);
+    else
+        OPURE_LAUNCH(dev, (k_wide_reduce_norm<WF, AF, 4>), dim3(wp.p.M), dim3(RN_THREADS), 0, wp, gain, xn);
+    OPURE_LAUNCH_CHECK("k_wide_reduce_norm");
+    return OPURE_OK;
+}
+
+template <int WF, int AF, int EPI>
+int launch_wide_epi_only(opure_dev* dev, const WParams& wp)
+{
+    OPURE_LAUNCH(dev, (k_gemm_wide<WF, AF, EPI>), dim3(wp.nrg * wp.ncg * wp.splits), dim3(256 * WideDepth<WF>::KH), 0, wp);
+    OPURE_LAUNCH_CHECK("k_gemm_wide");
+    return OPURE_OK;
+}
+
 template <int WF, int AF, int EPI>
 int launch_wide_epi(opure_dev* dev, const WParams& wp, uint32_t lds)
 {
     (void)lds;
-    OPURE_LAUNCH(dev, (k_gemm_wide<WF, AF, EPI>), dim3(wp.nrg * wp.ncg * wp.splits), dim3(256 * WideDepth<WF>::KH), 0, wp);
-    OPURE_LAUNCH_CHECK("k_gemm_wide");
+    const int rc0 = launch_wide_epi_only<WF, AF, EPI>(dev, wp);
+    if (rc0) return rc0;
     if (wp.splits > 1u)
     {
         const uint32_t n = wp.p.tiles * wp.mt;
@@ -351,10 +466,17 @@ int launch_wide_epi(opure_dev* dev, const WParams& wp, uint32_t lds)
 }
 
 // every epilogue but the per-workgroup argmax partials (wide callers store
-// fp32 logits and take the argmax over them)
+// fp32 logits and take the argmax over them); a residual with K splits and a
+// fused rmsnorm (gain != null) adds its splits in k_wide_reduce_norm
 template <int WF, int AF>
-int launch_wide_format(opure_dev* dev, uint32_t epi, const WParams& wp, uint32_t lds)
+int launch_wide_format(opure_dev* dev, uint32_t epi, const WParams& wp, uint32_t lds, const float* gain = nullptr,
+                       void* xn = nullptr)
 {
+    if (gain && epi == opure_hip::EPI_RESIDUAL && wp.splits > 1u)
+    {
+        const int rc = launch_wide_epi_only<WF, AF, opure_hip::EPI_RESIDUAL>(dev, wp);
+        return rc ? rc : launch_wide_reduce_norm<WF, AF>(dev, wp, gain, xn);
+    }
     using namespace opure_hip;
     switch (epi)
     {

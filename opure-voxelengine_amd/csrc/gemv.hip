@@ -16,10 +16,10 @@ int launch_f32(opure_dev*, uint32_t, uint32_t, bool, const KParams&, const Recip
 int launch_i8(opure_dev*, uint32_t, uint32_t, bool, const KParams&, const Recipe&, uint32_t, uint32_t);
 int launch_i4_f16(opure_dev*, uint32_t, uint32_t, bool, const KParams&, const Recipe&, uint32_t, uint32_t);
 int launch_i4_bf16(opure_dev*, uint32_t, uint32_t, bool, const KParams&, const Recipe&, uint32_t, uint32_t);
-int launch_wide_i8(opure_dev*, uint32_t, const WParams&, uint32_t);
+int launch_wide_i8(opure_dev*, uint32_t, const WParams&, uint32_t, const float*, void*);
 int launch_valu_i8(opure_dev*, uint32_t, const KParams&);
-int launch_wide_i4_f16(opure_dev*, uint32_t, const WParams&, uint32_t);
-int launch_wide_i4_bf16(opure_dev*, uint32_t, const WParams&, uint32_t);
+int launch_wide_i4_f16(opure_dev*, uint32_t, const WParams&, uint32_t, const float*, void*);
+int launch_wide_i4_bf16(opure_dev*, uint32_t, const WParams&, uint32_t, const float*, void*);
 
 }  // namespace opure_gemv
 
@@ -304,6 +304,15 @@ int gemv_validate(const GemvCall& c)
         OPURE_REQUIRE(c.epi != EPI_LOGITS, OPURE_E_UNSUPPORTED,
                       "gemv: argmax partials are built for at most %d rows (store the logits instead)", OPURE_MAX_ROWS);
         OPURE_REQUIRE(!c.gain || c.xn_scratch, OPURE_E_INVALID, "gemv: rmsnorm over %u rows needs xn_scratch", c.M);
+        OPURE_REQUIRE(!c.norm_gain || (c.epi == EPI_RESIDUAL && c.norm_out && c.ss_out &&
+                                       (reinterpret_cast<uintptr_t>(c.norm_gain) & 15u) == 0),
+                      OPURE_E_INVALID, "gemv: a fused next rmsnorm needs the residual epilogue, norm_out, ss_out and "
+                      "a 16-byte aligned gain");
+    }
+    else
+    {
+        OPURE_REQUIRE(!c.norm_gain, OPURE_E_INVALID, "gemv: a fused next rmsnorm is built for more than %d rows",
+                      OPURE_MAX_ROWS);
     }
     OPURE_REQUIRE(c.W.out >= 16 && c.W.out % 16 == 0, OPURE_E_INVALID, "gemv: out=%u must be a positive multiple of 16",
                   c.W.out);
@@ -366,6 +375,11 @@ static int gemv_launch_wide(opure_dev* dev, const GemvCall& c)
     wp.splits = w.splits;
     wp.bps = w.bps;
     wp.part = static_cast<f4_t*>(c.part_scratch);
+    kp.eps = c.eps;
+    // a residual with K splits and the next rmsnorm: row-major partials, added
+    // and normalised per row by k_wide_reduce_norm (outputs up to 4096)
+    const bool fused_norm = c.norm_gain && c.epi == EPI_RESIDUAL && w.splits > 1u && w.splits <= 8u && c.W.out <= 4096u;
+    wp.part_rows = fused_norm ? 1u : 0u;
     if (c.gain)
     {
         // rmsnorm into the scratch rows first, then the GEMV reads them
@@ -378,9 +392,20 @@ static int gemv_launch_wide(opure_dev* dev, const GemvCall& c)
         kp.x = static_cast<const uint8_t*>(c.xn_scratch);
         kp.gain = nullptr;
     }
-    if (c.wfmt == OPURE_W_I8PC) return launch_wide_i8(dev, c.epi, wp, 0);
-    if (c.xfmt == OPURE_A_F16) return launch_wide_i4_f16(dev, c.epi, wp, 0);
-    return launch_wide_i4_bf16(dev, c.epi, wp, 0);
+    const float* ng = fused_norm ? c.norm_gain : nullptr;
+    int rc;
+    if (c.wfmt == OPURE_W_I8PC) rc = launch_wide_i8(dev, c.epi, wp, 0, ng, c.norm_out);
+    else if (c.xfmt == OPURE_A_F16) rc = launch_wide_i4_f16(dev, c.epi, wp, 0, ng, c.norm_out);
+    else rc = launch_wide_i4_bf16(dev, c.epi, wp, 0, ng, c.norm_out);
+    if (rc || !c.norm_gain || fused_norm) return rc;
+    // the same normalised rows from the residual just written (no splits to fuse into)
+    KParams np = kp;
+    np.x = static_cast<const uint8_t*>(c.y);
+    np.in = c.W.out;
+    np.gain = c.norm_gain;
+    np.ss_in = c.ss_out;
+    np.ss_tiles = c.W.out / 16u;
+    return rmsnorm_rows_launch(dev, np, c.xfmt, c.M, c.norm_out);
 }
 
 int gemv_launch(opure_dev* dev, const GemvCall& c)

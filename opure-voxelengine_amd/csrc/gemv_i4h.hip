@@ -11,9 +11,9 @@ int launch_i4_f16(opure_dev* dev, uint32_t epi, uint32_t nm, bool staged, const 
     return launch_format<OPURE_W_I4G128, OPURE_A_F16>(dev, epi, nm, staged, kp, r, grid, lds);
 }
 
-int launch_wide_i4_f16(opure_dev* dev, uint32_t epi, const WParams& wp, uint32_t lds)
+int launch_wide_i4_f16(opure_dev* dev, uint32_t epi, const WParams& wp, uint32_t lds, const float* gain, void* xn)
 {
-    return launch_wide_format<OPURE_W_I4G128, OPURE_A_F16>(dev, epi, wp, lds);
+    return launch_wide_format<OPURE_W_I4G128, OPURE_A_F16>(dev, epi, wp, lds, gain, xn);
 }
 
 }  // namespace opure_gemv

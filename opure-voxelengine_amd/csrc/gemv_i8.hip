@@ -22,9 +22,9 @@ int launch_valu_i8(opure_dev* dev, uint32_t epi, const KParams& kp)
     return opure_hip::set_error(OPURE_E_INVALID, "gemv: the vector-ALU engine has no epilogue %u", epi);
 }
 
-int launch_wide_i8(opure_dev* dev, uint32_t epi, const WParams& wp, uint32_t lds)
+int launch_wide_i8(opure_dev* dev, uint32_t epi, const WParams& wp, uint32_t lds, const float* gain, void* xn)
 {
-    return launch_wide_format<OPURE_W_I8PC, OPURE_A_F16>(dev, epi, wp, lds);
+    return launch_wide_format<OPURE_W_I8PC, OPURE_A_F16>(dev, epi, wp, lds, gain, xn);
 }
 
 }  // namespace opure_gemv

@@ -166,6 +166,11 @@ struct GemvCall {
     // more than OPURE_MAX_ROWS rows with K split over workgroups: the splits'
     // accumulators (gemv_scratch_bytes)
     void* part_scratch = nullptr;
+    // EPI_RESIDUAL over more than OPURE_MAX_ROWS rows: also write the next
+    // consumer's rmsnorm of the new residual, round(y * inv_rms * norm_gain),
+    // to norm_out [M][out] in xfmt (the same bits as the consumer's own pass)
+    const float* norm_gain = nullptr;
+    void* norm_out = nullptr;
     QkvEpilogue qkv{};
     LogitsEpilogue logits{};
 };

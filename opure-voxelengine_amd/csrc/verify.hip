@@ -212,10 +212,17 @@ static int check_model(const opure_model* m, const opure_kv* kv, uint32_t B, uin
 // append, attention, o_proj + residual, rmsnorm + gate/up + SwiGLU, down +
 // residual.  `c` carries the step-wide GEMV fields (formats, rows, scratch).
 // The body of RecordForward's layer loop (Opure_VoxelEngine.cpp:296-492).
+// Above OPURE_MAX_ROWS rows a residual GEMV also writes the next rmsnorm's
+// rows (GemvCall::norm_gain) into xn, so the consumer reads them instead of
+// running its own normalisation pass: xn_ready says the incoming xn holds
+// this layer's attention-norm rows, next_gain is the norm after the layer.
 static int layer_launch(opure_dev* dev, const opure_model* m, const opure_kv* kv, uint32_t L, uint32_t B, uint32_t R,
-                        const int32_t* seq_len, uint32_t max_ctx, const VerifyPlan& P, float* x, float* ss, GemvCall& c)
+                        const int32_t* seq_len, uint32_t max_ctx, const VerifyPlan& P, float* x, float* ss, GemvCall& c,
+                        bool xn_ready = false, const float* next_gain = nullptr)
 {
+    const bool wide = B * R > OPURE_MAX_ROWS;
     char* ws = static_cast<char*>(dev->ws);
+    void* xn = ws + P.xn;
     void* q = ws + P.q;
     void* att = ws + P.att;
     void* hbuf = ws + P.h;
@@ -223,10 +230,11 @@ static int layer_launch(opure_dev* dev, const opure_model* m, const opure_kv* kv
     int rc;
     const opure_layer_weights& W = m->layers[L];
     c.W = W.qkv;
-    c.x = x;
-    c.gain = W.attn_norm;
+    c.x = xn_ready ? xn : x;
+    c.gain = xn_ready ? nullptr : W.attn_norm;
     c.ss_in = ss;
     c.ss_out = nullptr;
+    c.norm_gain = nullptr;
     c.y = q;
     c.yfmt = m->afmt;
     c.epi = EPI_QKV;
@@ -261,14 +269,17 @@ static int layer_launch(opure_dev* dev, const opure_model* m, const opure_kv* kv
     c.y = x;
     c.yfmt = OPURE_A_F32;
     c.epi = EPI_RESIDUAL;
+    c.norm_gain = wide ? W.mlp_norm : nullptr;
+    c.norm_out = xn;
     if ((rc = gemv_validate(c)) || (rc = prof_begin(dev, OPURE_STAGE_O)) || (rc = gemv_launch(dev, c)) ||
         (rc = prof_end(dev)))
         return rc;
 
     c.W = W.gate_up;
-    c.x = x;
-    c.gain = W.mlp_norm;
+    c.x = wide ? xn : x;
+    c.gain = wide ? nullptr : W.mlp_norm;
     c.ss_out = nullptr;
+    c.norm_gain = nullptr;
     c.y = hbuf;
     c.yfmt = m->afmt;
     c.epi = EPI_SWIGLU;
@@ -283,6 +294,8 @@ static int layer_launch(opure_dev* dev, const opure_model* m, const opure_kv* kv
     c.y = x;
     c.yfmt = OPURE_A_F32;
     c.epi = EPI_RESIDUAL;
+    c.norm_gain = wide ? next_gain : nullptr;
+    c.norm_out = xn;
     if ((rc = gemv_validate(c)) || (rc = prof_begin(dev, OPURE_STAGE_DOWN)) || (rc = gemv_launch(dev, c)) ||
         (rc = prof_end(dev)))
         return rc;
@@ -405,20 +418,25 @@ int opure_verify_step(opure_dev* dev, const opure_verify_args* a)
     // `ss`; the next consumer (qkv, gate/up, LM head) applies the RMSNorm while
     // loading x.  Stream order keeps the single buffer consistent.
     GemvCall c = step_gemv(m, MR, P, ws, ss);
+    const bool wide = MR > OPURE_MAX_ROWS;
     for (uint32_t L = 0; L < m->n_layers; ++L)
-        if ((rc = layer_launch(dev, m, kv, L, B, R, a->seq_len, a->max_ctx, P, x, ss, c))) return rc;
+    {
+        const float* next = L + 1u < m->n_layers ? m->layers[L + 1u].attn_norm : (a->logits ? m->final_norm : nullptr);
+        if ((rc = layer_launch(dev, m, kv, L, B, R, a->seq_len, a->max_ctx, P, x, ss, c, wide && L > 0u, next)))
+            return rc;
+    }
     if (!a->logits) return OPURE_OK;
 
     c.W = m->lm_head;
-    c.x = x;
-    c.gain = m->final_norm;
+    c.x = wide ? static_cast<const void*>(ws + P.xn) : x;
+    c.gain = wide ? nullptr : m->final_norm;
+    c.norm_gain = nullptr;
     c.ss_out = nullptr;
     c.y = a->logits;
     c.yfmt = OPURE_A_F32;
     // up to OPURE_MAX_ROWS rows the LM head also leaves per-workgroup argmax
     // partials; beyond, the logits are stored and reduced per 4096 columns
-    const bool wide = MR > OPURE_MAX_ROWS;
-    c.epi = wide ? EPI_STORE : EPI_LOGITS;
+        c.epi = wide ? EPI_STORE : EPI_LOGITS;
     c.logits.am_val = reinterpret_cast<float*>(ws + P.am_val);
     c.logits.am_idx = reinterpret_cast<int32_t*>(ws + P.am_idx);
     if ((rc = gemv_validate(c)) || (rc = prof_begin(dev, OPURE_STAGE_LM_HEAD)) || (rc = gemv_launch(dev, c)) ||
