@@ -411,6 +411,10 @@ int opure_debug_set_wait_limit(opure_dev* dev, uint32_t sleeps);
  * engine comparison.  The verify step always uses the matrix cores. */
 enum { OPURE_GEMV_MFMA = 0, OPURE_GEMV_VALU = 1 };
 int opure_debug_set_gemv_engine(opure_dev* dev, uint32_t engine);
+/* Evaluates the SwiGLU epilogue's branch-free exponential and the oracle-order
+ * exponential the other kernels use on every one of the 2^32 fp32 bit
+ * patterns and counts the results that differ (bit for bit; 0 expected). */
+int opure_debug_exp_check(opure_dev* dev, uint64_t* mismatches);
 int opure_debug_verify_offsets(const opure_model* model, uint32_t batch, uint32_t rows, uint32_t max_ctx,
                                uint64_t offsets[5]);
 

@@ -416,10 +416,36 @@ __device__ __forceinline__ uint64_t kv_elem(uint32_t layer, uint32_t n_pages, ui
     return kvsel == 0u ? plane + static_cast<uint64_t>(slot) * hd + d : plane + static_cast<uint64_t>(d) * OPURE_PAGE_SIZE + slot;
 }
 
+// expf_ref without branches: the same operations wherever expf_ref computes
+// (x clamped into that range first, which changes nothing there), the NaN,
+// overflow and underflow results chosen by selects -- so the same bits
+__device__ __forceinline__ float expf_ref_sel(float x)
+{
+    const float LOG2E = static_cast<float>(1.4426950408889634);
+    const float LN2_HI = 0.693145751953125f;
+    const float LN2_LO = static_cast<float>(0.6931471805599453 - 0.693145751953125);
+    const float xc = fminf(fmaxf(x, -87.33654022216797f), 88.72283935546875f);
+    const float kf = __builtin_rintf(__fmul_rn(xc, LOG2E));
+    float r = __fmaf_rn(-kf, LN2_HI, xc);
+    r = __fmaf_rn(-kf, LN2_LO, r);
+    float p = static_cast<float>(1.0 / 5040.0);
+    p = __fmaf_rn(p, r, static_cast<float>(1.0 / 720.0));
+    p = __fmaf_rn(p, r, static_cast<float>(1.0 / 120.0));
+    p = __fmaf_rn(p, r, static_cast<float>(1.0 / 24.0));
+    p = __fmaf_rn(p, r, static_cast<float>(1.0 / 6.0));
+    p = __fmaf_rn(p, r, 0.5f);
+    p = __fmaf_rn(p, r, 1.0f);
+    p = __fmaf_rn(p, r, 1.0f);
+    const int k = static_cast<int>(kf);
+    // expf_ref: p * 2^k, or (p * 2^127) * 2 for k = 128 (a product by 1 is exact)
+    const float v = __fmul_rn(__fmul_rn(p, bits_f(static_cast<uint32_t>(min(k, 127) + 127) << 23)), k > 127 ? 2.0f : 1.0f);
+    return x != x ? x : (x > 88.72283935546875f ? __builtin_huge_valf() : (x < -87.33654022216797f ? 0.0f : v));
+}
+
 // silu(g) * u in the order of Opure_CpuReference.cpp:195-196
 __device__ __forceinline__ float swiglu(float g, float u)
 {
-    const float s = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf_ref(-g)));
+    const float s = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf_ref_sel(-g)));
     return __fmul_rn(__fmul_rn(g, s), u);
 }
 

@@ -499,9 +499,42 @@ __global__ void k_convert_f32(const float* src, void* dst, uint32_t afmt, uint64
 
 uint32_t grid_for(uint64_t n, uint32_t block) { const uint64_t g = (n + block - 1) / block; return g > 65535 ? 65535u : (g ? static_cast<uint32_t>(g) : 1u); }
 
+// every fp32 bit pattern in [base, base + gridDim.x * 256): expf_ref_sel
+// against expf_ref, counting words that differ
+__global__ void k_exp_check(uint32_t base, unsigned long long* bad)
+{
+    const uint32_t x = base + blockIdx.x * 256u + threadIdx.x;
+    const float v = __uint_as_float(x);
+    const bool diff = __float_as_uint(expf_ref(v)) != __float_as_uint(expf_ref_sel(v));
+    const uint64_t n = __ballot(diff);
+    if ((threadIdx.x & 63u) == 0 && n) atomicAdd(bad, static_cast<unsigned long long>(__popcll(n)));
+}
+
 }  // namespace
 
 extern "C" {
+
+int opure_debug_exp_check(opure_dev* dev, uint64_t* mismatches)
+{
+    OPURE_REQUIRE(dev && mismatches, OPURE_E_INVALID, "opure_debug_exp_check: null argument");
+    unsigned long long* bad = nullptr;
+    OPURE_HIP_TRY(hipMalloc(&bad, sizeof(unsigned long long)));
+    int rc = OPURE_OK;
+    if (hipMemsetAsync(bad, 0, sizeof(unsigned long long), dev->stream) != hipSuccess) rc = set_error(OPURE_E_HIP, "exp check: memset");
+    for (uint64_t base = 0; rc == OPURE_OK && base < (1ull << 32); base += (1ull << 26))
+    {
+        hipLaunchKernelGGL(k_exp_check, dim3((1u << 26) / 256u), dim3(256), 0, dev->stream, static_cast<uint32_t>(base), bad);
+        if (hipGetLastError() != hipSuccess) rc = set_error(OPURE_E_HIP, "exp check: launch");
+    }
+    unsigned long long h = 0;
+    if (rc == OPURE_OK && (hipMemcpyAsync(&h, bad, sizeof(h), hipMemcpyDeviceToHost, dev->stream) != hipSuccess ||
+                           hipStreamSynchronize(dev->stream) != hipSuccess))
+        rc = set_error(OPURE_E_HIP, "exp check: copy");
+    (void)hipFree(bad);
+    *mismatches = h;
+    return rc;
+}
+
 
 int opure_synth_normal_f32(opure_dev* dev, float* dst, uint64_t n, uint64_t seed, uint32_t tensor_id, float std_,
                            float mean)

@@ -152,6 +152,7 @@ def _declare(L):
         "opure_debug_workspace": ([vp, C.POINTER(vp), C.POINTER(u64)], i),
         "opure_debug_set_wait_limit": ([vp, u32], i),
         "opure_debug_set_gemv_engine": ([vp, u32], i),
+        "opure_debug_exp_check": ([vp, C.POINTER(u64)], i),
         "opure_debug_verify_offsets": ([C.POINTER(Model), u32, u32, u32, C.POINTER(u64)], i),
         "opure_tiled_bytes": ([u32, u32, u32, C.POINTER(u64), C.POINTER(u64)], i),
         "opure_tile_linear": ([vp, u32, u32, C.POINTER(Linear), vp, vp, C.POINTER(Linear)], i),

@@ -120,6 +120,15 @@ def test_narrowing_rounds_to_nearest_even(dev, afmt):
     assert bad.size == 0, [(hex(int(x.view(np.uint32)[i])), hex(int(got[i])), hex(int(want[i]))) for i in bad[:8]]
 
 
+def test_branch_free_exp_same_bits(dev):
+    """The SwiGLU epilogue's select-based exponential returns the bits of the
+    oracle-order exponential on all 2^32 fp32 inputs (NaNs, infinities,
+    subnormal results, the 2^127 * 2 overflow step included)."""
+    n = C.c_uint64(1)
+    H.check(H.lib().opure_debug_exp_check(dev.h, C.byref(n)))
+    assert n.value == 0
+
+
 @pytest.mark.parametrize("wfmt", [H.W_F32, H.W_I8PC, H.W_I4G128])
 @pytest.mark.parametrize("layout", [H.LAYOUT_TILED, H.LAYOUT_TILED_SWIGLU])
 def test_tile_linear_layout(dev, wfmt, layout):
