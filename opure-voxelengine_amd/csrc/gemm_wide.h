@@ -244,6 +244,21 @@ __global__ __launch_bounds__(256 * WideDepth<WF>::KH) void k_gemm_wide(WParams w
         }
     };
 
+    // int8 with one split: the row scales of the tiles this wave finishes, loaded
+    // now rather than after the K loop (a round trip off the epilogue)
+    constexpr uint32_t FT = KH == 1 ? TA : TA / 2u;      // tiles a wave finishes
+    f4_t scl[FT];
+    if constexpr (WF == OPURE_W_I8PC)
+    {
+#pragma unroll
+        for (uint32_t h = 0; h < FT; ++h)
+        {
+            const uint32_t t = min(tile0 + (KH == 1 ? h : kh * FT + h), p.tiles - 1u);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) scl[h][i] = f16_to_f32(static_cast<const uint16_t*>(p.sc)[t * 16u + 4u * g4 + i]);
+        }
+    }
+
     // Half kh takes blocks b_begin + kh, + kh + KH, ...; a step moves both
     // halves one block on, with one barrier for the whole workgroup.
     const uint32_t steps = (b_end - b_begin + KH - 1u) / KH;
@@ -268,7 +283,8 @@ __global__ __launch_bounds__(256 * WideDepth<WF>::KH) void k_gemm_wide(WParams w
         }
     }
 
-    auto finish = [&](uint32_t a, uint32_t j, const f4_t& tot) {
+    // a: the tile within the wave's TA, h: its index among the FT it finishes
+    auto finish = [&](uint32_t a, uint32_t h, uint32_t j, const f4_t& tot) {
         const uint32_t tile = tile0 + a;
         if (tile >= p.tiles || j >= tb) return;
         const uint32_t ct = ct0 + wc + WIDE_WC * j;
@@ -276,7 +292,7 @@ __global__ __launch_bounds__(256 * WideDepth<WF>::KH) void k_gemm_wide(WParams w
         {
             float bv = 0.0f;
             int32_t bi = 0;
-            epilogue<WF, EPI>(p, tile, 16u * ct + r16, g4, tot, bv, bi);
+            epilogue<WF, EPI>(p, tile, 16u * ct + r16, g4, tot, bv, bi, WF == OPURE_W_I8PC ? &scl[h] : nullptr);
         }
         else if (wp.part_rows)
         {
@@ -295,7 +311,7 @@ __global__ __launch_bounds__(256 * WideDepth<WF>::KH) void k_gemm_wide(WParams w
 #pragma unroll
         for (uint32_t a = 0; a < TA; ++a)
 #pragma unroll
-            for (uint32_t j = 0; j < TB; ++j) finish(a, j, acc[a][j]);
+            for (uint32_t j = 0; j < TB; ++j) finish(a, a, j, acc[a][j]);
     }
     else
     {
@@ -321,7 +337,7 @@ __global__ __launch_bounds__(256 * WideDepth<WF>::KH) void k_gemm_wide(WParams w
                 const f4_t other = __builtin_bit_cast(f4_t, in[(h * TB + j) * 64u + lane]);
                 const f4_t mine = kh == 0 ? acc[h][j] : acc[HT + h][j];
                 const f4_t even = kh == 0 ? mine : other, odd = kh == 0 ? other : mine;
-                finish(keep + h, j, even + odd);
+                finish(keep + h, h, j, even + odd);
             }
     }
 }

@@ -430,7 +430,7 @@ __device__ __forceinline__ void store2_act_rt(void* base, uint64_t i, float a, f
 // tile for X row m, stored with one vector store where the layout allows.
 template <int WF, int EPI>
 __device__ __forceinline__ void epilogue(const KParams& p, uint32_t tile, uint32_t m, uint32_t g4, f4_t tot,
-                                         float& best_v, int32_t& best_i)
+                                         float& best_v, int32_t& best_i, const f4_t* scale = nullptr)
 {
     const uint32_t M = p.M;
     float v[4];
@@ -438,8 +438,9 @@ __device__ __forceinline__ void epilogue(const KParams& p, uint32_t tile, uint32
     for (int i = 0; i < 4; ++i)
     {
         v[i] = tot[i];
+        // int8: the row scales, loaded here or passed in (the same values)
         if constexpr (WF == OPURE_W_I8PC)
-            v[i] = __fmul_rn(v[i], f16_to_f32(static_cast<const uint16_t*>(p.sc)[tile * 16u + 4u * g4 + i]));
+            v[i] = __fmul_rn(v[i], scale ? (*scale)[i] : f16_to_f32(static_cast<const uint16_t*>(p.sc)[tile * 16u + 4u * g4 + i]));
     }
     if constexpr (EPI == opure_hip::EPI_LOGITS)
     {
