@@ -28,9 +28,12 @@
 //
 //  With one split the epilogue runs here; with several, each split writes
 //  its raw accumulators and k_wide_reduce adds the splits in split order and
-//  runs the epilogue.  The split count depends on the weight shape only, and
-//  each (row, column) sums its blocks in order, so a row's result does not
-//  depend on how many rows share the call, and runs are reproducible.
+//  runs the epilogue (k_wide_reduce_norm for a residual that feeds an
+//  rmsnorm: it also writes the normalised rows).  The split count depends on
+//  the weight shape only, and each (row, column) sums its blocks in a fixed
+//  order (each wave set's blocks in order, then the sets added), so a row's
+//  result does not depend on how many rows share the call, and runs are
+//  reproducible.
 // ============================================================================
 #pragma once
 
