@@ -423,6 +423,7 @@ struct RejectParams {
     const int32_t* drafts;
     uint32_t drafts_stride;
     uint32_t K, V, slices;
+    uint32_t phase;           // k_rej_rowstat rows: 0 all, 1 position 0's two, 2 the rest (see k_rej_rowstat)
     float tau;
     uint64_t seed;
     const uint32_t* pos_base;
@@ -474,15 +475,42 @@ __device__ __forceinline__ const float* rej_row(const RejectParams& p, uint32_t 
                     : p.draft + (static_cast<uint64_t>(b) * p.K + (r - p.K - 1u)) * p.V;
 }
 
+// The accept test of draft j of sequence b (draft token x, target row
+// statistics P, draft row statistics Q): u * q(x) < p(x), the rule accept =
+// min(1, p/q), as exact products of the row sums
+__device__ __forceinline__ bool rej_accepts(const RejectParams& p, uint32_t b, uint32_t pb, uint32_t j, int32_t x,
+                                            const RowStat& P, const RowStat& Q)
+{
+    if (x < 0 || static_cast<uint32_t>(x) >= p.V) return false;
+    const float u = uniform24(philox_u32(p.seed, pb + j, b, 1u));
+    const double lhs = __dmul_rn(__dmul_rn(static_cast<double>(u), static_cast<double>(Q.ex)), static_cast<double>(P.S));
+    const double rhs = __dmul_rn(static_cast<double>(P.ex), static_cast<double>(Q.S));
+    return lhs < rhs;
+}
+
 // REG: the row is read once, as float4s held in registers (V % 4 == 0,
 // V <= 4 * RNT * RVEC, 16-byte aligned rows); otherwise it is read twice.
+// Rows by p.phase: 0 every row (blockIdx.x = row); 1 the target and draft
+// rows of position 0 (blockIdx.x 0, 1); 2 the other rows (target 1..K, draft
+// 1..K-1), where a sequence whose first draft was rejected needs none of them
+// -- the stages after this read only the rows up to the first rejection -- so
+// its workgroups test draft 0 from phase 1's statistics and leave.
 template <bool REG, bool DIV>
 __global__ __launch_bounds__(RNT) void k_rej_rowstat(RejectParams p)
 {
     typedef float f4v __attribute__((ext_vector_type(4)));
     __shared__ float fred[RNT / 64];
     __shared__ uint64_t ured[RNT / 64];
-    const uint32_t r = blockIdx.x, b = blockIdx.y, V = p.V, K = p.K;
+    const uint32_t b = blockIdx.y, V = p.V, K = p.K;
+    const uint32_t r = p.phase == 0u ? blockIdx.x
+                     : p.phase == 1u ? (blockIdx.x == 0u ? 0u : K + 1u)
+                                     : (blockIdx.x < K ? blockIdx.x + 1u : blockIdx.x + 2u);
+    if (p.phase == 2u)
+    {
+        const RowStat* st = p.stats + static_cast<uint64_t>(b) * (2u * K + 1u);
+        const uint32_t pb = p.pos_base ? p.pos_base[b] : 0u;
+        if (!rej_accepts(p, b, pb, 0u, p.drafts[static_cast<uint64_t>(b) * p.drafts_stride], st[0], st[K + 1u])) return;
+    }
     const float tau = p.tau;
     const float* row = rej_row(p, b, r);
     float mx = -__builtin_huge_valf();
@@ -563,19 +591,7 @@ __device__ __forceinline__ void rej_stage(const RejectParams& p, uint32_t b, boo
 __device__ uint32_t rej_first_reject(const RejectParams& p, uint32_t b, uint32_t pb, const SeqShared& sh)
 {
     for (uint32_t j = 0; j < p.K; ++j)
-    {
-        const int32_t x = sh.dr[j];
-        bool acc = false;
-        if (x >= 0 && static_cast<uint32_t>(x) < p.V)
-        {
-            const RowStat P = sh.st[j], Q = sh.st[p.K + 1u + j];
-            const float u = uniform24(philox_u32(p.seed, pb + j, b, 1u));
-            const double lhs = __dmul_rn(__dmul_rn(static_cast<double>(u), static_cast<double>(Q.ex)), static_cast<double>(P.S));
-            const double rhs = __dmul_rn(static_cast<double>(P.ex), static_cast<double>(Q.S));
-            acc = lhs < rhs;
-        }
-        if (!acc) return j;
-    }
+        if (!rej_accepts(p, b, pb, j, sh.dr[j], sh.st[j], sh.st[p.K + 1u + j])) return j;
     return p.K;
 }
 
@@ -981,12 +997,24 @@ int accept_rejection_launch(opure_dev* dev, const opure_accept_args* a, void* ws
     r.new_seq_len = new_seq_len;
     const bool aligned = ((reinterpret_cast<uintptr_t>(a->target_logits) | reinterpret_cast<uintptr_t>(a->draft_logits)) & 15u) == 0;
     const bool reg = V % 4u == 0 && V <= 4u * RNT * RVEC && aligned, div = r.tau != 1.0f;
-    const dim3 rows(2u * K + 1u, B), slices(r.slices, B);
-    if (reg && div) OPURE_LAUNCH(dev, (k_rej_rowstat<true, true>), rows, dim3(RNT), 0, r);
-    if (reg && !div) OPURE_LAUNCH(dev, (k_rej_rowstat<true, false>), rows, dim3(RNT), 0, r);
-    if (!reg && div) OPURE_LAUNCH(dev, (k_rej_rowstat<false, true>), rows, dim3(RNT), 0, r);
-    if (!reg && !div) OPURE_LAUNCH(dev, (k_rej_rowstat<false, false>), rows, dim3(RNT), 0, r);
-    OPURE_LAUNCH_CHECK("k_rej_rowstat");
+    const dim3 slices(r.slices, B);
+    // with drafts and rows held in registers (one read a row): position 0's
+    // two rows first, then the other rows only for sequences whose first
+    // draft was accepted.  Rows read twice (the 128k vocabulary) keep one
+    // launch: a first phase of 2 rows a sequence leaves most CUs idle for the
+    // length of two full-row reads (C5's stage 182 -> 261 us with the split).
+    const bool split = K > 0u && reg;
+    for (uint32_t phase : {1u, 2u})
+    {
+        r.phase = split ? phase : 0u;
+        const dim3 rows(!split ? 2u * K + 1u : (phase == 1u ? 2u : 2u * K - 1u), B);
+        if (reg && div) OPURE_LAUNCH(dev, (k_rej_rowstat<true, true>), rows, dim3(RNT), 0, r);
+        if (reg && !div) OPURE_LAUNCH(dev, (k_rej_rowstat<true, false>), rows, dim3(RNT), 0, r);
+        if (!reg && div) OPURE_LAUNCH(dev, (k_rej_rowstat<false, true>), rows, dim3(RNT), 0, r);
+        if (!reg && !div) OPURE_LAUNCH(dev, (k_rej_rowstat<false, false>), rows, dim3(RNT), 0, r);
+        OPURE_LAUNCH_CHECK("k_rej_rowstat");
+        if (!split) break;
+    }
     if (div) OPURE_LAUNCH(dev, k_rej_slice<true>, slices, dim3(NT), 0, r);
     else OPURE_LAUNCH(dev, k_rej_slice<false>, slices, dim3(NT), 0, r);
     OPURE_LAUNCH_CHECK("k_rej_slice");
