@@ -532,8 +532,18 @@ def bench_c2(args):
     accs = [dev.download(st["ac"], np.int32, (B,)) for st in sets]
     tokens = float(np.mean([a.sum() + B for a in accs]))     # accepted drafts + the final token, per sequence
     value = tokens / (ms * 1e-3)
-    read = B * (2 * K + 1) * V * 4
-    written = B * V * 4 + B * (K + 2) * 4
+    # bytes the stage moves for these inputs: the row statistics read target
+    # and draft row 0 of every sequence and the other rows only where draft 0
+    # was accepted; the residual pass reads target row n (and draft row n when
+    # n < K) and writes the draw weights, which the draw pass reads before it
+    # writes the distribution
+    def stage_read(acc):
+        rows = 0
+        for n in acc.tolist():
+            rows += 2 + (2 * K - 1 if n >= 1 else 0) + (2 if n < K else 1) + 1
+        return rows * V * 4
+    read = int(np.mean([stage_read(a) for a in accs]))
+    written = 2 * B * V * 4 + B * (K + 2) * 4
     gbs = (read + written) / (ms * 1e-3) / 1e9
     log(f"accept_rejection: {ms * 1e3:.2f} us/step, {gbs:.0f} GB/s, mean accepted {np.mean(accs):.3f}")
     line = {
@@ -547,7 +557,9 @@ def bench_c2(args):
                    "mean_accepted": round(float(np.mean(accs)), 4), "wall_ms_per_step": round(wall, 5)},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "opure_accept_rejection (k_rej_rowstat + k_rej_slice + k_rej_draw), whole stage",
+                     "kernel": "opure_accept_rejection (k_rej_rowstat + k_rej_slice + k_rej_draw), whole stage; "
+                               "bytes = the rows it reads for these inputs (rows past a sequence's first "
+                               "rejection are skipped when draft 0 is rejected) + the distributions written",
                      "bytes_per_launch": read + written, "avg_us": round(ms * 1e3, 2)},
     }
     if args.cpu_baseline == "auto":
