@@ -400,7 +400,9 @@ __global__ __launch_bounds__(GNT) void k_accept_greedy(GreedyParams p)
 // Rejection sampling in three launches, all rows and slices in parallel:
 //   k_rej_rowstat  one 1024-thread workgroup per logit row (K+1 target rows
 //                  and K draft rows of each sequence): m = max l, S = sum of
-//                  fixed(e_v), and e(x) of the row's draft token
+//                  fixed(e_v), and e(x) of the row's draft token; rows too
+//                  long to hold in registers take the same statistics from
+//                  their slices instead (k_rej_smax, k_rej_ssum, k_rej_rowfin)
 //   k_rej_slice    per (slice, sequence): n from the accept tests, then the
 //                  draw weights of row n for the slice (residual max(0,p-q),
 //                  or p_K after K accepts) into a [B][V] buffer, and the
@@ -414,7 +416,7 @@ struct RowStat { float m, ex; uint64_t S; };
 struct SlicePart { uint64_t R, P; };
 
 constexpr uint32_t RNT = 1024;                 // k_rej_rowstat threads
-constexpr uint32_t RVEC = 12;                  // float4s of logits held per thread by k_rej_rowstat<true>
+constexpr uint32_t RVEC = 12;                  // float4s of logits held per thread by k_rej_rowstat
 constexpr uint32_t SLICE = 4096;               // elements per slice of k_rej_slice / k_rej_draw
 
 struct RejectParams {
@@ -431,6 +433,9 @@ struct RejectParams {
     int32_t* accepted;
     float* dist;              // [B][V] or null
     RowStat* stats;           // [B][2K+1]: target rows 0..K, then draft rows
+    float* smax;              // [B][2K+1][slices] slice maxima        } rows too long for
+    uint64_t* ssum;           // [B][2K+1][slices] slice sums of fixed } registers
+    float* sex;               // [B][2K+1] e(x) of the row's draft token }
     SlicePart* parts;         // [B][slices]
     float* wbuf;              // [B][V] draw weights of row n
     const int32_t* seq_len;   // optional new_seq_len = seq_len + n + 1
@@ -488,23 +493,29 @@ __device__ __forceinline__ bool rej_accepts(const RejectParams& p, uint32_t b, u
     return lhs < rhs;
 }
 
-// REG: the row is read once, as float4s held in registers (V % 4 == 0,
-// V <= 4 * RNT * RVEC, 16-byte aligned rows); otherwise it is read twice.
+// row of blockIdx i in a phase: 0 every row, 1 position 0's target and draft
+// rows, 2 the other rows (target 1..K, draft 1..K-1)
+__device__ __forceinline__ uint32_t rej_phase_row(const RejectParams& p, uint32_t i)
+{
+    return p.phase == 0u ? i : p.phase == 1u ? (i == 0u ? 0u : p.K + 1u) : (i < p.K ? i + 1u : i + 2u);
+}
+
+// The row is read once, as float4s held in registers (V % 4 == 0,
+// V <= 4 * RNT * RVEC, 16-byte aligned rows; longer rows go through the
+// slices below).
 // Rows by p.phase: 0 every row (blockIdx.x = row); 1 the target and draft
 // rows of position 0 (blockIdx.x 0, 1); 2 the other rows (target 1..K, draft
 // 1..K-1), where a sequence whose first draft was rejected needs none of them
 // -- the stages after this read only the rows up to the first rejection -- so
 // its workgroups test draft 0 from phase 1's statistics and leave.
-template <bool REG, bool DIV>
+template <bool DIV>
 __global__ __launch_bounds__(RNT) void k_rej_rowstat(RejectParams p)
 {
     typedef float f4v __attribute__((ext_vector_type(4)));
     __shared__ float fred[RNT / 64];
     __shared__ uint64_t ured[RNT / 64];
     const uint32_t b = blockIdx.y, V = p.V, K = p.K;
-    const uint32_t r = p.phase == 0u ? blockIdx.x
-                     : p.phase == 1u ? (blockIdx.x == 0u ? 0u : K + 1u)
-                                     : (blockIdx.x < K ? blockIdx.x + 1u : blockIdx.x + 2u);
+    const uint32_t r = rej_phase_row(p, blockIdx.x);
     if (p.phase == 2u)
     {
         const RowStat* st = p.stats + static_cast<uint64_t>(b) * (2u * K + 1u);
@@ -514,44 +525,29 @@ __global__ __launch_bounds__(RNT) void k_rej_rowstat(RejectParams p)
     const float tau = p.tau;
     const float* row = rej_row(p, b, r);
     float mx = -__builtin_huge_valf();
-    f4v vals[REG ? RVEC : 1];
+    f4v vals[RVEC];
     const uint32_t nv = V / 4u;
-    if constexpr (REG)
+    const f4v* row4 = reinterpret_cast<const f4v*>(row);
+#pragma unroll
+    for (uint32_t i = 0; i < RVEC; ++i)
     {
-        const f4v* row4 = reinterpret_cast<const f4v*>(row);
+        const uint32_t q = threadIdx.x + i * RNT;
+        vals[i] = q < nv ? row4[q] : f4v{-__builtin_huge_valf(), -__builtin_huge_valf(), -__builtin_huge_valf(),
+                                         -__builtin_huge_valf()};
 #pragma unroll
-        for (uint32_t i = 0; i < RVEC; ++i)
+        for (int e = 0; e < 4; ++e)
         {
-            const uint32_t q = threadIdx.x + i * RNT;
-            vals[i] = q < nv ? row4[q] : f4v{-__builtin_huge_valf(), -__builtin_huge_valf(), -__builtin_huge_valf(),
-                                             -__builtin_huge_valf()};
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-            {
-                vals[i][e] = scaled_logit<DIV>(vals[i][e], tau);
-                mx = fmaxf(mx, vals[i][e]);
-            }
+            vals[i][e] = scaled_logit<DIV>(vals[i][e], tau);
+            mx = fmaxf(mx, vals[i][e]);
         }
     }
-    else
-    {
-        for (uint32_t v = threadIdx.x; v < V; v += RNT) mx = fmaxf(mx, scaled_logit<DIV>(row[v], tau));
-    }
     mx = block_max_n<RNT>(mx, fred);
+    // padding lanes hold -inf: exp gives 0, fixed 0
     double sd = 0.0;
-    if constexpr (REG)
-    {
-        // padding lanes hold -inf: exp gives 0, fixed 0
 #pragma unroll
-        for (uint32_t i = 0; i < RVEC; ++i)
+    for (uint32_t i = 0; i < RVEC; ++i)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) sd += fixed_d(expf_ref_nonpos(__fsub_rn(vals[i][e], mx)));
-    }
-    else
-    {
-        for (uint32_t v = threadIdx.x; v < V; v += RNT)
-            sd += fixed_d(expf_ref_nonpos(__fsub_rn(scaled_logit<DIV>(row[v], tau), mx)));
-    }
+        for (int e = 0; e < 4; ++e) sd += fixed_d(expf_ref_nonpos(__fsub_rn(vals[i][e], mx)));
     const uint64_t s = block_sum_u64_n<RNT>(fixed_sum_u64(sd), ured);
     if (threadIdx.x == 0)
     {
@@ -564,6 +560,118 @@ __global__ __launch_bounds__(RNT) void k_rej_rowstat(RejectParams p)
         }
         p.stats[static_cast<uint64_t>(b) * (2u * K + 1u) + r] = RowStat{mx, ex, s};
     }
+}
+
+// ---- statistics of rows too long for registers, from their slices ----------
+// k_rej_smax writes each SLICE-logit slice's maximum; k_rej_ssum takes the
+// row maximum from the slice maxima and writes the slice's exact sum of
+// fixed(e) and, in the slice holding the row's draft token (slice 0 when the
+// row has none), e(x); k_rej_rowfin puts each row's RowStat together: the
+// maximum of the slice maxima and the u64 sum of the slice sums.  A maximum
+// and an integer sum do not depend on the order of their terms, so the
+// RowStat has the bits of k_rej_rowstat's one-workgroup reduction, while a
+// row is spread over `slices` workgroups.  Rows by p.phase as in
+// k_rej_rowstat (blockIdx.y); in phase 2 a sequence whose first draft was
+// rejected reads no rows.
+
+// RowStat of row r of sequence b from its slices, by one wave (lanes over the
+// slices; slices <= 64)
+__device__ RowStat rej_stat_from_slices(const RejectParams& p, uint32_t b, uint32_t r, uint32_t lane)
+{
+    const uint64_t rb = static_cast<uint64_t>(b) * (2u * p.K + 1u) + r;
+    float m = -__builtin_huge_valf();
+    uint64_t s = 0;
+    if (lane < p.slices)
+    {
+        m = p.smax[rb * p.slices + lane];
+        s = p.ssum[rb * p.slices + lane];
+    }
+    const float ex = p.sex[rb];
+    m = wave_max64(m);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) s += shfl_xor_u64(s, o);
+    return RowStat{m, ex, s};
+}
+
+// phase 2: whether sequence b's first draft was accepted, from the slices of
+// rows 0 and K + 1 (wave 0 decides, the workgroup reads the answer)
+__device__ bool rej_first_accepted_sliced(const RejectParams& p, uint32_t b, uint32_t* flag)
+{
+    if (threadIdx.x < 64u)
+    {
+        const uint32_t lane = threadIdx.x, pb = p.pos_base ? p.pos_base[b] : 0u;
+        const int32_t x = p.drafts[static_cast<uint64_t>(b) * p.drafts_stride];
+        const RowStat P = rej_stat_from_slices(p, b, 0u, lane);
+        const RowStat Q = rej_stat_from_slices(p, b, p.K + 1u, lane);
+        if (lane == 0u) *flag = rej_accepts(p, b, pb, 0u, x, P, Q) ? 1u : 0u;
+    }
+    __syncthreads();
+    return *flag != 0u;
+}
+
+template <bool DIV>
+__global__ __launch_bounds__(NT) void k_rej_smax(RejectParams p)
+{
+    __shared__ float fred[NT / 64];
+    __shared__ uint32_t go;
+    constexpr uint32_t PER = SLICE / NT;
+    const uint32_t sl = blockIdx.x, b = blockIdx.z, r = rej_phase_row(p, blockIdx.y), V = p.V;
+    if (p.phase == 2u && !rej_first_accepted_sliced(p, b, &go)) return;
+    const float* row = rej_row(p, b, r);
+    const uint32_t v0 = sl * SLICE;
+    float x[PER];
+#pragma unroll
+    for (uint32_t i = 0; i < PER; ++i) x[i] = row[min(v0 + i * NT + threadIdx.x, V - 1u)];
+    float mx = -__builtin_huge_valf();
+#pragma unroll
+    for (uint32_t i = 0; i < PER; ++i)
+        if (v0 + i * NT + threadIdx.x < V) mx = fmaxf(mx, scaled_logit<DIV>(x[i], p.tau));
+    mx = block_max_n<NT>(mx, fred);
+    if (threadIdx.x == 0u) p.smax[(static_cast<uint64_t>(b) * (2u * p.K + 1u) + r) * p.slices + sl] = mx;
+}
+
+template <bool DIV>
+__global__ __launch_bounds__(NT) void k_rej_ssum(RejectParams p)
+{
+    __shared__ float fred[NT / 64];
+    __shared__ uint64_t ured[NT / 64];
+    __shared__ uint32_t go;
+    constexpr uint32_t PER = SLICE / NT;
+    const uint32_t sl = blockIdx.x, b = blockIdx.z, r = rej_phase_row(p, blockIdx.y), V = p.V, K = p.K;
+    if (p.phase == 2u && !rej_first_accepted_sliced(p, b, &go)) return;
+    const float tau = p.tau;
+    const float* row = rej_row(p, b, r);
+    const uint64_t rb = static_cast<uint64_t>(b) * (2u * K + 1u) + r;
+    const uint32_t v0 = sl * SLICE;
+    // the slice's logits and the row's slice maxima in one round
+    float x[PER];
+#pragma unroll
+    for (uint32_t i = 0; i < PER; ++i) x[i] = row[min(v0 + i * NT + threadIdx.x, V - 1u)];
+    const float ms = threadIdx.x < p.slices ? p.smax[rb * p.slices + threadIdx.x] : -__builtin_huge_valf();
+    const float m = block_max_n<NT>(ms, fred);
+    double sd = 0.0;
+#pragma unroll
+    for (uint32_t i = 0; i < PER; ++i)
+        if (v0 + i * NT + threadIdx.x < V) sd += fixed_d(expf_ref_nonpos(__fsub_rn(scaled_logit<DIV>(x[i], tau), m)));
+    const uint64_t s = block_sum_u64_n<NT>(fixed_sum_u64(sd), ured);
+    if (threadIdx.x == 0u)
+    {
+        p.ssum[rb * p.slices + sl] = s;
+        const int32_t xt = r != K ? p.drafts[static_cast<uint64_t>(b) * p.drafts_stride + (r <= K ? r : r - K - 1u)] : -1;
+        const bool valid = xt >= 0 && static_cast<uint32_t>(xt) < V;
+        if (valid ? static_cast<uint32_t>(xt) / SLICE == sl : sl == 0u)
+            p.sex[rb] = valid ? expf_ref(__fsub_rn(scaled_logit<DIV>(row[xt], tau), m)) : 0.0f;
+    }
+}
+
+// one wave per row: the RowStat of every row of the sequences (rows a phase
+// skipped come out of stale slices and are never read)
+__global__ __launch_bounds__(NT) void k_rej_rowfin(RejectParams p)
+{
+    const uint32_t b = blockIdx.y, nrow = 2u * p.K + 1u, r = blockIdx.x * (NT / 64u) + (threadIdx.x >> 6);
+    if (r >= nrow) return;                              // whole wave
+    const RowStat st = rej_stat_from_slices(p, b, r, threadIdx.x & 63u);
+    if ((threadIdx.x & 63u) == 0u) p.stats[static_cast<uint64_t>(b) * nrow + r] = st;
 }
 
 constexpr uint32_t REJ_MAX_K = 63;              // drafts per sequence (k + 1 <= 64)
@@ -870,12 +978,19 @@ uint32_t argmax_parts(uint32_t V) { return (V + 4095u) / 4096u; }
 
 uint32_t rej_slices(uint32_t V) { return (V + SLICE - 1u) / SLICE; }
 
+// slice maxima, slice sums and e(x) of the rows read by slices
+static uint64_t rej_slice_stat_bytes(uint32_t batch, uint32_t k, uint32_t vocab)
+{
+    const uint64_t rows = static_cast<uint64_t>(batch) * (2u * k + 1u), sl = rej_slices(vocab);
+    return align_up(rows * sl * 4u, 256) + align_up(rows * sl * 8u, 256) + align_up(rows * 4u, 256);
+}
+
 uint64_t accept_ws_bytes(uint32_t batch, uint32_t k, uint32_t vocab, uint32_t mode)
 {
     if (mode == OPURE_ACCEPT_REJECTION)
         return align_up(static_cast<uint64_t>(batch) * (2u * k + 1u) * sizeof(RowStat), 256) +
                align_up(static_cast<uint64_t>(batch) * rej_slices(vocab) * sizeof(SlicePart), 256) +
-               align_up(static_cast<uint64_t>(batch) * vocab * 4u, 256);
+               align_up(static_cast<uint64_t>(batch) * vocab * 4u, 256) + rej_slice_stat_bytes(batch, k, vocab);
     return 2u * align_up(static_cast<uint64_t>(argmax_parts(vocab)) * batch * (k + 1u) * 4u, 256);
 }
 
@@ -993,27 +1108,49 @@ int accept_rejection_launch(opure_dev* dev, const opure_accept_args* a, void* ws
     r.parts = reinterpret_cast<SlicePart*>(w);
     w += align_up(static_cast<uint64_t>(B) * r.slices * sizeof(SlicePart), 256);
     r.wbuf = reinterpret_cast<float*>(w);
+    w += align_up(static_cast<uint64_t>(B) * V * 4u, 256);
+    const uint64_t nrow = static_cast<uint64_t>(B) * (2u * K + 1u);
+    r.smax = reinterpret_cast<float*>(w);
+    w += align_up(nrow * r.slices * 4u, 256);
+    r.ssum = reinterpret_cast<uint64_t*>(w);
+    w += align_up(nrow * r.slices * 8u, 256);
+    r.sex = reinterpret_cast<float*>(w);
     r.seq_len = seq_len;
     r.new_seq_len = new_seq_len;
     const bool aligned = ((reinterpret_cast<uintptr_t>(a->target_logits) | reinterpret_cast<uintptr_t>(a->draft_logits)) & 15u) == 0;
     const bool reg = V % 4u == 0 && V <= 4u * RNT * RVEC && aligned, div = r.tau != 1.0f;
     const dim3 slices(r.slices, B);
-    // with drafts and rows held in registers (one read a row): position 0's
-    // two rows first, then the other rows only for sequences whose first
-    // draft was accepted.  Rows read twice (the 128k vocabulary) keep one
-    // launch: a first phase of 2 rows a sequence leaves most CUs idle for the
-    // length of two full-row reads (C5's stage 182 -> 261 us with the split).
-    const bool split = K > 0u && reg;
+    // Position 0's two rows first, then the other rows only for sequences
+    // whose first draft was accepted.  Rows held in registers take one
+    // workgroup each; longer rows (the 128k vocabulary) are spread over their
+    // slices, so the first phase still fills the chip.
+    const bool split = K > 0u;
     for (uint32_t phase : {1u, 2u})
     {
         r.phase = split ? phase : 0u;
-        const dim3 rows(!split ? 2u * K + 1u : (phase == 1u ? 2u : 2u * K - 1u), B);
-        if (reg && div) OPURE_LAUNCH(dev, (k_rej_rowstat<true, true>), rows, dim3(RNT), 0, r);
-        if (reg && !div) OPURE_LAUNCH(dev, (k_rej_rowstat<true, false>), rows, dim3(RNT), 0, r);
-        if (!reg && div) OPURE_LAUNCH(dev, (k_rej_rowstat<false, true>), rows, dim3(RNT), 0, r);
-        if (!reg && !div) OPURE_LAUNCH(dev, (k_rej_rowstat<false, false>), rows, dim3(RNT), 0, r);
-        OPURE_LAUNCH_CHECK("k_rej_rowstat");
+        const uint32_t nr = !split ? 2u * K + 1u : (phase == 1u ? 2u : 2u * K - 1u);
+        if (reg)
+        {
+            if (div) OPURE_LAUNCH(dev, (k_rej_rowstat<true>), dim3(nr, B), dim3(RNT), 0, r);
+            else OPURE_LAUNCH(dev, (k_rej_rowstat<false>), dim3(nr, B), dim3(RNT), 0, r);
+            OPURE_LAUNCH_CHECK("k_rej_rowstat");
+        }
+        else
+        {
+            const dim3 g(r.slices, nr, B);
+            if (div) OPURE_LAUNCH(dev, k_rej_smax<true>, g, dim3(NT), 0, r);
+            else OPURE_LAUNCH(dev, k_rej_smax<false>, g, dim3(NT), 0, r);
+            OPURE_LAUNCH_CHECK("k_rej_smax");
+            if (div) OPURE_LAUNCH(dev, k_rej_ssum<true>, g, dim3(NT), 0, r);
+            else OPURE_LAUNCH(dev, k_rej_ssum<false>, g, dim3(NT), 0, r);
+            OPURE_LAUNCH_CHECK("k_rej_ssum");
+        }
         if (!split) break;
+    }
+    if (!reg)
+    {
+        OPURE_LAUNCH(dev, k_rej_rowfin, dim3((2u * K + 1u + NT / 64u - 1u) / (NT / 64u), B), dim3(NT), 0, r);
+        OPURE_LAUNCH_CHECK("k_rej_rowfin");
     }
     if (div) OPURE_LAUNCH(dev, k_rej_slice<true>, slices, dim3(NT), 0, r);
     else OPURE_LAUNCH(dev, k_rej_slice<false>, slices, dim3(NT), 0, r);

@@ -574,8 +574,11 @@ def test_accept_greedy_bit_exact(dev):
     assert np.array_equal(acc, w_acc) and np.array_equal(out, w_out)
 
 
-@pytest.mark.parametrize("B,K,V,tau", [(8, 8, 49152, 1.0), (4, 3, 1000, 0.8), (64, 8, 49152, 1.0)],
-                         ids=["b8k8", "small-t0.8", "c2-full"])
+# 49152-logit rows fit the one-workgroup-a-row statistics; longer or
+# unaligned rows take them from their 4096-logit slices
+@pytest.mark.parametrize("B,K,V,tau", [(8, 8, 49152, 1.0), (4, 3, 1000, 0.8), (64, 8, 49152, 1.0),
+                                       (8, 5, 128256, 1.0), (6, 4, 50001, 0.8), (5, 1, 65539, 1.0)],
+                         ids=["b8k8", "small-t0.8", "c2-full", "sliced-128k", "sliced-odd-t0.8", "sliced-k1"])
 def test_accept_rejection_bit_exact(dev, B, K, V, tau):
     say("rejection", B, K, V, tau)
     rng = np.random.default_rng(B * 100 + K)
