@@ -1401,10 +1401,18 @@ __global__ __launch_bounds__((PC_NC + PC_NL) * 64) void k_gemv_pc(KParams p)
                     static_cast<const uint32_t*>(p.sc) + (static_cast<uint64_t>(tile) * G + ps * SB) * 16u + lane,
                     (__attribute__((address_space(3))) void*)(base + SB * 1024u), 4, 0, 0);
         };
+        // The compute waves' prologue barriers.  The first is met before any
+        // weight load is issued: the compute waves' X has landed by then, and
+        // weights issued earlier queue with the X loads in the CU's memory
+        // pipeline and hold the prologue back.  The others are joined with
+        // bare s_barrier: a loader publishes nothing through them (its
+        // hand-off is the LDS counts), and __syncthreads would first wait for
+        // every load it has in flight.
+        __builtin_amdgcn_s_barrier();
         bool joined = false;
         auto join = [&] {
 #pragma unroll
-            for (int i = 0; i < NBAR; ++i) __syncthreads();
+            for (int i = 1; i < NBAR; ++i) __builtin_amdgcn_s_barrier();
             joined = true;
         };
         // Steps are signalled R - 1 iterations behind the issue: after issuing
