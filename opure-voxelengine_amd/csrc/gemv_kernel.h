@@ -676,6 +676,17 @@ __device__ __forceinline__ void epilogue_elem(const KParams& p, uint32_t tile, u
     }
 }
 
+// A workgroup barrier for data in LDS: each wave waits for its own LDS
+// accesses, not for the global loads it has in flight, which __syncthreads
+// drains first (a prologue's barrier would then wait for the first weight
+// blocks to land before the X staging could go on).
+__device__ __forceinline__ void lds_barrier()
+{
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
 // The staged prologue shared by the kernels.  Issue order: the first X
 // staging round, the rows' sums of squares, then `issue` (the first weight
 // loads).  Loads retire in issue order, so the staging below waits for L2
@@ -727,7 +738,7 @@ __device__ __forceinline__ void staged_prologue(const KParams& p, uint8_t* lds, 
             const float v = inv_rms_finish(p, ssum);
             if (lane == 0) sinv[m] = v;
         }
-        __syncthreads();
+        lds_barrier();
     }
     stage_store<WF, AF, NORM, NTH, KR>(p, r0, 0u, 0u, lds, sinv);
     // further rounds when the rows or the columns exceed one round
@@ -743,7 +754,7 @@ __device__ __forceinline__ void staged_prologue(const KParams& p, uint8_t* lds, 
             stage_issue<AF, NORM, NTH, KR>(p, r, j0, i0);
             stage_store<WF, AF, NORM, NTH, KR>(p, r, j0, i0, lds, sinv);
         }
-    __syncthreads();
+    lds_barrier();
     late();
 }
 
@@ -1159,7 +1170,7 @@ __global__ __launch_bounds__(512) void k_gemv_wpt(KParams p)
             }
             if (r16 == 0) *reinterpret_cast<f4_t*>(xsl + blk * 16u + 4u * g4) = xs;
         }
-        __syncthreads();
+        lds_barrier();
     }
 
     f4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -1495,7 +1506,7 @@ __global__ __launch_bounds__((PC_NC + PC_NL) * 64) void k_gemv_pc(KParams p)
             }
             if (r16 == 0) *reinterpret_cast<f4_t*>(xsl + blk * 16u + 4u * g4) = xs;
         }
-        __syncthreads();
+        lds_barrier();
     }
 
     f4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
