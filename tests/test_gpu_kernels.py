@@ -558,6 +558,28 @@ def run_accept(dev, fn, t, q, drafts, temperature=1.0, seed=0, pos_base=None, wa
     return res
 
 
+@pytest.mark.parametrize("V", [1000, 70000], ids=["registers", "sliced"])
+def test_accept_rejection_no_drafts(dev, V):
+    """k = 0: nothing to test, the token is drawn from the target row alone,
+    whose statistics come from one phase (one workgroup a row, or its
+    slices); the ids equal the oracle's."""
+    say("rejection without drafts", V)
+    rng = np.random.default_rng(V)
+    B = 3
+    t = (rng.standard_normal((B, 1, V)) * 3).astype(np.float32)
+    w_out, w_acc, _ = O.accept_rejection(t, np.zeros((B, 0, V), np.float32), np.zeros((B, 0), np.int32), 0.9, 77)
+    tb, db = dev.upload(t), dev.upload(np.zeros(1, np.int32))
+    ot, ac = dev.alloc(B * 4), dev.alloc(B * 4)
+    a = H.AcceptArgs(B, 0, V, int(tb), None, int(db), 0, 0.9, 77, None, int(ot), int(ac), None)
+    H.check(H.lib().opure_accept_rejection(dev.h, C.byref(a)))
+    dev.sync()
+    out, acc = dev.download(ot, np.int32, (B, 1)), dev.download(ac, np.int32, (B,))
+    for b in (tb, db, ot, ac):
+        b.free()
+    assert np.array_equal(acc, w_acc) and (acc == 0).all()
+    assert np.array_equal(out, w_out)
+
+
 def test_accept_greedy_bit_exact(dev):
     rng = np.random.default_rng(41)
     B, K, V = 6, 5, 50000
