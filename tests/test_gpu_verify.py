@@ -293,9 +293,11 @@ def test_c1_shape_speculative_equals_greedy(dev):
         greedy_orc, gaps = spec_loop.greedy(orc_step, prompt, n_new)
     finally:
         O.set_threads(1)
+    # the prompt and seeds give every oracle step a top-1/top-2 gap well above
+    # the fp32 logit bar (measured 3.3e-3), so the ids must agree exactly
     say("oracle min gap", min(gaps))
-    if min(gaps) > 1e-4:
-        assert greedy_orc == greedy_gpu
+    assert min(gaps) > 1e-4
+    assert greedy_orc == greedy_gpu
 
 
 @pytest.mark.parametrize("fmt", FMTS[1:], ids=FMT_IDS[1:])
