@@ -265,9 +265,11 @@ int opure_accept_rejection(opure_dev* dev, const opure_accept_args* a);
  * Its scratch is a device array of OPURE_NOALLOC_SCRATCH_BYTES built into the
  * library (one per GPU, held until the process ends); the call never
  * allocates or frees.  A shape needs batch * (2k + 1) * 16, batch *
- * ceil(vocab / 4096) * 16 and batch * vocab * 4 bytes of it (each rounded up
- * to 256); one that does not fit returns OPURE_E_CAPACITY (at vocab 128256,
- * up to 65 sequences fit).  Every call on one GPU shares that GPU's array, so calls
+ * ceil(vocab / 4096) * 16, batch * vocab * 4 and, for the rows' slice
+ * statistics, batch * (2k + 1) * (ceil(vocab / 4096) * 12 + 4) bytes of it
+ * (each part rounded up to 256); one that does not fit returns
+ * OPURE_E_CAPACITY (at vocab 128256, up to 65 sequences fit with one draft
+ * each, 64 with 3 to 7).  Every call on one GPU shares that GPU's array, so calls
  * that overlap on one GPU (streams of two opure_dev handles) race. */
 #define OPURE_NOALLOC_SCRATCH_BYTES (32ull << 20)
 int opure_accept_rejection_noalloc(opure_dev* dev, const opure_accept_args* a);
