@@ -47,6 +47,7 @@ struct AttnParams {
     uint32_t n_heads, n_kv, hd, rows, n_pages, max_pages, layer, nch, chunk, afmt;
     float scale;
     uint32_t qoff;       // matrix-core path: first query row of this launch
+    uint32_t zt;         // matrix-core path: row blocks of 16 * NT rows along blockIdx.z (b = z / zt)
     uint32_t* err;       // opure_dev::err: a row past max_ctx sets ERR_POSITION
 };
 
@@ -358,14 +359,16 @@ constexpr uint32_t attn_mfma_lds()
     return NWV * (HD / 16u) * NT * 64u * 16u + NWV * NT * 16u * 2u * 4u;
 }
 
-template <int HD, int AF, int NT, int KK, int NWV>
+// ZS: blockIdx.z holds (sequence, block of 16 * NT query rows) as b * zt + block
+template <int HD, int AF, int NT, int KK, int NWV, bool ZS>
 __global__ __launch_bounds__(NWV * 64) void k_attn_mfma(AttnParams p)
 {
     constexpr uint32_t KS = HD / 32u, DT = HD / 16u, EB = 2u, TPW = 32u * KK;
     extern __shared__ __align__(16) uint8_t lds_raw[];
     f4_t (*cacc)[DT][NT][64] = reinterpret_cast<f4_t (*)[DT][NT][64]>(lds_raw);
     float (*cml)[NT][16][2] = reinterpret_cast<float (*)[NT][16][2]>(lds_raw + NWV * DT * NT * 64u * 16u);
-    const uint32_t kh = blockIdx.x, c = blockIdx.y, b = blockIdx.z;
+    const uint32_t kh = blockIdx.x, c = blockIdx.y, b = ZS ? blockIdx.z / p.zt : blockIdx.z;
+    const uint32_t qoff = ZS ? (blockIdx.z - b * p.zt) * 16u * NT : p.qoff;
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u, g = lane >> 4, r = lane & 15u;
     const uint32_t group = p.n_heads / p.n_kv, R = p.rows, Gq = group * R;
     const uint32_t t0 = c * NWV * TPW;
@@ -398,7 +401,7 @@ __global__ __launch_bounds__(NWV * 64) void k_attn_mfma(AttnParams p)
 #pragma unroll
     for (int n = 0; n < NT; ++n)
     {
-        const uint32_t qi = min(p.qoff + 16u * n + r, Gq - 1u);
+        const uint32_t qi = min(qoff + 16u * n + r, Gq - 1u);
         const uint32_t j = qi / group, head = kh * group + (qi - j * group);
         qj[n] = j;
         const uint8_t* qrow = static_cast<const uint8_t*>(p.q) + ((static_cast<uint64_t>(b * R + j) * p.n_heads + head) * HD) * EB;
@@ -576,7 +579,7 @@ __global__ __launch_bounds__(NWV * 64) void k_attn_mfma(AttnParams p)
     for (uint32_t task = wave; task < DT * NT; task += NWV)
     {
         const uint32_t dt = task / NT, n = task - dt * NT;
-        const uint32_t qi = p.qoff + 16u * n + r;
+        const uint32_t qi = qoff + 16u * n + r;
         float mw[NWV], lw[NWV];
 #pragma unroll
         for (int w = 0; w < NWV; ++w)
@@ -692,18 +695,18 @@ __global__ __launch_bounds__(64) void k_attn_combine(AttnParams p)
     }
 }
 
-template <int HD, int AF, int NT, int KK, int NWV>
+template <int HD, int AF, int NT, int KK, int NWV, bool ZS = false>
 int launch_mfma(opure_dev* dev, dim3 grid, const AttnParams& p)
 {
     constexpr uint32_t lds = attn_mfma_lds<HD, NT, NWV>();
     static bool configured = false;
     if (!configured)
     {
-        OPURE_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_attn_mfma<HD, AF, NT, KK, NWV>),
+        OPURE_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_attn_mfma<HD, AF, NT, KK, NWV, ZS>),
                                           hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
         configured = true;
     }
-    OPURE_LAUNCH(dev, (k_attn_mfma<HD, AF, NT, KK, NWV>), grid, dim3(NWV * 64), lds, p);
+    OPURE_LAUNCH(dev, (k_attn_mfma<HD, AF, NT, KK, NWV, ZS>), grid, dim3(NWV * 64), lds, p);
     OPURE_LAUNCH_CHECK("k_attn_mfma");
     return OPURE_OK;
 }
@@ -815,26 +818,48 @@ int attn_launch(opure_dev* dev, const opure_model* m, const opure_kv* kv, uint32
     p.part_ml = part + align_up(q_elems * p.hd * 4u, 256) / 4u;
     const dim3 grid(p.n_kv, p.nch, batch);
     const uint32_t hd = p.hd;
+    p.zt = 1u;
     if (use_mfma(hd, p.afmt, Gq))
     {
-        // query rows in launches of up to 2 tiles of 16 (each row's result is the same in any launch)
-        for (uint32_t q0 = 0; q0 < Gq; q0 += 32u)
+        // head_dim 64 on a grid of few workgroups (the 1B shape at batch 1:
+        // 136 -> 272 workgroups): one 16-row block of query rows a
+        // workgroup, every block in one launch, so the chip fills; otherwise
+        // launches of up to 2 blocks a workgroup (at head_dim 128 the split
+        // grid measured slower).  Rows are independent in the kernel: each
+        // row's result is the same either way.
+        const uint32_t blocks = (Gq + 15u) / 16u, n_cu = dev->n_cu > 0 ? static_cast<uint32_t>(dev->n_cu) : 256u;
+        if (hd == 64u && blocks >= 2u && static_cast<uint64_t>(p.n_kv) * p.nch * batch * blocks <= 2ull * n_cu &&
+            batch * blocks <= 65535u)
         {
             AttnParams pq = p;
-            pq.qoff = q0;
-            const bool one = Gq - q0 <= 16u;
+            pq.qoff = 0u;
+            pq.zt = blocks;
+            const dim3 g(p.n_kv, p.nch, batch * blocks);
             int rc;
-            // head_dim 64: 4 waves x 32 tokens; 128: 8 waves x 32 tokens (two
-            // waves a SIMD, 128 KB of merge buffers)
-            if (hd == 64u && p.afmt == OPURE_A_F16)
-                rc = one ? launch_mfma<64, OPURE_A_F16, 1, 1, 4>(dev, grid, pq) : launch_mfma<64, OPURE_A_F16, 2, 1, 4>(dev, grid, pq);
-            else if (hd == 64u)
-                rc = one ? launch_mfma<64, OPURE_A_BF16, 1, 1, 4>(dev, grid, pq) : launch_mfma<64, OPURE_A_BF16, 2, 1, 4>(dev, grid, pq);
-            else if (p.afmt == OPURE_A_F16)
-                rc = one ? launch_mfma<128, OPURE_A_F16, 1, 2, 4>(dev, grid, pq) : launch_mfma<128, OPURE_A_F16, 2, 2, 4>(dev, grid, pq);
-            else
-                rc = one ? launch_mfma<128, OPURE_A_BF16, 1, 2, 4>(dev, grid, pq) : launch_mfma<128, OPURE_A_BF16, 2, 2, 4>(dev, grid, pq);
+            if (p.afmt == OPURE_A_F16) rc = launch_mfma<64, OPURE_A_F16, 1, 1, 4, true>(dev, g, pq);
+            else rc = launch_mfma<64, OPURE_A_BF16, 1, 1, 4, true>(dev, g, pq);
             if (rc) return rc;
+        }
+        else
+        {
+            for (uint32_t q0 = 0; q0 < Gq; q0 += 32u)
+            {
+                AttnParams pq = p;
+                pq.qoff = q0;
+                const bool one = Gq - q0 <= 16u;
+                int rc;
+                // head_dim 64: 4 waves x 32 tokens; 128: 4 waves x 64 tokens (two
+                // k-steps a wave)
+                if (hd == 64u && p.afmt == OPURE_A_F16)
+                    rc = one ? launch_mfma<64, OPURE_A_F16, 1, 1, 4>(dev, grid, pq) : launch_mfma<64, OPURE_A_F16, 2, 1, 4>(dev, grid, pq);
+                else if (hd == 64u)
+                    rc = one ? launch_mfma<64, OPURE_A_BF16, 1, 1, 4>(dev, grid, pq) : launch_mfma<64, OPURE_A_BF16, 2, 1, 4>(dev, grid, pq);
+                else if (p.afmt == OPURE_A_F16)
+                    rc = one ? launch_mfma<128, OPURE_A_F16, 1, 2, 4>(dev, grid, pq) : launch_mfma<128, OPURE_A_F16, 2, 2, 4>(dev, grid, pq);
+                else
+                    rc = one ? launch_mfma<128, OPURE_A_BF16, 1, 2, 4>(dev, grid, pq) : launch_mfma<128, OPURE_A_BF16, 2, 2, 4>(dev, grid, pq);
+                if (rc) return rc;
+            }
         }
     }
     else if (p.chunk == 64u && (hd == 64u || hd == 128u))
