@@ -308,8 +308,11 @@ struct GreedyParams {
 // the LM head's per-tile partials for 8 rows at a time, four partials' loads
 // in flight together, then each row is reduced across the workgroup.  The
 // winner (greater value, then lower index) is a total order, so the result
-// does not depend on the reduction order.
-constexpr uint32_t GNT = 1024;
+// does not depend on the reduction order.  256 threads: the LM head leaves
+// one partial per CU and row, and 1024 threads only lengthened the
+// workgroup's reductions (C3 9.3 -> 8.1 us, C4 11.0 -> 9.7 us; 64 and 128
+// threads measured the same as 256).
+constexpr uint32_t GNT = 256;
 
 __global__ __launch_bounds__(GNT) void k_accept_greedy(GreedyParams p)
 {
