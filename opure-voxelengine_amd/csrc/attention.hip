@@ -360,258 +360,267 @@ constexpr uint32_t attn_mfma_lds()
 }
 
 // ZS: blockIdx.z holds (sequence, block of 16 * NT query rows) as b * zt + block
-template <int HD, int AF, int NT, int KK, int NWV, bool ZS>
+// CL: a workgroup takes chunks blockIdx.y, blockIdx.y + gridDim.y, ...
+template <int HD, int AF, int NT, int KK, int NWV, bool ZS, bool CL = false>
 __global__ __launch_bounds__(NWV * 64) void k_attn_mfma(AttnParams p)
 {
     constexpr uint32_t KS = HD / 32u, DT = HD / 16u, EB = 2u, TPW = 32u * KK;
     extern __shared__ __align__(16) uint8_t lds_raw[];
     f4_t (*cacc)[DT][NT][64] = reinterpret_cast<f4_t (*)[DT][NT][64]>(lds_raw);
     float (*cml)[NT][16][2] = reinterpret_cast<float (*)[NT][16][2]>(lds_raw + NWV * DT * NT * 64u * 16u);
-    const uint32_t kh = blockIdx.x, c = blockIdx.y, b = ZS ? blockIdx.z / p.zt : blockIdx.z;
+    const uint32_t kh = blockIdx.x, b = ZS ? blockIdx.z / p.zt : blockIdx.z;
     const uint32_t qoff = ZS ? (blockIdx.z - b * p.zt) * 16u * NT : p.qoff;
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u, g = lane >> 4, r = lane & 15u;
     const uint32_t group = p.n_heads / p.n_kv, R = p.rows, Gq = group * R;
-    const uint32_t t0 = c * NWV * TPW;
-    const uint32_t tw = t0 + TPW * wave;
     const int32_t* pt = p.page_table + static_cast<uint64_t>(b) * p.max_pages;
     const uint8_t* pool = static_cast<const uint8_t*>(p.pool);
     const uint32_t nan2 = AF == OPURE_A_F16 ? 0x7E007E00u : 0x7FC07FC0u;
 
-    // ---- the sequence length, the page-table entries of this wave's tokens
-    //      and Q^T in one round trip: none of them depends on another, and the
-    //      entries are loaded unconditionally (index clamped to the table) and
-    //      checked only when used, so no load waits behind another -----------
-    const int32_t seq = p.seq_len[b];
-    int32_t pgk[KK][2], pgv[KK];
-    auto raw_entry = [&](uint32_t tok) { return pt[min(tok / OPURE_PAGE_SIZE, p.max_pages - 1u)]; };
-#pragma unroll
-    for (uint32_t kk = 0; kk < KK; ++kk)
+    // chunks blockIdx.y, blockIdx.y + gridDim.y, ...: one a workgroup, or
+    // (CL) two or more where the launch folds its grid; the partial of chunk
+    // c does not depend on which workgroup computes it
+    for (uint32_t c = blockIdx.y; c < (CL ? p.nch : blockIdx.y + 1u); c += CL ? gridDim.y : 1u)
     {
-        const uint32_t tb = tw + 32u * kk;
-#pragma unroll
-        for (uint32_t T = 0; T < 2; ++T) pgk[kk][T] = raw_entry(tb + 8u * (r >> 2) + (r & 3u) + 4u * T);
-        pgv[kk] = raw_entry(tb + 8u * g);
-    }
-    // the entry of `tok` as page_of gives it, from its raw load
-    auto checked = [&](uint32_t tok, int32_t pg) -> int32_t {
-        return tok / OPURE_PAGE_SIZE < p.max_pages && pg >= 0 && static_cast<uint32_t>(pg) < p.n_pages ? pg : -1;
-    };
-    u4v qop[NT][KS];
-    uint32_t qj[NT];
-#pragma unroll
-    for (int n = 0; n < NT; ++n)
-    {
-        const uint32_t qi = min(qoff + 16u * n + r, Gq - 1u);
-        const uint32_t j = qi / group, head = kh * group + (qi - j * group);
-        qj[n] = j;
-        const uint8_t* qrow = static_cast<const uint8_t*>(p.q) + ((static_cast<uint64_t>(b * R + j) * p.n_heads + head) * HD) * EB;
-#pragma unroll
-        for (uint32_t s = 0; s < KS; ++s) qop[n][s] = *reinterpret_cast<const u4v*>(qrow + (32u * s + 8u * g) * EB);
-    }
-    // keeps the loads above issued before the exit below (the compiler would
-    // otherwise test the length first and make them wait for it)
-    asm volatile("" ::: "memory");
-    const uint32_t ctx = static_cast<uint32_t>(seq);
-    const uint32_t total = ctx + R;
-    if (t0 >= total) return;                          // whole workgroup: no row reaches this chunk
-    const bool active = tw < total;
-    uint32_t lim[NT];
-#pragma unroll
-    for (int n = 0; n < NT; ++n) lim[n] = ctx + qj[n];
-
-    // ---- then K (both score tiles of each k-step) and V^T --------------------
-    u4v kop[KK][2][KS], vop[KK][DT];
-#pragma unroll
-    for (uint32_t kk = 0; kk < KK; ++kk)
-    {
-        const uint32_t tb = tw + 32u * kk;
-#pragma unroll
-        for (uint32_t T = 0; T < 2; ++T)
-        {
-            const uint32_t tok = tb + 8u * (r >> 2) + (r & 3u) + 4u * T;
-            const int32_t pg = active && tok < total ? checked(tok, pgk[kk][T]) : -1;
-            const uint32_t f = active && tok < total ? nan2 : 0u;
-#pragma unroll
-            for (uint32_t s = 0; s < KS; ++s)
-                kop[kk][T][s] = pg >= 0 ? *reinterpret_cast<const u4v*>(
-                                              pool + kv_elem(p.layer, p.n_pages, static_cast<uint32_t>(pg), 0u, p.n_kv, kh,
-                                                             HD, tok % OPURE_PAGE_SIZE, 32u * s + 8u * g) * EB)
-                                        : u4v{f, f, f, f};
-        }
-        const uint32_t tok = tb + 8u * g;             // 8 tokens of one page
-        const int32_t pg = active && tok < total ? checked(tok, pgv[kk]) : -1;
-        const uint32_t f = active && tok < total ? nan2 : 0u;
-#pragma unroll
-        for (uint32_t dt = 0; dt < DT; ++dt)
-        {
-            if (pg >= 0)
-            {
-                vop[kk][dt] = *reinterpret_cast<const u4v*>(pool + kv_elem(p.layer, p.n_pages, static_cast<uint32_t>(pg), 1u,
-                                                                           p.n_kv, kh, HD, tok % OPURE_PAGE_SIZE,
-                                                                           16u * dt + r) * EB);
-                if (tok + 8u > total) vop[kk][dt] = mask_tail<AF>(vop[kk][dt], total - tok);   // stale slots read 0
-            }
-            else
-            {
-                vop[kk][dt] = u4v{f, f, f, f};
-            }
-        }
-    }
-
-    // ---- scores, masked past each row's position --------------------------
-    float sc[KK][2][NT][4];
-#pragma unroll
-    for (uint32_t kk = 0; kk < KK; ++kk)
-    {
-        const uint32_t tb = tw + 32u * kk;
-#pragma unroll
-        for (uint32_t T = 0; T < 2; ++T)
-#pragma unroll
-            for (int n = 0; n < NT; ++n)
-            {
-                f4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-                for (uint32_t s = 0; s < KS; ++s) acc = mfma32<AF>(kop[kk][T][s], qop[n][s], acc);
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-                {
-                    const uint32_t tok = tb + 8u * g + 4u * T + i;
-                    sc[kk][T][n][i] = active && tok <= lim[n] ? __fmul_rn(acc[i], p.scale) : -__builtin_huge_valf();
-                }
-            }
-    }
-
-    // ---- softmax statistics of each query row over this wave's tokens -----
-    // P^T = hi + lo (fp16) or hi + mid + lo (bf16), every part in the 16-bit format
-    constexpr bool P3 = AF == OPURE_A_BF16;
-    float mrow[NT], lrow[NT];
-    u4v pop[KK][NT], plo[KK][NT], plo2[KK][NT];
-#pragma unroll
-    for (int n = 0; n < NT; ++n)
-    {
-        float mx = -__builtin_huge_valf();
-#pragma unroll
-        for (uint32_t kk = 0; kk < KK; ++kk)
-#pragma unroll
-            for (uint32_t T = 0; T < 2; ++T)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sc[kk][T][n][i]);
-        mx = max_xor32(max_xor16(mx));
-        float sum = 0.0f;
+        const uint32_t t0 = c * NWV * TPW;
+        const uint32_t tw = t0 + TPW * wave;
+        // ---- the sequence length, the page-table entries of this wave's tokens
+        //      and Q^T in one round trip: none of them depends on another, and the
+        //      entries are loaded unconditionally (index clamped to the table) and
+        //      checked only when used, so no load waits behind another -----------
+        const int32_t seq = p.seq_len[b];
+        int32_t pgk[KK][2], pgv[KK];
+        auto raw_entry = [&](uint32_t tok) { return pt[min(tok / OPURE_PAGE_SIZE, p.max_pages - 1u)]; };
 #pragma unroll
         for (uint32_t kk = 0; kk < KK; ++kk)
         {
-            float e[8];
+            const uint32_t tb = tw + 32u * kk;
 #pragma unroll
-            for (uint32_t T = 0; T < 2; ++T)
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-                {
-                    const float v = sc[kk][T][n][i];
-                    e[4 * T + i] = v == -__builtin_huge_valf() ? 0.0f : exp_hw(__fsub_rn(v, mx));
-                    sum += e[4 * T + i];
-                }
-            pop[kk][n] = u4v{pack_pair<AF>(e[0], e[1]), pack_pair<AF>(e[2], e[3]), pack_pair<AF>(e[4], e[5]),
-                             pack_pair<AF>(e[6], e[7])};
-            float lo[8];
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-            {
-                const uint32_t pr = pop[kk][n][i];
-                lo[2 * i] = __fsub_rn(e[2 * i], unpack_lo<AF>(pr));
-                lo[2 * i + 1] = __fsub_rn(e[2 * i + 1], unpack_hi<AF>(pr));
-            }
-            plo[kk][n] = u4v{pack_pair<AF>(lo[0], lo[1]), pack_pair<AF>(lo[2], lo[3]), pack_pair<AF>(lo[4], lo[5]),
-                             pack_pair<AF>(lo[6], lo[7])};
-            if constexpr (P3)
-            {
-                // the remainders are exact in fp32: e - hi and (e - hi) - mid
-                float lo2[8];
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-                {
-                    const uint32_t pr = plo[kk][n][i];
-                    lo2[2 * i] = __fsub_rn(lo[2 * i], unpack_lo<AF>(pr));
-                    lo2[2 * i + 1] = __fsub_rn(lo[2 * i + 1], unpack_hi<AF>(pr));
-                }
-                plo2[kk][n] = u4v{pack_pair<AF>(lo2[0], lo2[1]), pack_pair<AF>(lo2[2], lo2[3]),
-                                  pack_pair<AF>(lo2[4], lo2[5]), pack_pair<AF>(lo2[6], lo2[7])};
-            }
+            for (uint32_t T = 0; T < 2; ++T) pgk[kk][T] = raw_entry(tb + 8u * (r >> 2) + (r & 3u) + 4u * T);
+            pgv[kk] = raw_entry(tb + 8u * g);
         }
-        sum = add_xor32(add_xor16(sum));
-        mrow[n] = mx;
-        lrow[n] = sum;
-    }
-
-    // ---- O^T = V^T P^T ------------------------------------------------------
-    f4_t o[DT][NT];
-#pragma unroll
-    for (uint32_t dt = 0; dt < DT; ++dt)
+        // the entry of `tok` as page_of gives it, from its raw load
+        auto checked = [&](uint32_t tok, int32_t pg) -> int32_t {
+            return tok / OPURE_PAGE_SIZE < p.max_pages && pg >= 0 && static_cast<uint32_t>(pg) < p.n_pages ? pg : -1;
+        };
+        u4v qop[NT][KS];
+        uint32_t qj[NT];
 #pragma unroll
         for (int n = 0; n < NT; ++n)
         {
-            o[dt][n] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+            const uint32_t qi = min(qoff + 16u * n + r, Gq - 1u);
+            const uint32_t j = qi / group, head = kh * group + (qi - j * group);
+            qj[n] = j;
+            const uint8_t* qrow = static_cast<const uint8_t*>(p.q) + ((static_cast<uint64_t>(b * R + j) * p.n_heads + head) * HD) * EB;
+#pragma unroll
+            for (uint32_t s = 0; s < KS; ++s) qop[n][s] = *reinterpret_cast<const u4v*>(qrow + (32u * s + 8u * g) * EB);
+        }
+        // keeps the loads above issued before the exit below (the compiler would
+        // otherwise test the length first and make them wait for it)
+        asm volatile("" ::: "memory");
+        const uint32_t ctx = static_cast<uint32_t>(seq);
+        const uint32_t total = ctx + R;
+        if (t0 >= total) return;                          // whole workgroup: no row reaches this chunk
+        const bool active = tw < total;
+        uint32_t lim[NT];
+#pragma unroll
+        for (int n = 0; n < NT; ++n) lim[n] = ctx + qj[n];
+
+        // ---- then K (both score tiles of each k-step) and V^T --------------------
+        u4v kop[KK][2][KS], vop[KK][DT];
+#pragma unroll
+        for (uint32_t kk = 0; kk < KK; ++kk)
+        {
+            const uint32_t tb = tw + 32u * kk;
+#pragma unroll
+            for (uint32_t T = 0; T < 2; ++T)
+            {
+                const uint32_t tok = tb + 8u * (r >> 2) + (r & 3u) + 4u * T;
+                const int32_t pg = active && tok < total ? checked(tok, pgk[kk][T]) : -1;
+                const uint32_t f = active && tok < total ? nan2 : 0u;
+#pragma unroll
+                for (uint32_t s = 0; s < KS; ++s)
+                    kop[kk][T][s] = pg >= 0 ? *reinterpret_cast<const u4v*>(
+                                                  pool + kv_elem(p.layer, p.n_pages, static_cast<uint32_t>(pg), 0u, p.n_kv, kh,
+                                                                 HD, tok % OPURE_PAGE_SIZE, 32u * s + 8u * g) * EB)
+                                            : u4v{f, f, f, f};
+            }
+            const uint32_t tok = tb + 8u * g;             // 8 tokens of one page
+            const int32_t pg = active && tok < total ? checked(tok, pgv[kk]) : -1;
+            const uint32_t f = active && tok < total ? nan2 : 0u;
+#pragma unroll
+            for (uint32_t dt = 0; dt < DT; ++dt)
+            {
+                if (pg >= 0)
+                {
+                    vop[kk][dt] = *reinterpret_cast<const u4v*>(pool + kv_elem(p.layer, p.n_pages, static_cast<uint32_t>(pg), 1u,
+                                                                               p.n_kv, kh, HD, tok % OPURE_PAGE_SIZE,
+                                                                               16u * dt + r) * EB);
+                    if (tok + 8u > total) vop[kk][dt] = mask_tail<AF>(vop[kk][dt], total - tok);   // stale slots read 0
+                }
+                else
+                {
+                    vop[kk][dt] = u4v{f, f, f, f};
+                }
+            }
+        }
+
+        // ---- scores, masked past each row's position --------------------------
+        float sc[KK][2][NT][4];
+#pragma unroll
+        for (uint32_t kk = 0; kk < KK; ++kk)
+        {
+            const uint32_t tb = tw + 32u * kk;
+#pragma unroll
+            for (uint32_t T = 0; T < 2; ++T)
+#pragma unroll
+                for (int n = 0; n < NT; ++n)
+                {
+                    f4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                    for (uint32_t s = 0; s < KS; ++s) acc = mfma32<AF>(kop[kk][T][s], qop[n][s], acc);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                    {
+                        const uint32_t tok = tb + 8u * g + 4u * T + i;
+                        sc[kk][T][n][i] = active && tok <= lim[n] ? __fmul_rn(acc[i], p.scale) : -__builtin_huge_valf();
+                    }
+                }
+        }
+
+        // ---- softmax statistics of each query row over this wave's tokens -----
+        // P^T = hi + lo (fp16) or hi + mid + lo (bf16), every part in the 16-bit format
+        constexpr bool P3 = AF == OPURE_A_BF16;
+        float mrow[NT], lrow[NT];
+        u4v pop[KK][NT], plo[KK][NT], plo2[KK][NT];
+#pragma unroll
+        for (int n = 0; n < NT; ++n)
+        {
+            float mx = -__builtin_huge_valf();
+#pragma unroll
+            for (uint32_t kk = 0; kk < KK; ++kk)
+#pragma unroll
+                for (uint32_t T = 0; T < 2; ++T)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sc[kk][T][n][i]);
+            mx = max_xor32(max_xor16(mx));
+            float sum = 0.0f;
 #pragma unroll
             for (uint32_t kk = 0; kk < KK; ++kk)
             {
-                if constexpr (P3) o[dt][n] = mfma32<AF>(vop[kk][dt], plo2[kk][n], o[dt][n]);
-                o[dt][n] = mfma32<AF>(vop[kk][dt], plo[kk][n], o[dt][n]);
-                o[dt][n] = mfma32<AF>(vop[kk][dt], pop[kk][n], o[dt][n]);
+                float e[8];
+#pragma unroll
+                for (uint32_t T = 0; T < 2; ++T)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                    {
+                        const float v = sc[kk][T][n][i];
+                        e[4 * T + i] = v == -__builtin_huge_valf() ? 0.0f : exp_hw(__fsub_rn(v, mx));
+                        sum += e[4 * T + i];
+                    }
+                pop[kk][n] = u4v{pack_pair<AF>(e[0], e[1]), pack_pair<AF>(e[2], e[3]), pack_pair<AF>(e[4], e[5]),
+                                 pack_pair<AF>(e[6], e[7])};
+                float lo[8];
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                {
+                    const uint32_t pr = pop[kk][n][i];
+                    lo[2 * i] = __fsub_rn(e[2 * i], unpack_lo<AF>(pr));
+                    lo[2 * i + 1] = __fsub_rn(e[2 * i + 1], unpack_hi<AF>(pr));
+                }
+                plo[kk][n] = u4v{pack_pair<AF>(lo[0], lo[1]), pack_pair<AF>(lo[2], lo[3]), pack_pair<AF>(lo[4], lo[5]),
+                                 pack_pair<AF>(lo[6], lo[7])};
+                if constexpr (P3)
+                {
+                    // the remainders are exact in fp32: e - hi and (e - hi) - mid
+                    float lo2[8];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                    {
+                        const uint32_t pr = plo[kk][n][i];
+                        lo2[2 * i] = __fsub_rn(lo[2 * i], unpack_lo<AF>(pr));
+                        lo2[2 * i + 1] = __fsub_rn(lo[2 * i + 1], unpack_hi<AF>(pr));
+                    }
+                    plo2[kk][n] = u4v{pack_pair<AF>(lo2[0], lo2[1]), pack_pair<AF>(lo2[2], lo2[3]),
+                                      pack_pair<AF>(lo2[4], lo2[5]), pack_pair<AF>(lo2[6], lo2[7])};
+                }
             }
+            sum = add_xor32(add_xor16(sum));
+            mrow[n] = mx;
+            lrow[n] = sum;
         }
 
-    // ---- merge the waves in wave order: m = max, weights exp(m_w - m) -------
+        // ---- O^T = V^T P^T ------------------------------------------------------
+        f4_t o[DT][NT];
 #pragma unroll
-    for (uint32_t dt = 0; dt < DT; ++dt)
+        for (uint32_t dt = 0; dt < DT; ++dt)
 #pragma unroll
-        for (int n = 0; n < NT; ++n) cacc[wave][dt][n][lane] = o[dt][n];
-    if (g == 0)
-    {
+            for (int n = 0; n < NT; ++n)
+            {
+                o[dt][n] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int n = 0; n < NT; ++n)
+                for (uint32_t kk = 0; kk < KK; ++kk)
+                {
+                    if constexpr (P3) o[dt][n] = mfma32<AF>(vop[kk][dt], plo2[kk][n], o[dt][n]);
+                    o[dt][n] = mfma32<AF>(vop[kk][dt], plo[kk][n], o[dt][n]);
+                    o[dt][n] = mfma32<AF>(vop[kk][dt], pop[kk][n], o[dt][n]);
+                }
+            }
+
+        // ---- merge the waves in wave order: m = max, weights exp(m_w - m) -------
+#pragma unroll
+        for (uint32_t dt = 0; dt < DT; ++dt)
+#pragma unroll
+            for (int n = 0; n < NT; ++n) cacc[wave][dt][n][lane] = o[dt][n];
+        if (g == 0)
         {
-            cml[wave][n][r][0] = mrow[n];
-            cml[wave][n][r][1] = lrow[n];
-        }
-    }
-    __syncthreads();
-    const uint64_t pbase = ((static_cast<uint64_t>(b) * p.n_kv + kh) * p.nch + c) * Gq;
-    for (uint32_t task = wave; task < DT * NT; task += NWV)
-    {
-        const uint32_t dt = task / NT, n = task - dt * NT;
-        const uint32_t qi = qoff + 16u * n + r;
-        float mw[NWV], lw[NWV];
 #pragma unroll
-        for (int w = 0; w < NWV; ++w)
+            for (int n = 0; n < NT; ++n)
+            {
+                cml[wave][n][r][0] = mrow[n];
+                cml[wave][n][r][1] = lrow[n];
+            }
+        }
+        __syncthreads();
+        const uint64_t pbase = ((static_cast<uint64_t>(b) * p.n_kv + kh) * p.nch + c) * Gq;
+        for (uint32_t task = wave; task < DT * NT; task += NWV)
         {
-            mw[w] = cml[w][n][r][0];
-            lw[w] = cml[w][n][r][1];
+            const uint32_t dt = task / NT, n = task - dt * NT;
+            const uint32_t qi = qoff + 16u * n + r;
+            float mw[NWV], lw[NWV];
+#pragma unroll
+            for (int w = 0; w < NWV; ++w)
+            {
+                mw[w] = cml[w][n][r][0];
+                lw[w] = cml[w][n][r][1];
+            }
+            float M = mw[0];
+#pragma unroll
+            for (int w = 1; w < NWV; ++w) M = fmaxf(M, mw[w]);
+            float ew[NWV];
+#pragma unroll
+            for (int w = 0; w < NWV; ++w)
+                ew[w] = mw[w] == -__builtin_huge_valf() ? 0.0f : expf_ref_nonpos(__fsub_rn(mw[w], M));
+            if (qi >= Gq) continue;
+            if (dt == 0 && g == 0)
+            {
+                float L = __fmul_rn(ew[0], lw[0]);
+#pragma unroll
+                for (int w = 1; w < NWV; ++w) L = __fmaf_rn(ew[w], lw[w], L);
+                p.part_ml[(pbase + qi) * 2u] = M;
+                p.part_ml[(pbase + qi) * 2u + 1u] = L;
+            }
+            f4_t a = cacc[0][dt][n][lane] * ew[0];
+#pragma unroll
+            for (int w = 1; w < NWV; ++w)
+            {
+                const f4_t v = cacc[w][dt][n][lane];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) a[i] = __fmaf_rn(ew[w], v[i], a[i]);
+            }
+            *reinterpret_cast<f4_t*>(p.part_acc + (pbase + qi) * HD + 16u * dt + 4u * g) = a;
         }
-        float M = mw[0];
-#pragma unroll
-        for (int w = 1; w < NWV; ++w) M = fmaxf(M, mw[w]);
-        float ew[NWV];
-#pragma unroll
-        for (int w = 0; w < NWV; ++w)
-            ew[w] = mw[w] == -__builtin_huge_valf() ? 0.0f : expf_ref_nonpos(__fsub_rn(mw[w], M));
-        if (qi >= Gq) continue;
-        if (dt == 0 && g == 0)
-        {
-            float L = __fmul_rn(ew[0], lw[0]);
-#pragma unroll
-            for (int w = 1; w < NWV; ++w) L = __fmaf_rn(ew[w], lw[w], L);
-            p.part_ml[(pbase + qi) * 2u] = M;
-            p.part_ml[(pbase + qi) * 2u + 1u] = L;
-        }
-        f4_t a = cacc[0][dt][n][lane] * ew[0];
-#pragma unroll
-        for (int w = 1; w < NWV; ++w)
-        {
-            const f4_t v = cacc[w][dt][n][lane];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) a[i] = __fmaf_rn(ew[w], v[i], a[i]);
-        }
-        *reinterpret_cast<f4_t*>(p.part_acc + (pbase + qi) * HD + 16u * dt + 4u * g) = a;
+        // the next chunk writes the merge buffers again
+        if (CL && c + gridDim.y < p.nch) __syncthreads();
     }
 }
 
@@ -695,18 +704,18 @@ __global__ __launch_bounds__(64) void k_attn_combine(AttnParams p)
     }
 }
 
-template <int HD, int AF, int NT, int KK, int NWV, bool ZS = false>
+template <int HD, int AF, int NT, int KK, int NWV, bool ZS = false, bool CL = false>
 int launch_mfma(opure_dev* dev, dim3 grid, const AttnParams& p)
 {
     constexpr uint32_t lds = attn_mfma_lds<HD, NT, NWV>();
     static bool configured = false;
     if (!configured)
     {
-        OPURE_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_attn_mfma<HD, AF, NT, KK, NWV, ZS>),
+        OPURE_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_attn_mfma<HD, AF, NT, KK, NWV, ZS, CL>),
                                           hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
         configured = true;
     }
-    OPURE_LAUNCH(dev, (k_attn_mfma<HD, AF, NT, KK, NWV, ZS>), grid, dim3(NWV * 64), lds, p);
+    OPURE_LAUNCH(dev, (k_attn_mfma<HD, AF, NT, KK, NWV, ZS, CL>), grid, dim3(NWV * 64), lds, p);
     OPURE_LAUNCH_CHECK("k_attn_mfma");
     return OPURE_OK;
 }
@@ -842,6 +851,11 @@ int attn_launch(opure_dev* dev, const opure_model* m, const opure_kv* kv, uint32
         }
         else
         {
+            // a grid of many workgroups (a batch of ragged sequences) folded to
+            // two chunks a workgroup: a chunk past a sequence's end costs a
+            // workgroup a round trip, and half as many of them are launched
+            const bool fold = hd == 64u && static_cast<uint64_t>(p.n_kv) * p.nch * batch > 8ull * n_cu;
+            const dim3 fgrid(p.n_kv, (p.nch + 1u) / 2u, batch);
             for (uint32_t q0 = 0; q0 < Gq; q0 += 32u)
             {
                 AttnParams pq = p;
@@ -850,7 +864,13 @@ int attn_launch(opure_dev* dev, const opure_model* m, const opure_kv* kv, uint32
                 int rc;
                 // head_dim 64: 4 waves x 32 tokens; 128: 4 waves x 64 tokens (two
                 // k-steps a wave)
-                if (hd == 64u && p.afmt == OPURE_A_F16)
+                if (fold && p.afmt == OPURE_A_F16)
+                    rc = one ? launch_mfma<64, OPURE_A_F16, 1, 1, 4, false, true>(dev, fgrid, pq)
+                             : launch_mfma<64, OPURE_A_F16, 2, 1, 4, false, true>(dev, fgrid, pq);
+                else if (fold)
+                    rc = one ? launch_mfma<64, OPURE_A_BF16, 1, 1, 4, false, true>(dev, fgrid, pq)
+                             : launch_mfma<64, OPURE_A_BF16, 2, 1, 4, false, true>(dev, fgrid, pq);
+                else if (hd == 64u && p.afmt == OPURE_A_F16)
                     rc = one ? launch_mfma<64, OPURE_A_F16, 1, 1, 4>(dev, grid, pq) : launch_mfma<64, OPURE_A_F16, 2, 1, 4>(dev, grid, pq);
                 else if (hd == 64u)
                     rc = one ? launch_mfma<64, OPURE_A_BF16, 1, 1, 4>(dev, grid, pq) : launch_mfma<64, OPURE_A_BF16, 2, 1, 4>(dev, grid, pq);

@@ -596,6 +596,35 @@ def test_accept_greedy_bit_exact(dev):
     assert np.array_equal(acc, w_acc) and np.array_equal(out, w_out)
 
 
+def test_attention_folded_grid_same_bits(dev):
+    """A batch big enough that the launch folds two chunks into a workgroup
+    (head_dim 64, 16 sequences of up to 9000 tokens) gives every sequence
+    the bits of that sequence scored alone (one chunk a workgroup)."""
+    say("attention folded grid")
+    rng = np.random.default_rng(5)
+    nh, nkv, hd, R, ps = 8, 2, 64, 3, 16
+    ctx = [int(c) for c in rng.integers(100, 9000, size=16)]
+    B = len(ctx)
+    mp = [(c + R + ps - 1) // ps for c in ctx]
+    n_pages = sum(mp) + 4
+    hm = O.HostModel(n_layers=1, hidden=64, n_heads=nh, n_kv_heads=nkv, head_dim=hd, ffn=64, vocab=64,
+                     wfmt=O.W_F32, afmt=H.A_F16, attn_scale=hd ** -0.5, max_pos=max(ctx) + 64, seed=1)
+    kv = O.HostKV(hm, n_pages=n_pages, batch=B, max_pages_per_seq=max(mp))
+    kv.fill_random(rng, 1.0)
+    perm = rng.permutation(n_pages)
+    o = 0
+    for b in range(B):
+        kv.page_table[b, :mp[b]] = perm[o:o + mp[b]]
+        o += mp[b]
+    q_bits, _ = to_act(rng.standard_normal((B * R, nh * hd)) * 1.5, H.A_F16)
+    m = attn_model(nh, nkv, hd, H.A_F16, hd ** -0.5)
+    got = run_attn(dev, m, kv.pool, kv.page_table, ctx, R, q_bits)
+    assert np.isfinite(from_act(got, H.A_F16)).all()
+    for b in (0, 5, 11, 15):
+        one = run_attn(dev, m, kv.pool, kv.page_table[b:b + 1], [ctx[b]], R, q_bits[b * R:(b + 1) * R])
+        assert np.array_equal(one, got[b * R:(b + 1) * R]), b
+
+
 # 49152-logit rows fit the one-workgroup-a-row statistics; longer or
 # unaligned rows take them from their 4096-logit slices
 @pytest.mark.parametrize("B,K,V,tau", [(8, 8, 49152, 1.0), (4, 3, 1000, 0.8), (64, 8, 49152, 1.0),
