@@ -582,26 +582,27 @@ __global__ __launch_bounds__(NWV * 64) void k_attn_mfma(AttnParams p)
         }
         __syncthreads();
         const uint64_t pbase = ((static_cast<uint64_t>(b) * p.n_kv + kh) * p.nch + c) * Gq;
-        for (uint32_t task = wave; task < DT * NT; task += NWV)
+        // wave w merges row block w % NT, channel tiles w / NT, w / NT + NWV / NT,
+        // ...: the block's weights once, then every tile's loads in one round
+        static_assert(NWV % NT == 0 && (DT * NT) % NWV == 0, "whole channel tiles of one row block a wave");
+        const uint32_t n = wave % NT, qi = qoff + 16u * n + r;
+        float mw[NWV], lw[NWV];
+#pragma unroll
+        for (int w = 0; w < NWV; ++w)
         {
-            const uint32_t dt = task / NT, n = task - dt * NT;
-            const uint32_t qi = qoff + 16u * n + r;
-            float mw[NWV], lw[NWV];
+            mw[w] = cml[w][n][r][0];
+            lw[w] = cml[w][n][r][1];
+        }
+        float M = mw[0];
 #pragma unroll
-            for (int w = 0; w < NWV; ++w)
-            {
-                mw[w] = cml[w][n][r][0];
-                lw[w] = cml[w][n][r][1];
-            }
-            float M = mw[0];
+        for (int w = 1; w < NWV; ++w) M = fmaxf(M, mw[w]);
+        float ew[NWV];
 #pragma unroll
-            for (int w = 1; w < NWV; ++w) M = fmaxf(M, mw[w]);
-            float ew[NWV];
-#pragma unroll
-            for (int w = 0; w < NWV; ++w)
-                ew[w] = mw[w] == -__builtin_huge_valf() ? 0.0f : expf_ref_nonpos(__fsub_rn(mw[w], M));
-            if (qi >= Gq) continue;
-            if (dt == 0 && g == 0)
+        for (int w = 0; w < NWV; ++w)
+            ew[w] = mw[w] == -__builtin_huge_valf() ? 0.0f : expf_ref_nonpos(__fsub_rn(mw[w], M));
+        if (qi < Gq)
+        {
+            if (wave < NT && g == 0)
             {
                 float L = __fmul_rn(ew[0], lw[0]);
 #pragma unroll
@@ -609,15 +610,20 @@ __global__ __launch_bounds__(NWV * 64) void k_attn_mfma(AttnParams p)
                 p.part_ml[(pbase + qi) * 2u] = M;
                 p.part_ml[(pbase + qi) * 2u + 1u] = L;
             }
-            f4_t a = cacc[0][dt][n][lane] * ew[0];
 #pragma unroll
-            for (int w = 1; w < NWV; ++w)
+            for (uint32_t j = 0; j < DT * NT / NWV; ++j)
             {
-                const f4_t v = cacc[w][dt][n][lane];
+                const uint32_t dt = wave / NT + (NWV / NT) * j;
+                f4_t a = cacc[0][dt][n][lane] * ew[0];
 #pragma unroll
-                for (int i = 0; i < 4; ++i) a[i] = __fmaf_rn(ew[w], v[i], a[i]);
+                for (int w = 1; w < NWV; ++w)
+                {
+                    const f4_t v = cacc[w][dt][n][lane];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) a[i] = __fmaf_rn(ew[w], v[i], a[i]);
+                }
+                *reinterpret_cast<f4_t*>(p.part_acc + (pbase + qi) * HD + 16u * dt + 4u * g) = a;
             }
-            *reinterpret_cast<f4_t*>(p.part_acc + (pbase + qi) * HD + 16u * dt + 4u * g) = a;
         }
         // the next chunk writes the merge buffers again
         if (CL && c + gridDim.y < p.nch) __syncthreads();
