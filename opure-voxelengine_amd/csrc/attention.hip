@@ -332,8 +332,9 @@ __device__ __forceinline__ uint32_t pack_pair(float a, float b)
 //   is exactly its B operand of
 //   O^T = V^T P^T A = V^T tile (channel r, tokens tb + 8g..8g+7: 16 contiguous
 //                 bytes of a channel-major V plane)
-// All K and V loads are issued before the first MFMA.  The waves' (max, sum,
-// output) go to LDS; then the (channel tile, query tile) pieces of the merge
+// All K and V loads are issued before the first MFMA (in the folded kernel
+// unconditionally, so the scores and the softmax run while V lands).  The
+// waves' (max, sum, output) go to LDS; then the (channel tile, query tile) pieces of the merge
 // are shared out over the waves, each merging in wave order, and the chunk's
 // partial is written for the combine kernel.
 // exp(x) for x <= 0 as 2^(x log2 e) on the transcendental unit (v_exp_f32,
@@ -425,8 +426,17 @@ __global__ __launch_bounds__(NWV * 64) void k_attn_mfma(AttnParams p)
 #pragma unroll
         for (int n = 0; n < NT; ++n) lim[n] = ctx + qj[n];
 
-        // ---- then K (both score tiles of each k-step) and V^T --------------------
+        // ---- then K (both score tiles of each k-step) and V^T.  In the folded
+        //      kernel (a grid of many workgroups) every load is unconditional -- a
+        //      lane without a valid page reads page 0 and takes its fill when the
+        //      operand is used -- so the loads are one straight run and the scores
+        //      and softmax wait only for K while V lands (C5 3.294 -> 3.252 ms).
+        //      Elsewhere each load sits under its page test and the first product
+        //      waits for all of them: at one workgroup a CU (C3, C4) that measured
+        //      faster, 2-10 us a step ------------------------------------------
         u4v kop[KK][2][KS], vop[KK][DT];
+        bool kok[KK][2], vok[KK];
+        uint32_t kfill[KK][2], vfill[KK], vlen[KK];
 #pragma unroll
         for (uint32_t kk = 0; kk < KK; ++kk)
         {
@@ -437,32 +447,85 @@ __global__ __launch_bounds__(NWV * 64) void k_attn_mfma(AttnParams p)
                 const uint32_t tok = tb + 8u * (r >> 2) + (r & 3u) + 4u * T;
                 const int32_t pg = active && tok < total ? checked(tok, pgk[kk][T]) : -1;
                 const uint32_t f = active && tok < total ? nan2 : 0u;
+                if constexpr (CL)
+                {
+                    kfill[kk][T] = f;
+                    kok[kk][T] = pg >= 0;
+                    const uint32_t pgc = pg >= 0 ? static_cast<uint32_t>(pg) : 0u;
 #pragma unroll
-                for (uint32_t s = 0; s < KS; ++s)
-                    kop[kk][T][s] = pg >= 0 ? *reinterpret_cast<const u4v*>(
-                                                  pool + kv_elem(p.layer, p.n_pages, static_cast<uint32_t>(pg), 0u, p.n_kv, kh,
-                                                                 HD, tok % OPURE_PAGE_SIZE, 32u * s + 8u * g) * EB)
-                                            : u4v{f, f, f, f};
+                    for (uint32_t s = 0; s < KS; ++s)
+                        kop[kk][T][s] = *reinterpret_cast<const u4v*>(
+                            pool + kv_elem(p.layer, p.n_pages, pgc, 0u, p.n_kv, kh, HD, tok % OPURE_PAGE_SIZE, 32u * s + 8u * g) * EB);
+                }
+                else
+                {
+#pragma unroll
+                    for (uint32_t s = 0; s < KS; ++s)
+                        kop[kk][T][s] = pg >= 0 ? *reinterpret_cast<const u4v*>(
+                                                      pool + kv_elem(p.layer, p.n_pages, static_cast<uint32_t>(pg), 0u, p.n_kv, kh,
+                                                                     HD, tok % OPURE_PAGE_SIZE, 32u * s + 8u * g) * EB)
+                                                : u4v{f, f, f, f};
+                }
             }
             const uint32_t tok = tb + 8u * g;             // 8 tokens of one page
             const int32_t pg = active && tok < total ? checked(tok, pgv[kk]) : -1;
             const uint32_t f = active && tok < total ? nan2 : 0u;
-#pragma unroll
-            for (uint32_t dt = 0; dt < DT; ++dt)
+            if constexpr (CL)
             {
-                if (pg >= 0)
+                vfill[kk] = f;
+                vok[kk] = pg >= 0;
+                vlen[kk] = tok < total ? total - tok : 0u;
+                const uint32_t pgc = pg >= 0 ? static_cast<uint32_t>(pg) : 0u;
+#pragma unroll
+                for (uint32_t dt = 0; dt < DT; ++dt)
+                    vop[kk][dt] = *reinterpret_cast<const u4v*>(
+                        pool + kv_elem(p.layer, p.n_pages, pgc, 1u, p.n_kv, kh, HD, tok % OPURE_PAGE_SIZE, 16u * dt + r) * EB);
+            }
+            else
+            {
+#pragma unroll
+                for (uint32_t dt = 0; dt < DT; ++dt)
                 {
-                    vop[kk][dt] = *reinterpret_cast<const u4v*>(pool + kv_elem(p.layer, p.n_pages, static_cast<uint32_t>(pg), 1u,
-                                                                               p.n_kv, kh, HD, tok % OPURE_PAGE_SIZE,
-                                                                               16u * dt + r) * EB);
-                    if (tok + 8u > total) vop[kk][dt] = mask_tail<AF>(vop[kk][dt], total - tok);   // stale slots read 0
-                }
-                else
-                {
-                    vop[kk][dt] = u4v{f, f, f, f};
+                    if (pg >= 0)
+                    {
+                        vop[kk][dt] = *reinterpret_cast<const u4v*>(pool + kv_elem(p.layer, p.n_pages, static_cast<uint32_t>(pg), 1u,
+                                                                                   p.n_kv, kh, HD, tok % OPURE_PAGE_SIZE,
+                                                                                   16u * dt + r) * EB);
+                        if (tok + 8u > total) vop[kk][dt] = mask_tail<AF>(vop[kk][dt], total - tok);   // stale slots read 0
+                    }
+                    else
+                    {
+                        vop[kk][dt] = u4v{f, f, f, f};
+                    }
                 }
             }
         }
+        // the folded kernel's operands as used: the fill where the page is
+        // missing, and V's slots past the cache read 0
+        auto fix_k = [&](uint32_t kk) {
+            if constexpr (CL)
+#pragma unroll
+                for (uint32_t T = 0; T < 2; ++T)
+#pragma unroll
+                    for (uint32_t s = 0; s < KS; ++s)
+                    {
+                        const uint32_t f = kfill[kk][T];
+                        kop[kk][T][s] = kok[kk][T] ? kop[kk][T][s] : u4v{f, f, f, f};
+                    }
+        };
+        auto fix_v = [&](uint32_t kk) {
+            if constexpr (CL)
+            {
+                const uint32_t f = vfill[kk];
+#pragma unroll
+                for (uint32_t dt = 0; dt < DT; ++dt) vop[kk][dt] = vok[kk] ? vop[kk][dt] : u4v{f, f, f, f};
+                if (vok[kk] && vlen[kk] < 8u)
+#pragma unroll
+                    for (uint32_t dt = 0; dt < DT; ++dt) vop[kk][dt] = mask_tail<AF>(vop[kk][dt], vlen[kk]);
+            }
+        };
+        // every K and V load is issued before the first product
+        if constexpr (CL) __builtin_amdgcn_sched_barrier(0);
 
         // ---- scores, masked past each row's position --------------------------
         float sc[KK][2][NT][4];
@@ -470,6 +533,7 @@ __global__ __launch_bounds__(NWV * 64) void k_attn_mfma(AttnParams p)
         for (uint32_t kk = 0; kk < KK; ++kk)
         {
             const uint32_t tb = tw + 32u * kk;
+            fix_k(kk);
 #pragma unroll
             for (uint32_t T = 0; T < 2; ++T)
 #pragma unroll
@@ -550,6 +614,8 @@ __global__ __launch_bounds__(NWV * 64) void k_attn_mfma(AttnParams p)
         }
 
         // ---- O^T = V^T P^T ------------------------------------------------------
+#pragma unroll
+        for (uint32_t kk = 0; kk < KK; ++kk) fix_v(kk);
         f4_t o[DT][NT];
 #pragma unroll
         for (uint32_t dt = 0; dt < DT; ++dt)
