@@ -625,6 +625,41 @@ def test_attention_folded_grid_same_bits(dev):
         assert np.array_equal(one, got[b * R:(b + 1) * R]), b
 
 
+def test_attention_folded_grid_missing_page(dev):
+    """The folded kernel loads every K/V operand unconditionally (a lane whose
+    page entry is missing reads page 0) and applies the fill when the operand is
+    used: a sequence with a -1 entry inside its context reads NaN there, as the
+    one-chunk-a-workgroup kernel does, and its neighbours keep their bits."""
+    say("attention folded grid, missing page")
+    rng = np.random.default_rng(6)
+    nh, nkv, hd, R, ps = 8, 2, 64, 3, 16
+    ctx = [int(c) for c in rng.integers(4000, 9000, size=15)] + [8999]   # 71 chunks: 2 x 71 x 16 > 8 x 256
+    B = len(ctx)
+    mp = [(c + R + ps - 1) // ps for c in ctx]
+    n_pages = sum(mp) + 4
+    hm = O.HostModel(n_layers=1, hidden=64, n_heads=nh, n_kv_heads=nkv, head_dim=hd, ffn=64, vocab=64,
+                     wfmt=O.W_F32, afmt=H.A_F16, attn_scale=hd ** -0.5, max_pos=max(ctx) + 64, seed=1)
+    kv = O.HostKV(hm, n_pages=n_pages, batch=B, max_pages_per_seq=max(mp))
+    kv.fill_random(rng, 1.0)
+    perm = rng.permutation(n_pages)
+    o = 0
+    for b in range(B):
+        kv.page_table[b, :mp[b]] = perm[o:o + mp[b]]
+        o += mp[b]
+    kv.page_table[5, 3] = -1                          # tokens 48..63 of sequence 5
+    q_bits, _ = to_act(rng.standard_normal((B * R, nh * hd)) * 1.5, H.A_F16)
+    m = attn_model(nh, nkv, hd, H.A_F16, hd ** -0.5)
+    got = run_attn(dev, m, kv.pool, kv.page_table, ctx, R, q_bits)
+    vals = from_act(got, H.A_F16).reshape(B, R, -1)
+    assert np.isnan(vals[5]).all()
+    assert np.isfinite(np.delete(vals, 5, axis=0)).all()
+    one = run_attn(dev, m, kv.pool, kv.page_table[5:6], [ctx[5]], R, q_bits[5 * R:6 * R])
+    assert np.isnan(from_act(one, H.A_F16)).all()
+    for b in (0, 4, 6, 15):
+        one = run_attn(dev, m, kv.pool, kv.page_table[b:b + 1], [ctx[b]], R, q_bits[b * R:(b + 1) * R])
+        assert np.array_equal(one, got[b * R:(b + 1) * R]), b
+
+
 # 49152-logit rows fit the one-workgroup-a-row statistics; longer or
 # unaligned rows take them from their 4096-logit slices
 @pytest.mark.parametrize("B,K,V,tau", [(8, 8, 49152, 1.0), (4, 3, 1000, 0.8), (64, 8, 49152, 1.0),
