@@ -254,6 +254,7 @@ def bench_c5(args):
     V, L, nkv, hd = cfg["vocab"], cfg["n_layers"], cfg["n_kv_heads"], cfg["head_dim"]
     dev = H.Dev(0)
     log("device", dev.name)
+    peak = measure_peak(dev)
     rng = np.random.default_rng(seed)
     ctx = rng.integers(512, 8193, size=B).astype(np.int32)
     need = (ctx + R + 15) // 16
@@ -374,7 +375,9 @@ def bench_c5(args):
         line["roofline"] = {"bound": "hbm", "achieved": round(att["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                             "frac": round(att["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
                             "kernel": "paged attention (k_attn_mfma + k_attn_combine) of one layer, K/V bytes",
-                            "bytes_per_launch": att["bytes_per_launch"], "avg_us": round(att["avg_us"], 2)}
+                            "bytes_per_launch": att["bytes_per_launch"], "avg_us": round(att["avg_us"], 2),
+                            "measured_peak_GBps": peak["read_GBps"],
+                            "frac_of_measured_peak": round(att["gbs"] / peak["read_GBps"], 4), "measured_peak": peak}
         line["stages_us_per_step"] = {st: round(d["us_per_step"], 1) for st, d in stages.items()}
     if args.cpu_baseline == "auto":
         sys.path.insert(0, os.path.join(ROOT, "oracle"))
@@ -497,6 +500,7 @@ def bench_c2(args):
     B, K, V, tau, seed = 64, 8, 49152, 1.0, 2024
     dev = H.Dev(0)
     log("device", dev.name)
+    peak = measure_peak(dev)
     L = H.lib()
     sets = []
     for i in range(3):
@@ -560,7 +564,9 @@ def bench_c2(args):
                      "kernel": "opure_accept_rejection (k_rej_rowstat + k_rej_slice + k_rej_draw), whole stage; "
                                "bytes = the rows it reads for these inputs (rows past a sequence's first "
                                "rejection are skipped when draft 0 is rejected) + the distributions written",
-                     "bytes_per_launch": read + written, "avg_us": round(ms * 1e3, 2)},
+                     "bytes_per_launch": read + written, "avg_us": round(ms * 1e3, 2),
+                     "measured_peak_GBps": peak["read_GBps"], "frac_of_measured_peak": round(gbs / peak["read_GBps"], 4),
+                     "measured_peak": peak},
     }
     if args.cpu_baseline == "auto":
         sys.path.insert(0, os.path.join(ROOT, "oracle"))
@@ -603,12 +609,63 @@ def copy_calibration():
     dev.close()
 
 
+def measure_peak(dev, read_gib=2, reps=5):
+    """The box's streaming peak, timed with the library's HIP events: `reps`
+    read-only passes over read_gib GiB and copies of read_gib/2 GiB (both far
+    above the 256 MB last-level cache), 16-byte nontemporal accesses
+    (opure_bw_measure).  The roofline fractions are also given against the
+    read figure, beside the published 8 TB/s."""
+    n = read_gib << 30
+    src = dev.alloc(n)
+    try:
+        dev.fill_u32(src, 0x3C003C00, n // 4)
+        read = dev.bw_measure(H.BW_READ, src, None, n, reps)
+        half = n // 2
+        copy = dev.bw_measure(H.BW_COPY, src, int(src) + half, half, reps)
+    finally:
+        src.free()
+    log(f"measured peak: read {read:.0f} GB/s, copy {copy:.0f} GB/s (read + written)")
+    return {"read_GBps": round(read, 1), "copy_GBps": round(copy, 1),
+            "method": f"opure_bw_measure: {reps} read-only passes over {read_gib} GiB and {reps} copies of "
+                      f"{read_gib / 2:g} GiB, 16-byte nontemporal accesses, 4 x 512-thread workgroups a CU, "
+                      "HIP events on the library's stream"}
+
+
+# Stages of a verify step that run the same kernel instantiation at these
+# shapes (the dispatch rules of gemv.hip): a profiler's kernel summary adds
+# them into one row, so the roofline reports that row as well.
+SHARED_KERNEL = {"c3": {("o_proj", "down"): "k_gemv<1, 1, 1, 16, 1, 1, false, 0> (o_proj and down)"}}
+
+
+def kernel_rows(config, stages):
+    """Per kernel instantiation: algorithmic bytes per step / kernel time per
+    step (stages sharing one instantiation combined)."""
+    rows = {}
+    shared = SHARED_KERNEL.get(config, {})
+    seen = set()
+    for group, name in shared.items():
+        if all(st in stages for st in group):
+            by = sum(stages[st]["bytes_per_launch"] * stages[st]["launches_per_step"] for st in group)
+            us = sum(stages[st]["us_per_step"] for st in group)
+            rows[name] = dict(us_per_step=us, bytes_per_step=by, gbs=by / (us * 1e-6) / 1e9)
+            seen.update(group)
+    for st, d in stages.items():
+        if st in seen or not d.get("gbs"):
+            continue
+        rows[f"{kernel_of(config, st)} ({st})"] = dict(
+            us_per_step=d["us_per_step"], bytes_per_step=d["bytes_per_launch"] * d["launches_per_step"], gbs=d["gbs"])
+    return rows
+
+
 def kernel_of(config, stage):
     """The GEMV kernel a verify-step stage runs at these shapes: loader waves
     for the 8B gate/up (7 tiles a CU), waves owning whole tiles for 1024 tiles
     and more, the K-split kernel below."""
     if stage == "gate_up" and config == "c4":
         return "k_gemv_pc"
+    other = {"attention": "k_attn_mfma + k_attn_combine", "embed": "k_embed", "accept": "k_accept_greedy"}
+    if stage in other:
+        return other[stage]
     return "k_gemv_wpt" if stage in ("gate_up", "lm_head") else "k_gemv"
 
 
@@ -656,6 +713,7 @@ def main():
 
     dev = H.Dev(0)
     log("device", dev.name)
+    peak = measure_peak(dev)
     w = build_workload(dev, args.config)
     cfg, ctx, R, K = w["cfg"], w["ctx"], w["R"], w["K"]
     res = time_graph(dev, w["step"], w["tokens"], ctx, args.warmup, args.steps, args.eager)
@@ -704,6 +762,7 @@ def main():
                    "random_drafts_accepted": res_r["accepted"],
                    "step_bytes": step_bytes["total"], "step_GBps": round(step_gbs, 1),
                    "step_frac_of_hbm_peak": round(step_gbs / HBM_PEAK_GBS, 4),
+                   "step_frac_of_measured_peak": round(step_gbs / peak["read_GBps"], 4),
                    "wall_ms_per_step": round(res["wall_ms_per_step"], 4)},
     }
     if kern:
@@ -715,7 +774,17 @@ def main():
                             "bytes_per_launch": kern["bytes_per_launch"], "avg_us": round(kern["avg_us"], 2),
                             "timing": "kernel execution time from start/stop events stamped by each dispatch "
                                       "(hipExtLaunchKernelGGL) over 10 eager steps, averaged per launch",
-                            "traffic_source": tr["source"] if tr else None}
+                            "traffic_source": tr["source"] if tr else None,
+                            "measured_peak_GBps": peak["read_GBps"],
+                            "frac_of_measured_peak": round(kern["gbs"] / peak["read_GBps"], 4),
+                            "measured_peak": peak}
+        krows = kernel_rows(args.config, stages)
+        top = max(krows, key=lambda k: krows[k]["us_per_step"])
+        line["roofline"]["kernels"] = {
+            k: {"us_per_step": round(d["us_per_step"], 1), "GBps": round(d["gbs"], 1),
+                "frac": round(d["gbs"] / HBM_PEAK_GBS, 4), "frac_of_measured_peak": round(d["gbs"] / peak["read_GBps"], 4)}
+            for k, d in sorted(krows.items(), key=lambda kv: -kv[1]["us_per_step"])}
+        line["roofline"]["top_kernel"] = top
         line["stages"] = {st: {"launches_per_step": round(d["launches_per_step"], 2), "us": round(d["avg_us"], 2),
                                "us_per_step": round(d["us_per_step"], 1),
                                "GBps": round(d["gbs"], 1) if d["gbs"] else None,

@@ -115,6 +115,19 @@ int opure_timer_begin(opure_dev* dev);
 int opure_timer_end(opure_dev* dev);
 int opure_timer_ms(opure_dev* dev, float* ms);
 
+/* ---- streaming bandwidth of the device: `reps` launches that read `bytes`
+ *      of src (OPURE_BW_READ) or copy them to dst (OPURE_BW_COPY), 16-byte
+ *      nontemporal accesses, four 512-thread workgroups a CU, timed with the
+ *      device's HIP events after one warm-up launch.  *gbs = bytes moved per
+ *      second / 1e9 (a copy moves 2 * bytes).  The peak the kernels' roofline
+ *      fractions are read against, beside the published 8 TB/s; the
+ *      counterpart of the GEMV microbench's effective-GB/s line
+ *      (Opure_TestHarness.cpp:1714-1754).  Pointers and bytes are 16-byte
+ *      multiples; choose bytes well above the 256 MB last-level cache. */
+enum { OPURE_BW_READ = 0, OPURE_BW_COPY = 1 };
+int opure_bw_measure(opure_dev* dev, uint32_t mode, const void* src, void* dst, uint64_t bytes, uint32_t reps,
+                     double* gbs);
+
 /* ---- host helper: RoPE cos/sin table.  OPURE_ROPE_GPU uses theta^(-2p/hd)
  *      for pair p (Opure_RoPE.usf:56); OPURE_ROPE_CPUREF uses theta^(-4p/hd)
  *      (Opure_CpuReference.cpp:179).  Computed in double, stored as float. */

@@ -50,15 +50,28 @@ def _compile(src: str, obj: str) -> str:
     return obj
 
 
-def build(jobs: int = 8, verbose: bool = False) -> str:
+def _stale(src: str, obj: str, headers_mtime: float) -> bool:
+    return not os.path.exists(obj) or os.path.getmtime(obj) < max(os.path.getmtime(src), headers_mtime)
+
+
+def build(jobs: int = 8, verbose: bool = False, incremental: bool = False) -> str:
+    """Compiles every HIP source (incremental: only those older than their
+    object or than any header) and links both libraries."""
     os.makedirs(BUILD, exist_ok=True)
     os.makedirs(LIB, exist_ok=True)
+    headers = [os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".h")]
+    headers += [os.path.join(ROOT, "include", f) for f in os.listdir(os.path.join(ROOT, "include"))]
+    hm = max(os.path.getmtime(h) for h in headers)
     objs = []
     with cf.ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
         futs = []
         for s in HIP_SOURCES:
             obj = os.path.join(BUILD, s.replace(".hip", ".o"))
-            futs.append(ex.submit(_compile, os.path.join(CSRC, s), obj))
+            src = os.path.join(CSRC, s)
+            if incremental and not _stale(src, obj, hm):
+                objs.append(obj)
+                continue
+            futs.append(ex.submit(_compile, src, obj))
         for f in futs:
             objs.append(f.result())
     tmp = HIP_LIB + ".tmp"
@@ -87,6 +100,7 @@ def build(jobs: int = 8, verbose: bool = False) -> str:
 if __name__ == "__main__":
     ap = argparse.ArgumentParser()
     ap.add_argument("--jobs", type=int, default=8)
+    ap.add_argument("--incremental", action="store_true", help="recompile only sources older than a header or object")
     args = ap.parse_args()
-    build(args.jobs, verbose=True)
+    build(args.jobs, verbose=True, incremental=args.incremental)
     sys.exit(0)

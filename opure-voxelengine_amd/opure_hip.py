@@ -23,6 +23,7 @@ ROPE_GPU, ROPE_CPUREF = 0, 1
 EPI_STORE, EPI_RESIDUAL, EPI_SWIGLU = 0, 1, 2
 STAGES = ("embed", "qkv", "attention", "o_proj", "gate_up", "down", "lm_head", "accept")
 ACCEPT_NONE, ACCEPT_GREEDY, ACCEPT_REJECTION = 0, 1, 2
+BW_READ, BW_COPY = 0, 1
 GEMV_MFMA, GEMV_VALU = 0, 1
 
 
@@ -135,6 +136,7 @@ def _declare(L):
         "opure_graph_launch": ([vp, vp], i), "opure_graph_destroy": ([vp], i),
         "opure_timer_begin": ([vp], i), "opure_timer_end": ([vp], i),
         "opure_timer_ms": ([vp, C.POINTER(f32)], i),
+        "opure_bw_measure": ([vp, u32, vp, vp, u64, u32, C.POINTER(C.c_double)], i),
         "opure_rope_table": ([C.c_double, u32, u32, u32, vp, vp], i),
         "opure_gemv_batched_f32": ([vp, C.POINTER(GemvArgs)], i),
         "opure_gemv_batched_i8pc": ([vp, C.POINTER(GemvArgs)], i),
@@ -251,6 +253,13 @@ class Dev:
         ms = C.c_float()
         check(lib().opure_timer_ms(self.h, C.byref(ms)))
         return float(ms.value)
+
+    def bw_measure(self, mode: int, src, dst, nbytes: int, reps: int) -> float:
+        """GB/s of `reps` read-only (BW_READ) or copy (BW_COPY) launches over nbytes."""
+        g = C.c_double()
+        check(lib().opure_bw_measure(self.h, mode, int(src), int(dst) if dst is not None else None, nbytes, reps,
+                                     C.byref(g)))
+        return float(g.value)
 
     def tile(self, wfmt: int, src: "Linear", layout: int = LAYOUT_TILED):
         """Tiled copy of a row-major device linear: (Linear, [buffers to keep alive])."""

@@ -768,3 +768,23 @@ def test_device_quantisers_match_oracle(dev, wfmt):
         assert np.array_equal(dev.download(q, np.uint8, (out, inn // 2)), want["w"])
         assert np.array_equal(dev.download(s, np.uint16, (out, G)), want["scale"])
         assert np.array_equal(dev.download(z, np.uint16, (out, G)), want["zero"])
+
+
+# ---------------------------------------------------------------------------
+def test_bw_measure_copies_and_reports(dev):
+    """opure_bw_measure: a copy leaves dst equal to src, both modes report a
+    positive rate below the published 8 TB/s ceiling of a read, and bad
+    arguments are refused before any launch."""
+    n = 64 << 20
+    src, dst = dev.alloc(n), dev.alloc(n)
+    H.check(H.lib().opure_synth_normal_f32(dev.h, int(src), n // 4, 5, 0, 1.0, 0.0))
+    dev.fill_u32(dst, 0, n // 4)
+    read = dev.bw_measure(H.BW_READ, src, None, n, 3)
+    copy = dev.bw_measure(H.BW_COPY, src, dst, n, 2)
+    assert 0.0 < read and 0.0 < copy
+    a = dev.download(src, np.uint32, (n // 4,))
+    b = dev.download(dst, np.uint32, (n // 4,))
+    assert np.array_equal(a, b)
+    g = C.c_double()
+    assert H.lib().opure_bw_measure(dev.h, H.BW_COPY, int(src), None, n, 1, C.byref(g)) == H.E_INVALID
+    assert H.lib().opure_bw_measure(dev.h, H.BW_READ, int(src), None, n - 8, 1, C.byref(g)) == H.E_INVALID
