@@ -61,6 +61,12 @@ int opure_engine_destroy(opure_engine* e);
 int opure_engine_generate(opure_engine* e, const int32_t* prompt, uint32_t n_prompt, uint32_t n_new, int32_t* out,
                           opure_engine_stats* stats);
 
+/* ForwardLogits of the reference (Opure_VoxelEngine.h:141-147), its parity
+ * entry point: prefills tokens[0..n) into a fresh cache of the target and
+ * writes the last position's logits[vocab]; *argmax (may be NULL) = their
+ * argmax, ties to the lowest index. */
+int opure_engine_forward_logits(opure_engine* e, const int32_t* tokens, uint32_t n, float* logits, uint32_t* argmax);
+
 /* Greedy speculative decoding: the emitted ids equal opure_engine_generate's
  * for any draft model.  out[n_new]; accepted_hist[hist_cap] (may be NULL)
  * receives the accepted count of each verify step, in order. */
@@ -137,12 +143,27 @@ enum {
     OPURE_ROLE_DOWN = 5, OPURE_ROLE_ATTN_NORM = 6, OPURE_ROLE_MLP_NORM = 7, OPURE_ROLE_FINAL_NORM = 8
 };
 
+/* RoPE pairing the stored q_proj / k_proj rows were trained with.  The kernels
+ * (and the reference: Opure_RoPE.usf:7-10, Opure_CpuReference.cpp:171-189)
+ * rotate adjacent channels (2p, 2p+1) of a head.  ADJACENT uses the rows as
+ * stored, which is what the reference does with every file it loads,
+ * including HF checkpoints.  HALF is for checkpoints trained with
+ * rotate-half pairs (p, p + head_dim/2), such as HF Llama's q_proj / k_proj:
+ * each head's rows are permuted at load, new row 2p = row p and new row 2p+1
+ * = row p + head_dim/2 (with their scales and zero points), so the adjacent
+ * rotation computes the checkpoint's attention exactly (the same permutation
+ * of q and k leaves every q.k unchanged; v and o_proj are untouched).  To
+ * convert a file offline instead, apply that permutation to the rows of
+ * q_proj and k_proj of every layer and load it as ADJACENT. */
+enum { OPURE_ROPE_PAIRS_ADJACENT = 0, OPURE_ROPE_PAIRS_HALF = 1 };
+
 typedef struct opure_load_options {
     uint32_t max_positions;   /* RoPE table rows; 0: config.json's max_position_embeddings */
     int32_t  wfmt;            /* OPURE_W_* to compute in; -1: as stored (the first q_proj's form) */
     int32_t  afmt;            /* OPURE_A_*; -1: quantization_config.activation_dtype, else F32 / F16 / BF16
                                * for float / int8 / int4 weights */
     float    attn_scale;      /* 0: 1/sqrt(head_dim); 1.0: the reference's unscaled scores */
+    uint32_t rope_pairs;      /* OPURE_ROPE_PAIRS_*: 0 (ADJACENT, the reference) or HALF (HF rotate-half files) */
 } opure_load_options;
 
 typedef struct opure_model_info {

@@ -1177,6 +1177,7 @@ int rollback_validate(const opure_rollback_args* a)
     OPURE_REQUIRE(a && a->model && a->kv && a->kv->pool && a->kv->page_table && a->seq_len && a->accepted &&
                       a->new_seq_len, OPURE_E_INVALID, "rollback: null argument");
     OPURE_REQUIRE(a->batch >= 1 && a->kv->page_size == OPURE_PAGE_SIZE, OPURE_E_INVALID, "rollback: bad shape");
+    OPURE_REQUIRE(a->kv->n_pages >= 1 && a->kv->max_pages_per_seq >= 1, OPURE_E_INVALID, "rollback: the cache has no pages");
     // a rollback follows a verify step of k + 1 <= OPURE_MAX_ROWS rows, so its
     // positions lie in two pages at most
     OPURE_REQUIRE(a->k + 1u <= OPURE_MAX_ROWS, OPURE_E_CAPACITY, "rollback: k = %u drafts, more than a verify step holds",

@@ -847,6 +847,8 @@ int attn_validate(const opure_model* m, const opure_kv* kv, uint32_t batch, uint
                   "attention: head_dim %u not in 16..256 step 16", m->head_dim);
     OPURE_REQUIRE(kv->page_size == OPURE_PAGE_SIZE, OPURE_E_UNSUPPORTED, "attention: page_size must be %d",
                   OPURE_PAGE_SIZE);
+    // the folded kernel reads page 0 for a missing page entry (and masks it), so the pool holds one page at least
+    OPURE_REQUIRE(kv->n_pages >= 1 && kv->max_pages_per_seq >= 1, OPURE_E_INVALID, "attention: the cache has no pages");
     OPURE_REQUIRE(batch >= 1 && rows >= 1 && rows <= OPURE_MAX_ROWS && batch * rows <= OPURE_MAX_BATCH_ROWS,
                   OPURE_E_CAPACITY, "attention: %u rows per sequence x batch %u beyond %d / %d", rows, batch,
                   OPURE_MAX_ROWS, OPURE_MAX_BATCH_ROWS);

@@ -94,6 +94,7 @@ opure::engine::LoadOptions load_options(const opure_load_options* o)
         r.wfmt = o->wfmt;
         r.afmt = o->afmt;
         r.attnScale = o->attn_scale;
+        r.ropePairs = o->rope_pairs;
     }
     return r;
 }
@@ -164,12 +165,9 @@ int opure_engine_initialize(opure_dev* dev, const char* target_dir, const char* 
     *out = nullptr;
     opure_engine* e = new (std::nothrow) opure_engine();
     if (!e) return fail(OPURE_E_OOM, "opure_engine_initialize: host allocation failed");
+    // the engine's Initialize(modelDir, opts, dev, ...): it loads and owns both models
     const int rc = guarded([&] {
-        const auto lo = load_options(load);
-        e->target = std::make_unique<opure::engine::LoadedModel>(dev, opure::engine::ModelFiles(target_dir, lo));
-        if (draft_dir)
-            e->draft = std::make_unique<opure::engine::LoadedModel>(dev, opure::engine::ModelFiles(draft_dir, lo));
-        e->impl.Initialize(dev, e->target->Desc(), e->draft ? &e->draft->Desc() : nullptr, engine_options(opts));
+        e->impl.Initialize(target_dir, engine_options(opts), dev, load_options(load), draft_dir ? draft_dir : "");
     });
     if (rc != OPURE_OK)
     {
@@ -315,6 +313,24 @@ int opure_engine_generate(opure_engine* e, const int32_t* prompt, uint32_t n_pro
         const auto r = e->impl.Generate(to_tokens(prompt, n_prompt), n_new);
         for (uint32_t i = 0; i < n_new; ++i) out[i] = i < r.generated.size() ? static_cast<int32_t>(r.generated[i]) : -1;
         fill_stats(stats, r);
+    });
+}
+
+int opure_engine_forward_logits(opure_engine* e, const int32_t* tokens, uint32_t n, float* logits, uint32_t* argmax)
+{
+    if (!e || !tokens || !n || !logits) return fail(OPURE_E_INVALID, "opure_engine_forward_logits: bad argument");
+    return guarded([&] {
+        std::vector<float> l;
+        e->impl.ForwardLogits(to_tokens(tokens, n), l);
+        std::memcpy(logits, l.data(), l.size() * sizeof(float));
+        if (argmax)
+        {
+            // ties to the lowest index, as the step's argmax
+            uint32_t best = 0;
+            for (uint32_t i = 1; i < l.size(); ++i)
+                if (l[i] > l[best]) best = i;
+            *argmax = best;
+        }
     });
 }
 

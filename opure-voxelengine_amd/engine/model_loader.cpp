@@ -95,6 +95,20 @@ float load_float(Dtype d, const uint8_t* p, uint64_t i)
 
 bool is_float(Dtype d) { return d == Dtype::F32 || d == Dtype::F16 || d == Dtype::BF16; }
 
+// A stored scale narrowed to the fp16 (int8) or bf16 (int4) the kernels read:
+// a finite nonzero scale that would round to zero or overflow to infinity
+// (and silently zero or blow up its whole linear) is refused.
+uint16_t narrow_scale(double v, bool to_bf16, const std::string& tensor)
+{
+    const float f = static_cast<float>(v);
+    const uint16_t h = to_bf16 ? f32_to_bf16(f) : f32_to_f16(f);
+    const uint16_t mag = h & 0x7FFFu, inf = to_bf16 ? 0x7F80u : 0x7C00u;
+    if (std::isfinite(v) && v != 0.0 && (mag == 0 || mag == inf))
+        fail(OPURE_E_UNSUPPORTED, tensor + ": scale " + std::to_string(v) + " is outside the " +
+                                      (to_bf16 ? "bf16" : "fp16") + " range the kernels read");
+    return h;
+}
+
 std::string shape_str(const std::vector<int64_t>& s)
 {
     std::string r = "[";
@@ -151,6 +165,30 @@ const char* role_name(Role r)
 }
 
 std::string layer_prefix(uint32_t i) { return "model.layers." + std::to_string(i) + "."; }
+
+// Rows [row0, row0 + heads * hd) of h, head by head: new row 2p = row p, new
+// row 2p + 1 = row p + hd/2, with the rows' scales and zero points (a
+// rotate-half checkpoint's q / k rows in the adjacent-pair order the kernels
+// rotate).
+void permute_half_to_adjacent(HostLinear& h, uint32_t row0, uint32_t heads, uint32_t hd)
+{
+    for (std::vector<uint8_t>* v : {&h.w, &h.scale, &h.zero})
+    {
+        if (v->empty()) continue;
+        const uint64_t rb = v->size() / h.out;                   // bytes per row of this array
+        std::vector<uint8_t> head(rb * hd);
+        for (uint32_t i = 0; i < heads; ++i)
+        {
+            uint8_t* base = v->data() + (static_cast<uint64_t>(row0) + static_cast<uint64_t>(i) * hd) * rb;
+            std::memcpy(head.data(), base, head.size());
+            for (uint32_t p = 0; p < hd / 2; ++p)
+            {
+                std::memcpy(base + (2ull * p) * rb, head.data() + static_cast<uint64_t>(p) * rb, rb);
+                std::memcpy(base + (2ull * p + 1) * rb, head.data() + (static_cast<uint64_t>(p) + hd / 2) * rb, rb);
+            }
+        }
+    }
+}
 
 }  // namespace
 
@@ -232,6 +270,12 @@ ModelFiles::ModelFiles(const std::string& dir, const LoadOptions& opts) : dir_(d
         for (const auto& [name, file] : map->obj)
         {
             if (file.kind != Json::String) fail(OPURE_E_INVALID, "weight_map entry of '" + name + "' is not a file name");
+            // a shard is a file inside the model directory: no absolute path, no '..'
+            const fs::path sp(file.str);
+            bool up = false;
+            for (const fs::path& c : sp) up = up || c == "..";
+            if (file.str.empty() || sp.is_absolute() || up)
+                fail(OPURE_E_INVALID, "weight_map names shard '" + file.str + "' outside the model directory");
             if (seen.insert(file.str).second) shards.push_back(file.str);
         }
     }
@@ -239,8 +283,14 @@ ModelFiles::ModelFiles(const std::string& dir, const LoadOptions& opts) : dir_(d
     {
         shards.push_back("model.safetensors");
     }
+    const fs::path root = fs::weakly_canonical(fs::path(dir));
     for (const std::string& s : shards)
     {
+        // ... and it does not leave the directory through a link either
+        const fs::path full = fs::weakly_canonical(fs::path(dir) / s);
+        const auto [r_end, f_it] = std::mismatch(root.begin(), root.end(), full.begin(), full.end());
+        if (r_end != root.end()) fail(OPURE_E_INVALID, "shard '" + s + "' resolves outside the model directory");
+        (void)f_it;
         auto f = std::make_unique<WeightStreamer>();
         f->Open((fs::path(dir) / s).string());
         fileBytes_ += fs::file_size(fs::path(dir) / s);
@@ -255,6 +305,8 @@ ModelFiles::ModelFiles(const std::string& dir, const LoadOptions& opts) : dir_(d
                            : cfg_.activationAfmt >= 0 ? static_cast<uint32_t>(cfg_.activationAfmt) : default_afmt(wfmt_);
     if (afmt_ > OPURE_A_BF16) fail(OPURE_E_INVALID, "afmt " + std::to_string(afmt_));
     attnScale_ = opts.attnScale > 0.0f ? opts.attnScale : static_cast<float>(1.0 / std::sqrt(static_cast<double>(cfg_.headDim)));
+    if (opts.ropePairs > OPURE_ROPE_PAIRS_HALF) fail(OPURE_E_INVALID, "rope_pairs " + std::to_string(opts.ropePairs));
+    ropePairs_ = opts.ropePairs;
     maxPos_ = opts.maxPositions ? opts.maxPositions : cfg_.maxPositionEmbeddings;
     if (!maxPos_) fail(OPURE_E_INVALID, "no RoPE length: config.json has no max_position_embeddings and none was given");
 
@@ -415,9 +467,9 @@ void ModelFiles::ReadPart(const Part& p, uint32_t in, HostLinear& h, uint32_t ro
         auto* s = reinterpret_cast<uint16_t*>(h.scale.data()) + row0;
         for (uint32_t o = 0; o < p.out; ++o)
         {
-            if (!p.scale) s[o] = f32_to_f16(static_cast<float>(w.headerScale));
+            if (!p.scale) s[o] = narrow_scale(w.headerScale, false, w.name);
             else if (p.scale->dtype == Dtype::F16) std::memcpy(&s[o], sc + 2 * o, 2);
-            else s[o] = f32_to_f16(load_float(p.scale->dtype, sc, o));
+            else s[o] = narrow_scale(load_float(p.scale->dtype, sc, o), false, p.scale->name);
         }
         return;
     }
@@ -439,9 +491,9 @@ void ModelFiles::ReadPart(const Part& p, uint32_t in, HostLinear& h, uint32_t ro
     const uint16_t zero_const = w.dtype == Dtype::I4 ? f32_to_bf16(8.0f) : 0u;
     for (uint64_t i = 0; i < static_cast<uint64_t>(p.out) * groups; ++i)
     {
-        if (!p.scale) s[i] = f32_to_bf16(static_cast<float>(w.headerScale));
+        if (!p.scale) s[i] = narrow_scale(w.headerScale, true, w.name);
         else if (p.scale->dtype == Dtype::BF16) std::memcpy(&s[i], sc + 2 * i, 2);
-        else s[i] = f32_to_bf16(load_float(p.scale->dtype, sc, i));
+        else s[i] = narrow_scale(load_float(p.scale->dtype, sc, i), true, p.scale->name);
         if (!zs) z[i] = zero_const;
         else if (p.zero->dtype == Dtype::BF16) std::memcpy(&z[i], zs + 2 * i, 2);
         else z[i] = f32_to_bf16(load_float(p.zero->dtype, zs, i));
@@ -497,6 +549,11 @@ HostLinear ModelFiles::Read(Role role, uint32_t layer) const
     {
         ReadPart(p, h.in, h, row);
         row += p.out;
+    }
+    if (role == Role::Qkv && ropePairs_ == OPURE_ROPE_PAIRS_HALF)
+    {
+        permute_half_to_adjacent(h, 0, cfg_.nHeads, cfg_.headDim);                          // q
+        permute_half_to_adjacent(h, cfg_.nHeads * cfg_.headDim, cfg_.nKvHeads, cfg_.headDim);  // k
     }
     return h;
 }

@@ -32,6 +32,7 @@
 #include <string>
 #include <vector>
 
+#include "opure_engine.h"
 #include "opure_hip.h"
 #include "weight_streamer.h"
 
@@ -42,6 +43,7 @@ struct LoadOptions {
     int32_t  wfmt = -1;          // OPURE_W_* to compute in; -1: the format the linears are stored in
     int32_t  afmt = -1;          // OPURE_A_*; -1: quantization_config.activation_dtype, else the format's default
     float    attnScale = 0.0f;   // 0: 1/sqrt(head_dim) (HF Llama); 1: the reference's unscaled scores
+    uint32_t ropePairs = OPURE_ROPE_PAIRS_ADJACENT;   // HALF: q/k rows of each head permuted at load
 };
 
 // config.json (the fields the reference's ModelConfig::Parse reads,
@@ -83,6 +85,7 @@ public:
     [[nodiscard]] uint32_t Afmt() const { return afmt_; }
     [[nodiscard]] float AttnScale() const { return attnScale_; }
     [[nodiscard]] uint32_t MaxPositions() const { return maxPos_; }
+    [[nodiscard]] uint32_t RopePairs() const { return ropePairs_; }
     [[nodiscard]] uint32_t TensorCount() const;
     [[nodiscard]] uint64_t FileBytes() const { return fileBytes_; }
 
@@ -112,6 +115,7 @@ private:
     uint32_t storedWfmt_ = OPURE_W_F32, wfmt_ = OPURE_W_F32, afmt_ = OPURE_A_F32;
     float attnScale_ = 1.0f;
     uint32_t maxPos_ = 0;
+    uint32_t ropePairs_ = OPURE_ROPE_PAIRS_ADJACENT;
 };
 
 // A model on the device: tiled linears, fp32 norms, the RoPE table and the

@@ -10,6 +10,8 @@
 // ============================================================================
 #include "voxel_engine.h"
 
+#include "model_loader.h"
+
 #include <algorithm>
 #include <chrono>
 #include <cstring>
@@ -126,6 +128,26 @@ void VoxelEngine::Shutdown()
     rbIo_ = nullptr;
     dev_ = nullptr;
     ready_ = false;
+    ownedDraft_.reset();
+    ownedTarget_.reset();
+}
+
+void VoxelEngine::Initialize(const std::string& modelDir, const EngineOptions& opts, opure_dev* dev,
+                             const LoadOptions& load, const std::string& draftDir)
+{
+    Shutdown();
+    if (!dev) throw Error(OPURE_E_INVALID, "VoxelEngine::Initialize: null device");
+    auto target = std::make_unique<LoadedModel>(dev, ModelFiles(modelDir, load));
+    std::unique_ptr<LoadedModel> draft;
+    if (!draftDir.empty()) draft = std::make_unique<LoadedModel>(dev, ModelFiles(draftDir, load));
+    Initialize(dev, target->Desc(), draft ? &draft->Desc() : nullptr, opts);
+    ownedTarget_ = std::move(target);
+    ownedDraft_ = std::move(draft);
+}
+
+void VoxelEngine::Initialize(const std::string& modelDir, const EngineOptions& opts, opure_dev* dev)
+{
+    Initialize(modelDir, opts, dev, LoadOptions{});
 }
 
 void VoxelEngine::Initialize(opure_dev* dev, const opure_model& target, const opure_model* draft,
@@ -502,6 +524,40 @@ GenerateResult VoxelEngine::Generate(const std::vector<uint32_t>& prompt, uint32
     ++metrics_.generateCalls;
     metrics_.tokensEmitted += r.generated.size();
     return r;
+}
+
+GenerateResult VoxelEngine::Generate(const std::vector<uint32_t>& tokens, const EngineOptions& opts)
+{
+    const int32_t stop = opts_.stopToken;
+    opts_.stopToken = opts.stopToken;
+    try
+    {
+        GenerateResult r = Generate(tokens, opts.maxNewTokens);
+        opts_.stopToken = stop;
+        return r;
+    }
+    catch (...)
+    {
+        opts_.stopToken = stop;
+        throw;
+    }
+}
+
+uint32_t VoxelEngine::ForwardArgMax(const std::vector<uint32_t>& tokens)
+{
+    if (!ready_) throw Error(OPURE_E_INVALID, "VoxelEngine::ForwardArgMax: not initialised");
+    if (tokens.empty()) throw Error(OPURE_E_INVALID, "VoxelEngine::ForwardArgMax: no tokens");
+    reset_row(dev_, target_->pool, target_->row, target_->kv.page_table);
+    target_->rowsDirty16 = true;
+    return Prefill(false, tokens, 0, true);
+}
+
+void VoxelEngine::ForwardLogits(const std::vector<uint32_t>& tokens, std::vector<float>& logitsOut)
+{
+    (void)ForwardArgMax(tokens);
+    // the last position's row of the one-row decode step that Prefill ran last
+    logitsOut.resize(target_->desc.vocab);
+    Check(opure_buf_download(dev_, logitsOut.data(), decode_->logits, 0, logitsOut.size() * 4ull), "logits download");
 }
 
 GenerateResult VoxelEngine::GenerateSpeculative(const std::vector<uint32_t>& prompt, uint32_t nNew)

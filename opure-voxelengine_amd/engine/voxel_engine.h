@@ -56,7 +56,13 @@ struct EngineOptions {
     uint32_t draftTokens = 4;       // K
     bool     useGraphs = true;      // replay captured hipGraphs for the fixed-shape steps
     int32_t  stopToken = -1;        // < 0: none
+    // the reference's fields (Opure_VoxelEngine.h:55-65), read by Generate(tokens, opts)
+    uint32_t maxNewTokens = 256;    // hard cap on generated tokens
+    float    temperature = 0.0f;    // not read: generation is greedy, as in the reference
 };
+
+class LoadedModel;                  // model_loader.h
+struct LoadOptions;
 
 // One verify step on explicit rows (VerifyStep): the drafts kept and the
 // target's own token after them.
@@ -114,11 +120,28 @@ public:
     // buffers and host layer arrays must outlive the engine.  Allocates the
     // KV pools and step buffers; throws Error on failure.
     void Initialize(opure_dev* dev, const opure_model& target, const opure_model* draft, const EngineOptions& opts);
+    // Initialize(modelDir, opts, dev, lib) of the reference
+    // (Opure_VoxelEngine.h:127-128): loads the target from its model directory
+    // (config.json + safetensors, model_loader.h) and the draft from draftDir
+    // when it is not empty; the engine owns both until Shutdown.  The shader
+    // library has no counterpart (the kernels are libopure_hip.so).
+    void Initialize(const std::string& modelDir, const EngineOptions& opts, opure_dev* dev, const LoadOptions& load,
+                    const std::string& draftDir = {});
+    void Initialize(const std::string& modelDir, const EngineOptions& opts, opure_dev* dev);
     void Shutdown();
     [[nodiscard]] bool IsReady() const { return ready_; }
 
     // Greedy decoding of the target, one token per step.
     [[nodiscard]] GenerateResult Generate(const std::vector<uint32_t>& prompt, uint32_t nNew);
+    // Generate(tokens, opts) of the reference (Opure_VoxelEngine.h:137-138):
+    // prefills `tokens`, then greedy decoding of opts.maxNewTokens tokens or
+    // up to opts.stopToken (< 0: none), with a fresh cache.
+    [[nodiscard]] GenerateResult Generate(const std::vector<uint32_t>& tokens, const EngineOptions& opts);
+    // ForwardArgMax / ForwardLogits of the reference (Opure_VoxelEngine.h:
+    // 141-147), its parity entry points: prefills `tokens` into a fresh cache
+    // and returns the argmax of the last position / its logits [vocab].
+    [[nodiscard]] uint32_t ForwardArgMax(const std::vector<uint32_t>& tokens);
+    void ForwardLogits(const std::vector<uint32_t>& tokens, std::vector<float>& logitsOut);
     // Greedy speculative decoding with the draft model.
     [[nodiscard]] GenerateResult GenerateSpeculative(const std::vector<uint32_t>& prompt, uint32_t nNew);
 
@@ -160,6 +183,8 @@ private:
     opure_dev* dev_ = nullptr;
     EngineOptions opts_{};
     bool ready_ = false;
+    // models loaded by Initialize(modelDir, ...): released after the engine's buffers
+    std::unique_ptr<LoadedModel> ownedTarget_, ownedDraft_;
     std::unique_ptr<ModelState> target_, draft_;
     // one speculative iteration's inputs (one upload) and outputs (one download)
     void* io_ = nullptr;            // int32 [dseq K+1 | dtok K+1 | vseq | vtok K+1]

@@ -9,6 +9,7 @@
 #include <unistd.h>
 
 #include <cerrno>
+#include <cmath>
 #include <cstring>
 #include <fstream>
 #include <sstream>
@@ -27,6 +28,8 @@ namespace {
 struct Reader {
     std::string_view s;
     size_t i = 0;
+    int depth = 0;                       // open objects and arrays
+    static constexpr int kMaxDepth = 64;  // deeper headers are refused, not recursed into
 
     [[noreturn]] void fail(const char* what) const
     {
@@ -103,11 +106,16 @@ struct Reader {
         if (i >= s.size()) fail("unexpected end");
         Json v;
         const char c = s[i];
+        if ((c == '{' || c == '[') && ++depth > kMaxDepth) fail("nesting deeper than 64 levels");
         if (c == '{')
         {
             ++i;
             v.kind = Json::Object;
-            if (eat('}')) return v;
+            if (eat('}'))
+            {
+                --depth;
+                return v;
+            }
             do
             {
                 std::string k = string();
@@ -115,17 +123,23 @@ struct Reader {
                 v.obj.emplace_back(std::move(k), value());
             } while (eat(','));
             if (!eat('}')) fail("expected '}'");
+            --depth;
         }
         else if (c == '[')
         {
             ++i;
             v.kind = Json::Array;
-            if (eat(']')) return v;
+            if (eat(']'))
+            {
+                --depth;
+                return v;
+            }
             do
             {
                 v.arr.push_back(value());
             } while (eat(','));
             if (!eat(']')) fail("expected ']'");
+            --depth;
         }
         else if (c == '"')
         {
@@ -201,17 +215,20 @@ const char* DtypeName(Dtype d)
 
 uint64_t StoredBytes(Dtype d, uint64_t n)
 {
+    uint64_t per = 1;
     switch (d)
     {
-    case Dtype::F32: return 4u * n;
+    case Dtype::F32: per = 4; break;
     case Dtype::F16:
-    case Dtype::BF16: return 2u * n;
+    case Dtype::BF16: per = 2; break;
     case Dtype::U8:
     case Dtype::I8: return n;
     case Dtype::U4:
-    case Dtype::I4: return (n + 1u) / 2u;
+    case Dtype::I4: return n / 2u + (n & 1u);
     }
-    return 0;
+    uint64_t b = 0;
+    if (__builtin_mul_overflow(n, per, &b)) throw Error(OPURE_E_INVALID, "safetensors: tensor size overflows 64 bits");
+    return b;
 }
 
 namespace {
@@ -233,7 +250,9 @@ Dtype parse_dtype(const std::string& s, const std::string& tensor)
 uint64_t Tensor::ElementCount() const
 {
     uint64_t n = 1;
-    for (int64_t d : shape) n *= static_cast<uint64_t>(d);
+    for (int64_t d : shape)
+        if (__builtin_mul_overflow(n, static_cast<uint64_t>(d), &n))
+            throw Error(OPURE_E_INVALID, "safetensors: element count of '" + name + "' overflows 64 bits");
     return n;
 }
 
@@ -296,14 +315,16 @@ void WeightStreamer::ParseHeader(const uint8_t* header, uint64_t len)
         Tensor t;
         t.name = name;
         t.dtype = parse_dtype(dt->str, name);
+        // dimensions and offsets are integers below 2^53 (exact in the double a JSON number is read into)
+        constexpr double kMaxInt = 9007199254740992.0;
+        auto integral = [&](const Json& d) { return d.kind == Json::Number && d.num >= 0 && d.num < kMaxInt && d.num == std::floor(d.num); };
         for (const Json& d : sh->arr)
         {
-            if (d.kind != Json::Number || d.num < 0) throw Error(OPURE_E_INVALID, "safetensors: bad shape of '" + name + "'");
+            if (!integral(d)) throw Error(OPURE_E_INVALID, "safetensors: bad shape of '" + name + "'");
             t.shape.push_back(static_cast<int64_t>(d.num));
         }
         const double b = off->arr[0].num, e = off->arr[1].num;
-        if (off->arr[0].kind != Json::Number || off->arr[1].kind != Json::Number || b < 0 || e < b ||
-            e > static_cast<double>(payloadBytes))
+        if (!integral(off->arr[0]) || !integral(off->arr[1]) || e < b || e > static_cast<double>(payloadBytes))
             throw Error(OPURE_E_INVALID, "safetensors: data_offsets of '" + name + "' out of order or past the payload");
         const uint64_t expect = StoredBytes(t.dtype, t.ElementCount());
         if (static_cast<uint64_t>(e - b) != expect)

@@ -32,7 +32,8 @@ class Metrics(C.Structure):
 
 
 class LoadOptions(C.Structure):
-    _fields_ = [("max_positions", C.c_uint32), ("wfmt", C.c_int32), ("afmt", C.c_int32), ("attn_scale", C.c_float)]
+    _fields_ = [("max_positions", C.c_uint32), ("wfmt", C.c_int32), ("afmt", C.c_int32), ("attn_scale", C.c_float),
+                ("rope_pairs", C.c_uint32)]
 
 
 class ModelInfo(C.Structure):
@@ -55,6 +56,7 @@ class TensorInfo(C.Structure):
                 ("scale", C.c_double)]
 
 
+ROPE_PAIRS_ADJACENT, ROPE_PAIRS_HALF = 0, 1
 ROLE_EMBED, ROLE_LM_HEAD, ROLE_QKV, ROLE_O, ROLE_GATE_UP, ROLE_DOWN, ROLE_ATTN_NORM, ROLE_MLP_NORM, ROLE_FINAL_NORM = \
     range(9)
 DTYPES = ("F32", "F16", "BF16", "U8", "I8", "U4", "I4")
@@ -82,6 +84,7 @@ def lib():
         L.opure_page_pool_release.argtypes = [vp, vp, u32]
         L.opure_page_pool_grow_seq.argtypes = [vp, vp, u32, u32, C.POINTER(u32)]
         L.opure_engine_verify_step.argtypes = [vp, vp, u32, u32, vp, C.POINTER(u32)]
+        L.opure_engine_forward_logits.argtypes = [vp, vp, u32, vp, C.POINTER(u32)]
         L.opure_engine_rollback_kv.argtypes = [vp, u32, u32, u32, C.POINTER(u32)]
         L.opure_engine_pages.argtypes = [vp, i, C.POINTER(u32), C.POINTER(u32), vp, u32, C.POINTER(u32)]
         cp = C.c_char_p
@@ -107,7 +110,8 @@ def lib():
                   "opure_engine_generate_speculative", "opure_engine_get_metrics", "opure_engine_reset_metrics",
                   "opure_page_pool_create", "opure_page_pool_destroy", "opure_page_pool_available",
                   "opure_page_pool_alloc", "opure_page_pool_release", "opure_page_pool_grow_seq",
-                  "opure_engine_verify_step", "opure_engine_rollback_kv", "opure_engine_pages"):
+                  "opure_engine_verify_step", "opure_engine_rollback_kv", "opure_engine_pages",
+                  "opure_engine_forward_logits"):
             getattr(L, f).restype = i
         _lib = L
     return _lib
@@ -152,6 +156,14 @@ class Engine:
         st = Stats()
         check(lib().opure_engine_generate(self.h, p.ctypes.data, p.size, n_new, out.ctypes.data, C.byref(st)))
         return out, st
+
+    def forward_logits(self, tokens, vocab: int):
+        """(logits [vocab], argmax) of the last of `tokens` prefilled into a fresh cache."""
+        t = np.ascontiguousarray(tokens, dtype=np.int32)
+        out = np.zeros(vocab, dtype=np.float32)
+        am = C.c_uint32()
+        check(lib().opure_engine_forward_logits(self.h, t.ctypes.data, t.size, out.ctypes.data, C.byref(am)))
+        return out, int(am.value)
 
     def verify_step(self, tokens, seq_len: int):
         """(accepted, emitted ids): one verify step of the target on these rows."""
@@ -245,8 +257,9 @@ class PagePool:
         return added.value
 
 
-def load_options(max_positions: int = 0, wfmt: int = -1, afmt: int = -1, attn_scale: float = 0.0) -> LoadOptions:
-    return LoadOptions(max_positions, wfmt, afmt, attn_scale)
+def load_options(max_positions: int = 0, wfmt: int = -1, afmt: int = -1, attn_scale: float = 0.0,
+                 rope_pairs: int = ROPE_PAIRS_ADJACENT) -> LoadOptions:
+    return LoadOptions(max_positions, wfmt, afmt, attn_scale, rope_pairs)
 
 
 class ModelFiles:

@@ -42,8 +42,11 @@ def embed_rows(model, tokens):
     return W[tokens].astype(np.float32)
 
 
-def forward(model, pool, page_table, tokens, seq_len):
-    """pool: numpy copy of the paged cache (modified in place); returns logits [B,R,V]."""
+def forward(model, pool, page_table, tokens, seq_len, rope_pairs="adjacent"):
+    """pool: numpy copy of the paged cache (modified in place); returns logits [B,R,V].
+    rope_pairs: "adjacent" rotates channels (2p, 2p+1) of a head (the
+    reference's RoPE), "half" rotates (p, p + hd/2) (HF Llama's rotate_half),
+    both with the angle pos * theta^(-2p/hd) of pair p."""
     c = model.cfg
     afmt = c["afmt"]
     B, R = tokens.shape
@@ -64,15 +67,18 @@ def forward(model, pool, page_table, tokens, seq_len):
         inv = 1.0 / np.sqrt((x64 * x64).sum(-1, keepdims=True) / h + np.float32(c["rms_eps"]))
         return round_act((x64 * inv * g.astype(np.float64)).astype(np.float32), afmt)
 
+    first = slice(0, None, 2) if rope_pairs == "adjacent" else slice(0, hd // 2)
+    second = slice(1, None, 2) if rope_pairs == "adjacent" else slice(hd // 2, hd)
+
     def rope(v, pos):
-        # v [..., heads, hd]; interleaved pairs
+        # v [..., heads, hd]; channel first[p] pairs with second[p]
         cs = model.rope_cos[pos].astype(np.float64)
         sn = model.rope_sin[pos].astype(np.float64)
-        e0 = v[..., 0::2].astype(np.float64)
-        e1 = v[..., 1::2].astype(np.float64)
+        e0 = v[..., first].astype(np.float64)
+        e1 = v[..., second].astype(np.float64)
         out = np.empty_like(v)
-        out[..., 0::2] = (e0 * cs - e1 * sn).astype(np.float32)
-        out[..., 1::2] = (e0 * sn + e1 * cs).astype(np.float32)
+        out[..., first] = (e0 * cs - e1 * sn).astype(np.float32)
+        out[..., second] = (e0 * sn + e1 * cs).astype(np.float32)
         return out
 
     x = embed_rows(model, tokens.reshape(-1)).reshape(B, R, h)

@@ -147,3 +147,25 @@ def test_engine_error_paths_without_device():
     assert b"cannot open" in L.opure_engine_last_error()
     assert L.opure_model_files_open(b"/nonexistent", None, C.byref(h)) == H.E_INVALID
     assert b"config.json" in L.opure_engine_last_error()
+
+
+def test_empty_page_pool_is_refused_before_any_launch():
+    """A cache with no pages (n_pages = 0 or no page-table columns) is refused
+    by attention, rollback and (through attention's check) the verify step,
+    before anything touches the device: the folded attention kernel reads
+    page 0 for a missing entry, so a pool must hold one page.  The device
+    handle below is a placeholder the calls never dereference."""
+    L = H.lib()
+    fake = C.create_string_buffer(256)                      # stands in for device pointers and the handle
+    addr = C.addressof(fake)
+    m = H.Model()
+    m.n_layers, m.hidden, m.n_heads, m.n_kv_heads, m.head_dim = 1, 256, 4, 2, 64
+    m.ffn, m.vocab, m.afmt, m.wfmt = 512, 1024, H.A_F16, H.W_I8PC
+    for n_pages, max_pages in ((0, 4), (4, 0)):
+        kv = H.KV(addr, n_pages, H.PAGE_SIZE, addr, max_pages)
+        a = H.AttnArgs(C.pointer(m), C.pointer(kv), 0, 1, 4, addr, 16, addr, addr)
+        assert L.opure_attn_decode_paged(addr, C.byref(a)) == H.E_INVALID
+        assert b"no pages" in L.opure_last_error()
+        rb = H.RollbackArgs(C.pointer(m), C.pointer(kv), 1, 3, addr, addr, addr, None, 0, None, 0, 0)
+        assert L.opure_kv_rollback(addr, C.byref(rb)) == H.E_INVALID
+        assert b"no pages" in L.opure_last_error()

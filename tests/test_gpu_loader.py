@@ -159,3 +159,30 @@ def test_engine_from_directories(dev, tmp_path):
     assert np.array_equal(sa, ga)
     a.close()
     b.close()
+
+
+@pytest.mark.parametrize("pairs", ["adjacent", "half"])
+def test_forward_logits_from_directory(dev, tmp_path, pairs):
+    """The engine's ForwardLogits (opure_engine_forward_logits) on a model
+    loaded from its directory by the engine itself (Initialize(modelDir, ...)):
+    the last position's logits of a 12-token prompt against the numpy forward
+    of the stored weights, fp32 (1e-4).  "half": the directory holds a
+    rotate-half checkpoint and is loaded with rope_pairs = HALF, so the
+    kernels' adjacent-pair RoPE on the permuted rows must give the
+    rotate-half forward of the rows as stored."""
+    import npref
+    m = small_model(O.W_F32, O.A_F32, n_layers=2, seed=21, max_pos=256)
+    d = W.write_model_dir(str(tmp_path / pairs), m)
+    lo = E.load_options(attn_scale=float(m.cfg["attn_scale"]),
+                        rope_pairs=E.ROPE_PAIRS_HALF if pairs == "half" else E.ROPE_PAIRS_ADJACENT)
+    eng = E.Engine.from_dirs(dev, d, None, load=lo, max_positions=64, draft_tokens=4)
+    n = 12
+    tokens = np.random.default_rng(8).integers(0, m.cfg["vocab"], size=(1, n)).astype(np.int32)
+    got, am = eng.forward_logits(tokens[0], m.cfg["vocab"])
+    kv = O.HostKV(m, n_pages=4, batch=1, max_pages_per_seq=4)
+    kv.page_table[0] = np.arange(4)
+    want = npref.forward(m, np.zeros_like(kv.pool), kv.page_table, tokens, np.zeros(1, np.int32), rope_pairs=pairs)[0, -1]
+    err = float(np.abs(got - want).max())
+    say(pairs, "forward_logits max_abs vs numpy", err)
+    assert err <= 1e-4 and am == int(np.argmax(got))
+    eng.close()

@@ -317,3 +317,155 @@ def test_truncated_and_garbled_files(tmp_path):
     assert "json" in str(_err(d))
     os.remove(d / "config.json")
     assert "config.json" in str(_err(d))
+
+
+# ---- RoPE pairing of the stored q / k rows -------------------------------------
+def test_rope_pairs_half_matches_a_rotate_half_forward(tmp_path):
+    """A checkpoint trained with rotate-half RoPE (HF Llama's pairs (p, p + hd/2)),
+    loaded with rope_pairs = HALF: the loader permutes each head's q / k rows
+    (new 2p = old p, new 2p+1 = old p + hd/2, scales and zero points with them),
+    and the oracle's adjacent-pair forward on the loaded weights equals an
+    independent numpy forward that applies rotate-half RoPE to the weights as
+    stored.  Loaded as ADJACENT (the reference's reading) the same file gives
+    a different forward, so the option is what makes it right."""
+    import npref
+    m = small(O.W_F32, O.A_F32, n_layers=2, seed=12)
+    d = W.write_model_dir(str(tmp_path / "hf"), m)
+    f = E.ModelFiles(d, E.load_options(attn_scale=0.125, rope_pairs=E.ROPE_PAIRS_HALF))
+    c = m.cfg
+    nh, nkv, hd = c["n_heads"], c["n_kv_heads"], c["head_dim"]
+    layers = []
+    for i, L in enumerate(m.layers):
+        got = f.read(E.ROLE_QKV, i)
+        q = got["w"].view(np.float32).reshape(got["out"], got["in"])
+        src = L["qkv"]["w"]
+        perm = np.arange(got["out"])
+        for h0, n in ((0, nh), (nh * hd, nkv)):
+            for hh in range(n):
+                b = h0 + hh * hd
+                perm[b:b + hd:2] = b + np.arange(hd // 2)
+                perm[b + 1:b + hd:2] = b + hd // 2 + np.arange(hd // 2)
+        assert np.array_equal(q, src[perm])                     # q and k permuted per head, v as stored
+        layers.append(dict(L, qkv=dict(L["qkv"], w=np.ascontiguousarray(q))))
+    loaded = O.HostModel.from_arrays(c, dict(embed=m.embed, lm_head=m.lm_head, final_norm=m.final_norm,
+                                             rope_cos=m.rope_cos, rope_sin=m.rope_sin, layers=layers))
+    R = 8
+    tokens = np.random.default_rng(3).integers(0, c["vocab"], size=(1, R)).astype(np.int32)
+    seq = np.zeros(1, np.int32)
+    kv = O.HostKV(loaded, n_pages=4, batch=1, max_pages_per_seq=4)
+    kv.page_table[0] = np.arange(4)
+    got = O.verify_forward(loaded, kv, tokens, seq)
+    pool = np.zeros_like(kv.pool)
+    want = npref.forward(m, pool, kv.page_table, tokens, seq, rope_pairs="half")
+    assert np.abs(got - want).max() <= 1e-4
+    kv2 = O.HostKV(m, n_pages=4, batch=1, max_pages_per_seq=4)
+    kv2.page_table[0] = np.arange(4)
+    assert np.abs(O.verify_forward(m, kv2, tokens, seq) - want).max() > 1e-2
+    f.close()
+
+
+def test_rope_pairs_half_moves_scales_with_rows(tmp_path):
+    """int8 and int4 files: the permuted q / k rows keep their own scales (and
+    int4 zero points)."""
+    for wfmt, afmt in ((O.W_I8PC, O.A_F16), (O.W_I4G128, O.A_BF16)):
+        m = small(wfmt, afmt, n_layers=1, seed=13)
+        d = W.write_model_dir(str(tmp_path / f"m{wfmt}"), m)
+        plain = E.ModelFiles(d).read(E.ROLE_QKV, 0)
+        half = E.ModelFiles(d, E.load_options(rope_pairs=E.ROPE_PAIRS_HALF)).read(E.ROLE_QKV, 0)
+        out, hd = plain["out"], m.cfg["head_dim"]
+        qk = (m.cfg["n_heads"] + m.cfg["n_kv_heads"]) * hd
+        perm = np.arange(out)
+        for b in range(0, qk, hd):
+            perm[b:b + hd:2] = b + np.arange(hd // 2)
+            perm[b + 1:b + hd:2] = b + hd // 2 + np.arange(hd // 2)
+        for key in ("w", "scale", "zero"):
+            if plain[key] is None:
+                continue
+            a, b = plain[key].reshape(out, -1), half[key].reshape(out, -1)
+            assert np.array_equal(b, a[perm]), key
+    with pytest.raises(H.OpureError) as e:
+        E.ModelFiles(d, E.load_options(rope_pairs=2))
+    assert e.value.code == H.E_INVALID and "rope_pairs" in str(e.value)
+
+
+# ---- untrusted headers, shard names and scales ----------------------------------
+def test_hostile_headers_are_refused(tmp_path):
+    """Shapes whose element count overflows 64 bits, dimensions that are not
+    integers below 2^53, and headers nested past 64 levels fail with an error
+    (the reader never wraps a size or recurses without bound)."""
+    m = small(O.W_F32, O.A_F32, n_layers=1)
+    name = "model.layers.0.mlp.down_proj.weight"
+
+    def patched(fn):
+        d = _dir_with(tmp_path, m, patch=fn)
+        return _err(d)
+
+    def huge(h):
+        h[name]["shape"] = [2 ** 32, 2 ** 32]
+        h[name]["data_offsets"] = [0, 0]
+    e = patched(huge)
+    assert e.code == H.E_INVALID and "overflows" in str(e)
+
+    def big_dim(h):
+        h[name]["shape"] = [2 ** 60, 1]
+    assert "bad shape" in str(patched(big_dim))
+
+    def frac_dim(h):
+        h[name]["shape"] = [256.5, 512]
+    assert "bad shape" in str(patched(frac_dim))
+
+    def frac_off(h):
+        a, b = h[name]["data_offsets"]
+        h[name]["data_offsets"] = [a + 0.5, b + 0.5]
+    assert "data_offsets" in str(patched(frac_off))
+
+    def deep(h):
+        v = 1
+        for _ in range(200):
+            v = [v]
+        h["__metadata__"] = {"nest": v}
+    e = patched(deep)
+    assert e.code == H.E_INVALID and "nesting" in str(e)
+
+
+def test_shard_names_stay_inside_the_directory(tmp_path):
+    m = small(O.W_I8PC, O.A_F16, tied=False)
+    d = W.write_model_dir(str(tmp_path / "m"), m, shards=2)
+    idx = os.path.join(d, "model.safetensors.index.json")
+    doc = json.load(open(idx))
+    first = next(iter(doc["weight_map"]))
+    outside = tmp_path / "elsewhere.safetensors"
+    outside.write_bytes(open(os.path.join(d, doc["weight_map"][first]), "rb").read())
+    for bad in ("../elsewhere.safetensors", str(outside)):
+        doc["weight_map"][first] = bad
+        json.dump(doc, open(idx, "w"))
+        e = _err(d)
+        assert e.code == H.E_INVALID and "outside the model directory" in str(e)
+    # a link inside the directory that points out of it
+    os.symlink(str(outside), os.path.join(d, "link.safetensors"))
+    doc["weight_map"][first] = "link.safetensors"
+    json.dump(doc, open(idx, "w"))
+    assert "resolves outside" in str(_err(d))
+
+
+def test_scales_outside_the_kernel_range_are_refused(tmp_path):
+    """A finite nonzero scale that rounds to 0 or to infinity in the fp16 (int8)
+    or bf16 (int4) the kernels read would zero or blow up its linear: refused."""
+    m = small(O.W_I8PC, O.A_F16, n_layers=1)
+    t = W.model_tensors(m)
+    sname = "model.layers.0.self_attn.o_proj.weight_scale"
+    for val in (1e-9, 1e6):
+        bad = [(n, "F32", sh, np.full(sh, val, np.float32).tobytes(), x) if n == sname else (n, dt, sh, r, x)
+               for n, dt, sh, r, x in t]
+        f = E.ModelFiles(str(_dir_with(tmp_path, m, bad)))
+        with pytest.raises(H.OpureError) as e:
+            f.read(E.ROLE_O, 0)
+        assert e.value.code == H.E_UNSUPPORTED and "fp16 range" in str(e.value)
+        f.close()
+    m4 = small(O.W_I4G128, O.A_BF16, n_layers=1)
+    t4 = [e for e in W.model_tensors(m4, int4_dtype="U4") if not e[0].endswith((".weight_scale", ".weight_zero"))]
+    t4 = [(n, dt, sh, raw, {"scale": 1e-45} if dt == "U4" else None) for n, dt, sh, raw, _ in t4]
+    f = E.ModelFiles(str(_dir_with(tmp_path, m4, t4)))
+    with pytest.raises(H.OpureError) as e:
+        f.read(E.ROLE_DOWN, 0)
+    assert e.value.code == H.E_UNSUPPORTED and "bf16 range" in str(e.value)
