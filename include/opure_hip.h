@@ -420,10 +420,11 @@ int opure_debug_workspace(opure_dev* dev, void** ptr, uint64_t* bytes);
  * up at once, so the failure report can be checked while every wave still
  * runs to its end. */
 int opure_debug_set_wait_limit(opure_dev* dev, uint32_t sleeps);
-/* GEMV engine of opure_gemv_batched_i8pc at M <= 8 rows with fp16 X and a
- * STORE / RESIDUAL / SWIGLU epilogue: the matrix-core kernels (default) or the
- * vector-ALU kernel (v_dot2_f32_f16, one output row per lane), kept for the
- * engine comparison.  The verify step always uses the matrix cores. */
+/* GEMV engine of opure_gemv_batched_* at M <= 8 rows with a STORE / RESIDUAL /
+ * SWIGLU epilogue: the matrix-core kernels (default) or the vector-ALU kernel
+ * (one output row per lane: v_fma_f32 for fp32 weights, v_dot2_f32_f16 for
+ * int8 and uint4 with fp16 X, v_dot2_f32_bf16 for uint4 with bf16 X), kept for
+ * the engine comparison.  The verify step always uses the matrix cores. */
 enum { OPURE_GEMV_MFMA = 0, OPURE_GEMV_VALU = 1 };
 int opure_debug_set_gemv_engine(opure_dev* dev, uint32_t engine);
 /* Evaluates the SwiGLU epilogue's branch-free exponential and the oracle-order

@@ -17,7 +17,10 @@ int launch_i8(opure_dev*, uint32_t, uint32_t, bool, const KParams&, const Recipe
 int launch_i4_f16(opure_dev*, uint32_t, uint32_t, bool, const KParams&, const Recipe&, uint32_t, uint32_t);
 int launch_i4_bf16(opure_dev*, uint32_t, uint32_t, bool, const KParams&, const Recipe&, uint32_t, uint32_t);
 int launch_wide_i8(opure_dev*, uint32_t, const WParams&, uint32_t, const float*, void*);
+int launch_valu_f32(opure_dev*, uint32_t, const KParams&);
 int launch_valu_i8(opure_dev*, uint32_t, const KParams&);
+int launch_valu_i4_f16(opure_dev*, uint32_t, const KParams&);
+int launch_valu_i4_bf16(opure_dev*, uint32_t, const KParams&);
 int launch_wide_i4_f16(opure_dev*, uint32_t, const WParams&, uint32_t, const float*, void*);
 int launch_wide_i4_bf16(opure_dev*, uint32_t, const WParams&, uint32_t, const float*, void*);
 
@@ -440,11 +443,14 @@ int gemv_launch(opure_dev* dev, const GemvCall& c)
     kp.ring = pl.ring;
     kp.qkv = c.qkv;
     kp.lg = c.logits;
-    // the vector-ALU engine, where it is chosen and built (int8 weights, fp16 X,
-    // at most 8 rows, a plain epilogue)
-    if (dev->gemv_engine == OPURE_GEMV_VALU && c.wfmt == OPURE_W_I8PC && c.xfmt == OPURE_A_F16 && c.M <= VALU_MAXM &&
-        !norm && (c.epi == EPI_STORE || c.epi == EPI_RESIDUAL || c.epi == EPI_SWIGLU))
-        return launch_valu_i8(dev, c.epi, kp);
+    // the vector-ALU engine, where it is chosen (at most 8 rows, a plain epilogue)
+    if (dev->gemv_engine == OPURE_GEMV_VALU && c.M <= VALU_MAXM && !norm &&
+        (c.epi == EPI_STORE || c.epi == EPI_RESIDUAL || c.epi == EPI_SWIGLU))
+    {
+        if (c.wfmt == OPURE_W_F32) return launch_valu_f32(dev, c.epi, kp);
+        if (c.wfmt == OPURE_W_I8PC) return launch_valu_i8(dev, c.epi, kp);
+        return c.xfmt == OPURE_A_F16 ? launch_valu_i4_f16(dev, c.epi, kp) : launch_valu_i4_bf16(dev, c.epi, kp);
+    }
     // Without the fused rmsnorm, shapes under 320 tiles (at most one group a
     // CU) take their X fragments from memory with the weights instead of
     // staging X in LDS: the first blocks then wait for no barrier and no

@@ -10,4 +10,9 @@ int launch_f32(opure_dev* dev, uint32_t epi, uint32_t nm, bool staged, const KPa
     return launch_format<OPURE_W_F32, OPURE_A_F32>(dev, epi, nm, staged, kp, r, grid, lds);
 }
 
+int launch_valu_f32(opure_dev* dev, uint32_t epi, const KParams& kp)
+{
+    return launch_valu<OPURE_W_F32, OPURE_A_F32>(dev, epi, kp);
+}
+
 }  // namespace opure_gemv

@@ -16,4 +16,9 @@ int launch_wide_i4_bf16(opure_dev* dev, uint32_t epi, const WParams& wp, uint32_
     return launch_wide_format<OPURE_W_I4G128, OPURE_A_BF16>(dev, epi, wp, lds, gain, xn);
 }
 
+int launch_valu_i4_bf16(opure_dev* dev, uint32_t epi, const KParams& kp)
+{
+    return launch_valu<OPURE_W_I4G128, OPURE_A_BF16>(dev, epi, kp);
+}
+
 }  // namespace opure_gemv

@@ -13,13 +13,7 @@ int launch_i8(opure_dev* dev, uint32_t epi, uint32_t nm, bool staged, const KPar
 
 int launch_valu_i8(opure_dev* dev, uint32_t epi, const KParams& kp)
 {
-    switch (epi)
-    {
-    case opure_hip::EPI_STORE: return launch_valu<opure_hip::EPI_STORE>(dev, kp);
-    case opure_hip::EPI_RESIDUAL: return launch_valu<opure_hip::EPI_RESIDUAL>(dev, kp);
-    case opure_hip::EPI_SWIGLU: return launch_valu<opure_hip::EPI_SWIGLU>(dev, kp);
-    }
-    return opure_hip::set_error(OPURE_E_INVALID, "gemv: the vector-ALU engine has no epilogue %u", epi);
+    return launch_valu<OPURE_W_I8PC, OPURE_A_F16>(dev, epi, kp);
 }
 
 int launch_wide_i8(opure_dev* dev, uint32_t epi, const WParams& wp, uint32_t lds, const float* gain, void* xn)

@@ -1619,49 +1619,111 @@ __global__ __launch_bounds__((PC_NC + PC_NL) * 64) void k_gemv_pc(KParams p)
 }
 
 // Vector-ALU GEMV, the other side of the engine choice (opure_debug_set_gemv_engine):
-// int8 weights, fp16 X, M <= 8 rows, no fused rmsnorm.  One workgroup of 16
-// waves per tile, K split over the waves as in k_gemv (wave w takes blocks w,
-// w + 16, ...).  Lane (g4, r16) holds 16 int8 of row r16 in each block, widens
-// them once to fp16 pairs and takes v_dot2_f32_f16 against the same 16 values
-// of every X row, so each X fragment feeds one output row per lane where the
-// matrix core feeds 16.  The 4 lanes of a row add by butterfly, the waves in
-// wave order through LDS; then the element epilogue.  Sums are ordered
-// differently from the matrix-core path (results agree to rounding).
+// M <= 8 rows, no fused rmsnorm; fp32 weights with fp32 X (v_fma_f32), int8
+// with fp16 X (v_dot2_f32_f16), uint4 g128 with fp16 or bf16 X (v_dot2_f32_f16
+// / v_dot2_f32_bf16 on the same operand pairs as the matrix-core path, the
+// group's scale and zero point applied to the lane's partial through the
+// lane's sum of X, see U4).  One workgroup of 16 waves per tile, K split over
+// the waves as in k_gemv (wave w takes blocks w, w + 16, ...).  Lane (g4, r16)
+// holds its k-slice of row r16 in each block (4 fp32, 16 int8 or 32 uint4),
+// widens it once and takes it against the same k values of every X row, so
+// each X fragment feeds one output row per lane where the matrix core feeds
+// 16.  The 4 lanes of a row add by butterfly, the waves in wave order through
+// LDS; then the element epilogue.  Sums are ordered differently from the
+// matrix-core path (results agree to rounding).
 constexpr uint32_t VALU_NW = 16, VALU_MAXM = 8;
 
-template <int EPI>
+template <int WF, int AF, int EPI>
 __global__ __launch_bounds__(VALU_NW * 64) void k_gemv_valu(KParams p)
 {
+    constexpr uint32_t KB = Fmt<WF>::KB;                 // k values per block
+    constexpr uint32_t VALS = KB / 4u;                   // k values per lane per block
+    constexpr uint32_t EB = AF == OPURE_A_F32 ? 4u : 2u;
+    constexpr uint32_t XW = VALS * EB / 4u;              // X dwords per lane per block and row
     __shared__ float red[VALU_NW][VALU_MAXM][16];
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
     const uint32_t g4 = lane >> 4, r16 = lane & 15u;
-    const uint32_t tile = blockIdx.x, nblk = p.nblk, M = p.M;
+    const uint32_t tile = blockIdx.x, nblk = p.nblk, M = p.M, G = p.in / 128u;
     float acc[VALU_MAXM];
 #pragma unroll
     for (uint32_t m = 0; m < VALU_MAXM; ++m) acc[m] = 0.0f;
     const u4_t* wp = reinterpret_cast<const u4_t*>(p.w + (static_cast<uint64_t>(tile) * nblk << 10) + (lane << 4));
-    const half2_t* xp = reinterpret_cast<const half2_t*>(p.x) + 8u * g4;      // k = 64 blk + 16 g4 .. + 16
-    u4_t wn = __builtin_nontemporal_load(wp + 64u * min(wave, nblk - 1u));
+    const uint32_t* sp = static_cast<const uint32_t*>(p.sc) + static_cast<uint64_t>(tile) * G * 16u + r16;
+    const uint32_t b0 = min(wave, nblk - 1u);
+    u4_t wn = __builtin_nontemporal_load(wp + 64u * b0);
+    uint32_t sn = WF == OPURE_W_I4G128 ? sp[16u * b0] : 0u;
     for (uint32_t blk = wave; blk < nblk; blk += VALU_NW)
     {
         const u4_t w = wn;
-        if (blk + VALU_NW < nblk) wn = __builtin_nontemporal_load(wp + 64u * (blk + VALU_NW));
-        half2_t wh[8];
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
+        const uint32_t sz = sn;
+        if (blk + VALU_NW < nblk)
         {
-            uint32_t lo, hi;
-            u8x4_to_f16(w[j], lo, hi);
-            wh[2 * j] = __builtin_bit_cast(half2_t, lo);
-            wh[2 * j + 1] = __builtin_bit_cast(half2_t, hi);
+            wn = __builtin_nontemporal_load(wp + 64u * (blk + VALU_NW));
+            if constexpr (WF == OPURE_W_I4G128) sn = sp[16u * (blk + VALU_NW)];
         }
+        // the widened weights of the lane's k-slice
+        [[maybe_unused]] uint32_t wh[WF == OPURE_W_I4G128 ? 16 : 8];
+        if constexpr (WF == OPURE_W_I8PC)
+        {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) u8x4_to_f16(w[j], wh[2 * j], wh[2 * j + 1]);
+        }
+        else if constexpr (WF == OPURE_W_I4G128)
+        {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+            {
+                uint32_t a[4];
+                u4x8_pairs<AF>(w[j], a);
+#pragma unroll
+                for (int t = 0; t < 4; ++t) wh[4 * j + t] = a[t];
+            }
+        }
+        [[maybe_unused]] float sc = 0.0f, zo = 0.0f;
+        if constexpr (WF == OPURE_W_I4G128) u4_group<AF>(sz, sc, zo);
 #pragma unroll
         for (uint32_t m = 0; m < VALU_MAXM; ++m)
         {
             if (m >= M) break;                               // uniform
-            const half2_t* xr = xp + (static_cast<uint64_t>(m) * p.in + 64u * blk) / 2u;
+            const u4_t* xr = reinterpret_cast<const u4_t*>(p.x + (static_cast<uint64_t>(m) * p.in + KB * blk + VALS * g4) * EB);
+            uint32_t xd[XW];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) acc[m] = __builtin_amdgcn_fdot2(wh[j], xr[j], acc[m], false);
+            for (uint32_t i = 0; i < XW / 4u; ++i)
+            {
+                const u4_t v = xr[i];
+                xd[4 * i] = v[0]; xd[4 * i + 1] = v[1]; xd[4 * i + 2] = v[2]; xd[4 * i + 3] = v[3];
+            }
+            if constexpr (WF == OPURE_W_F32)
+            {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[m] = __fmaf_rn(__uint_as_float(w[i]), __uint_as_float(xd[i]), acc[m]);
+            }
+            else if constexpr (WF == OPURE_W_I8PC)
+            {
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+                    acc[m] = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, wh[j]), __builtin_bit_cast(half2_t, xd[j]),
+                                                    acc[m], false);
+            }
+            else
+            {
+                float b = 0.0f;
+#pragma unroll
+                for (int j = 0; j < 16; ++j)
+                {
+                    if constexpr (AF == OPURE_A_F16)
+                        b = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, wh[j]), __builtin_bit_cast(half2_t, xd[j]), b,
+                                                   false);
+                    else
+                        b = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, wh[j]),
+                                                            __builtin_bit_cast(bf16x2_t, xd[j]), b, false);
+                }
+                const float xs = __fadd_rn(__fadd_rn(unit_sum<AF>(xd[0], xd[1], xd[2], xd[3]),
+                                                     unit_sum<AF>(xd[4], xd[5], xd[6], xd[7])),
+                                           __fadd_rn(unit_sum<AF>(xd[8], xd[9], xd[10], xd[11]),
+                                                     unit_sum<AF>(xd[12], xd[13], xd[14], xd[15])));
+                acc[m] = __fmaf_rn(sc, __fmaf_rn(-zo, xs, b), acc[m]);
+            }
         }
     }
 #pragma unroll
@@ -1684,14 +1746,26 @@ __global__ __launch_bounds__(VALU_NW * 64) void k_gemv_valu(KParams p)
         for (uint32_t w = 1; w < VALU_NW; ++w) v = __fadd_rn(v, red[w][m][c]);
         float bv = 0.0f;
         int32_t bi = 0;
-        epilogue_elem<OPURE_W_I8PC, EPI>(p, tile, m, c, v, bv, bi);
+        epilogue_elem<WF, EPI>(p, tile, m, c, v, bv, bi);
     }
 }
 
-template <int EPI>
-int launch_valu(opure_dev* dev, const KParams& kp)
+template <int WF, int AF>
+int launch_valu(opure_dev* dev, uint32_t epi, const KParams& kp)
 {
-    OPURE_LAUNCH(dev, k_gemv_valu<EPI>, dim3(kp.tiles), dim3(VALU_NW * 64), 0, kp);
+    switch (epi)
+    {
+    case opure_hip::EPI_STORE:
+        OPURE_LAUNCH(dev, (k_gemv_valu<WF, AF, opure_hip::EPI_STORE>), dim3(kp.tiles), dim3(VALU_NW * 64), 0, kp);
+        break;
+    case opure_hip::EPI_RESIDUAL:
+        OPURE_LAUNCH(dev, (k_gemv_valu<WF, AF, opure_hip::EPI_RESIDUAL>), dim3(kp.tiles), dim3(VALU_NW * 64), 0, kp);
+        break;
+    case opure_hip::EPI_SWIGLU:
+        OPURE_LAUNCH(dev, (k_gemv_valu<WF, AF, opure_hip::EPI_SWIGLU>), dim3(kp.tiles), dim3(VALU_NW * 64), 0, kp);
+        break;
+    default: return opure_hip::set_error(OPURE_E_INVALID, "gemv: the vector-ALU engine has no epilogue %u", epi);
+    }
     OPURE_LAUNCH_CHECK("k_gemv_valu");
     return OPURE_OK;
 }

@@ -302,41 +302,47 @@ def test_gemv_swiglu_matches_oracle(dev, case):
             b.free()
 
 
-VALU_CASES = [(3072, 2048), (2048, 8192), (16384, 2048), (128256, 2048)]
+VALU_CASES = [(H.W_I8PC, H.A_F16, 3072, 2048), (H.W_I8PC, H.A_F16, 2048, 8192), (H.W_I8PC, H.A_F16, 16384, 2048),
+              (H.W_I8PC, H.A_F16, 128256, 2048), (H.W_F32, H.A_F32, 960, 576), (H.W_F32, H.A_F32, 576, 1536),
+              (H.W_F32, H.A_F32, 3072, 576), (H.W_I4G128, H.A_BF16, 6144, 4096), (H.W_I4G128, H.A_BF16, 4096, 14336),
+              (H.W_I4G128, H.A_F16, 4096, 4096)]
+VALU_IDS = [f"{['f32', 'i8', 'i4'][w]}{['', '-f16', '-bf16'][a]}-{o}x{i}" for w, a, o, i in VALU_CASES]
 
 
-@pytest.mark.parametrize("case", VALU_CASES, ids=[f"{o}x{i}" for o, i in VALU_CASES])
+@pytest.mark.parametrize("case", VALU_CASES, ids=VALU_IDS)
 def test_gemv_valu_engine_matches_oracle(dev, case):
-    """The vector-ALU engine (int8 weights, fp16 X, M <= 8) against the
+    """The vector-ALU engine (M <= 8: fp32, int8, uint4 weights) against the
     oracle, to the matrix-core path's bound, for every epilogue it takes."""
-    out, inn = case
-    say("gemv valu", case)
-    rng = np.random.default_rng(out * 3 + inn)
-    lin = O.make_linear(rng, out, inn, H.W_I8PC)
+    wfmt, afmt, out, inn = case
+    say("gemv valu", VALU_IDS[VALU_CASES.index(case)])
+    rng = np.random.default_rng(out * 3 + inn + wfmt)
+    lin = O.make_linear(rng, out, inn, wfmt)
     desc, keep = dev_linear(dev, lin)
-    x_bits, x_f = to_act(rng.standard_normal((16, inn)), H.A_F16)
-    ref = O.gemv(lin, H.W_I8PC, x_f)
-    absref = np.abs(x_f).astype(np.float64) @ np.abs(O.dequant(lin, H.W_I8PC)).T
+    x_bits, x_f = to_act(rng.standard_normal((16, inn)), afmt)
+    ref = O.gemv(lin, wfmt, x_f)
+    absref = np.abs(x_f).astype(np.float64) @ np.abs(O.dequant(lin, wfmt)).T
+    rel = 1e-5 if wfmt != H.W_I4G128 else 2e-5      # uint4: the group correction subtracts (OFF + MUL z) * sum x
     H.check(H.lib().opure_debug_set_gemv_engine(dev.h, H.GEMV_VALU))
     try:
-        for M in (1, 6, 8):
-            y = run_gemv(dev, H.W_I8PC, desc, x_bits, M, H.A_F16, H.A_F32, H.EPI_STORE)
+        for M in (1, 5, 6, 8):
+            y = run_gemv(dev, wfmt, desc, x_bits, M, afmt, H.A_F32, H.EPI_STORE)
             err = np.abs(y - ref[:M])
-            assert np.all(err <= 1e-5 * absref[:M] + 1e-6), (M, err.max())
+            assert np.all(err <= rel * absref[:M] + 1e-6), (M, err.max())
         y0 = rng.standard_normal((8, out)).astype(np.float32)
-        yv = run_gemv(dev, H.W_I8PC, desc, x_bits, 6, H.A_F16, H.A_F32, H.EPI_STORE)
-        yr = run_gemv(dev, H.W_I8PC, desc, x_bits, 6, H.A_F16, H.A_F32, H.EPI_RESIDUAL, y_init=y0)
+        yv = run_gemv(dev, wfmt, desc, x_bits, 6, afmt, H.A_F32, H.EPI_STORE)
+        yr = run_gemv(dev, wfmt, desc, x_bits, 6, afmt, H.A_F32, H.EPI_RESIDUAL, y_init=y0)
         assert np.array_equal(yr, (y0[:6] + yv).astype(np.float32))
-        if out <= 16384:
+        if out <= 16384 and out % 32 == 0:
             F = out // 2
             g, u = ref[:6, :F].copy(), ref[:6, F:].copy()
             h = np.zeros_like(g)
             O.lib().orc_swiglu(g.ctypes.data, u.ctypes.data, h.ctypes.data, g.size)
-            ys = from_act(run_gemv(dev, H.W_I8PC, desc, x_bits, 6, H.A_F16, H.A_F16, H.EPI_SWIGLU), H.A_F16)
-            np.testing.assert_allclose(ys, h, rtol=2e-3, atol=1e-4 * max(1.0, np.abs(h).max()))
+            ys = from_act(run_gemv(dev, wfmt, desc, x_bits, 6, afmt, afmt, H.EPI_SWIGLU), afmt)
+            tol = 1e-4 if afmt == H.A_F32 else (2e-3 if afmt == H.A_F16 else 1.6e-2)
+            np.testing.assert_allclose(ys, h, rtol=tol, atol=1e-4 * max(1.0, np.abs(h).max()))
         # rows past 8 fall back to the matrix cores
-        y16 = run_gemv(dev, H.W_I8PC, desc, x_bits, 16, H.A_F16, H.A_F32, H.EPI_STORE)
-        assert np.all(np.abs(y16 - ref) <= 1e-5 * absref + 1e-6)
+        y16 = run_gemv(dev, wfmt, desc, x_bits, 16, afmt, H.A_F32, H.EPI_STORE)
+        assert np.all(np.abs(y16 - ref) <= rel * absref + 1e-6)
     finally:
         H.check(H.lib().opure_debug_set_gemv_engine(dev.h, H.GEMV_MFMA))
     for b in keep:
