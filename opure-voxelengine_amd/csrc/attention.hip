@@ -42,9 +42,11 @@ struct AttnParams {
     const void* pool;
     const int32_t* page_table;
     const int32_t* seq_len;
-    float* part_acc;     // [B][nkv][nch][Gq][hd]
-    float* part_ml;      // [B][nkv][nch][Gq][2]
+    float* part_acc;     // [B][nkv][npart][Gq][hd]
+    float* part_ml;      // [B][nkv][npart][Gq][2]
     uint32_t n_heads, n_kv, hd, rows, n_pages, max_pages, layer, nch, chunk, afmt;
+    uint32_t npart;      // partials a (sequence, KV head): one a chunk, or one a group of cpp chunks
+    uint32_t cpp;        // chunks a partial
     float scale;
     uint32_t qoff;       // matrix-core path: first query row of this launch
     uint32_t zt;         // matrix-core path: row blocks of 16 * NT rows along blockIdx.z (b = z / zt)
@@ -140,7 +142,7 @@ __global__ __launch_bounds__(256) void k_attn_chunk_generic(AttnParams p)
 
     // per-row softmax over the chunk: one wave per row, CH <= 64 lanes
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
-    const uint64_t pbase = ((static_cast<uint64_t>(b) * p.n_kv + kh) * p.nch + c) * Gq;
+    const uint64_t pbase = ((static_cast<uint64_t>(b) * p.n_kv + kh) * p.npart + c) * Gq;
     for (uint32_t qi = wave; qi < Gq; qi += 4u)
     {
         const float s = lane < CH ? S[qi * CH + lane] : -__builtin_huge_valf();
@@ -254,7 +256,7 @@ __global__ __launch_bounds__(256) void k_attn_chunk(AttnParams p)
         for (uint32_t t = 0; t < CH; ++t)
             vc[i][t] = d < HD ? load_act_rt(vt + d * VROWB, t, AF) : 0.0f;
     }
-    const uint64_t pbase = ((static_cast<uint64_t>(b) * p.n_kv + kh) * p.nch + c) * Gq;
+    const uint64_t pbase = ((static_cast<uint64_t>(b) * p.n_kv + kh) * p.npart + c) * Gq;
     const uint32_t pos = t0 + lane;
     for (uint32_t qi = wave; qi < Gq; qi += 4u)
     {
@@ -360,12 +362,37 @@ constexpr uint32_t attn_mfma_lds()
     return NWV * (HD / 16u) * NT * 64u * 16u + NWV * NT * 16u * 2u * 4u;
 }
 
-// ZS: blockIdx.z holds (sequence, block of 16 * NT query rows) as b * zt + block
-// CL: a workgroup takes chunks blockIdx.y, blockIdx.y + gridDim.y, ...
-template <int HD, int AF, int NT, int KK, int NWV, bool ZS, bool CL = false>
-__global__ __launch_bounds__(NWV * 64) void k_attn_mfma(AttnParams p)
+// Chunks that one workgroup of the folded head_dim-64 launch (a grid of many
+// sequences) merges into one partial, so that it writes a quarter of the
+// partials and the combine reads a quarter.  The combine merges the chunk
+// partials of the other head_dim-64 launches in groups of as many chunks, with
+// the same operations, so a row's bits do not depend on the launch that scored it.
+constexpr uint32_t ATTN_GROUP = 4;
+
+// One step of the in-order merge of a group's chunks: the running state
+// (m, l, acc) and the next chunk (mc, lc, ac) become
+// (max(m, mc), sa l + sb lc, sa acc + sb ac) with sa = exp(m - max) and
+// sb = exp(mc - max) on the transcendental unit (exp_hw: the running merge is
+// a chain of these, and the kernel and the combine both take them from here),
+// a side whose maximum is -inf weighing 0.
+__device__ __forceinline__ void merge_scales(float m, float mc, float& mn, float& sa, float& sb)
 {
-    constexpr uint32_t KS = HD / 32u, DT = HD / 16u, EB = 2u, TPW = 32u * KK;
+    mn = fmaxf(m, mc);
+    sa = m == -__builtin_huge_valf() ? 0.0f : exp_hw(__fsub_rn(m, mn));
+    sb = mc == -__builtin_huge_valf() ? 0.0f : exp_hw(__fsub_rn(mc, mn));
+}
+__device__ __forceinline__ float merge_val(float sa, float a, float sb, float c)
+{
+    return __fmaf_rn(sb, c, __fmul_rn(sa, a));
+}
+
+// ZS: blockIdx.z holds (sequence, block of 16 * NT query rows) as b * zt + block
+// CL: a workgroup takes the ATTN_GROUP chunks from ATTN_GROUP * blockIdx.y and
+//     writes their merge as partial blockIdx.y
+template <int HD, int AF, int NT, int KK, int NWV, bool ZS, bool CL = false>
+__global__ __launch_bounds__(NWV * 64) __attribute__((amdgpu_waves_per_eu(CL ? 4 : 1))) void k_attn_mfma(AttnParams p)
+{
+    constexpr uint32_t KS = HD / 32u, DT = HD / 16u, EB = 2u, TPW = 32u * KK, OWN = DT * NT / NWV;
     extern __shared__ __align__(16) uint8_t lds_raw[];
     f4_t (*cacc)[DT][NT][64] = reinterpret_cast<f4_t (*)[DT][NT][64]>(lds_raw);
     float (*cml)[NT][16][2] = reinterpret_cast<float (*)[NT][16][2]>(lds_raw + NWV * DT * NT * 64u * 16u);
@@ -376,55 +403,69 @@ __global__ __launch_bounds__(NWV * 64) void k_attn_mfma(AttnParams p)
     const int32_t* pt = p.page_table + static_cast<uint64_t>(b) * p.max_pages;
     const uint8_t* pool = static_cast<const uint8_t*>(p.pool);
     const uint32_t nan2 = AF == OPURE_A_F16 ? 0x7E007E00u : 0x7FC07FC0u;
+    // chunks c_first .. c_end - 1 of this workgroup
+    const uint32_t c_first = CL ? blockIdx.y * ATTN_GROUP : blockIdx.y;
+    const uint32_t c_end = CL ? min(c_first + ATTN_GROUP, p.nch) : c_first + 1u;
 
-    // chunks blockIdx.y, blockIdx.y + gridDim.y, ...: one a workgroup, or
-    // (CL) two or more where the launch folds its grid; the partial of chunk
-    // c does not depend on which workgroup computes it
-    for (uint32_t c = blockIdx.y; c < (CL ? p.nch : blockIdx.y + 1u); c += CL ? gridDim.y : 1u)
-    {
-        const uint32_t t0 = c * NWV * TPW;
-        const uint32_t tw = t0 + TPW * wave;
-        // ---- the sequence length, the page-table entries of this wave's tokens
-        //      and Q^T in one round trip: none of them depends on another, and the
-        //      entries are loaded unconditionally (index clamped to the table) and
-        //      checked only when used, so no load waits behind another -----------
-        const int32_t seq = p.seq_len[b];
-        int32_t pgk[KK][2], pgv[KK];
-        auto raw_entry = [&](uint32_t tok) { return pt[min(tok / OPURE_PAGE_SIZE, p.max_pages - 1u)]; };
+    // ---- the sequence length, the page-table entries of the first chunk's
+    //      tokens and Q^T in one round trip: none of them depends on another,
+    //      and the entries are loaded unconditionally (index clamped to the
+    //      table) and checked only when used, so no load waits behind another
+    const int32_t seq = p.seq_len[b];
+    auto raw_entry = [&](uint32_t tok) { return pt[min(tok / OPURE_PAGE_SIZE, p.max_pages - 1u)]; };
+    auto load_entries = [&](uint32_t c, int32_t (&ek)[KK][2], int32_t (&ev)[KK]) {
+        const uint32_t tw = c * NWV * TPW + TPW * wave;
 #pragma unroll
         for (uint32_t kk = 0; kk < KK; ++kk)
         {
             const uint32_t tb = tw + 32u * kk;
 #pragma unroll
-            for (uint32_t T = 0; T < 2; ++T) pgk[kk][T] = raw_entry(tb + 8u * (r >> 2) + (r & 3u) + 4u * T);
-            pgv[kk] = raw_entry(tb + 8u * g);
+            for (uint32_t T = 0; T < 2; ++T) ek[kk][T] = raw_entry(tb + 8u * (r >> 2) + (r & 3u) + 4u * T);
+            ev[kk] = raw_entry(tb + 8u * g);
         }
-        // the entry of `tok` as page_of gives it, from its raw load
-        auto checked = [&](uint32_t tok, int32_t pg) -> int32_t {
-            return tok / OPURE_PAGE_SIZE < p.max_pages && pg >= 0 && static_cast<uint32_t>(pg) < p.n_pages ? pg : -1;
-        };
-        u4v qop[NT][KS];
-        uint32_t qj[NT];
+    };
+    int32_t pgk[KK][2], pgv[KK];
+    load_entries(c_first, pgk, pgv);
+    // the entry of `tok` as page_of gives it, from its raw load
+    auto checked = [&](uint32_t tok, int32_t pg) -> int32_t {
+        return tok / OPURE_PAGE_SIZE < p.max_pages && pg >= 0 && static_cast<uint32_t>(pg) < p.n_pages ? pg : -1;
+    };
+    u4v qop[NT][KS];
+    uint32_t qj[NT];
 #pragma unroll
-        for (int n = 0; n < NT; ++n)
-        {
-            const uint32_t qi = min(qoff + 16u * n + r, Gq - 1u);
-            const uint32_t j = qi / group, head = kh * group + (qi - j * group);
-            qj[n] = j;
-            const uint8_t* qrow = static_cast<const uint8_t*>(p.q) + ((static_cast<uint64_t>(b * R + j) * p.n_heads + head) * HD) * EB;
+    for (int n = 0; n < NT; ++n)
+    {
+        const uint32_t qi = min(qoff + 16u * n + r, Gq - 1u);
+        const uint32_t j = qi / group, head = kh * group + (qi - j * group);
+        qj[n] = j;
+        const uint8_t* qrow = static_cast<const uint8_t*>(p.q) + ((static_cast<uint64_t>(b * R + j) * p.n_heads + head) * HD) * EB;
 #pragma unroll
-            for (uint32_t s = 0; s < KS; ++s) qop[n][s] = *reinterpret_cast<const u4v*>(qrow + (32u * s + 8u * g) * EB);
-        }
-        // keeps the loads above issued before the exit below (the compiler would
-        // otherwise test the length first and make them wait for it)
-        asm volatile("" ::: "memory");
-        const uint32_t ctx = static_cast<uint32_t>(seq);
-        const uint32_t total = ctx + R;
-        if (t0 >= total) return;                          // whole workgroup: no row reaches this chunk
+        for (uint32_t s = 0; s < KS; ++s) qop[n][s] = *reinterpret_cast<const u4v*>(qrow + (32u * s + 8u * g) * EB);
+    }
+    // keeps the loads above issued before the exit below (the compiler would
+    // otherwise test the length first and make them wait for it)
+    asm volatile("" ::: "memory");
+    const uint32_t ctx = static_cast<uint32_t>(seq);
+    const uint32_t total = ctx + R;
+    if (c_first * NWV * TPW >= total) return;             // whole workgroup: no row reaches its chunks
+    uint32_t lim[NT];
+#pragma unroll
+    for (int n = 0; n < NT; ++n) lim[n] = ctx + qj[n];
+    // the merge's share of wave w: row block w % NT, channel tiles w / NT,
+    // w / NT + NWV / NT, ...; the row's last chunk (the folded merge takes
+    // chunks up to it) and the merged state of the chunks so far
+    static_assert(NWV % NT == 0 && (DT * NT) % NWV == 0, "whole channel tiles of one row block a wave");
+    const uint32_t n_own = wave % NT, qi_own = qoff + 16u * n_own + r;
+    const uint32_t last_own = (ctx + min(qi_own, Gq - 1u) / group) / p.chunk;
+    float sm = 0.0f, sl = 0.0f;
+    f4_t sacc[OWN];
+
+    for (uint32_t c = c_first; c < c_end; ++c)
+    {
+        const uint32_t t0 = c * NWV * TPW;
+        const uint32_t tw = t0 + TPW * wave;
+        if (t0 >= total) break;                           // whole workgroup: past the sequence
         const bool active = tw < total;
-        uint32_t lim[NT];
-#pragma unroll
-        for (int n = 0; n < NT; ++n) lim[n] = ctx + qj[n];
 
         // ---- then K (both score tiles of each k-step) and V^T.  In the folded
         //      kernel (a grid of many workgroups) every load is unconditional -- a
@@ -524,6 +565,10 @@ __global__ __launch_bounds__(NWV * 64) void k_attn_mfma(AttnParams p)
                     for (uint32_t dt = 0; dt < DT; ++dt) vop[kk][dt] = mask_tail<AF>(vop[kk][dt], vlen[kk]);
             }
         };
+        // the next chunk's page-table entries (clamped, as the first's) land
+        // while this chunk computes
+        int32_t npk[KK][2], npv[KK];
+        if constexpr (CL) load_entries(c + 1u, npk, npv);
         // every K and V load is issued before the first product
         if constexpr (CL) __builtin_amdgcn_sched_barrier(0);
 
@@ -647,17 +692,14 @@ __global__ __launch_bounds__(NWV * 64) void k_attn_mfma(AttnParams p)
             }
         }
         __syncthreads();
-        const uint64_t pbase = ((static_cast<uint64_t>(b) * p.n_kv + kh) * p.nch + c) * Gq;
-        // wave w merges row block w % NT, channel tiles w / NT, w / NT + NWV / NT,
-        // ...: the block's weights once, then every tile's loads in one round
-        static_assert(NWV % NT == 0 && (DT * NT) % NWV == 0, "whole channel tiles of one row block a wave");
-        const uint32_t n = wave % NT, qi = qoff + 16u * n + r;
+        // the chunk's (max, sum, output) of this wave's share: the block's
+        // weights once, then every tile's loads in one round
         float mw[NWV], lw[NWV];
 #pragma unroll
         for (int w = 0; w < NWV; ++w)
         {
-            mw[w] = cml[w][n][r][0];
-            lw[w] = cml[w][n][r][1];
+            mw[w] = cml[w][n_own][r][0];
+            lw[w] = cml[w][n_own][r][1];
         }
         float M = mw[0];
 #pragma unroll
@@ -666,62 +708,132 @@ __global__ __launch_bounds__(NWV * 64) void k_attn_mfma(AttnParams p)
 #pragma unroll
         for (int w = 0; w < NWV; ++w)
             ew[w] = mw[w] == -__builtin_huge_valf() ? 0.0f : expf_ref_nonpos(__fsub_rn(mw[w], M));
-        if (qi < Gq)
+        float L = __fmul_rn(ew[0], lw[0]);
+#pragma unroll
+        for (int w = 1; w < NWV; ++w) L = __fmaf_rn(ew[w], lw[w], L);
+        f4_t a[OWN];
+#pragma unroll
+        for (uint32_t j = 0; j < OWN; ++j)
+        {
+            const uint32_t dt = wave / NT + (NWV / NT) * j;
+            a[j] = cacc[0][dt][n_own][lane] * ew[0];
+#pragma unroll
+            for (int w = 1; w < NWV; ++w)
+            {
+                const f4_t v = cacc[w][dt][n_own][lane];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) a[j][i] = __fmaf_rn(ew[w], v[i], a[j][i]);
+            }
+        }
+        if constexpr (!CL)
+        {
+            // the chunk's partial
+            const uint64_t pbase = ((static_cast<uint64_t>(b) * p.n_kv + kh) * p.npart + c) * Gq;
+            if (qi_own < Gq)
+            {
+                if (wave < NT && g == 0)
+                {
+                    p.part_ml[(pbase + qi_own) * 2u] = M;
+                    p.part_ml[(pbase + qi_own) * 2u + 1u] = L;
+                }
+#pragma unroll
+                for (uint32_t j = 0; j < OWN; ++j)
+                    *reinterpret_cast<f4_t*>(p.part_acc + (pbase + qi_own) * HD + 16u * (wave / NT + (NWV / NT) * j) +
+                                             4u * g) = a[j];
+            }
+        }
+        else
+        {
+            // merged, in chunk order, with the group's chunks so far that the
+            // row sees (chunks past the row's last are left out, as the combine
+            // leaves them out)
+            if (c == c_first)
+            {
+                sm = M;
+                sl = L;
+#pragma unroll
+                for (uint32_t j = 0; j < OWN; ++j) sacc[j] = a[j];
+            }
+            else if (c <= last_own)
+            {
+                float mn, sa, sb;
+                merge_scales(sm, M, mn, sa, sb);
+                sm = mn;
+                sl = merge_val(sa, sl, sb, L);
+#pragma unroll
+                for (uint32_t j = 0; j < OWN; ++j)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) sacc[j][i] = merge_val(sa, sacc[j][i], sb, a[j][i]);
+            }
+#pragma unroll
+            for (uint32_t kk = 0; kk < KK; ++kk)
+            {
+                pgk[kk][0] = npk[kk][0];
+                pgk[kk][1] = npk[kk][1];
+                pgv[kk] = npv[kk];
+            }
+            // the next chunk writes the merge buffers again
+            if (c + 1u < c_end) __syncthreads();
+        }
+    }
+    if constexpr (CL)
+    {
+        // the group's partial
+        const uint64_t pbase = ((static_cast<uint64_t>(b) * p.n_kv + kh) * p.npart + blockIdx.y) * Gq;
+        if (qi_own < Gq)
         {
             if (wave < NT && g == 0)
             {
-                float L = __fmul_rn(ew[0], lw[0]);
-#pragma unroll
-                for (int w = 1; w < NWV; ++w) L = __fmaf_rn(ew[w], lw[w], L);
-                p.part_ml[(pbase + qi) * 2u] = M;
-                p.part_ml[(pbase + qi) * 2u + 1u] = L;
+                p.part_ml[(pbase + qi_own) * 2u] = sm;
+                p.part_ml[(pbase + qi_own) * 2u + 1u] = sl;
             }
 #pragma unroll
-            for (uint32_t j = 0; j < DT * NT / NWV; ++j)
-            {
-                const uint32_t dt = wave / NT + (NWV / NT) * j;
-                f4_t a = cacc[0][dt][n][lane] * ew[0];
-#pragma unroll
-                for (int w = 1; w < NWV; ++w)
-                {
-                    const f4_t v = cacc[w][dt][n][lane];
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) a[i] = __fmaf_rn(ew[w], v[i], a[i]);
-                }
-                *reinterpret_cast<f4_t*>(p.part_acc + (pbase + qi) * HD + 16u * dt + 4u * g) = a;
-            }
+            for (uint32_t j = 0; j < OWN; ++j)
+                *reinterpret_cast<f4_t*>(p.part_acc + (pbase + qi_own) * HD + 16u * (wave / NT + (NWV / NT) * j) + 4u * g) =
+                    sacc[j];
         }
-        // the next chunk writes the merge buffers again
-        if (CL && c + gridDim.y < p.nch) __syncthreads();
     }
 }
 
-// One wave per (row, query head): merge that row's chunks 0..last in order.
-// Lanes first take chunks (max, then weights and the denominator with a fixed
-// butterfly), then channels d = lane + 64 i (i < DPL), summing the chunks'
-// outputs in chunk order.  The first CB chunks' outputs are loaded together
-// with the statistics, so a context of up to CB chunks costs one round trip.
-template <int DPL>
+// One wave per (row, query head): merge that row's items 0..last in order.
+// An item is a partial, or (GRP > 1) a group of GRP chunk partials merged in
+// chunk order by merge_scales/merge_val, as the folded attention kernel merges
+// its chunks into one partial -- so a row's bits are the same whichever
+// launch scored it.  Lanes first take items (max, then weights and the
+// denominator with a fixed butterfly), then channels d = lane + 64 i
+// (i < DPL), summing the items' outputs in order.  The first CB partials'
+// outputs are loaded together with the statistics, so a context of up to CB
+// partials costs one round trip.
+template <int DPL, int GRP>
 __global__ __launch_bounds__(64) void k_attn_combine(AttnParams p)
 {
-    constexpr uint32_t CB = 32;
-    __shared__ float wsh[1024];
+    constexpr uint32_t CB = 32, NI = 1024u / GRP, NS = GRP > 1 ? 1024u : 1u, NG = GRP > 1 ? NI : 1u;
+    __shared__ float wsh[NI];                              // the items' weights
+    __shared__ float gsc[2][NS];                           // GRP > 1: each chunk's merge scales (state, chunk)
+    __shared__ float gml[2][NG];                           // GRP > 1: each group's (max, sum)
     const uint32_t head = blockIdx.x, rr = blockIdx.y;    // rr = b * R + j
     const uint32_t R = p.rows, b = rr / R, j = rr - b * R;
     const uint32_t group = p.n_heads / p.n_kv, kh = head / group, qi = j * group + (head - kh * group);
     const uint32_t Gq = group * R, hd = p.hd, lane = threadIdx.x;
     const int32_t seq = p.seq_len[b];
-    const uint64_t base = (static_cast<uint64_t>(b) * p.n_kv + kh) * p.nch;
-    // chunks are clamped to the launch's last, not the row's: these loads do
-    // not wait for the sequence length, and chunks past the row's last are
+    const uint64_t base = (static_cast<uint64_t>(b) * p.n_kv + kh) * p.npart;
+    // partials are clamped to the launch's last, not the row's: these loads do
+    // not wait for the sequence length, and partials past the row's last are
     // loaded but never used
     auto acc_at = [&](uint32_t c, int i) {
         const uint32_t d = min(lane + 64u * i, hd - 1u);
-        return p.part_acc[((base + min(c, p.nch - 1u)) * Gq + qi) * hd + d];
+        return p.part_acc[((base + min(c, p.npart - 1u)) * Gq + qi) * hd + d];
     };
-    // statistics of chunks lane, lane + 64, ... and the first CB chunks' outputs
-    const uint32_t c0 = min(lane, p.nch - 1u);
-    const float m0 = p.part_ml[((base + c0) * Gq + qi) * 2u], l0 = p.part_ml[((base + c0) * Gq + qi) * 2u + 1u];
+    auto ml_at = [&](uint32_t c, uint32_t k) { return p.part_ml[((base + min(c, p.npart - 1u)) * Gq + qi) * 2u + k]; };
+    // the statistics of item `lane`'s partials and the first CB partials'
+    // outputs, in one round trip
+    float m0[GRP], l0[GRP];
+#pragma unroll
+    for (uint32_t k = 0; k < GRP; ++k)
+    {
+        m0[k] = ml_at(lane * GRP + k, 0u);
+        l0[k] = ml_at(lane * GRP + k, 1u);
+    }
     float v[CB][DPL];
 #pragma unroll
     for (uint32_t c = 0; c < CB; ++c)
@@ -735,17 +847,68 @@ __global__ __launch_bounds__(64) void k_attn_combine(AttnParams p)
         last = p.nch - 1u;
         if (lane == 0u && p.err) p.err[ERR_POSITION] = 1u;
     }
-    float mx = -__builtin_huge_valf();
-    if (lane <= last) mx = fmaxf(mx, m0);
-    for (uint32_t c = lane + 64u; c <= last; c += 64u) mx = fmaxf(mx, p.part_ml[((base + c) * Gq + qi) * 2u]);
+    const uint32_t lastp = last / p.cpp, lasti = lastp / GRP;   // the row's last partial, last item
+    // item i's (max, sum): the partial's, or its group's merge
+    auto item = [&](uint32_t i, float& m, float& l) {
+        m = i == lane ? m0[0] : ml_at(i * GRP, 0u);
+        l = i == lane ? l0[0] : ml_at(i * GRP, 1u);
+        if constexpr (GRP > 1)
+        {
+            float mc[GRP], lc[GRP];
+#pragma unroll
+            for (uint32_t k = 1; k < GRP; ++k)
+            {
+                mc[k] = i == lane ? m0[k] : ml_at(i * GRP + k, 0u);
+                lc[k] = i == lane ? l0[k] : ml_at(i * GRP + k, 1u);
+            }
+            // without branches, so the steps' exponentials (which wait only
+            // for the running maximum) overlap; a chunk past the row's last
+            // leaves the state as it is
+#pragma unroll
+            for (uint32_t k = 1; k < GRP; ++k)
+            {
+                const bool in = i * GRP + k <= lastp;
+                float mn, sa, sb;
+                merge_scales(m, mc[k], mn, sa, sb);
+                const float ln = merge_val(sa, l, sb, lc[k]);
+                m = in ? mn : m;
+                l = in ? ln : l;
+                gsc[0][i * GRP + k] = sa;
+                gsc[1][i * GRP + k] = sb;
+            }
+            gml[0][i] = m;
+            gml[1][i] = l;
+        }
+    };
+    float mx = -__builtin_huge_valf(), mf = 0.0f, lf = 0.0f;  // (GRP > 1) item `lane`'s merge
+    for (uint32_t i = lane; i <= lasti; i += 64u)
+    {
+        float m, l;
+        if constexpr (GRP > 1)
+        {
+            item(i, m, l);
+            if (i == lane)
+            {
+                mf = m;
+                lf = l;
+            }
+        }
+        else m = i == lane ? m0[0] : ml_at(i, 0u);
+        mx = fmaxf(mx, m);
+    }
     mx = wave_max64(mx);
     float den = 0.0f;
-    for (uint32_t c = lane; c <= last; c += 64u)
+    for (uint32_t i = lane; i <= lasti; i += 64u)
     {
-        const float m = c == lane ? m0 : p.part_ml[((base + c) * Gq + qi) * 2u];
-        const float l = c == lane ? l0 : p.part_ml[((base + c) * Gq + qi) * 2u + 1u];
+        float m, l;
+        if constexpr (GRP > 1)
+        {
+            m = i == lane ? mf : gml[0][i];               // this lane's own entries
+            l = i == lane ? lf : gml[1][i];
+        }
+        else item(i, m, l);
         const float w = m == -__builtin_huge_valf() ? 0.0f : expf_ref(__fsub_rn(m, mx));
-        wsh[c] = w;
+        wsh[i] = w;
         den = __fmaf_rn(w, l, den);
     }
     den = wave_sum64(den);
@@ -754,19 +917,33 @@ __global__ __launch_bounds__(64) void k_attn_combine(AttnParams p)
     float num[DPL];
 #pragma unroll
     for (int i = 0; i < DPL; ++i) num[i] = 0.0f;
+    // item s's output, channel i, from its partials' outputs x(c, i)
+    auto item_acc = [&](uint32_t s, int i, auto&& x) {
+        float a = x(s * GRP, i);
+        if constexpr (GRP > 1)
 #pragma unroll
-    for (uint32_t c = 0; c < CB; ++c)
+            for (uint32_t k = 1; k < GRP; ++k)
+            {
+                const uint32_t c = s * GRP + k;
+                const float an = merge_val(gsc[0][c], a, gsc[1][c], x(c, i));
+                a = c <= lastp ? an : a;
+            }
+        return a;
+    };
+    auto pre = [&](uint32_t c, int i) { return v[c][i]; };
+#pragma unroll
+    for (uint32_t s = 0; s < CB / GRP; ++s)
     {
-        const bool in = c <= last;                  // past the last chunk: skipped, not added as zero
-        const float w = wsh[in ? c : 0u];
+        const bool in = s <= lasti;                  // past the last item: skipped, not added as zero
+        const float w = wsh[in ? s : 0u];
 #pragma unroll
-        for (int i = 0; i < DPL; ++i) num[i] = in ? __fmaf_rn(w, v[c][i], num[i]) : num[i];
+        for (int i = 0; i < DPL; ++i) num[i] = in ? __fmaf_rn(w, item_acc(s, i, pre), num[i]) : num[i];
     }
-    for (uint32_t c = CB; c <= last; ++c)
+    for (uint32_t s = CB / GRP; s <= lasti; ++s)
     {
-        const float w = wsh[c];
+        const float w = wsh[s];
 #pragma unroll
-        for (int i = 0; i < DPL; ++i) num[i] = __fmaf_rn(w, acc_at(c, i), num[i]);
+        for (int i = 0; i < DPL; ++i) num[i] = __fmaf_rn(w, item_acc(s, i, acc_at), num[i]);
     }
 #pragma unroll
     for (int i = 0; i < DPL; ++i)
@@ -902,6 +1079,12 @@ int attn_launch(opure_dev* dev, const opure_model* m, const opure_kv* kv, uint32
     const dim3 grid(p.n_kv, p.nch, batch);
     const uint32_t hd = p.hd;
     p.zt = 1u;
+    p.npart = p.nch;
+    p.cpp = 1u;
+    // head_dim 64 on matrix cores: the combine merges groups of ATTN_GROUP
+    // chunks as the folded kernel does (1 item = 1 group), unless the folded
+    // kernel wrote the groups' partials itself
+    uint32_t grp = use_mfma(hd, p.afmt, Gq) && hd == 64u ? ATTN_GROUP : 1u;
     if (use_mfma(hd, p.afmt, Gq))
     {
         // head_dim 64 on a grid of few workgroups (the 1B shape at batch 1:
@@ -926,10 +1109,18 @@ int attn_launch(opure_dev* dev, const opure_model* m, const opure_kv* kv, uint32
         else
         {
             // a grid of many workgroups (a batch of ragged sequences) folded to
-            // two chunks a workgroup: a chunk past a sequence's end costs a
-            // workgroup a round trip, and half as many of them are launched
+            // ATTN_GROUP chunks a workgroup, merged into one partial: a quarter
+            // of the partials written and read, a chunk's page-table entries
+            // loaded while the chunk before computes, a chunk past a
+            // sequence's end costs no round trip of its own
             const bool fold = hd == 64u && static_cast<uint64_t>(p.n_kv) * p.nch * batch > 8ull * n_cu;
-            const dim3 fgrid(p.n_kv, (p.nch + 1u) / 2u, batch);
+            const dim3 fgrid(p.n_kv, (p.nch + ATTN_GROUP - 1u) / ATTN_GROUP, batch);
+            if (fold)
+            {
+                p.npart = fgrid.y;
+                p.cpp = ATTN_GROUP;
+                grp = 1u;
+            }
             for (uint32_t q0 = 0; q0 < Gq; q0 += 32u)
             {
                 AttnParams pq = p;
@@ -982,13 +1173,15 @@ int attn_launch(opure_dev* dev, const opure_model* m, const opure_kv* kv, uint32
         OPURE_LAUNCH_CHECK("k_attn_chunk_generic");
     }
     const dim3 cgrid(p.n_heads, batch * rows);
-    switch ((p.hd + 63u) / 64u)
-    {
-    case 1: OPURE_LAUNCH(dev, k_attn_combine<1>, cgrid, dim3(64), 0, p); break;
-    case 2: OPURE_LAUNCH(dev, k_attn_combine<2>, cgrid, dim3(64), 0, p); break;
-    case 3: OPURE_LAUNCH(dev, k_attn_combine<3>, cgrid, dim3(64), 0, p); break;
-    default: OPURE_LAUNCH(dev, k_attn_combine<4>, cgrid, dim3(64), 0, p); break;
-    }
+    if (grp > 1u) OPURE_LAUNCH(dev, (k_attn_combine<1, ATTN_GROUP>), cgrid, dim3(64), 0, p);
+    else
+        switch ((p.hd + 63u) / 64u)
+        {
+        case 1: OPURE_LAUNCH(dev, (k_attn_combine<1, 1>), cgrid, dim3(64), 0, p); break;
+        case 2: OPURE_LAUNCH(dev, (k_attn_combine<2, 1>), cgrid, dim3(64), 0, p); break;
+        case 3: OPURE_LAUNCH(dev, (k_attn_combine<3, 1>), cgrid, dim3(64), 0, p); break;
+        default: OPURE_LAUNCH(dev, (k_attn_combine<4, 1>), cgrid, dim3(64), 0, p); break;
+        }
     OPURE_LAUNCH_CHECK("k_attn_combine");
     return OPURE_OK;
 }

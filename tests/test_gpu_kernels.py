@@ -490,6 +490,8 @@ ATTN_CASES = [
     (H.A_F32, 64, 5, [131, 37]),
     (H.A_F16, 64, 5, [131, 37]),
     (H.A_BF16, 64, 5, [131, 37]),
+    (H.A_F16, 64, 6, [2100, 700]),           # 17 and 6 chunks: groups of 4 merged by the combine
+    (H.A_BF16, 64, 6, [2100, 700]),
     (H.A_F16, 128, 8, [1100, 531]),
     (H.A_BF16, 128, 8, [1100, 531]),
 ]
@@ -629,6 +631,59 @@ def test_attention_folded_grid_same_bits(dev):
     for b in (0, 5, 11, 15):
         one = run_attn(dev, m, kv.pool, kv.page_table[b:b + 1], [ctx[b]], R, q_bits[b * R:(b + 1) * R])
         assert np.array_equal(one, got[b * R:(b + 1) * R]), b
+
+
+# contexts whose rows end on either side of a 128-token chunk and a 512-token
+# group boundary (rows 0..2 of a sequence see different numbers of a group's chunks)
+FOLD_EDGES = [126, 127, 128, 510, 511, 512, 1021, 1022, 1023, 2045, 2046, 2047, 4094, 4095, 8189, 8190]
+
+
+@pytest.mark.parametrize("afmt,case", [(H.A_F16, "edges"), (H.A_BF16, "edges"), (H.A_BF16, "random")])
+def test_attention_folded_groups_same_bits(dev, afmt, case):
+    """The folded launch (head_dim 64, a grid of many sequences) merges each
+    group of 4 chunks (512 tokens) inside its workgroup and writes one partial
+    a group; a launch of one sequence writes one partial a chunk and its
+    combine merges the same groups.  Every sequence gets the same bits either
+    way, also where a row's last chunk is inside a group or the first of one,
+    and the rows stay within one storage ulp of the oracle."""
+    say("attention folded groups", afmt, case)
+    rng = np.random.default_rng(7 + afmt)
+    nh, nkv, hd, R, ps = 8, 2, 64, 3, 16
+    ctx = FOLD_EDGES if case == "edges" else [int(c) for c in rng.integers(100, 9000, size=16)]
+    B = len(ctx)
+    assert nkv * -(-(max(ctx) + R) // 128) * B > 8 * 256        # the launch folds
+    mp = [(c + R + ps - 1) // ps for c in ctx]
+    n_pages = sum(mp) + 4
+    hm = O.HostModel(n_layers=1, hidden=64, n_heads=nh, n_kv_heads=nkv, head_dim=hd, ffn=64, vocab=64,
+                     wfmt=O.W_F32, afmt=afmt, attn_scale=hd ** -0.5, max_pos=max(ctx) + 64, seed=1)
+    kv = O.HostKV(hm, n_pages=n_pages, batch=B, max_pages_per_seq=max(mp))
+    kv.fill_random(rng, 1.0)
+    perm = rng.permutation(n_pages)
+    o = 0
+    for b in range(B):
+        kv.page_table[b, :mp[b]] = perm[o:o + mp[b]]
+        o += mp[b]
+    q_bits, q_f = to_act(rng.standard_normal((B * R, nh * hd)) * 1.5, afmt)
+    m = attn_model(nh, nkv, hd, afmt, hd ** -0.5)
+    got = run_attn(dev, m, kv.pool, kv.page_table, ctx, R, q_bits)
+    for b in range(B):
+        one = run_attn(dev, m, kv.pool, kv.page_table[b:b + 1], [ctx[b]], R, q_bits[b * R:(b + 1) * R])
+        assert np.array_equal(one, got[b * R:(b + 1) * R]), (b, ctx[b])
+    kv._mk()
+    O.set_threads(16)
+    try:
+        got_f = from_act(got, afmt)
+        ulp = 2.0 ** -10 if afmt == H.A_F16 else 2.0 ** -7
+        for b in (0, 5, 10, 15):
+            qb = np.ascontiguousarray(q_f[b * R:(b + 1) * R])
+            ob = np.zeros_like(qb)
+            O.lib().orc_attention_paged(C.byref(hm.desc), C.byref(kv.desc), 0, b, ctx[b], R, qb.ctypes.data,
+                                        ob.ctypes.data)
+            want_r = to_act(ob, afmt)[1]
+            gb = got_f[b * R:(b + 1) * R]
+            assert (np.abs(gb - want_r) <= ulp * np.abs(want_r) + 1e-6).all(), (b, ctx[b])
+    finally:
+        O.set_threads(1)
 
 
 def test_attention_folded_grid_missing_page(dev):
