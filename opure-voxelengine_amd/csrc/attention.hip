@@ -803,11 +803,13 @@ __global__ __launch_bounds__(NWV * 64) __attribute__((amdgpu_waves_per_eu(CL ? 4
 // denominator with a fixed butterfly), then channels d = lane + 64 i
 // (i < DPL), summing the items' outputs in order.  The first CB partials'
 // outputs are loaded together with the statistics, so a context of up to CB
-// partials costs one round trip.
-template <int DPL, int GRP>
+// partials costs one round trip (CB 20 where a launch has at most 20
+// partials: fewer loads of the clamped last one).
+template <int DPL, int GRP, uint32_t CB = 32u>
 __global__ __launch_bounds__(64) void k_attn_combine(AttnParams p)
 {
-    constexpr uint32_t CB = 32, NI = 1024u / GRP, NS = GRP > 1 ? 1024u : 1u, NG = GRP > 1 ? NI : 1u;
+    static_assert(CB % GRP == 0, "whole groups preloaded");
+    constexpr uint32_t NI = 1024u / GRP, NS = GRP > 1 ? 1024u : 1u, NG = GRP > 1 ? NI : 1u;
     __shared__ float wsh[NI];                              // the items' weights
     __shared__ float gsc[2][NS];                           // GRP > 1: each chunk's merge scales (state, chunk)
     __shared__ float gml[2][NG];                           // GRP > 1: each group's (max, sum)
@@ -1173,11 +1175,16 @@ int attn_launch(opure_dev* dev, const opure_model* m, const opure_kv* kv, uint32
         OPURE_LAUNCH_CHECK("k_attn_chunk_generic");
     }
     const dim3 cgrid(p.n_heads, batch * rows);
-    if (grp > 1u) OPURE_LAUNCH(dev, (k_attn_combine<1, ATTN_GROUP>), cgrid, dim3(64), 0, p);
+    const bool few = p.npart <= 20u;
+    if (grp > 1u && few) OPURE_LAUNCH(dev, (k_attn_combine<1, ATTN_GROUP, 20u>), cgrid, dim3(64), 0, p);
+    else if (grp > 1u) OPURE_LAUNCH(dev, (k_attn_combine<1, ATTN_GROUP>), cgrid, dim3(64), 0, p);
     else
         switch ((p.hd + 63u) / 64u)
         {
-        case 1: OPURE_LAUNCH(dev, (k_attn_combine<1, 1>), cgrid, dim3(64), 0, p); break;
+        case 1:
+            if (few) OPURE_LAUNCH(dev, (k_attn_combine<1, 1, 20u>), cgrid, dim3(64), 0, p);
+            else OPURE_LAUNCH(dev, (k_attn_combine<1, 1>), cgrid, dim3(64), 0, p);
+            break;
         case 2: OPURE_LAUNCH(dev, (k_attn_combine<2, 1>), cgrid, dim3(64), 0, p); break;
         case 3: OPURE_LAUNCH(dev, (k_attn_combine<3, 1>), cgrid, dim3(64), 0, p); break;
         default: OPURE_LAUNCH(dev, (k_attn_combine<4, 1>), cgrid, dim3(64), 0, p); break;
