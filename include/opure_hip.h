@@ -415,8 +415,9 @@ int opure_profile_read(opure_dev* dev, uint32_t counts[OPURE_STAGE_COUNT], doubl
  *      [hidden/16][rows], feeding the fused RMSNorm), q (afmt), att (afmt),
  *      h (afmt). */
 int opure_debug_workspace(opure_dev* dev, void** ptr, uint64_t* bytes);
-/* Sleeps a bounded wait between the waves of a workgroup takes before it gives
- * up (default 4M).  A test hook: 0 makes any wait that is not already met give
+/* Sleeps a bounded wait takes before it gives up (default 4M): between the
+ * waves of a GEMV workgroup, or between the slices of a sequence in the
+ * one-launch rejection step.  A test hook: 0 makes any wait that is not already met give
  * up at once, so the failure report can be checked while every wave still
  * runs to its end. */
 int opure_debug_set_wait_limit(opure_dev* dev, uint32_t sleeps);
@@ -427,6 +428,12 @@ int opure_debug_set_wait_limit(opure_dev* dev, uint32_t sleeps);
  * the engine comparison.  The verify step always uses the matrix cores. */
 enum { OPURE_GEMV_MFMA = 0, OPURE_GEMV_VALU = 1 };
 int opure_debug_set_gemv_engine(opure_dev* dev, uint32_t engine);
+/* Launches of opure_accept_rejection (and of the rejection step inside
+ * opure_verify_step): one launch whose slices of a sequence wait for each
+ * other (default), or the separate row-statistics, slice and draw launches,
+ * kept for comparison.  Both give the same bits. */
+enum { OPURE_REJ_ONE_LAUNCH = 0, OPURE_REJ_STAGED = 1 };
+int opure_debug_set_rejection_launches(opure_dev* dev, uint32_t mode);
 /* Evaluates the SwiGLU epilogue's branch-free exponential and the oracle-order
  * exponential the other kernels use on every one of the 2^32 fp32 bit
  * patterns and counts the results that differ (bit for bit; 0 expected). */

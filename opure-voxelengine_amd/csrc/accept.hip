@@ -443,6 +443,13 @@ struct RejectParams {
     float* wbuf;              // [B][V] draw weights of row n
     const int32_t* seq_len;   // optional new_seq_len = seq_len + n + 1
     int32_t* new_seq_len;
+    // the one-launch sampler (k_rej_fused): the sequences' launch counts and
+    // their slices' published values [REJ_SYNC_SEQS][REJ_MAX_SLICES][6], the
+    // bound on a wait (sleeps) and the error word it sets past it
+    uint32_t* epoch;
+    uint64_t* slots;
+    uint32_t wait_limit;
+    uint32_t* err;
 };
 
 template <uint32_t NTH>
@@ -941,6 +948,308 @@ __global__ __launch_bounds__(NT) void k_rej_draw(RejectParams p)
     }
 }
 
+// ---- the whole rejection step in one launch ---------------------------------
+// Grid (slices, B), NT threads.  Workgroup (sl, b) holds slice sl (elements
+// v0 + i NT + t) of the rows sequence b needs, in registers: target row j and
+// draft row K + 1 + j for j = 0, 1, ... up to the first rejected draft n, or
+// the bonus row K after K accepts; then it forms the slice's draw weights
+// (the residual of row n, or p_K) and draws.  The slices of a sequence hand
+// each other their slice maxima, slice sums and draw-weight sums through
+// per-sequence slots in device memory: each value is published with one
+// 64-bit store at the coherence point that carries a tag (the sequence's
+// launch count and the round), and a slice waits for a round by polling the
+// sequence's slots, one lane a slice, until every tag matches -- the values
+// arrive with the wait.  A wait is bounded: past the device's wait limit
+// ERR_WAIT is set and the launch's outputs are invalid.  Workgroups are
+// dispatched in order, each die in order, so a sequence's slices are resident
+// or finished before any slice of a later sequence starts: a wait never
+// depends on a workgroup that cannot run.  Every value comes from the
+// operations of k_rej_rowstat, k_rej_slice and k_rej_draw, and a maximum or an
+// integer sum does not depend on how its terms are shared out, so the bits are
+// theirs.
+enum { SLOT_MT = 0, SLOT_MQ = 1, SLOT_ST = 2, SLOT_SQ = 3, SLOT_PR = 4, SLOT_PP = 5, SLOT_N = 6 };
+
+// a slot word: a maximum as (tag << 32) | float bits, a sum (a slice's sum of
+// at most SLICE fixed-point terms < 2^44) as (tag << 48) | sum
+__device__ __forceinline__ uint64_t slot_f32(uint32_t tag, float v) { return (static_cast<uint64_t>(tag) << 32) | __float_as_uint(v); }
+__device__ __forceinline__ uint64_t slot_u64(uint32_t tag, uint64_t v) { return (static_cast<uint64_t>(tag) << 48) | v; }
+__device__ __forceinline__ void slot_put(uint64_t* a, uint64_t v)
+{
+    __hip_atomic_store(a, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Wave 0: waits until every slice of the sequence has published slots ka and
+// kb with `tag` (in bits `shift` up), and leaves slice `lane`'s two words in
+// wa, wb (lanes >= slices: 0)
+__device__ void rej_gather(const RejectParams& p, const uint64_t* seq_slots, uint32_t ka, uint32_t kb, uint32_t tag,
+                           uint32_t shift, uint64_t& wa, uint64_t& wb)
+{
+    const uint32_t lane = threadIdx.x;
+    const bool mine = lane < p.slices;
+    wa = wb = 0;
+    for (uint32_t n = 0;; ++n)
+    {
+        bool ok = true;
+        if (mine)
+        {
+            wa = __hip_atomic_load(const_cast<uint64_t*>(seq_slots) + lane * SLOT_N + ka, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            wb = __hip_atomic_load(const_cast<uint64_t*>(seq_slots) + lane * SLOT_N + kb, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            ok = (wa >> shift) == tag && (wb >> shift) == tag;
+        }
+        if (__all(ok)) break;
+        if (n >= p.wait_limit)
+        {
+            if (lane == 0u) p.err[ERR_WAIT] = 1u;
+            break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+}
+
+// block max / exact u64 sum of two values a thread, one barrier pair
+__device__ __forceinline__ void block_max2(float& a, float& c, float (*red)[2])
+{
+    a = wave_max64(a);
+    c = wave_max64(c);
+    __syncthreads();
+    if ((threadIdx.x & 63u) == 0u)
+    {
+        red[threadIdx.x >> 6][0] = a;
+        red[threadIdx.x >> 6][1] = c;
+    }
+    __syncthreads();
+    a = red[0][0];
+    c = red[0][1];
+#pragma unroll
+    for (uint32_t w = 1; w < NT / 64u; ++w)
+    {
+        a = fmaxf(a, red[w][0]);
+        c = fmaxf(c, red[w][1]);
+    }
+}
+__device__ __forceinline__ void block_sum2_u64(uint64_t& a, uint64_t& c, uint64_t (*red)[2])
+{
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1)
+    {
+        a += shfl_xor_u64(a, o);
+        c += shfl_xor_u64(c, o);
+    }
+    __syncthreads();
+    if ((threadIdx.x & 63u) == 0u)
+    {
+        red[threadIdx.x >> 6][0] = a;
+        red[threadIdx.x >> 6][1] = c;
+    }
+    __syncthreads();
+    a = 0;
+    c = 0;
+#pragma unroll
+    for (uint32_t w = 0; w < NT / 64u; ++w)
+    {
+        a += red[w][0];
+        c += red[w][1];
+    }
+}
+
+__device__ __forceinline__ uint64_t wave_sum_u64(uint64_t v)
+{
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += shfl_xor_u64(v, o);
+    return v;
+}
+
+template <bool DIV>
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_rej_fused(RejectParams p)
+{
+    __shared__ float fred2[NT / 64][2];
+    __shared__ uint64_t ured2[NT / 64][2];
+    __shared__ uint64_t wsum[NT / 64];
+    __shared__ int32_t s_tok;
+    __shared__ uint32_t s_epoch;
+    __shared__ float bmax[2];
+    __shared__ uint64_t bsum[2], bpart[4];
+    __shared__ __align__(16) float stage[SLICE];
+    const uint32_t sl = blockIdx.x, b = blockIdx.y, K = p.K, V = p.V, S = p.slices, t = threadIdx.x;
+    const float tau = p.tau;
+    const uint32_t pb = p.pos_base ? p.pos_base[b] : 0u;
+    const uint32_t v0 = sl * SLICE, v1 = min(V, v0 + SLICE);
+    uint64_t* seq_slots = p.slots + static_cast<uint64_t>(b) * REJ_MAX_SLICES * SLOT_N;
+    uint64_t* my_slots = seq_slots + sl * SLOT_N;
+    if (t == 0u) s_epoch = __hip_atomic_load(p.epoch + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    auto inside = [&](uint32_t i) { return v0 + i * NT + t < V; };
+    auto load = [&](const float* row, float (&x)[PER]) {
+#pragma unroll
+        for (uint32_t i = 0; i < PER; ++i) x[i] = row[min(v0 + i * NT + t, V - 1u)];
+    };
+    uint32_t round = 0, j = 0;
+    float tl[PER], ql[PER];
+    RowStat P{}, Q{};
+    __syncthreads();
+    const uint32_t ep = (s_epoch & 0xFFu) << 8;           // a round's tag: (launch count mod 256, round)
+    for (;; ++j)
+    {
+        // ---- statistics of target row j and draft row K + 1 + j --------------
+        const bool hq = j < K;
+        const float* tr = rej_row(p, b, j);
+        const float* qr = hq ? rej_row(p, b, K + 1u + j) : tr;
+        load(tr, tl);
+        if (hq) load(qr, ql);
+        const int32_t x = hq ? p.drafts[static_cast<uint64_t>(b) * p.drafts_stride + j] : -1;
+        const bool xv = x >= 0 && static_cast<uint32_t>(x) < V;
+        const float xt = xv ? tr[x] : 0.0f, xq = xv ? qr[x] : 0.0f;
+        float mt = -__builtin_huge_valf(), mq = -__builtin_huge_valf();
+#pragma unroll
+        for (uint32_t i = 0; i < PER; ++i)
+            if (inside(i))
+            {
+                mt = fmaxf(mt, scaled_logit<DIV>(tl[i], tau));
+                if (hq) mq = fmaxf(mq, scaled_logit<DIV>(ql[i], tau));
+            }
+        block_max2(mt, mq, fred2);
+        const uint32_t tag_m = ep | ++round;
+        if (t == 0u)
+        {
+            slot_put(my_slots + SLOT_MT, slot_f32(tag_m, mt));
+            slot_put(my_slots + SLOT_MQ, slot_f32(tag_m, mq));
+        }
+        if (t < 64u)
+        {
+            uint64_t wa, wb;
+            rej_gather(p, seq_slots, SLOT_MT, SLOT_MQ, tag_m, 32u, wa, wb);
+            const float a = wave_max64(t < S ? __uint_as_float(static_cast<uint32_t>(wa)) : -__builtin_huge_valf());
+            const float c = wave_max64(t < S ? __uint_as_float(static_cast<uint32_t>(wb)) : -__builtin_huge_valf());
+            if (t == 0u)
+            {
+                bmax[0] = a;
+                bmax[1] = c;
+            }
+        }
+        __syncthreads();
+        const float Mt = bmax[0], Mq = bmax[1];
+        double st = 0.0, sq = 0.0;
+#pragma unroll
+        for (uint32_t i = 0; i < PER; ++i)
+            if (inside(i))
+            {
+                st += fixed_d(expf_ref_nonpos(__fsub_rn(scaled_logit<DIV>(tl[i], tau), Mt)));
+                if (hq) sq += fixed_d(expf_ref_nonpos(__fsub_rn(scaled_logit<DIV>(ql[i], tau), Mq)));
+            }
+        uint64_t St = fixed_sum_u64(st), Sq = fixed_sum_u64(sq);
+        block_sum2_u64(St, Sq, ured2);
+        const uint32_t tag_s = ep | ++round;
+        if (t == 0u)
+        {
+            slot_put(my_slots + SLOT_ST, slot_u64(tag_s, St));
+            slot_put(my_slots + SLOT_SQ, slot_u64(tag_s, Sq));
+        }
+        if (t < 64u)
+        {
+            uint64_t wa, wb;
+            rej_gather(p, seq_slots, SLOT_ST, SLOT_SQ, tag_s, 48u, wa, wb);
+            const uint64_t lo48 = (1ull << 48) - 1ull;
+            const uint64_t a = wave_sum_u64(t < S ? wa & lo48 : 0ull), c = wave_sum_u64(t < S ? wb & lo48 : 0ull);
+            if (t == 0u)
+            {
+                bsum[0] = a;
+                bsum[1] = c;
+            }
+        }
+        __syncthreads();
+        P = RowStat{Mt, xv ? expf_ref(__fsub_rn(scaled_logit<DIV>(xt, tau), Mt)) : 0.0f, bsum[0]};
+        if (!hq) break;                                   // all K accepted: the bonus row's statistics
+        Q = RowStat{Mq, xv ? expf_ref(__fsub_rn(scaled_logit<DIV>(xq, tau), Mq)) : 0.0f, bsum[1]};
+        if (!rej_accepts(p, b, pb, j, x, P, Q)) break;
+    }
+    const uint32_t n = j;
+
+    // ---- the slice's draw weights: the residual of row n, or p_K ---------------
+    // (straight into LDS, where the draw below takes each thread's contiguous run)
+    const double invP = __ddiv_rn(4294967296.0, static_cast<double>(P.S));
+    double rs = 0.0, ps = 0.0;
+    if (n < K)
+    {
+        const double invQ = __ddiv_rn(4294967296.0, static_cast<double>(Q.S));
+#pragma unroll
+        for (uint32_t i = 0; i < PER; ++i)
+        {
+            const float ep = inside(i) ? expf_ref_nonpos(__fsub_rn(scaled_logit<DIV>(tl[i], tau), P.m)) : 0.0f;
+            const float eq = inside(i) ? expf_ref_nonpos(__fsub_rn(scaled_logit<DIV>(ql[i], tau), Q.m)) : 0.0f;
+            const float pf = static_cast<float>(__dmul_rn(static_cast<double>(ep), invP));
+            const float qf = static_cast<float>(__dmul_rn(static_cast<double>(eq), invQ));
+            const float d = __fsub_rn(pf, qf);
+            const float wi = inside(i) && d > 0.0f ? d : 0.0f;
+            stage[i * NT + t] = wi;
+            rs += fixed_d(wi);
+            ps += fixed_d(ep);
+        }
+    }
+    else
+    {
+#pragma unroll
+        for (uint32_t i = 0; i < PER; ++i)
+        {
+            const float ep = inside(i) ? expf_ref_nonpos(__fsub_rn(scaled_logit<DIV>(tl[i], tau), P.m)) : 0.0f;
+            stage[i * NT + t] = ep;
+            ps += fixed_d(ep);
+        }
+    }
+    uint64_t Rs = fixed_sum_u64(rs), Ps = fixed_sum_u64(ps);
+    block_sum2_u64(Rs, Ps, ured2);
+    const uint32_t tag_p = ep | ++round;
+    if (t == 0u)
+    {
+        slot_put(my_slots + SLOT_PR, slot_u64(tag_p, Rs));
+        slot_put(my_slots + SLOT_PP, slot_u64(tag_p, Ps));
+    }
+    if (t < 64u)
+    {
+        uint64_t wa, wb;
+        rej_gather(p, seq_slots, SLOT_PR, SLOT_PP, tag_p, 48u, wa, wb);
+        const uint64_t lo48 = (1ull << 48) - 1ull, ra = t < S ? wa & lo48 : 0ull, pa = t < S ? wb & lo48 : 0ull;
+        const uint64_t r_all = wave_sum_u64(ra), p_all = wave_sum_u64(pa);
+        const uint64_t r_x = wave_sum_u64(t < sl ? ra : 0ull), p_x = wave_sum_u64(t < sl ? pa : 0ull);
+        if (t == 0u)
+        {
+            bpart[0] = r_all;
+            bpart[1] = p_all;
+            bpart[2] = r_x;
+            bpart[3] = p_x;
+        }
+    }
+    __syncthreads();
+    const uint64_t Rt = bpart[0], Pt = bpart[1], Rx = bpart[2], Px = bpart[3];
+    // every slice has read this launch's count: slice 0 moves it on for the next
+    if (sl == 0u && t == 0u) __hip_atomic_store(p.epoch + b, s_epoch + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+
+    // ---- the draw -----------------------------------------------------------------
+    const uint32_t U = philox_u32(p.seed, pb + n, b, 2u);
+    auto threshold = [&](uint64_t total) {
+        const uint64_t hi = __umul64hi(static_cast<uint64_t>(U), total);
+        const uint64_t lo = static_cast<uint64_t>(U) * total;
+        return (hi << 32) | (lo >> 32);
+    };
+    const bool from_p = n < K && Rt == 0;                 // the residual has no mass: draw from p_n
+    if (from_p)
+#pragma unroll
+        for (uint32_t i = 0; i < PER; ++i)
+            stage[i * NT + t] = inside(i) ? expf_ref_nonpos(__fsub_rn(scaled_logit<DIV>(tl[i], tau), P.m)) : 0.0f;
+    // each thread's contiguous run of the slice, as rej_draw_slice walks it
+    __syncthreads();
+    float wl[PER];
+#pragma unroll
+    for (uint32_t i = 0; i < PER; ++i) wl[i] = stage[PER * t + i];
+    __syncthreads();
+    if (from_p) rej_draw_slice(p, b, n, v0, v1, Pt, Px, Ps, threshold(Pt), wl, wsum, &s_tok, stage);
+    else
+    {
+        const bool resid = n < K;
+        const uint64_t total = resid ? Rt : Pt;
+        rej_draw_slice(p, b, n, v0, v1, total, resid ? Rx : Px, resid ? Rs : Ps, threshold(total), wl, wsum, &s_tok,
+                       stage);
+    }
+}
+
 // ---------------------------------------------------------------------------
 struct SampleParams {
     const float* logits;
@@ -1118,11 +1427,23 @@ int accept_rejection_launch(opure_dev* dev, const opure_accept_args* a, void* ws
     r.ssum = reinterpret_cast<uint64_t*>(w);
     w += align_up(nrow * r.slices * 8u, 256);
     r.sex = reinterpret_cast<float*>(w);
+    r.epoch = static_cast<uint32_t*>(dev->rej_sync);
+    r.slots = reinterpret_cast<uint64_t*>(static_cast<char*>(dev->rej_sync) + REJ_SYNC_SEQS * sizeof(uint32_t));
+    r.wait_limit = dev->wait_limit;
+    r.err = dev->err;
     r.seq_len = seq_len;
     r.new_seq_len = new_seq_len;
+    const dim3 slices(r.slices, B);
+    if (dev->rej_sync && dev->err && B <= REJ_SYNC_SEQS && dev->rej_mode == OPURE_REJ_ONE_LAUNCH)
+    {
+        // one launch: every slice of every sequence (see k_rej_fused)
+        if (r.tau != 1.0f) OPURE_LAUNCH(dev, k_rej_fused<true>, slices, dim3(NT), 0, r);
+        else OPURE_LAUNCH(dev, k_rej_fused<false>, slices, dim3(NT), 0, r);
+        OPURE_LAUNCH_CHECK("k_rej_fused");
+        return OPURE_OK;
+    }
     const bool aligned = ((reinterpret_cast<uintptr_t>(a->target_logits) | reinterpret_cast<uintptr_t>(a->draft_logits)) & 15u) == 0;
     const bool reg = V % 4u == 0 && V <= 4u * RNT * RVEC && aligned, div = r.tau != 1.0f;
-    const dim3 slices(r.slices, B);
     // Position 0's two rows first, then the other rows only for sequences
     // whose first draft was accepted.  Rows held in registers take one
     // workgroup each; longer rows (the 128k vocabulary) are spread over their

@@ -15,6 +15,9 @@
 // ---------------------------------------------------------------------------
 //  Host side: device object, errors, workspace
 // ---------------------------------------------------------------------------
+constexpr uint32_t REJ_SYNC_SEQS = 4096;
+constexpr uint64_t REJ_SYNC_BYTES = REJ_SYNC_SEQS * 4ull + REJ_SYNC_SEQS * 64ull * 6ull * 8ull;
+
 struct opure_dev {
     int         ordinal = 0;
     hipStream_t stream = nullptr;
@@ -29,6 +32,11 @@ struct opure_dev {
     uint64_t    ws_bytes = 0;
     // device address of opure_accept_rejection_noalloc's scratch array (looked up once)
     void*       noalloc_scratch = nullptr;
+    // The one-launch rejection sampler's per-sequence state (REJ_SYNC_BYTES,
+    // zeroed once at creation): a launch count a sequence [REJ_SYNC_SEQS] u32,
+    // then the sequences' slots [REJ_SYNC_SEQS][64 slices][6] u64, whose tags
+    // carry the launch count, so no clear is needed between launches.
+    void*       rej_sync = nullptr;
     // Conditions a kernel found that make its outputs invalid, one word each
     // (ERR_* below), in pinned host memory: a kernel sets a word with an
     // ordinary store, the host reads and clears it after the stream is idle
@@ -39,6 +47,8 @@ struct opure_dev {
     uint32_t    wait_limit = 1u << 22;
     // GEMV engine of opure_gemv_batched_i8pc for M <= 8 (opure_debug_set_gemv_engine)
     uint32_t    gemv_engine = OPURE_GEMV_MFMA;
+    // launches of the rejection step (opure_debug_set_rejection_launches)
+    uint32_t    rej_mode = OPURE_REJ_ONE_LAUNCH;
     // captured graphs still alive: a workspace they point into is kept, not
     // freed, when a larger call replaces it
     uint32_t    live_graphs = 0;

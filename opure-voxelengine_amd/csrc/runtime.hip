@@ -72,8 +72,8 @@ int check_device_errors(opure_dev* dev)
     uint32_t w[ERR_WORDS];
     for (uint32_t i = 0; i < ERR_WORDS; ++i) { w[i] = dev->err[i]; dev->err[i] = 0u; }
     if (w[ERR_WAIT])
-        return set_error(OPURE_E_DEVICE, "a bounded wait between waves gave up in a GEMV (after %u sleeps): that "
-                         "launch's outputs are invalid%s%s", dev->wait_limit,
+        return set_error(OPURE_E_DEVICE, "a bounded wait gave up (between a GEMV's waves, or between a rejection "
+                         "step's slices; after %u sleeps): that launch's outputs are invalid%s%s", dev->wait_limit,
                          w[ERR_TOKEN] ? "; a token id was outside the vocabulary" : "",
                          w[ERR_POSITION] ? "; a position reached past max_ctx or the page table" : "");
     if (w[ERR_TOKEN])
@@ -152,8 +152,12 @@ int opure_dev_create(int ordinal, opure_dev** out)
     if (e == hipSuccess) e = hipEventCreate(&d->ev_end);
     if (e == hipSuccess) e = hipHostMalloc(reinterpret_cast<void**>(&d->err), ERR_WORDS * sizeof(uint32_t),
                                            hipHostMallocCoherent);
+    if (e == hipSuccess) e = hipMalloc(&d->rej_sync, REJ_SYNC_BYTES);
+    if (e == hipSuccess) e = hipMemsetAsync(d->rej_sync, 0, REJ_SYNC_BYTES, d->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(d->stream);
     if (e != hipSuccess)
     {
+        if (d->rej_sync) hipFree(d->rej_sync);
         if (d->err) hipHostFree(d->err);
         if (d->ev_end) hipEventDestroy(d->ev_end);
         if (d->ev_begin) hipEventDestroy(d->ev_begin);
@@ -174,6 +178,7 @@ int opure_dev_destroy(opure_dev* dev)
     if (dev->ws) hipFree(dev->ws);
     for (void* p : dev->retired_ws) hipFree(p);
     if (dev->err) hipHostFree(dev->err);
+    if (dev->rej_sync) hipFree(dev->rej_sync);
     for (hipEvent_t e : dev->prof_ev) hipEventDestroy(e);
     if (dev->ev_begin) hipEventDestroy(dev->ev_begin);
     if (dev->ev_end) hipEventDestroy(dev->ev_end);
@@ -338,6 +343,15 @@ int opure_debug_set_gemv_engine(opure_dev* dev, uint32_t engine)
     OPURE_REQUIRE(engine == OPURE_GEMV_MFMA || engine == OPURE_GEMV_VALU, OPURE_E_INVALID,
                   "opure_debug_set_gemv_engine: engine %u", engine);
     dev->gemv_engine = engine;
+    return OPURE_OK;
+}
+
+int opure_debug_set_rejection_launches(opure_dev* dev, uint32_t mode)
+{
+    OPURE_REQUIRE(dev, OPURE_E_INVALID, "opure_debug_set_rejection_launches: null device");
+    OPURE_REQUIRE(mode == OPURE_REJ_ONE_LAUNCH || mode == OPURE_REJ_STAGED, OPURE_E_INVALID,
+                  "opure_debug_set_rejection_launches: mode %u", mode);
+    dev->rej_mode = mode;
     return OPURE_OK;
 }
 

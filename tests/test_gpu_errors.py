@@ -107,6 +107,45 @@ def test_gemv_wait_that_gives_up_is_reported(dev):
     assert np.array_equal(dev.download(yb, np.uint16, (M, out // 2)), ref)
 
 
+def test_rejection_wait_gives_up_then_recovers(dev):
+    """The one-launch rejection step's slices wait for each other with the
+    same bounded wait.  At 0 sleeps a slice whose wait is not already met
+    gives up at once: the launch completes and the sync reports it (unless
+    every wait happened to be met).  Either way the sequences' launch counts
+    move on, so the next launches at the default limit never take a value
+    the failed launch published for one of theirs, and match the oracle bit
+    for bit."""
+    rng = np.random.default_rng(9)
+    B, K, V, tau = 16, 4, 30000, 0.8
+    t = (rng.standard_normal((B, K + 1, V)) * 3).astype(np.float32)
+    q = (rng.standard_normal((B, K, V)) * 3).astype(np.float32)
+    q[: B // 2] = t[: B // 2, :K] + (rng.standard_normal((B // 2, K, V)) * 0.05).astype(np.float32)
+    pos = np.repeat(np.arange(K)[None], B, 0).ravel()
+    seq = np.repeat(np.arange(B)[:, None], K, 1).ravel()
+    drafts = O.sample_rows(q.reshape(B * K, V), tau, 5, pos, seq, 0).reshape(B, K)
+    w_out, w_acc, _ = O.accept_rejection(t, q, drafts, tau, 5, None)
+    tb, qb, db = dev.upload(t), dev.upload(q), dev.upload(drafts.astype(np.int32))
+    ot, ac = dev.alloc(B * (K + 1) * 4), dev.alloc(B * 4)
+    a = H.AcceptArgs(B, K, V, int(tb), int(qb), int(db), K, tau, 5, None, int(ot), int(ac), None)
+    L = H.lib()
+    H.check(L.opure_debug_set_wait_limit(dev.h, 0))
+    try:
+        H.check(L.opure_accept_rejection(dev.h, C.byref(a)))
+        code = sync_code(dev)
+        assert code in (H.OK, H.E_DEVICE)
+        if code == H.E_DEVICE:
+            assert b"gave up" in L.opure_last_error()
+    finally:
+        H.check(L.opure_debug_set_wait_limit(dev.h, 1 << 22))
+    for _ in range(2):
+        H.check(L.opure_accept_rejection(dev.h, C.byref(a)))
+        assert sync_code(dev) == H.OK
+        assert np.array_equal(dev.download(ac, np.int32, (B,)), w_acc)
+        assert np.array_equal(dev.download(ot, np.int32, (B, K + 1)), w_out)
+    for buf in (tb, qb, db, ot, ac):
+        buf.free()
+
+
 def test_graph_survives_workspace_growth(dev):
     """A step captured into a graph, then an eager call that needs a larger
     workspace: the graph still replays to the eager result of its own shape."""

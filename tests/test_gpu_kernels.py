@@ -745,6 +745,40 @@ def test_accept_rejection_bit_exact(dev, B, K, V, tau):
     say("mean accepted", acc.mean())
 
 
+REJ_LAUNCH_CASES = [(64, 8, 49152, 1.0), (8, 5, 128256, 0.8), (4, 3, 1000, 0.8), (6, 4, 50001, 0.8), (5, 1, 65539, 1.0)]
+
+
+@pytest.mark.parametrize("B,K,V,tau", REJ_LAUNCH_CASES, ids=["c2", "sliced-128k", "small", "odd-v", "k1-odd-v"])
+def test_accept_rejection_one_launch_same_bits_as_staged(dev, B, K, V, tau):
+    """The one-launch rejection step (the slices of a sequence hand each other
+    their maxima and sums and wait for each other) against the staged
+    launches: ids, accepted lengths and the distribution bit for bit.  Half
+    the sequences draft close to the target, so they accept several drafts
+    and run several positions' statistics in the one launch."""
+    say("rejection one launch vs staged", B, K, V, tau)
+    rng = np.random.default_rng(B * 7 + K + V)
+    t = (rng.standard_normal((B, K + 1, V)) * 3).astype(np.float32)
+    q = (rng.standard_normal((B, K, V)) * 3).astype(np.float32)
+    q[: B // 2] = t[: B // 2, :K] + (rng.standard_normal((B // 2, K, V)) * 0.05).astype(np.float32)
+    pos = np.repeat(np.arange(K)[None], B, 0).ravel()
+    seq = np.repeat(np.arange(B)[:, None], K, 1).ravel()
+    drafts = O.sample_rows(q.reshape(B * K, V), tau, 77, pos, seq, 0).reshape(B, K)
+    pos_base = rng.integers(0, 4096, size=B)
+    L = H.lib()
+    got = {}
+    try:
+        for mode in (H.REJ_STAGED, H.REJ_ONE_LAUNCH):
+            H.check(L.opure_debug_set_rejection_launches(dev.h, mode))
+            got[mode] = run_accept(dev, L.opure_accept_rejection, t, q, drafts, tau, 77, pos_base, True)
+    finally:
+        H.check(L.opure_debug_set_rejection_launches(dev.h, H.REJ_ONE_LAUNCH))
+    (o1, a1, d1), (o2, a2, d2) = got[H.REJ_STAGED], got[H.REJ_ONE_LAUNCH]
+    assert np.array_equal(a1, a2) and np.array_equal(o1, o2)
+    assert np.array_equal(d1.view(np.uint32), d2.view(np.uint32))
+    say("accepted", a2.tolist()[:16])
+    assert a2.max() >= 2 or K < 2                           # some sequence ran several positions
+
+
 def test_sample_rows_and_philox_bit_exact(dev):
     rng = np.random.default_rng(51)
     rows, V = 37, 32000
