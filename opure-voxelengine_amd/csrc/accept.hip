@@ -1069,7 +1069,12 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
     __shared__ uint32_t s_epoch;
     __shared__ float bmax[2];
     __shared__ uint64_t bsum[2], bpart[4];
-    __shared__ __align__(16) float stage[SLICE];
+    // et: the slice's e = exp(x - max) of target row j, then (row n) the draw
+    // weights of p; eq: the same for draft row K + 1 + j, then the residual.
+    // Each thread keeps to its own elements (i NT + t) until the draw.
+    __shared__ __align__(16) float et[SLICE];
+    __shared__ __align__(16) float eq[SLICE];
+    float* stage = et;
     const uint32_t sl = blockIdx.x, b = blockIdx.y, K = p.K, V = p.V, S = p.slices, t = threadIdx.x;
     const float tau = p.tau;
     const uint32_t pb = p.pos_base ? p.pos_base[b] : 0u;
@@ -1130,11 +1135,17 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
         double st = 0.0, sq = 0.0;
 #pragma unroll
         for (uint32_t i = 0; i < PER; ++i)
-            if (inside(i))
+        {
+            const float e = inside(i) ? expf_ref_nonpos(__fsub_rn(scaled_logit<DIV>(tl[i], tau), Mt)) : 0.0f;
+            et[i * NT + t] = e;
+            st += fixed_d(e);
+            if (hq)
             {
-                st += fixed_d(expf_ref_nonpos(__fsub_rn(scaled_logit<DIV>(tl[i], tau), Mt)));
-                if (hq) sq += fixed_d(expf_ref_nonpos(__fsub_rn(scaled_logit<DIV>(ql[i], tau), Mq)));
+                const float f = inside(i) ? expf_ref_nonpos(__fsub_rn(scaled_logit<DIV>(ql[i], tau), Mq)) : 0.0f;
+                eq[i * NT + t] = f;
+                sq += fixed_d(f);
             }
+        }
         uint64_t St = fixed_sum_u64(st), Sq = fixed_sum_u64(sq);
         block_sum2_u64(St, Sq, ured2);
         const uint32_t tag_s = ep | ++round;
@@ -1163,8 +1174,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
     }
     const uint32_t n = j;
 
-    // ---- the slice's draw weights: the residual of row n, or p_K ---------------
-    // (straight into LDS, where the draw below takes each thread's contiguous run)
+    // ---- the slice's draw weights: the residual of row n (into eq), or p_K ----
     const double invP = __ddiv_rn(4294967296.0, static_cast<double>(P.S));
     double rs = 0.0, ps = 0.0;
     if (n < K)
@@ -1173,13 +1183,12 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
 #pragma unroll
         for (uint32_t i = 0; i < PER; ++i)
         {
-            const float ep = inside(i) ? expf_ref_nonpos(__fsub_rn(scaled_logit<DIV>(tl[i], tau), P.m)) : 0.0f;
-            const float eq = inside(i) ? expf_ref_nonpos(__fsub_rn(scaled_logit<DIV>(ql[i], tau), Q.m)) : 0.0f;
+            const float ep = et[i * NT + t];
             const float pf = static_cast<float>(__dmul_rn(static_cast<double>(ep), invP));
-            const float qf = static_cast<float>(__dmul_rn(static_cast<double>(eq), invQ));
+            const float qf = static_cast<float>(__dmul_rn(static_cast<double>(eq[i * NT + t]), invQ));
             const float d = __fsub_rn(pf, qf);
             const float wi = inside(i) && d > 0.0f ? d : 0.0f;
-            stage[i * NT + t] = wi;
+            eq[i * NT + t] = wi;
             rs += fixed_d(wi);
             ps += fixed_d(ep);
         }
@@ -1187,12 +1196,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
     else
     {
 #pragma unroll
-        for (uint32_t i = 0; i < PER; ++i)
-        {
-            const float ep = inside(i) ? expf_ref_nonpos(__fsub_rn(scaled_logit<DIV>(tl[i], tau), P.m)) : 0.0f;
-            stage[i * NT + t] = ep;
-            ps += fixed_d(ep);
-        }
+        for (uint32_t i = 0; i < PER; ++i) ps += fixed_d(et[i * NT + t]);
     }
     uint64_t Rs = fixed_sum_u64(rs), Ps = fixed_sum_u64(ps);
     block_sum2_u64(Rs, Ps, ured2);
@@ -1230,15 +1234,13 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
         return (hi << 32) | (lo >> 32);
     };
     const bool from_p = n < K && Rt == 0;                 // the residual has no mass: draw from p_n
-    if (from_p)
-#pragma unroll
-        for (uint32_t i = 0; i < PER; ++i)
-            stage[i * NT + t] = inside(i) ? expf_ref_nonpos(__fsub_rn(scaled_logit<DIV>(tl[i], tau), P.m)) : 0.0f;
-    // each thread's contiguous run of the slice, as rej_draw_slice walks it
+    // each thread's contiguous run of the slice, as rej_draw_slice walks it:
+    // the residual, or p (p_K after K accepts, p_n when the residual is empty)
+    const float* wsrc = n < K && !from_p ? eq : et;
     __syncthreads();
     float wl[PER];
 #pragma unroll
-    for (uint32_t i = 0; i < PER; ++i) wl[i] = stage[PER * t + i];
+    for (uint32_t i = 0; i < PER; ++i) wl[i] = wsrc[PER * t + i];
     __syncthreads();
     if (from_p) rej_draw_slice(p, b, n, v0, v1, Pt, Px, Ps, threshold(Pt), wl, wsum, &s_tok, stage);
     else
