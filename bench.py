@@ -561,9 +561,9 @@ def bench_c2(args):
                    "mean_accepted": round(float(np.mean(accs)), 4), "wall_ms_per_step": round(wall, 5)},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "opure_accept_rejection (k_rej_rowstat + k_rej_slice + k_rej_draw), whole stage; "
+                     "kernel": "opure_accept_rejection (one launch of k_rej_fused), whole stage; "
                                "bytes = the rows it reads for these inputs (rows past a sequence's first "
-                               "rejection are skipped when draft 0 is rejected) + the distributions written",
+                               "rejected draft are never read) + the distributions written",
                      "bytes_per_launch": read + written, "avg_us": round(ms * 1e3, 2),
                      "measured_peak_GBps": peak["read_GBps"], "frac_of_measured_peak": round(gbs / peak["read_GBps"], 4),
                      "measured_peak": peak},
