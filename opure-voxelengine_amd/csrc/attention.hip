@@ -174,119 +174,499 @@ __global__ __launch_bounds__(256) void k_attn_chunk_generic(AttnParams p)
 // then keeps one K row per lane (lane = token) and one or two V columns per
 // lane (lane = channel) in registers and walks its share of the query rows:
 // scores = K row . q (q broadcast from LDS), a wave-wide softmax over the 64
-// tokens, and out[d] = sum_t p_t V[t][d] with p broadcast from LDS.
-template <int HD, int AF>
-__global__ __launch_bounds__(256) void k_attn_chunk(AttnParams p)
+// tokens, and out[d] = sum_t p_t V[t][d] with p broadcast from LDS.  The
+// sequence length, Q and the page-table entries of the workgroup's chunks load
+// in one round trip.
+// ALL: one workgroup takes every chunk of its (KV head, sequence) in turn (a
+// launch of at most ATTN_ALL_CHUNKS chunks), keeps the chunks' partials in LDS
+// and merges them with k_attn_combine's operations in its order, so the result
+// has the combine's bits and no combine launch follows.
+constexpr uint32_t ATTN_ALL_CHUNKS = 4;
+
+template <int HD>
+constexpr uint32_t attn_all_lds(uint32_t gq)
 {
-    constexpr uint32_t CH = 64, EB = AF == OPURE_A_F32 ? 4u : 2u;
+    return ATTN_ALL_CHUNKS * gq * (HD + 2u) * 4u;
+}
+
+// threads of the fast path's workgroup: head_dim 64 runs 8 waves (a row pair
+// a wave covers 16 query rows at once), 128 runs 4 (its registers)
+template <int HD>
+constexpr uint32_t attn_fast_threads()
+{
+    return HD == 64 ? 512u : 256u;
+}
+
+template <int HD, int AF, bool ALL>
+__global__ __launch_bounds__(attn_fast_threads<HD>()) void k_attn_chunk(AttnParams p)
+{
+    constexpr uint32_t NT = attn_fast_threads<HD>(), NWV = NT / 64u, RB = 2;   // RB: rows a wave scores together
+    constexpr uint32_t CH = 64, EB = AF == OPURE_A_F32 ? 4u : 2u, PPC = CH / OPURE_PAGE_SIZE;
     constexpr uint32_t ROWB = HD * EB + 16u;              // padded LDS row (bank spread)
     constexpr uint32_t DPL = (HD + 63u) / 64u;             // V channels per lane
     constexpr uint32_t VROWB = CH * EB + 16u;              // padded LDS V column (channel-major)
+    constexpr uint32_t NE = ALL ? ATTN_ALL_CHUNKS * PPC : PPC;   // page-table entries staged
     __shared__ __align__(16) uint8_t kt[CH * ROWB];
     __shared__ __align__(16) uint8_t vt[HD * VROWB];
-    __shared__ __align__(16) float pbuf[4][CH];
-    extern __shared__ __align__(16) float qs[];            // [Gq][HD]
+    __shared__ __align__(16) float pbuf[NWV][RB][CH];
+    __shared__ int32_t spg[NE];                            // the chunks' page-table entries (-1 past the table)
+    __shared__ float wsh[NWV][ATTN_ALL_CHUNKS];            // ALL: a row's chunk weights
+    extern __shared__ __align__(16) float qs[];            // [Gq][HD], then (ALL) the chunks' partials
 
-    const uint32_t kh = blockIdx.x, c = blockIdx.y, b = blockIdx.z;
+    const uint32_t kh = blockIdx.x, b = blockIdx.z;
     const uint32_t group = p.n_heads / p.n_kv, R = p.rows, Gq = group * R;
-    const uint32_t ctx = static_cast<uint32_t>(p.seq_len[b]);
-    const uint32_t total = ctx + R;
-    const uint32_t t0 = c * CH;
-    if (t0 >= total) return;
+    const uint32_t c_first = ALL ? 0u : blockIdx.y, c_end = ALL ? p.nch : blockIdx.y + 1u;
     const int32_t* pt = p.page_table + static_cast<uint64_t>(b) * p.max_pages;
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    float* pm = qs + Gq * HD;                              // ALL: [chunk][Gq] maxima
+    float* pl = pm + ATTN_ALL_CHUNKS * Gq;                 //      [chunk][Gq] sums
+    float* pa = pl + ATTN_ALL_CHUNKS * Gq;                 //      [chunk][Gq][HD] outputs
 
-    for (uint32_t e = threadIdx.x; e < Gq * HD; e += 256u)
+    // every load issued before any is waited for: the sequence length, the
+    // page entries, QU of Q's elements a thread (a row j's group of heads is
+    // contiguous in Q), then the stores to LDS
+    const int32_t seq = p.seq_len[b];
+    constexpr uint32_t QU = 8;
+    const uint32_t GH = group * HD;
+    float qv[QU];
+    auto q_load = [&](uint32_t e0) {
+#pragma unroll
+        for (uint32_t u = 0; u < QU; ++u)
+        {
+            const uint32_t e = e0 + threadIdx.x + NT * u, j = e / GH;
+            qv[u] = e < Gq * HD ? load_act_rt(p.q, (static_cast<uint64_t>(b * R + j) * p.n_heads + kh * group) * HD + (e - j * GH), AF)
+                                : 0.0f;
+        }
+    };
+    auto q_store = [&](uint32_t e0) {
+#pragma unroll
+        for (uint32_t u = 0; u < QU; ++u)
+        {
+            const uint32_t e = e0 + threadIdx.x + NT * u;
+            if (e < Gq * HD) qs[e] = qv[u];
+        }
+    };
+    q_load(0u);
+    int32_t pte = -1;
+    if (threadIdx.x < NE && c_first * PPC + threadIdx.x < p.max_pages) pte = pt[c_first * PPC + threadIdx.x];
+    q_store(0u);
+    for (uint32_t e0 = NT * QU; e0 < Gq * HD; e0 += NT * QU)   // more than NT * QU elements: a block at a time
     {
-        const uint32_t qi = e / HD, d = e - qi * HD;
-        const uint32_t j = qi / group, head = kh * group + (qi - j * group);
-        qs[e] = load_act_rt(p.q, (static_cast<uint64_t>(b * R + j) * p.n_heads + head) * HD + d, AF);
+        q_load(e0);
+        q_store(e0);
     }
+    if (threadIdx.x < NE) spg[threadIdx.x] = pte;
+    // keeps the loads above issued before the exit below
+    asm volatile("" ::: "memory");
+    const uint32_t ctx = static_cast<uint32_t>(seq);
+    const uint32_t total = ctx + R;
+    if (c_first * CH >= total) return;                    // no row reaches this chunk
+    __syncthreads();                                      // Q and the page entries staged
     // stage K rows (token-major) and V columns (channel-major, as stored):
     // 16-byte pieces; a page's 16 tokens of this head are contiguous in both planes
     constexpr uint32_t KP = HD * EB / 16u;                 // pieces per K row
     constexpr uint32_t VP = CH * EB / 16u;                 // pieces per V column of the chunk
     constexpr uint32_t TPP = 16u / EB;                     // tokens per V piece
+    constexpr uint32_t NPC = (CH * KP + HD * VP) / NT;     // pieces a thread stages a chunk
+    static_assert((CH * KP) % NT == 0 && (HD * VP) % NT == 0, "K and V pieces split evenly over the threads");
     const uint32_t nan = AF == OPURE_A_F32 ? 0x7FC00000u : (AF == OPURE_A_F16 ? 0x7E007E00u : 0x7FC07FC0u);
-    for (uint32_t e = threadIdx.x; e < CH * KP + HD * VP; e += 256u)
-    {
-        const bool isk = e < CH * KP;
+    u4v buf[NPC];
+    uint32_t tail = 0u;                                    // pieces whose slots past the cache read 0
+    auto piece = [&](uint32_t k, bool& isk, uint32_t& row, uint32_t& pc) {
+        const uint32_t e = threadIdx.x + NT * k;
+        isk = e < CH * KP;
         const uint32_t r = isk ? e : e - CH * KP;
-        const uint32_t row = isk ? r / KP : r / VP, pc = isk ? r - row * KP : r - row * VP;   // row: token or channel
-        const uint32_t pos = isk ? t0 + row : t0 + pc * TPP;
-        u4v val = {0u, 0u, 0u, 0u};
-        if (pos < total)
+        row = isk ? r / KP : r / VP;                       // token or channel
+        pc = isk ? r - row * KP : r - row * VP;
+    };
+    auto load = [&](uint32_t c) {
+        const uint32_t t0 = c * CH;
+        tail = 0u;
+#pragma unroll
+        for (uint32_t k = 0; k < NPC; ++k)
         {
-            const int32_t page = pos / OPURE_PAGE_SIZE < p.max_pages ? pt[pos / OPURE_PAGE_SIZE] : -1;
-            if (page >= 0 && static_cast<uint32_t>(page) < p.n_pages)
+            bool isk;
+            uint32_t row, pc;
+            piece(k, isk, row, pc);
+            const uint32_t pos = isk ? t0 + row : t0 + pc * TPP;
+            u4v val = {0u, 0u, 0u, 0u};
+            if (pos < total)
             {
-                const uint64_t idx = isk ? kv_elem(p.layer, p.n_pages, static_cast<uint32_t>(page), 0u, p.n_kv, kh, HD,
-                                                   pos % OPURE_PAGE_SIZE, pc * (16u / EB))
-                                         : kv_elem(p.layer, p.n_pages, static_cast<uint32_t>(page), 1u, p.n_kv, kh, HD,
-                                                   pos % OPURE_PAGE_SIZE, row);
-                val = *reinterpret_cast<const u4v*>(static_cast<const uint8_t*>(p.pool) + idx * EB);
-                if (!isk && pos + TPP > total) val = mask_tail<AF>(val, total - pos);   // slots past the cache read 0
+                const int32_t page = spg[pos / OPURE_PAGE_SIZE - c_first * PPC];
+                if (page >= 0 && static_cast<uint32_t>(page) < p.n_pages)
+                {
+                    const uint64_t idx = isk ? kv_elem(p.layer, p.n_pages, static_cast<uint32_t>(page), 0u, p.n_kv, kh, HD,
+                                                       pos % OPURE_PAGE_SIZE, pc * (16u / EB))
+                                             : kv_elem(p.layer, p.n_pages, static_cast<uint32_t>(page), 1u, p.n_kv, kh, HD,
+                                                       pos % OPURE_PAGE_SIZE, row);
+                    val = *reinterpret_cast<const u4v*>(static_cast<const uint8_t*>(p.pool) + idx * EB);
+                    if (!isk && pos + TPP > total) tail |= 1u << k;   // masked when stored: no wait here
+                }
+                else
+                {
+                    // a missing page or a length past the table reads as NaN, never out of bounds
+                    val = {nan, nan, nan, nan};
+                }
             }
-            else
-            {
-                // a missing page or a length past the table reads as NaN, never out of bounds
-                val = {nan, nan, nan, nan};
-            }
+            buf[k] = val;
         }
-        if (isk) *reinterpret_cast<u4v*>(kt + row * ROWB + pc * 16u) = val;
-        else *reinterpret_cast<u4v*>(vt + row * VROWB + pc * 16u) = val;
-    }
-    __syncthreads();
+    };
+    auto put = [&](uint32_t c) {
+#pragma unroll
+        for (uint32_t k = 0; k < NPC; ++k)
+        {
+            bool isk;
+            uint32_t row, pc;
+            piece(k, isk, row, pc);
+            u4v val = buf[k];
+            if (tail & (1u << k)) val = mask_tail<AF>(val, total - (c * CH + pc * TPP));   // slots past the cache read 0
+            if (isk) *reinterpret_cast<u4v*>(kt + row * ROWB + pc * 16u) = val;
+            else *reinterpret_cast<u4v*>(vt + row * VROWB + pc * 16u) = val;
+        }
+    };
+    for (uint32_t c = c_first; c < c_end; ++c)
+    {
+        const uint32_t t0 = c * CH;
+        if (t0 >= total) break;                           // whole workgroup: past the sequence
+        load(c);
+        if (c != c_first) __syncthreads();                // the chunk before's buffers read
+        put(c);
+        __syncthreads();
 
-    // this lane's K row (token t0 + lane) and V channels (lane, lane + 64)
-    float kr[HD];
+        // this lane's K row (token t0 + lane) and V channels (lane, lane + 64)
+        float kr[HD];
 #pragma unroll
-    for (uint32_t d = 0; d < HD; ++d)
-    {
-        if constexpr (AF == OPURE_A_F32) kr[d] = reinterpret_cast<const float*>(kt + lane * ROWB)[d];
-        else kr[d] = AF == OPURE_A_F16 ? f16_to_f32(reinterpret_cast<const uint16_t*>(kt + lane * ROWB)[d])
-                                       : bf16_to_f32(reinterpret_cast<const uint16_t*>(kt + lane * ROWB)[d]);
-    }
-    float vc[DPL][CH];
-#pragma unroll
-    for (uint32_t i = 0; i < DPL; ++i)
-    {
-        const uint32_t d = lane + 64u * i;
-#pragma unroll
-        for (uint32_t t = 0; t < CH; ++t)
-            vc[i][t] = d < HD ? load_act_rt(vt + d * VROWB, t, AF) : 0.0f;
-    }
-    const uint64_t pbase = ((static_cast<uint64_t>(b) * p.n_kv + kh) * p.npart + c) * Gq;
-    const uint32_t pos = t0 + lane;
-    for (uint32_t qi = wave; qi < Gq; qi += 4u)
-    {
-        const uint32_t j = qi / group;
-        const float* qr = qs + qi * HD;
-        float acc = 0.0f;
-#pragma unroll
-        for (uint32_t d = 0; d < HD; ++d) acc = __fmaf_rn(qr[d], kr[d], acc);
-        const float s = pos <= ctx + j ? __fmul_rn(acc, p.scale) : -__builtin_huge_valf();
-        const float mx = wave_max(s);
-        const float e = s == -__builtin_huge_valf() ? 0.0f : expf_ref(__fsub_rn(s, mx));
-        const float l = wave_sum(e);
-        pbuf[wave][lane] = e;
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        for (uint32_t d = 0; d < HD; ++d)
+        {
+            if constexpr (AF == OPURE_A_F32) kr[d] = reinterpret_cast<const float*>(kt + lane * ROWB)[d];
+            else kr[d] = AF == OPURE_A_F16 ? f16_to_f32(reinterpret_cast<const uint16_t*>(kt + lane * ROWB)[d])
+                                           : bf16_to_f32(reinterpret_cast<const uint16_t*>(kt + lane * ROWB)[d]);
+        }
+        float vc[DPL][CH];
 #pragma unroll
         for (uint32_t i = 0; i < DPL; ++i)
         {
-            float o = 0.0f;
-#pragma unroll
-            for (uint32_t t = 0; t < CH; ++t) o = __fmaf_rn(pbuf[wave][t], vc[i][t], o);
             const uint32_t d = lane + 64u * i;
-            if (d < HD) p.part_acc[(pbase + qi) * HD + d] = o;
+#pragma unroll
+            for (uint32_t t = 0; t < CH; ++t)
+                vc[i][t] = d < HD ? load_act_rt(vt + d * VROWB, t, AF) : 0.0f;
         }
-        if (lane == 0)
+        const uint64_t pbase = ((static_cast<uint64_t>(b) * p.n_kv + kh) * p.npart + c) * Gq;
+        const uint32_t pos = t0 + lane;
+        // rows q0 and q0 + NWV together: two independent chains of the same
+        // per-row operations (a missing second row scores row q0 again, unstored)
+        for (uint32_t q0 = wave; q0 < Gq; q0 += NWV * RB)
         {
-            p.part_ml[(pbase + qi) * 2u] = mx;
-            p.part_ml[(pbase + qi) * 2u + 1u] = l;
+            uint32_t qi[RB];
+            bool has[RB];
+            float acc[RB], mx[RB], l[RB];
+#pragma unroll
+            for (uint32_t r = 0; r < RB; ++r)
+            {
+                has[r] = q0 + NWV * r < Gq;
+                qi[r] = has[r] ? q0 + NWV * r : q0;
+                acc[r] = 0.0f;
+            }
+#pragma unroll
+            for (uint32_t d = 0; d < HD; ++d)
+#pragma unroll
+                for (uint32_t r = 0; r < RB; ++r) acc[r] = __fmaf_rn(qs[qi[r] * HD + d], kr[d], acc[r]);
+#pragma unroll
+            for (uint32_t r = 0; r < RB; ++r)
+            {
+                const uint32_t j = qi[r] / group;
+                const float sc = pos <= ctx + j ? __fmul_rn(acc[r], p.scale) : -__builtin_huge_valf();
+                mx[r] = wave_max(sc);
+                const float e = sc == -__builtin_huge_valf() ? 0.0f : expf_ref(__fsub_rn(sc, mx[r]));
+                l[r] = wave_sum(e);
+                pbuf[wave][r][lane] = e;
+            }
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+#pragma unroll
+            for (uint32_t i = 0; i < DPL; ++i)
+            {
+                float o[RB];
+#pragma unroll
+                for (uint32_t r = 0; r < RB; ++r) o[r] = 0.0f;
+#pragma unroll
+                for (uint32_t t = 0; t < CH; ++t)
+#pragma unroll
+                    for (uint32_t r = 0; r < RB; ++r) o[r] = __fmaf_rn(pbuf[wave][r][t], vc[i][t], o[r]);
+                const uint32_t d = lane + 64u * i;
+#pragma unroll
+                for (uint32_t r = 0; r < RB; ++r)
+                    if (has[r] && d < HD)
+                    {
+                        if constexpr (ALL) pa[(c * Gq + qi[r]) * HD + d] = o[r];
+                        else p.part_acc[(pbase + qi[r]) * HD + d] = o[r];
+                    }
+            }
+            if (lane == 0)
+#pragma unroll
+                for (uint32_t r = 0; r < RB; ++r)
+                    if (has[r])
+                    {
+                        if constexpr (ALL)
+                        {
+                            pm[c * Gq + qi[r]] = mx[r];
+                            pl[c * Gq + qi[r]] = l[r];
+                        }
+                        else
+                        {
+                            p.part_ml[(pbase + qi[r]) * 2u] = mx[r];
+                            p.part_ml[(pbase + qi[r]) * 2u + 1u] = l[r];
+                        }
+                    }
+            __builtin_amdgcn_wave_barrier();
+        }
+    }
+    if constexpr (ALL)
+    {
+        // ---- the merge of each row's chunks 0..last, as k_attn_combine does:
+        //      lanes over chunks for the maximum, the weights and the
+        //      denominator, then channels d = lane + 64 i over the chunks in order
+        __syncthreads();
+        const uint32_t nc = p.nch;
+        for (uint32_t qi = wave; qi < Gq; qi += NWV)
+        {
+            const uint32_t j = qi / group, head = kh * group + (qi - j * group);
+            uint32_t last = (ctx + j) / p.chunk;
+            if (last >= nc)
+            {
+                last = nc - 1u;
+                if (lane == 0u && p.err) p.err[ERR_POSITION] = 1u;
+            }
+            const uint32_t c0 = min(lane, nc - 1u);
+            const float m0 = pm[c0 * Gq + qi], l0 = pl[c0 * Gq + qi];
+            float mx = -__builtin_huge_valf();
+            if (lane <= last) mx = fmaxf(mx, m0);
+            mx = wave_max64(mx);
+            float den = 0.0f;
+            if (lane <= last)
+            {
+                const float w = m0 == -__builtin_huge_valf() ? 0.0f : expf_ref(__fsub_rn(m0, mx));
+                wsh[wave][lane] = w;
+                den = __fmaf_rn(w, l0, den);
+            }
+            den = wave_sum64(den);
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            const float dd = den > 0.0f ? den : 1.0f;
+#pragma unroll
+            for (uint32_t i = 0; i < DPL; ++i)
+            {
+                const uint32_t d = lane + 64u * i;
+                float num = 0.0f;
+#pragma unroll
+                for (uint32_t c = 0; c < ATTN_ALL_CHUNKS; ++c)
+                {
+                    const bool in = c <= last;
+                    const float w = wsh[wave][in ? c : 0u];
+                    const float v = pa[(min(c, nc - 1u) * Gq + qi) * HD + min(d, HD - 1u)];
+                    num = in ? __fmaf_rn(w, v, num) : num;
+                }
+                if (d < HD)
+                    store_act_rt(p.out, (static_cast<uint64_t>(b * R + j) * p.n_heads + head) * HD + d,
+                                 __fdiv_rn(num, dd), p.afmt);
+            }
+            __builtin_amdgcn_wave_barrier();
+        }
+    }
+}
+
+// Head_dim 64 over at most ATTN_SPLIT_CHUNKS chunks of 64 tokens (a short
+// context): a workgroup per (KV head, pair of query rows, sequence) with a
+// wave per chunk, so a batch of one sequence still spreads over many CUs.  A
+// wave loads its chunk's K rows (lane = token) and V columns (lane = channel)
+// straight into registers, all at once (a missing page's lanes read page 0
+// and are replaced when used), scores the pair of rows with the chunk
+// kernel's per-row operations and leaves the chunk's (max, sum, output) in
+// LDS; the waves then merge each row's chunks with k_attn_combine's
+// operations in its order.  A row has the bits of k_attn_chunk + combine.
+constexpr uint32_t ATTN_SPLIT_CHUNKS = 8;
+
+template <int AF>
+__global__ __launch_bounds__(64 * ATTN_SPLIT_CHUNKS) void k_attn_split(AttnParams p)
+{
+    constexpr uint32_t HD = 64, CH = 64, RB = 2, NW = ATTN_SPLIT_CHUNKS, PPC = CH / OPURE_PAGE_SIZE;
+    constexpr uint32_t EB = AF == OPURE_A_F32 ? 4u : 2u, EPP = 16u / EB;   // elements a 16-byte piece
+    __shared__ __align__(16) float qsm[NW][RB][HD];       // each wave's copy of the pair's Q rows
+    __shared__ __align__(16) float pbuf[NW][RB][CH];
+    __shared__ __align__(16) float pa[NW][RB][HD];        // the chunks' outputs
+    __shared__ float pm[NW][RB], pl[NW][RB];               // the chunks' maxima and sums
+    __shared__ float wsh[RB][NW];                          // a row's chunk weights
+
+    const uint32_t kh = blockIdx.x, b = blockIdx.z;
+    const uint32_t group = p.n_heads / p.n_kv, R = p.rows, Gq = group * R;
+    const uint32_t c = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63u;   // wave = chunk
+    const uint32_t nw = blockDim.x >> 6, q0 = blockIdx.y * RB;
+    const int32_t* pt = p.page_table + static_cast<uint64_t>(b) * p.max_pages;
+
+    // round trip 1: the sequence length, the pair's Q rows, the chunk's page entries
+    const int32_t seq = p.seq_len[b];
+    bool has[RB];
+    uint32_t qi[RB], jr[RB];
+    float qv[RB];
+#pragma unroll
+    for (uint32_t r = 0; r < RB; ++r)
+    {
+        has[r] = q0 + r < Gq;
+        qi[r] = has[r] ? q0 + r : q0;
+        jr[r] = qi[r] / group;
+        const uint32_t head = kh * group + (qi[r] - jr[r] * group);
+        qv[r] = load_act_rt(p.q, (static_cast<uint64_t>(b * R + jr[r]) * p.n_heads + head) * HD + lane, AF);
+    }
+    const uint32_t pi = c * PPC + (lane & (PPC - 1u));
+    const int32_t pe = pi < p.max_pages ? pt[pi] : -1;
+    asm volatile("" ::: "memory");                         // every load above issued before the entries are read
+    const uint32_t ctx = static_cast<uint32_t>(seq), total = ctx + R, t0 = c * CH;
+    int32_t pg[PPC];
+#pragma unroll
+    for (uint32_t i = 0; i < PPC; ++i) pg[i] = __builtin_amdgcn_readlane(pe, i);
+#pragma unroll
+    for (uint32_t r = 0; r < RB; ++r) qsm[c][r][lane] = qv[r];
+
+    if (t0 < total)   // wave-uniform: the chunk holds positions of the sequence
+    {
+        // round trip 2: K row of token t0 + lane, V column of channel `lane`
+        auto ok = [&](int32_t pg_) { return pg_ >= 0 && static_cast<uint32_t>(pg_) < p.n_pages; };
+        auto safe = [&](int32_t pg_) { return ok(pg_) ? static_cast<uint32_t>(pg_) : 0u; };
+        const uint32_t pos = t0 + lane, sl = lane / OPURE_PAGE_SIZE;
+        const int32_t kpg = sl == 0u ? pg[0] : sl == 1u ? pg[1] : sl == 2u ? pg[2] : pg[3];
+        const u4v* kp = reinterpret_cast<const u4v*>(static_cast<const uint8_t*>(p.pool) +
+                                                     kv_elem(p.layer, p.n_pages, safe(kpg), 0u, p.n_kv, kh, HD,
+                                                             pos % OPURE_PAGE_SIZE, 0u) * EB);
+        u4v kw[HD / EPP], vw[PPC][OPURE_PAGE_SIZE / EPP];
+#pragma unroll
+        for (uint32_t k = 0; k < HD / EPP; ++k) kw[k] = kp[k];
+#pragma unroll
+        for (uint32_t i = 0; i < PPC; ++i)
+        {
+            const u4v* vp = reinterpret_cast<const u4v*>(static_cast<const uint8_t*>(p.pool) +
+                                                         kv_elem(p.layer, p.n_pages, safe(pg[i]), 1u, p.n_kv, kh, HD, 0u,
+                                                                 lane) * EB);
+#pragma unroll
+            for (uint32_t k = 0; k < OPURE_PAGE_SIZE / EPP; ++k) vw[i][k] = vp[k];
+        }
+        // the fills: a position past the cache reads 0, a missing page (or an
+        // entry past the table) NaN, a V piece reaching past the cache keeps
+        // its slots before the end
+        const uint32_t nan = AF == OPURE_A_F32 ? 0x7FC00000u : (AF == OPURE_A_F16 ? 0x7E007E00u : 0x7FC07FC0u);
+        const u4v zero = {0u, 0u, 0u, 0u}, nanv = {nan, nan, nan, nan};
+#pragma unroll
+        for (uint32_t k = 0; k < HD / EPP; ++k) kw[k] = pos < total ? (ok(kpg) ? kw[k] : nanv) : zero;
+#pragma unroll
+        for (uint32_t i = 0; i < PPC; ++i)
+#pragma unroll
+            for (uint32_t k = 0; k < OPURE_PAGE_SIZE / EPP; ++k)
+            {
+                const uint32_t pp = t0 + i * OPURE_PAGE_SIZE + k * EPP;
+                u4v v = ok(pg[i]) ? (pp + EPP > total ? mask_tail<AF>(vw[i][k], total - pp) : vw[i][k]) : nanv;
+                vw[i][k] = pp < total ? v : zero;
+            }
+        float kr[HD], vc[CH];
+#pragma unroll
+        for (uint32_t d = 0; d < HD; ++d)
+        {
+            const uint32_t w = kw[d / EPP][(d % EPP) * EB / 4u];
+            if constexpr (AF == OPURE_A_F32) kr[d] = __uint_as_float(w);
+            else
+            {
+                const uint16_t h = static_cast<uint16_t>(d % 2u ? w >> 16 : w & 0xFFFFu);
+                kr[d] = AF == OPURE_A_F16 ? f16_to_f32(h) : bf16_to_f32(h);
+            }
+        }
+#pragma unroll
+        for (uint32_t t = 0; t < CH; ++t)
+        {
+            const uint32_t i = t / OPURE_PAGE_SIZE, s = t % OPURE_PAGE_SIZE;
+            const uint32_t w = vw[i][s / EPP][(s % EPP) * EB / 4u];
+            if constexpr (AF == OPURE_A_F32) vc[t] = __uint_as_float(w);
+            else
+            {
+                const uint16_t h = static_cast<uint16_t>(s % 2u ? w >> 16 : w & 0xFFFFu);
+                vc[t] = AF == OPURE_A_F16 ? f16_to_f32(h) : bf16_to_f32(h);
+            }
         }
         __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        float acc[RB], mx[RB], l[RB];
+#pragma unroll
+        for (uint32_t r = 0; r < RB; ++r) acc[r] = 0.0f;
+#pragma unroll
+        for (uint32_t d = 0; d < HD; ++d)
+#pragma unroll
+            for (uint32_t r = 0; r < RB; ++r) acc[r] = __fmaf_rn(qsm[c][r][d], kr[d], acc[r]);
+#pragma unroll
+        for (uint32_t r = 0; r < RB; ++r)
+        {
+            const float sc = pos <= ctx + jr[r] ? __fmul_rn(acc[r], p.scale) : -__builtin_huge_valf();
+            mx[r] = wave_max(sc);
+            const float e = sc == -__builtin_huge_valf() ? 0.0f : expf_ref(__fsub_rn(sc, mx[r]));
+            l[r] = wave_sum(e);
+            pbuf[c][r][lane] = e;
+        }
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        float o[RB];
+#pragma unroll
+        for (uint32_t r = 0; r < RB; ++r) o[r] = 0.0f;
+#pragma unroll
+        for (uint32_t t = 0; t < CH; ++t)
+#pragma unroll
+            for (uint32_t r = 0; r < RB; ++r) o[r] = __fmaf_rn(pbuf[c][r][t], vc[t], o[r]);
+#pragma unroll
+        for (uint32_t r = 0; r < RB; ++r)
+        {
+            pa[c][r][lane] = o[r];
+            if (lane == 0u)
+            {
+                pm[c][r] = mx[r];
+                pl[c][r] = l[r];
+            }
+        }
+    }
+    __syncthreads();
+
+    // the merge of each row's chunks 0..last, as k_attn_combine does: lanes
+    // over chunks for the maximum, the weights and the denominator, then
+    // channel `lane` over the chunks in order
+    for (uint32_t r = c; r < RB; r += nw)
+    {
+        if (!has[r]) continue;
+        uint32_t last = (ctx + jr[r]) / p.chunk;
+        if (last >= p.nch)
+        {
+            last = p.nch - 1u;
+            if (lane == 0u && p.err) p.err[ERR_POSITION] = 1u;
+        }
+        const uint32_t c0 = min(lane, NW - 1u);
+        const float m0 = pm[c0][r], l0 = pl[c0][r];
+        float mx = -__builtin_huge_valf();
+        if (lane <= last) mx = fmaxf(mx, m0);
+        mx = wave_max64(mx);
+        float den = 0.0f;
+        if (lane <= last)
+        {
+            const float w = m0 == -__builtin_huge_valf() ? 0.0f : expf_ref(__fsub_rn(m0, mx));
+            wsh[r][lane] = w;
+            den = __fmaf_rn(w, l0, den);
+        }
+        den = wave_sum64(den);
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        const float dd = den > 0.0f ? den : 1.0f;
+        float num = 0.0f;
+#pragma unroll
+        for (uint32_t cc = 0; cc < NW; ++cc)
+        {
+            const bool in = cc <= last;
+            num = in ? __fmaf_rn(wsh[r][in ? cc : 0u], pa[in ? cc : 0u][r][lane], num) : num;
+        }
+        const uint32_t head = kh * group + (qi[r] - jr[r] * group);
+        store_act_rt(p.out, (static_cast<uint64_t>(b * R + jr[r]) * p.n_heads + head) * HD + lane, __fdiv_rn(num, dd),
+                     p.afmt);
     }
 }
 
@@ -971,17 +1351,17 @@ int launch_mfma(opure_dev* dev, dim3 grid, const AttnParams& p)
     return OPURE_OK;
 }
 
-template <int HD, int AF>
+template <int HD, int AF, bool ALL>
 int launch_fast(opure_dev* dev, dim3 grid, uint32_t lds, const AttnParams& p)
 {
     static bool configured = false;
     if (!configured)
     {
-        OPURE_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_attn_chunk<HD, AF>),
+        OPURE_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_attn_chunk<HD, AF, ALL>),
                                           hipFuncAttributeMaxDynamicSharedMemorySize, 64 * 1024));
         configured = true;
     }
-    OPURE_LAUNCH(dev, (k_attn_chunk<HD, AF>), grid, dim3(256), lds, p);
+    OPURE_LAUNCH(dev, (k_attn_chunk<HD, AF, ALL>), grid, dim3(attn_fast_threads<HD>()), lds, p);
     OPURE_LAUNCH_CHECK("k_attn_chunk");
     return OPURE_OK;
 }
@@ -1149,17 +1529,37 @@ int attn_launch(opure_dev* dev, const opure_model* m, const opure_kv* kv, uint32
             }
         }
     }
+    else if (p.chunk == 64u && hd == 64u && p.nch <= ATTN_SPLIT_CHUNKS)
+    {
+        // a short context at head_dim 64: a workgroup a pair of query rows, a
+        // wave a chunk, merged in the workgroup (no combine launch)
+        const dim3 g(p.n_kv, (Gq + 1u) / 2u, batch), blk(64u * p.nch);
+        if (p.afmt == OPURE_A_F32) OPURE_LAUNCH(dev, k_attn_split<OPURE_A_F32>, g, blk, 0, p);
+        else if (p.afmt == OPURE_A_F16) OPURE_LAUNCH(dev, k_attn_split<OPURE_A_F16>, g, blk, 0, p);
+        else OPURE_LAUNCH(dev, k_attn_split<OPURE_A_BF16>, g, blk, 0, p);
+        OPURE_LAUNCH_CHECK("k_attn_split");
+        return OPURE_OK;
+    }
     else if (p.chunk == 64u && (hd == 64u || hd == 128u))
     {
-        const uint32_t lds = Gq * hd * 4u;
+        // head_dim 128 over at most ATTN_ALL_CHUNKS chunks: one workgroup a (KV
+        // head, sequence) takes them all and merges them itself (no combine launch)
+        const uint64_t all_lds = static_cast<uint64_t>(Gq) * hd * 4u + attn_all_lds<128>(Gq);
+        const bool all = hd == 128u && p.nch <= ATTN_ALL_CHUNKS && all_lds <= 48u * 1024u;
+        const uint32_t lds = all ? static_cast<uint32_t>(all_lds) : Gq * hd * 4u;
+        const dim3 g = all ? dim3(p.n_kv, 1u, batch) : grid;
         int rc;
-        if (hd == 64u && p.afmt == OPURE_A_F32) rc = launch_fast<64, OPURE_A_F32>(dev, grid, lds, p);
-        else if (hd == 64u && p.afmt == OPURE_A_F16) rc = launch_fast<64, OPURE_A_F16>(dev, grid, lds, p);
-        else if (hd == 64u) rc = launch_fast<64, OPURE_A_BF16>(dev, grid, lds, p);
-        else if (p.afmt == OPURE_A_F32) rc = launch_fast<128, OPURE_A_F32>(dev, grid, lds, p);
-        else if (p.afmt == OPURE_A_F16) rc = launch_fast<128, OPURE_A_F16>(dev, grid, lds, p);
-        else rc = launch_fast<128, OPURE_A_BF16>(dev, grid, lds, p);
+        if (hd == 64u && p.afmt == OPURE_A_F32) rc = launch_fast<64, OPURE_A_F32, false>(dev, g, lds, p);
+        else if (hd == 64u && p.afmt == OPURE_A_F16) rc = launch_fast<64, OPURE_A_F16, false>(dev, g, lds, p);
+        else if (hd == 64u) rc = launch_fast<64, OPURE_A_BF16, false>(dev, g, lds, p);
+        else if (p.afmt == OPURE_A_F32)
+            rc = all ? launch_fast<128, OPURE_A_F32, true>(dev, g, lds, p) : launch_fast<128, OPURE_A_F32, false>(dev, g, lds, p);
+        else if (p.afmt == OPURE_A_F16)
+            rc = all ? launch_fast<128, OPURE_A_F16, true>(dev, g, lds, p) : launch_fast<128, OPURE_A_F16, false>(dev, g, lds, p);
+        else
+            rc = all ? launch_fast<128, OPURE_A_BF16, true>(dev, g, lds, p) : launch_fast<128, OPURE_A_BF16, false>(dev, g, lds, p);
         if (rc) return rc;
+        if (all) return OPURE_OK;
     }
     else
     {

@@ -455,7 +455,7 @@ def attn_model(n_heads, n_kv, hd, afmt, scale=1.0, n_layers=1):
     return m
 
 
-def run_attn(dev, m, pool_bits, pt, seq_len, R, q_bits, layer=0):
+def run_attn(dev, m, pool_bits, pt, seq_len, R, q_bits, layer=0, max_ctx=None):
     B = pt.shape[0]
     pb = dev.upload(pool_bits)
     ptb = dev.upload(pt.astype(np.int32))
@@ -463,7 +463,8 @@ def run_attn(dev, m, pool_bits, pt, seq_len, R, q_bits, layer=0):
     qb = dev.upload(q_bits)
     ob = dev.alloc(q_bits.nbytes)
     kv = H.KV(int(pb), pool_bits.shape[1], 16, int(ptb), pt.shape[1])
-    a = H.AttnArgs(C.pointer(m), C.pointer(kv), layer, B, R, int(sl), int(max(seq_len)) + R, int(qb), int(ob))
+    a = H.AttnArgs(C.pointer(m), C.pointer(kv), layer, B, R, int(sl), int(max(seq_len)) + R if max_ctx is None else max_ctx,
+                   int(qb), int(ob))
     H.check(H.lib().opure_attn_decode_paged(dev.h, C.byref(a)))
     dev.sync()
     out = dev.download(ob, q_bits.dtype, q_bits.shape)
@@ -542,6 +543,69 @@ def test_attention_paged_matches_oracle(dev, case):
     for j in range(R):
         one = run_attn(dev, m, kv.pool, kv.page_table[:1], [ctx[0] + j], 1, q_bits[j:j + 1], layer=1)
         assert np.array_equal(one[0], got[j])
+
+
+# fp32 launches over few chunks of 64 tokens: head_dim, query heads, KV heads,
+# rows, contexts (rows ending on either side of chunk boundaries)
+FAST_ALL_CASES = [
+    (64, 9, 3, 5, [0, 1, 58, 59, 60, 63, 64, 122, 187, 251]),     # 4 chunks
+    (64, 8, 2, 3, [5, 130, 191, 255, 256, 300, 447, 509]),        # 8 chunks, an odd row count
+    (128, 8, 2, 4, [3, 60, 61, 125, 190, 252]),
+]
+
+
+@pytest.mark.parametrize("hd,nh,nkv,R,ctx", FAST_ALL_CASES, ids=["hd64-4", "hd64-8", "hd128"])
+def test_attention_one_workgroup_merge_same_bits(dev, hd, nh, nkv, R, ctx):
+    """fp32 over a short context merges a row's chunks inside one workgroup
+    (head_dim 64, up to 8 chunks: a workgroup a pair of query rows, a wave a
+    chunk; head_dim 128, up to 4 chunks: a workgroup a KV head, the chunks in
+    turn); a launch over more chunks (max_ctx 1024) writes one partial a chunk
+    and merges them in the combine launch.  Every row has the same bits either
+    way (a missing page's NaN included), and stays within fp32 tolerance of
+    the oracle."""
+    say("attention one-workgroup merge", hd, nh, nkv, R, ctx)
+    rng = np.random.default_rng(hd + R)
+    B, ps, wide = len(ctx), 16, 64
+    mp = [(c + R + ps - 1) // ps for c in ctx]
+    n_pages = sum(mp) + 4
+    hm = O.HostModel(n_layers=1, hidden=64, n_heads=nh, n_kv_heads=nkv, head_dim=hd, ffn=64, vocab=64,
+                     wfmt=O.W_F32, afmt=H.A_F32, attn_scale=hd ** -0.5, max_pos=1100, seed=1)
+    kv = O.HostKV(hm, n_pages=n_pages, batch=B, max_pages_per_seq=wide)
+    kv.fill_random(rng, 1.0)
+    kv.page_table[:] = -1
+    perm = rng.permutation(n_pages)
+    o = 0
+    for b in range(B):
+        kv.page_table[b, :mp[b]] = perm[o:o + mp[b]]
+        o += mp[b]
+    q_bits, q_f = to_act(rng.standard_normal((B * R, nh * hd)) * 1.5, H.A_F32)
+    m = attn_model(nh, nkv, hd, H.A_F32, hd ** -0.5)
+    assert max(ctx) + R <= (512 if hd == 64 else 256)
+    one = run_attn(dev, m, kv.pool, kv.page_table, ctx, R, q_bits)
+    many = run_attn(dev, m, kv.pool, kv.page_table, ctx, R, q_bits, max_ctx=1024)
+    assert np.array_equal(one.view(np.uint32), many.view(np.uint32))
+    kv._mk()
+    O.set_threads(16)
+    try:
+        for b in range(B):
+            qb = np.ascontiguousarray(q_f[b * R:(b + 1) * R])
+            ob = np.zeros_like(qb)
+            O.lib().orc_attention_paged(C.byref(hm.desc), C.byref(kv.desc), 0, b, ctx[b], R, qb.ctypes.data,
+                                        ob.ctypes.data)
+            np.testing.assert_allclose(from_act(one[b * R:(b + 1) * R], H.A_F32), ob, rtol=2e-5, atol=2e-5)
+    finally:
+        O.set_threads(1)
+    # a missing page inside sequence 3's context (tokens 16..31): its rows read
+    # NaN, the others keep their bits, both launches alike
+    pt = kv.page_table.copy()
+    pt[3, 1] = -1
+    one_m = run_attn(dev, m, kv.pool, pt, ctx, R, q_bits)
+    many_m = run_attn(dev, m, kv.pool, pt, ctx, R, q_bits, max_ctx=1024)
+    assert np.array_equal(one_m.view(np.uint32), many_m.view(np.uint32))
+    assert np.isnan(one_m[3 * R:4 * R]).all()
+    keep = np.ones(B * R, bool)
+    keep[3 * R:4 * R] = False
+    assert np.array_equal(one_m[keep].view(np.uint32), one[keep].view(np.uint32))
 
 
 # ---------------------------------------------------------------------------
