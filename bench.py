@@ -432,7 +432,7 @@ def bench_c1(args):
     tgt = synth.SynthModel(dev, cfg, seed=1234, max_pos=max_pos)
     drf = synth.SynthModel(dev, dict(cfg, n_layers=2), seed=4321, max_pos=max_pos)
     prompt = np.random.default_rng(7).integers(0, cfg["vocab"], P).astype(np.int32)
-    eng = E.Engine(dev, tgt.desc, drf.desc, max_positions=max_pos, draft_tokens=K)
+    eng = E.Engine(dev, tgt.desc, drf.desc, max_positions=max_pos, draft_tokens=K, use_graphs=not args.eager)
     for _ in range(max(1, args.warmup // 5)):
         eng.generate_speculative(prompt, n_new)
         eng.generate(prompt, n_new)
@@ -455,7 +455,8 @@ def bench_c1(args):
         "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "f32", "data": "synthetic: seeded N(0,0.02) target and draft, uniform random 32-token prompt",
         "config": {"workload": "c1: native engine GenerateSpeculative, 30-layer target + 2-layer draft, 32-token "
-                               "prompt, K=4, 64 new tokens, one step = the whole generation (prefill excluded)",
+                               "prompt, K=4, 64 new tokens, one step = the whole generation (prefill excluded), "
+                               + ("eager launches" if args.eager else "one hipGraph per speculative iteration"),
                    "accepted_per_verify_step": hist.tolist(), "verify_steps": int(st.verify_steps),
                    "draft_steps": int(st.draft_steps), "greedy_ms": round(gms, 4),
                    "greedy_tokens_per_s": round(n_new / (gms * 1e-3), 1),
