@@ -38,8 +38,8 @@ def sync_code(dev):
         return e.code
 
 
-def small_step(dev, B=1, R=4, max_ctx=256):
-    m = small_model(O.W_I8PC, O.A_F16)
+def small_step(dev, B=1, R=4, max_ctx=256, fmt=(O.W_I8PC, O.A_F16)):
+    m = small_model(*fmt)
     kv = random_cache(m, B, max_ctx, 32 * B, seed=3)
     dm, dkv = device_model(dev, m), device_kv(dev, m, kv)
     return m, kv, dkv, VerifyRunner(dev, dm, dkv, B, R, max_ctx)
@@ -65,8 +65,11 @@ def test_token_outside_vocabulary_is_reported(dev):
     assert np.isfinite(run.get_logits()).all()
 
 
-def test_position_past_max_ctx_is_reported(dev):
-    m, kv, dkv, run = small_step(dev, max_ctx=256)
+@pytest.mark.parametrize("fmt", [(O.W_I8PC, O.A_F16), (O.W_F32, O.A_F32)], ids=["i8-f16", "f32"])
+def test_position_past_max_ctx_is_reported(dev, fmt):
+    """Matrix-core attention + combine (f16), and the fp32 short-context
+    kernel that merges its chunks itself: both report the row past max_ctx."""
+    m, kv, dkv, run = small_step(dev, max_ctx=256, fmt=fmt)
     # the last row sits at 254 + 3 = 257, past max_ctx = 256 and the 16 pages of the table
     launch(dev, run, [[1, 2, 3, 4]], [254])
     assert sync_code(dev) == H.E_CAPACITY
