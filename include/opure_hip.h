@@ -416,8 +416,8 @@ int opure_profile_read(opure_dev* dev, uint32_t counts[OPURE_STAGE_COUNT], doubl
  *      h (afmt). */
 int opure_debug_workspace(opure_dev* dev, void** ptr, uint64_t* bytes);
 /* Sleeps a bounded wait takes before it gives up (default 4M): between the
- * waves of a GEMV workgroup, or between the slices of a sequence in the
- * one-launch rejection step.  A test hook: 0 makes any wait that is not already met give
+ * waves of a GEMV workgroup, between the slices of a sequence in the
+ * one-launch rejection step, or in the LM head's greedy acceptance.  A test hook: 0 makes any wait that is not already met give
  * up at once, so the failure report can be checked while every wave still
  * runs to its end. */
 int opure_debug_set_wait_limit(opure_dev* dev, uint32_t sleeps);
@@ -434,6 +434,13 @@ int opure_debug_set_gemv_engine(opure_dev* dev, uint32_t engine);
  * kept for comparison.  Both give the same bits. */
 enum { OPURE_REJ_ONE_LAUNCH = 0, OPURE_REJ_STAGED = 1 };
 int opure_debug_set_rejection_launches(opure_dev* dev, uint32_t mode);
+/* Greedy acceptance (and its rollback) inside opure_verify_step: run by the
+ * LM head's own launch where its kernel allows (default: the last workgroup
+ * gathers every workgroup's argmax through tagged words), or by a separate
+ * launch after it, kept for comparison.  Both give the same tokens, accepted
+ * lengths and rollback. */
+enum { OPURE_GREEDY_IN_LM_HEAD = 0, OPURE_GREEDY_SEPARATE = 1 };
+int opure_debug_set_greedy_acceptance(opure_dev* dev, uint32_t mode);
 /* Evaluates the SwiGLU epilogue's branch-free exponential and the oracle-order
  * exponential the other kernels use on every one of the 2^32 fp32 bit
  * patterns and counts the results that differ (bit for bit; 0 expected). */

@@ -287,6 +287,13 @@ uint32_t gemv_grid(const opure_dev* dev, const GemvCall& c)
     return make_plan(dev, c.wfmt, c.xfmt, c.W.out, c.W.in, c.M).grid;
 }
 
+bool gemv_is_wave_per_tile(const opure_dev* dev, const GemvCall& c)
+{
+    const Plan pl = make_plan(dev, c.wfmt, c.xfmt, c.W.out, c.W.in, c.M);
+    // wpt 2 is the loader-wave kernel (k_gemv_pc)
+    return pl.staged && (pl.r.wpt == 1u || pl.r.wpt == 4u);
+}
+
 int gemv_validate(const GemvCall& c)
 {
     const uint32_t wf = c.wfmt, af = c.xfmt;

@@ -39,6 +39,7 @@
 #pragma once
 
 #include "internal.h"
+#include "rollback.h"
 
 namespace opure_gemv {
 
@@ -1093,6 +1094,68 @@ __global__ __launch_bounds__(NW * 64) void k_gemv(KParams p)
 // w + 4 take the first and the second half of tile w's blocks, and after the
 // stream the second half's sum is added to the first's through LDS (lo + hi),
 // so all 8 waves load.
+// Greedy acceptance inside the LM head's launch, run by its last-dispatched
+// workgroup (512 threads) once every workgroup has published its rows' bests
+// as tagged words (acc_slots): per row the best (value, lowest index on ties)
+// over the workgroups -- an order-free reduction, so the tokens are
+// k_accept_greedy's -- then per sequence the accepted prefix, the emitted
+// tokens and the rollback.  Workgroups are dispatched in order, so every word
+// it waits for comes from a workgroup already running or finished; the wait is
+// bounded (ERR_WAIT).  Every workgroup read this launch's count before
+// publishing, so once all words carry it the count moves on.
+__device__ inline void greedy_accept_in_launch(const KParams& p, uint32_t M, uint32_t tag, const int32_t* draft,
+                                               int32_t* am, const opure_hip::RollbackPre* pre)
+{
+    constexpr uint32_t NW = 8;
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u, G = gridDim.x;
+    const uint64_t* sl = p.lg.acc_slots;
+    bool gave_up = false;
+    for (uint32_t r = wave; r < M; r += NW)
+    {
+        float bv = -__builtin_huge_valf();
+        int32_t bi = 0x7FFFFFFF;
+        for (uint32_t n = 0;; ++n)
+        {
+            bv = -__builtin_huge_valf();
+            bi = 0x7FFFFFFF;
+            bool ok = true;
+            for (uint32_t g = lane; g < G; g += 64u)
+            {
+                const uint64_t* w = sl + (static_cast<uint64_t>(g) * M + r) * 2u;
+                const uint64_t wv = __hip_atomic_load(const_cast<uint64_t*>(w), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                const uint64_t wi = __hip_atomic_load(const_cast<uint64_t*>(w) + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                ok = ok && (wv >> 32) == tag && (wi >> 32) == tag;
+                best_merge(bv, bi, __uint_as_float(static_cast<uint32_t>(wv)), static_cast<int32_t>(static_cast<uint32_t>(wi)));
+            }
+            if (__all(ok)) break;
+            if (n >= p.lg.wait_limit)
+            {
+                gave_up = true;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) best_merge(bv, bi, __shfl_xor(bv, o), __shfl_xor(bi, o));
+        if (lane == 0u) am[r] = bi == 0x7FFFFFFF ? 0 : bi;
+    }
+    if (gave_up && lane == 0u && p.err) p.err[ERR_WAIT] = 1u;
+    __syncthreads();
+    if (threadIdx.x == 0u)
+        __hip_atomic_store(p.lg.acc_epoch, tag + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t K = p.lg.K, R = K + 1u;
+    for (uint32_t b = 0; b < p.lg.batch; ++b)
+    {
+        uint32_t n = 0;
+        while (n < K && am[b * R + n] == draft[b * K + n]) ++n;
+        if (threadIdx.x < R)
+            p.lg.out_tokens[b * R + threadIdx.x] =
+                threadIdx.x < n ? draft[b * K + threadIdx.x] : (threadIdx.x == n ? am[b * R + n] : -1);
+        if (threadIdx.x == 0u) p.lg.accepted[b] = static_cast<int32_t>(n);
+        if (p.lg.rollback) opure_hip::rollback_seq(p.lg.rb, b, n, pre[b]);
+    }
+}
+
 template <int WF, int AF, int EPI, int U, bool NORM, int D, int SPLIT = 1>
 __global__ __launch_bounds__(512) void k_gemv_wpt(KParams p)
 {
@@ -1117,6 +1180,31 @@ __global__ __launch_bounds__(512) void k_gemv_wpt(KParams p)
     const uint32_t first = blockIdx.x + gridDim.x * (wave % TW), stride = gridDim.x * TW;
     const uint32_t ntile = first < p.tiles ? (p.tiles - first + stride - 1u) / stride : 0u;
     const uint32_t S = ntile * npass;
+
+    // in-launch greedy acceptance (EPI_LOGITS with acc_slots): this launch's
+    // count; the last workgroup also loads the drafts and each sequence's
+    // rollback reads, in flight with its weight stream
+    __shared__ int32_t acc_draft[OPURE_MAX_ROWS];
+    __shared__ int32_t acc_am[OPURE_MAX_ROWS];
+    __shared__ opure_hip::RollbackPre acc_pre[OPURE_MAX_ROWS];
+    uint32_t acc_tag = 0u;
+    bool acc_last = false;
+    if constexpr (EPI == opure_hip::EPI_LOGITS)
+        if (p.lg.acc_slots)
+        {
+            acc_tag = __hip_atomic_load(p.lg.acc_epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            acc_last = blockIdx.x == gridDim.x - 1u;
+            if (acc_last)
+            {
+                if (threadIdx.x < p.lg.batch * p.lg.K)
+                {
+                    const uint32_t b = threadIdx.x / p.lg.K, j = threadIdx.x - b * p.lg.K;
+                    acc_draft[threadIdx.x] = p.lg.drafts[static_cast<uint64_t>(b) * p.lg.drafts_stride + j];
+                }
+                if (p.lg.rollback && threadIdx.x >= 64u && threadIdx.x < 64u + p.lg.batch)
+                    acc_pre[threadIdx.x - 64u] = opure_hip::rollback_pre(p.lg.rb, threadIdx.x - 64u);
+            }
+        }
 
     struct PL {
         u4_t w[U];
@@ -1313,9 +1401,21 @@ __global__ __launch_bounds__(512) void k_gemv_wpt(KParams p)
             int32_t i = si[threadIdx.x];
 #pragma unroll
             for (int w = 1; w < NW; ++w) best_merge(v, i, sv[w * 16 + threadIdx.x], si[w * 16 + threadIdx.x]);
-            p.lg.am_val[static_cast<uint64_t>(blockIdx.x) * M + threadIdx.x] = v;
-            p.lg.am_idx[static_cast<uint64_t>(blockIdx.x) * M + threadIdx.x] = i;
+            if (p.lg.acc_slots)
+            {
+                uint64_t* w = p.lg.acc_slots + (static_cast<uint64_t>(blockIdx.x) * M + threadIdx.x) * 2u;
+                __hip_atomic_store(w, (static_cast<uint64_t>(acc_tag) << 32) | __float_as_uint(v), __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(w + 1, (static_cast<uint64_t>(acc_tag) << 32) | static_cast<uint32_t>(i),
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            else
+            {
+                p.lg.am_val[static_cast<uint64_t>(blockIdx.x) * M + threadIdx.x] = v;
+                p.lg.am_idx[static_cast<uint64_t>(blockIdx.x) * M + threadIdx.x] = i;
+            }
         }
+        if (acc_last) greedy_accept_in_launch(p, M, acc_tag, acc_draft, acc_am, acc_pre);
     }
 }
 

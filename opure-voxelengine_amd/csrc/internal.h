@@ -17,6 +17,11 @@
 // ---------------------------------------------------------------------------
 constexpr uint32_t REJ_SYNC_SEQS = 4096;
 constexpr uint64_t REJ_SYNC_BYTES = REJ_SYNC_SEQS * 4ull + REJ_SYNC_SEQS * 64ull * 6ull * 8ull;
+// The LM head's in-launch greedy acceptance: tagged (value, index) words of
+// up to ACC_SYNC_WGS workgroups x OPURE_MAX_ROWS rows, then the launch count
+constexpr uint32_t ACC_SYNC_WGS = 4096;
+constexpr uint64_t ACC_SYNC_SLOT_BYTES = uint64_t(ACC_SYNC_WGS) * 16u * 2u * 8u;
+constexpr uint64_t ACC_SYNC_BYTES = ACC_SYNC_SLOT_BYTES + 256u;
 
 struct opure_dev {
     int         ordinal = 0;
@@ -37,6 +42,14 @@ struct opure_dev {
     // then the sequences' slots [REJ_SYNC_SEQS][64 slices][6] u64, whose tags
     // carry the launch count, so no clear is needed between launches.
     void*       rej_sync = nullptr;
+    // The LM head's in-launch greedy acceptance state (ACC_SYNC_BYTES): the
+    // workgroups' tagged words, zeroed, then the launch count, which starts
+    // at 0x01010101 (a zero word never carries a live tag); reset after a
+    // bounded wait gave up (check_device_errors)
+    void*       acc_sync = nullptr;
+    // greedy acceptance inside the LM head's launch where the shape allows
+    // (opure_debug_set_greedy_acceptance)
+    uint32_t    greedy_mode = OPURE_GREEDY_IN_LM_HEAD;
     // Conditions a kernel found that make its outputs invalid, one word each
     // (ERR_* below), in pinned host memory: a kernel sets a word with an
     // ordinary store, the host reads and clears it after the stream is idle
@@ -86,6 +99,8 @@ const char* afmt_name(uint32_t afmt);
 int  ensure_workspace(opure_dev* dev, uint64_t bytes);
 // the error words a kernel reported since the last check, as an OPURE_E_* code (cleared)
 int  check_device_errors(opure_dev* dev);
+// zero the in-launch greedy acceptance's words and restart its launch count (async on dev->stream)
+hipError_t reset_acc_sync(opure_dev* dev);
 // open / close a stage of an eager verify step (no-op unless profiling, or while capturing)
 int  prof_begin(opure_dev* dev, uint32_t stage);
 int  prof_end(opure_dev* dev);
@@ -148,9 +163,34 @@ struct QkvEpilogue {
     uint32_t* err = nullptr;     // opure_dev::err: a row past the tables sets ERR_POSITION
 };
 
+// The KV rollback of a sequence after acceptance (rollback.h)
+struct RollbackParams {
+    void* pool;
+    int32_t* page_table;
+    uint32_t max_pages, n_pages, n_layers, n_kv, hd, afmt, K;
+    const int32_t* seq_len;
+    const int32_t* accepted;
+    int32_t* new_len;
+    int32_t* freed;
+    uint32_t freed_stride;
+    int32_t* n_freed;
+    uint32_t poison, poison_bits;
+};
+
 struct LogitsEpilogue {
     float*   am_val = nullptr;   // [workgroups][M]: best logit of each column per workgroup
     int32_t* am_idx = nullptr;   // its vocabulary index (lowest on ties)
+    // Greedy acceptance (and the rollback) inside the LM head's launch, when
+    // acc_slots is set (wave-per-tile kernel): every workgroup publishes its
+    // rows' bests as tagged words, the last-dispatched workgroup gathers them
+    // and accepts, as k_accept_greedy does from am_val / am_idx.
+    uint64_t* acc_slots = nullptr;   // [workgroups][M][2]: (tag << 32) | value bits, (tag << 32) | index
+    uint32_t* acc_epoch = nullptr;   // the launch count that tags them
+    const int32_t* drafts = nullptr; // [batch][drafts_stride], K of them a sequence
+    uint32_t drafts_stride = 0, K = 0, batch = 0, wait_limit = 0, rollback = 0;
+    int32_t* out_tokens = nullptr;   // [batch][K + 1]
+    int32_t* accepted = nullptr;     // [batch]
+    RollbackParams rb{};
 };
 
 struct GemvCall {
@@ -192,6 +232,9 @@ int gemv_launch(opure_dev* dev, const GemvCall& c);
 // workgroups gemv_launch runs for this call (EPI_LOGITS writes one argmax
 // partial per workgroup and column)
 uint32_t gemv_grid(const opure_dev* dev, const GemvCall& c);
+// whether gemv_launch runs this call on the wave-per-tile kernel (the one whose
+// EPI_LOGITS can accept greedily in the launch)
+bool gemv_is_wave_per_tile(const opure_dev* dev, const GemvCall& c);
 // device-side tiled-layout helpers shared with the embedding gather
 uint32_t tiled_block_k(uint32_t wfmt);      // k values per 64-byte block
 
@@ -208,6 +251,7 @@ uint32_t argmax_parts(uint32_t vocab);
 uint64_t accept_ws_bytes(uint32_t batch, uint32_t k, uint32_t vocab, uint32_t mode);
 int      accept_validate(const opure_accept_args* a, bool rejection);
 // `rb` (may be null): run that rollback inside the acceptance kernel
+RollbackParams rollback_params(const opure_rollback_args* a);
 int      greedy_from_partials(opure_dev* dev, const float* am_val, const int32_t* am_idx, uint32_t parts,
                               uint32_t batch, uint32_t K, const int32_t* drafts, uint32_t stride, int32_t* out_tokens,
                               int32_t* accepted, const opure_rollback_args* rb);

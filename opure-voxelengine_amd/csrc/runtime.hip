@@ -66,14 +66,31 @@ int ensure_workspace(opure_dev* dev, uint64_t bytes)
     return OPURE_OK;
 }
 
+hipError_t reset_acc_sync(opure_dev* dev)
+{
+    hipError_t e = hipMemsetAsync(dev->acc_sync, 0, ACC_SYNC_SLOT_BYTES, dev->stream);
+    if (e == hipSuccess)
+        e = hipMemsetAsync(static_cast<uint8_t*>(dev->acc_sync) + ACC_SYNC_SLOT_BYTES, 0x01, 4u, dev->stream);
+    return e;
+}
+
 int check_device_errors(opure_dev* dev)
 {
     if (!dev->err) return OPURE_OK;
     uint32_t w[ERR_WORDS];
     for (uint32_t i = 0; i < ERR_WORDS; ++i) { w[i] = dev->err[i]; dev->err[i] = 0u; }
+    if (w[ERR_WAIT] && dev->acc_sync && !dev->capturing)
+    {
+        // a given-up in-launch acceptance may leave words a later launch would
+        // take for its own: start that state afresh (the stream is idle here)
+        hipError_t e = reset_acc_sync(dev);
+        if (e == hipSuccess) e = hipStreamSynchronize(dev->stream);
+        if (e != hipSuccess) return hip_fail(e, "resetting the in-launch acceptance state");
+    }
     if (w[ERR_WAIT])
-        return set_error(OPURE_E_DEVICE, "a bounded wait gave up (between a GEMV's waves, or between a rejection "
-                         "step's slices; after %u sleeps): that launch's outputs are invalid%s%s", dev->wait_limit,
+        return set_error(OPURE_E_DEVICE, "a bounded wait gave up (between a GEMV's waves, between a rejection "
+                         "step's slices, or in the LM head's greedy acceptance; after %u sleeps): that launch's "
+                         "outputs are invalid%s%s", dev->wait_limit,
                          w[ERR_TOKEN] ? "; a token id was outside the vocabulary" : "",
                          w[ERR_POSITION] ? "; a position reached past max_ctx or the page table" : "");
     if (w[ERR_TOKEN])
@@ -154,9 +171,12 @@ int opure_dev_create(int ordinal, opure_dev** out)
                                            hipHostMallocCoherent);
     if (e == hipSuccess) e = hipMalloc(&d->rej_sync, REJ_SYNC_BYTES);
     if (e == hipSuccess) e = hipMemsetAsync(d->rej_sync, 0, REJ_SYNC_BYTES, d->stream);
+    if (e == hipSuccess) e = hipMalloc(&d->acc_sync, ACC_SYNC_BYTES);
+    if (e == hipSuccess) e = reset_acc_sync(d);
     if (e == hipSuccess) e = hipStreamSynchronize(d->stream);
     if (e != hipSuccess)
     {
+        if (d->acc_sync) hipFree(d->acc_sync);
         if (d->rej_sync) hipFree(d->rej_sync);
         if (d->err) hipHostFree(d->err);
         if (d->ev_end) hipEventDestroy(d->ev_end);
@@ -179,6 +199,7 @@ int opure_dev_destroy(opure_dev* dev)
     for (void* p : dev->retired_ws) hipFree(p);
     if (dev->err) hipHostFree(dev->err);
     if (dev->rej_sync) hipFree(dev->rej_sync);
+    if (dev->acc_sync) hipFree(dev->acc_sync);
     for (hipEvent_t e : dev->prof_ev) hipEventDestroy(e);
     if (dev->ev_begin) hipEventDestroy(dev->ev_begin);
     if (dev->ev_end) hipEventDestroy(dev->ev_end);
@@ -352,6 +373,15 @@ int opure_debug_set_rejection_launches(opure_dev* dev, uint32_t mode)
     OPURE_REQUIRE(mode == OPURE_REJ_ONE_LAUNCH || mode == OPURE_REJ_STAGED, OPURE_E_INVALID,
                   "opure_debug_set_rejection_launches: mode %u", mode);
     dev->rej_mode = mode;
+    return OPURE_OK;
+}
+
+int opure_debug_set_greedy_acceptance(opure_dev* dev, uint32_t mode)
+{
+    OPURE_REQUIRE(dev, OPURE_E_INVALID, "opure_debug_set_greedy_acceptance: null device");
+    OPURE_REQUIRE(mode == OPURE_GREEDY_IN_LM_HEAD || mode == OPURE_GREEDY_SEPARATE, OPURE_E_INVALID,
+                  "opure_debug_set_greedy_acceptance: mode %u", mode);
+    dev->greedy_mode = mode;
     return OPURE_OK;
 }
 

@@ -439,9 +439,7 @@ int opure_verify_step(opure_dev* dev, const opure_verify_args* a)
         c.epi = wide ? EPI_STORE : EPI_LOGITS;
     c.logits.am_val = reinterpret_cast<float*>(ws + P.am_val);
     c.logits.am_idx = reinterpret_cast<int32_t*>(ws + P.am_idx);
-    if ((rc = gemv_validate(c)) || (rc = prof_begin(dev, OPURE_STAGE_LM_HEAD)) || (rc = gemv_launch(dev, c)) ||
-        (rc = prof_end(dev)))
-        return rc;
+    if ((rc = gemv_validate(c))) return rc;
 
     opure_rollback_args rb{};
     if (a->rollback)
@@ -460,8 +458,29 @@ int opure_verify_step(opure_dev* dev, const opure_verify_args* a)
         rb.poison_bits = a->poison_bits;
         if ((rc = rollback_validate(&rb))) return rc;
     }
+    // greedy acceptance and the rollback inside the LM head's launch: its last
+    // workgroup gathers the others' argmax words (wave-per-tile kernel only)
+    const bool fused = a->accept_mode == OPURE_ACCEPT_GREEDY && !wide && dev->acc_sync &&
+                       dev->greedy_mode == OPURE_GREEDY_IN_LM_HEAD && gemv_is_wave_per_tile(dev, c) &&
+                       gemv_grid(dev, c) <= ACC_SYNC_WGS;
+    if (fused)
+    {
+        c.logits.acc_slots = static_cast<uint64_t*>(dev->acc_sync);
+        c.logits.acc_epoch = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(dev->acc_sync) + ACC_SYNC_SLOT_BYTES);
+        c.logits.drafts = a->tokens + 1;
+        c.logits.drafts_stride = R;
+        c.logits.K = R - 1u;
+        c.logits.batch = B;
+        c.logits.wait_limit = dev->wait_limit;
+        c.logits.out_tokens = a->out_tokens;
+        c.logits.accepted = a->accepted;
+        c.logits.rollback = a->rollback ? 1u : 0u;
+        if (a->rollback) c.logits.rb = rollback_params(&rb);
+    }
+    if ((rc = prof_begin(dev, OPURE_STAGE_LM_HEAD)) || (rc = gemv_launch(dev, c)) || (rc = prof_end(dev))) return rc;
+
     if (a->accept_mode != OPURE_ACCEPT_NONE && (rc = prof_begin(dev, OPURE_STAGE_ACCEPT))) return rc;
-    if (a->accept_mode == OPURE_ACCEPT_GREEDY)
+    if (a->accept_mode == OPURE_ACCEPT_GREEDY && !fused)
     {
         // greedy acceptance and the rollback run in one kernel
         uint32_t parts = 0;

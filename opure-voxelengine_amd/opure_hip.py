@@ -26,6 +26,7 @@ ACCEPT_NONE, ACCEPT_GREEDY, ACCEPT_REJECTION = 0, 1, 2
 BW_READ, BW_COPY = 0, 1
 GEMV_MFMA, GEMV_VALU = 0, 1
 REJ_ONE_LAUNCH, REJ_STAGED = 0, 1
+GREEDY_IN_LM_HEAD, GREEDY_SEPARATE = 0, 1
 
 
 class OpureError(RuntimeError):
@@ -156,6 +157,7 @@ def _declare(L):
         "opure_debug_set_wait_limit": ([vp, u32], i),
         "opure_debug_set_gemv_engine": ([vp, u32], i),
         "opure_debug_set_rejection_launches": ([vp, u32], i),
+        "opure_debug_set_greedy_acceptance": ([vp, u32], i),
         "opure_debug_exp_check": ([vp, C.POINTER(u64)], i),
         "opure_debug_verify_offsets": ([C.POINTER(Model), u32, u32, u32, C.POINTER(u64)], i),
         "opure_tiled_bytes": ([u32, u32, u32, C.POINTER(u64), C.POINTER(u64)], i),

@@ -185,6 +185,61 @@ def test_verify_with_rollback_matches_oracle(dev):
     assert diff[keep].max() <= 2e-2
 
 
+@pytest.mark.parametrize("fmt", [(O.W_I8PC, O.A_F16), (O.W_F32, O.A_F32), (O.W_I4G128, O.A_BF16)],
+                         ids=["i8-f16", "f32", "i4-bf16"])
+def test_greedy_acceptance_in_lm_head_same_as_separate(dev, fmt):
+    """A vocabulary of 2048 tiles puts the LM head on the wave-per-tile kernel,
+    whose last workgroup then accepts greedily and rolls back inside the
+    launch.  Tokens, accepted lengths, new lengths, freed pages, page table and
+    poisoned pool equal the separate acceptance launch's
+    (opure_debug_set_greedy_acceptance), on two steps in a row (the second
+    with the next launch count), and the oracle's acceptance of the logits."""
+    m = small_model(*fmt, vocab=32768)
+    B, R = 2, 6
+    kv = random_cache(m, B, 512, 64, seed=21)
+    seq_len = np.array([260, 97], np.int32)
+    kv_o = O.HostKV(m, n_pages=kv.n_pages, batch=B, max_pages_per_seq=kv.max_pages)
+    kv_o.pool[...] = kv.pool
+    kv_o.page_table[...] = kv.page_table
+    tokens = np.random.default_rng(8).integers(0, m.cfg["vocab"], size=(B, R)).astype(np.int32)
+    tokens = self_drafts(m, kv_o, kv.pool.copy(), tokens, seq_len, seq=0)
+    dm = device_model(dev, m)
+    poison = 0x7E00 if fmt[1] != O.A_F32 else 0x7FC00000
+    res = {}
+    lib = H.lib()
+    try:
+        for mode in (H.GREEDY_SEPARATE, H.GREEDY_IN_LM_HEAD):
+            H.check(lib.opure_debug_set_greedy_acceptance(dev.h, mode))
+            outs = []
+            for rep in range(2):
+                dkv = device_kv(dev, m, kv)
+                run = VerifyRunner(dev, dm, dkv, B, R, 512)
+                run.step(tokens, seq_len, accept=H.ACCEPT_GREEDY, rollback=True, poison=True, poison_bits=poison,
+                         free_pages=True)
+                out, acc = run.get_accept()
+                outs.append((run.get_logits(), out, acc, dev.download(run.new_len, np.int32, (B,)),
+                             dev.download(run.n_freed, np.int32, (B,)), dev.download(run.freed, np.int32, (B, 8)),
+                             dkv.get_page_table(), dkv.get_pool()))
+            res[mode] = outs
+    finally:
+        H.check(lib.opure_debug_set_greedy_acceptance(dev.h, H.GREEDY_IN_LM_HEAD))
+    sep, fus = res[H.GREEDY_SEPARATE], res[H.GREEDY_IN_LM_HEAD]
+    for rep in range(2):
+        for k, (x, y) in enumerate(zip(sep[rep], fus[rep])):
+            if k == 5:   # freed entries past n_freed are not written
+                for b in range(B):
+                    n = int(sep[rep][4][b])
+                    assert np.array_equal(x[b, :n], y[b, :n]), (rep, b)
+            else:   # bit for bit (the fp32 poison is a NaN)
+                assert np.array_equal(np.ascontiguousarray(x).view(np.uint8), np.ascontiguousarray(y).view(np.uint8)), (rep, k)
+    logits, out, acc = fus[0][0], fus[0][1], fus[0][2]
+    w_out, w_acc = O.accept_greedy(logits, tokens[:, 1:])
+    assert np.array_equal(out, w_out) and np.array_equal(acc, w_acc)
+    if fmt[1] != O.A_BF16:      # bf16 activations may part from the oracle's own greedy drafts
+        assert acc[0] == R - 1
+    say("accepted", acc.tolist(), "freed", fus[0][4].tolist())
+
+
 def _full_width(wfmt, afmt, shape, n_layers, vocab, seed, attn_scale):
     h, nh, nkv, hd, ff = shape
     return O.HostModel(n_layers=n_layers, hidden=h, n_heads=nh, n_kv_heads=nkv, head_dim=hd, ffn=ff, vocab=vocab,
