@@ -130,8 +130,12 @@ def test_rows_equal_single_row_steps(dev, fmt):
         assert np.array_equal(one.get_logits()[0, 0], lm[0, j]), j
 
 
-def test_graph_replay_equals_eager(dev):
-    m = small_model(O.W_I8PC, O.A_F16)
+@pytest.mark.parametrize("vocab", [1024, 32768], ids=["lm-head-k_gemv", "lm-head-wave-per-tile"])
+def test_graph_replay_equals_eager(dev, vocab):
+    """Replays of a captured greedy verify step equal the eager step, with
+    eager work between them; at 2048 vocabulary tiles the LM head accepts in
+    its own launch, each replay with the next launch count."""
+    m = small_model(O.W_I8PC, O.A_F16, vocab=vocab)
     kv = random_cache(m, 2, 256, 32, seed=13)
     dm, dkv = device_model(dev, m), device_kv(dev, m, kv)
     run = VerifyRunner(dev, dm, dkv, 2, 4, 256)
@@ -145,6 +149,7 @@ def test_graph_replay_equals_eager(dev):
     g = dev.graph_end()
     for i in range(4):
         dev.fill_u32(run.logits, 0x7FC00000, 2 * 4 * m.cfg["vocab"])   # eager work between replays
+        dev.fill_u32(run.out_tokens, 0xFFFFFFFF, 2 * 4)
         dev.sync()
         dev.graph_launch(g)
         dev.sync()
