@@ -190,24 +190,32 @@ def test_verify_with_rollback_matches_oracle(dev):
     assert diff[keep].max() <= 2e-2
 
 
+@pytest.mark.parametrize("shape", [(2, 6, (260, 97)), (1, 16, (300,))], ids=["2x6", "1x16"])
 @pytest.mark.parametrize("fmt", [(O.W_I8PC, O.A_F16), (O.W_F32, O.A_F32), (O.W_I4G128, O.A_BF16)],
                          ids=["i8-f16", "f32", "i4-bf16"])
-def test_greedy_acceptance_in_lm_head_same_as_separate(dev, fmt):
+def test_greedy_acceptance_in_lm_head_same_as_separate(dev, fmt, shape):
     """A vocabulary of 2048 tiles puts the LM head on the wave-per-tile kernel,
     whose last workgroup then accepts greedily and rolls back inside the
     launch.  Tokens, accepted lengths, new lengths, freed pages, page table and
     poisoned pool equal the separate acceptance launch's
     (opure_debug_set_greedy_acceptance), on two steps in a row (the second
-    with the next launch count), and the oracle's acceptance of the logits."""
+    with the next launch count), and the oracle's acceptance of the logits.
+    Shapes: two sequences of 6 rows, sequence 0 drafting its own greedy
+    continuation; one sequence of 16 rows (the most rows a step takes), whose
+    drafts past the eighth are moved off that continuation, so at most 8 are
+    accepted and the rollback poisons 7 or more positions."""
+    B, R, ctx = shape
+    say("greedy acceptance in the LM head", fmt, "batch", B, "rows", R)
     m = small_model(*fmt, vocab=32768)
-    B, R = 2, 6
     kv = random_cache(m, B, 512, 64, seed=21)
-    seq_len = np.array([260, 97], np.int32)
+    seq_len = np.array(ctx, np.int32)
     kv_o = O.HostKV(m, n_pages=kv.n_pages, batch=B, max_pages_per_seq=kv.max_pages)
     kv_o.pool[...] = kv.pool
     kv_o.page_table[...] = kv.page_table
     tokens = np.random.default_rng(8).integers(0, m.cfg["vocab"], size=(B, R)).astype(np.int32)
     tokens = self_drafts(m, kv_o, kv.pool.copy(), tokens, seq_len, seq=0)
+    if R > 9:
+        tokens[0, 9:] = (tokens[0, 9:] + 1) % m.cfg["vocab"]
     dm = device_model(dev, m)
     poison = 0x7E00 if fmt[1] != O.A_F32 else 0x7FC00000
     res = {}
@@ -240,7 +248,9 @@ def test_greedy_acceptance_in_lm_head_same_as_separate(dev, fmt):
     logits, out, acc = fus[0][0], fus[0][1], fus[0][2]
     w_out, w_acc = O.accept_greedy(logits, tokens[:, 1:])
     assert np.array_equal(out, w_out) and np.array_equal(acc, w_acc)
-    if fmt[1] != O.A_BF16:      # bf16 activations may part from the oracle's own greedy drafts
+    if R > 9:
+        assert acc[0] <= 8
+    elif fmt[1] != O.A_BF16:    # bf16 activations may part from the oracle's own greedy drafts
         assert acc[0] == R - 1
     say("accepted", acc.tolist(), "freed", fus[0][4].tolist())
 
