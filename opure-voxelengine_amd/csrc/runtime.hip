@@ -176,12 +176,12 @@ int opure_dev_create(int ordinal, opure_dev** out)
     if (e == hipSuccess) e = hipStreamSynchronize(d->stream);
     if (e != hipSuccess)
     {
-        if (d->acc_sync) hipFree(d->acc_sync);
-        if (d->rej_sync) hipFree(d->rej_sync);
-        if (d->err) hipHostFree(d->err);
-        if (d->ev_end) hipEventDestroy(d->ev_end);
-        if (d->ev_begin) hipEventDestroy(d->ev_begin);
-        if (d->stream) hipStreamDestroy(d->stream);
+        if (d->acc_sync) (void)hipFree(d->acc_sync);
+        if (d->rej_sync) (void)hipFree(d->rej_sync);
+        if (d->err) (void)hipHostFree(d->err);
+        if (d->ev_end) (void)hipEventDestroy(d->ev_end);
+        if (d->ev_begin) (void)hipEventDestroy(d->ev_begin);
+        if (d->stream) (void)hipStreamDestroy(d->stream);
         delete d;
         return hip_fail(e, "opure_dev_create");
     }
@@ -193,17 +193,18 @@ int opure_dev_create(int ordinal, opure_dev** out)
 int opure_dev_destroy(opure_dev* dev)
 {
     if (!dev) return OPURE_OK;
-    hipSetDevice(dev->ordinal);
-    hipStreamSynchronize(dev->stream);
-    if (dev->ws) hipFree(dev->ws);
-    for (void* p : dev->retired_ws) hipFree(p);
-    if (dev->err) hipHostFree(dev->err);
-    if (dev->rej_sync) hipFree(dev->rej_sync);
-    if (dev->acc_sync) hipFree(dev->acc_sync);
-    for (hipEvent_t e : dev->prof_ev) hipEventDestroy(e);
-    if (dev->ev_begin) hipEventDestroy(dev->ev_begin);
-    if (dev->ev_end) hipEventDestroy(dev->ev_end);
-    if (dev->stream) hipStreamDestroy(dev->stream);
+    // teardown: a failing release has no remedy here, so its result is dropped
+    (void)hipSetDevice(dev->ordinal);
+    (void)hipStreamSynchronize(dev->stream);
+    if (dev->ws) (void)hipFree(dev->ws);
+    for (void* p : dev->retired_ws) (void)hipFree(p);
+    if (dev->err) (void)hipHostFree(dev->err);
+    if (dev->rej_sync) (void)hipFree(dev->rej_sync);
+    if (dev->acc_sync) (void)hipFree(dev->acc_sync);
+    for (hipEvent_t e : dev->prof_ev) (void)hipEventDestroy(e);
+    if (dev->ev_begin) (void)hipEventDestroy(dev->ev_begin);
+    if (dev->ev_end) (void)hipEventDestroy(dev->ev_end);
+    if (dev->stream) (void)hipStreamDestroy(dev->stream);
     delete dev;
     return OPURE_OK;
 }
@@ -316,7 +317,7 @@ int opure_graph_end(opure_dev* dev, opure_graph** out)
     if (e == hipSuccess) e = hipGraphInstantiate(&g->exec, g->graph, nullptr, nullptr, 0);
     if (e != hipSuccess)
     {
-        if (g->graph) hipGraphDestroy(g->graph);
+        if (g->graph) (void)hipGraphDestroy(g->graph);
         delete g;
         return hip_fail(e, "opure_graph_end");
     }
@@ -336,15 +337,15 @@ int opure_graph_launch(opure_dev* dev, opure_graph* g)
 int opure_graph_destroy(opure_graph* g)
 {
     if (!g) return OPURE_OK;
-    if (g->exec) hipGraphExecDestroy(g->exec);
-    if (g->graph) hipGraphDestroy(g->graph);
+    if (g->exec) (void)hipGraphExecDestroy(g->exec);
+    if (g->graph) (void)hipGraphDestroy(g->graph);
     opure_dev* dev = g->dev;
     delete g;
     if (dev && dev->live_graphs && --dev->live_graphs == 0)
     {
         // no graph can point into a retired workspace any more
-        hipStreamSynchronize(dev->stream);
-        for (void* p : dev->retired_ws) hipFree(p);
+        (void)hipStreamSynchronize(dev->stream);
+        for (void* p : dev->retired_ws) (void)hipFree(p);
         dev->retired_ws.clear();
     }
     return OPURE_OK;
@@ -493,7 +494,7 @@ int opure_bw_measure(opure_dev* dev, uint32_t mode, const void* src, void* dst, 
     if (e == hipSuccess) e = hipEventSynchronize(dev->ev_end);
     float ms = 0.0f;
     if (e == hipSuccess) e = hipEventElapsedTime(&ms, dev->ev_begin, dev->ev_end);
-    hipFree(sink);
+    (void)hipFree(sink);
     if (e != hipSuccess) return hip_fail(e, "opure_bw_measure");
     const double moved = static_cast<double>(bytes) * (mode == OPURE_BW_COPY ? 2.0 : 1.0) * reps;
     *gbs = ms > 0.0f ? moved / (ms * 1e-3) / 1e9 : 0.0;
