@@ -1888,10 +1888,15 @@ int launch_pc(opure_dev* dev, const KParams& kp, uint32_t grid, uint32_t lds)
 #ifndef OPURE_WPT_DEPTH
 #define OPURE_WPT_DEPTH 3
 #endif
+// SPLIT 2 (at most one tile a wave) has two steps a wave at the shapes that
+// take it (the 1B gate/up: 16 of a tile's 32 blocks, 8 a step).  A ring of
+// three would load the second step twice (the prologue fills every slot), so
+// it takes a ring of two: both steps still issue in the prologue (C3 0.6713 ->
+// 0.6487 ms, gate/up 11.7 -> 10.2 us).
 template <int WF, int AF, int EPI, int U, bool NORM, int SPLIT = 1>
 int launch_wpt(opure_dev* dev, const KParams& kp, uint32_t grid, uint32_t lds)
 {
-    constexpr int D = OPURE_WPT_DEPTH;
+    constexpr int D = SPLIT == 2 ? 2 : OPURE_WPT_DEPTH;
     static bool configured = false;
     if (!configured)
     {
