@@ -1083,8 +1083,8 @@ __global__ __launch_bounds__(NW * 64) void k_gemv(KParams p)
 // Wave-per-tile GEMV for shapes with many tiles (1024 and more, so at least
 // four per CU): X staged in LDS as in k_gemv, but each wave owns whole tiles --
 // tile(k) = blockIdx.x + gridDim.x * (wave + NW * k) -- and runs U consecutive
-// blocks per step through a ring of three buffers, so no wave waits for
-// another between tiles.  A tile's sum is its blocks' in block order.  The
+// blocks per step through a ring of two buffers (one step in flight while
+// the other computes), so no wave waits for another between tiles.  A tile's sum is its blocks' in block order.  The
 // uint4 group sums of X are computed once per workgroup on the matrix cores
 // (the same MFMAs as in k_gemv, so the same bits) into LDS xs[G][16].  At a
 // tile's end the wave transposes its accumulator through its own 1 KB of LDS
@@ -1885,18 +1885,15 @@ int launch_pc(opure_dev* dev, const KParams& kp, uint32_t grid, uint32_t lds)
     return OPURE_OK;
 }
 
-#ifndef OPURE_WPT_DEPTH
-#define OPURE_WPT_DEPTH 3
-#endif
-// SPLIT 2 (at most one tile a wave) has two steps a wave at the shapes that
-// take it (the 1B gate/up: 16 of a tile's 32 blocks, 8 a step).  A ring of
-// three would load the second step twice (the prologue fills every slot), so
-// it takes a ring of two: both steps still issue in the prologue (C3 0.6713 ->
-// 0.6487 ms, gate/up 11.7 -> 10.2 us).
+// A ring of two steps.  Three kept one more 8 KB step a wave queued behind the
+// stream, and where a wave has only two steps (SPLIT 2: the 1B gate/up, 16 of
+// a tile's 32 blocks, 8 a step) the prologue, which fills every slot, loaded
+// the second step twice: two instead of three measured C3 0.6713 -> 0.6487 ms
+// (gate/up 11.7 -> 10.2 us), then the LM heads 0.2-0.6 % faster (C3, C1).
 template <int WF, int AF, int EPI, int U, bool NORM, int SPLIT = 1>
 int launch_wpt(opure_dev* dev, const KParams& kp, uint32_t grid, uint32_t lds)
 {
-    constexpr int D = SPLIT == 2 ? 2 : OPURE_WPT_DEPTH;
+    constexpr int D = 2;
     static bool configured = false;
     if (!configured)
     {
