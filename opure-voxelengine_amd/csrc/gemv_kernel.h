@@ -1885,11 +1885,14 @@ int launch_pc(opure_dev* dev, const KParams& kp, uint32_t grid, uint32_t lds)
     return OPURE_OK;
 }
 
-// A ring of two steps.  Three kept one more 8 KB step a wave queued behind the
+// A ring of two steps.  Three kept one more step a wave queued behind the
 // stream, and where a wave has only two steps (SPLIT 2: the 1B gate/up, 16 of
 // a tile's 32 blocks, 8 a step) the prologue, which fills every slot, loaded
 // the second step twice: two instead of three measured C3 0.6713 -> 0.6487 ms
 // (gate/up 11.7 -> 10.2 us), then the LM heads 0.2-0.6 % faster (C3, C1).
+// Whole-tile waves (the LM heads) take 4 blocks a step, 4 KB in flight a wave
+// (8 blocks: C3 0.647 -> 0.646 ms, C4 2.164 -> 2.154 ms; 2 blocks or a ring
+// of three slower); the split tiles keep 8 (4: C3 0.645 -> 0.650 ms).
 template <int WF, int AF, int EPI, int U, bool NORM, int SPLIT = 1>
 int launch_wpt(opure_dev* dev, const KParams& kp, uint32_t grid, uint32_t lds)
 {
@@ -1928,7 +1931,7 @@ int launch(opure_dev* dev, const KParams& kp, uint32_t grid, uint32_t lds)
 // 4096-long row (int4) so a workgroup's first one or two groups are in flight
 // from its start.
 struct Recipe { uint32_t nw, t, u, wpt = 0; };
-constexpr Recipe R_WPT{8, 1, 8, 1};   // at least four tiles per wave: waves own whole tiles (staged X)
+constexpr Recipe R_WPT{8, 1, 4, 1};   // at least four tiles per wave: waves own whole tiles (staged X)
 constexpr Recipe R_WIDE{8, 2, 4};     // many tiles: 2 tiles share each X fragment
 constexpr Recipe R_WIDE16{16, 2, 2};  // 320 to 1023 tiles: 2 tiles a group on 16 waves
 constexpr Recipe R_MID{8, 1, 4};      // about one tile per CU, rows of 8192 or more: 8 waves (paired X)
@@ -1950,7 +1953,7 @@ int launch_recipe(opure_dev* dev, const KParams& kp, const Recipe& r, uint32_t g
             if (r.wpt == 2) return launch_pc<WF, AF, EPI, NORM>(dev, kp, grid, lds);
             if (r.wpt == 4) return launch_wpt<WF, AF, EPI, 8, NORM, 2>(dev, kp, grid, lds);
         }
-        if (r.wpt) return launch_wpt<WF, AF, EPI, 8, NORM>(dev, kp, grid, lds);
+        if (r.wpt) return launch_wpt<WF, AF, EPI, 4, NORM>(dev, kp, grid, lds);
         if (r.nw == 16 && r.t == 2) return launch<WF, AF, EPI, 16, 2, 2, NORM, XM_STAGED>(dev, kp, grid, lds);
         if (r.nw == 8 && r.t == 2) return launch<WF, AF, EPI, 8, 2, 4, NORM, XM_STAGED>(dev, kp, grid, lds);
         if (r.nw == 8) return launch<WF, AF, EPI, 8, 1, 4, NORM, XM_STAGED>(dev, kp, grid, lds);
